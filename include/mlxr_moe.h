@@ -1,0 +1,233 @@
+/*
+ * mlxr_moe.h -- C ABI of the MI355X (gfx950) sparse-MoE block.
+ *
+ * Drop-in boundary for mlxr-lm's MoE hot path.  The reference reaches MLX
+ * through mlx-c (crates/mlxr-sys, bindgen of mlx.h); each entry point below
+ * replaces one mlx-c call (or one Rust module method built from several),
+ * cited as path:line under /root/reference.  Conventions, following mlx-c:
+ *
+ *   - Every function returns int: 0 = success (crates/mlxr/src/utils/mod.rs:
+ *     18-19).  On failure nothing is enqueued and mlxr_moe_last_error()
+ *     returns a description (thread-local, like the handler slot of
+ *     crates/mlxr/src/error.rs:229-258).  Nothing is thrown across the ABI.
+ *   - Arrays are caller-owned device pointers with explicit shapes (no
+ *     mlx_array handles).  Optional arrays are NULL (mlx_array_new()).
+ *     Optional ints use mlxr_moe_optional_int (mlx_optional_int,
+ *     crates/mlxr/src/ops/quantization.rs:16-21).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream)
+ *     and the call returns without synchronising; the caller syncs, as with
+ *     mlx_async_eval (crates/mlxr/src/transforms/mod.rs:65-83).
+ *   - Scratch memory is a caller-provided device workspace whose size the
+ *     matching *_workspace_size function returns; the library never
+ *     allocates device memory in these calls.
+ *   - Index values live on the device and are not read by the host.  An
+ *     index outside its range leaves its row out of the computation and sets
+ *     a device status word; mlxr_moe_workspace_status() reads it (and
+ *     synchronises the stream).
+ *
+ * dtypes: MLXR_MOE_FLOAT32, MLXR_MOE_BFLOAT16 (bf16 as raw uint16 bits).
+ * Quantisation: mode "affine" (or NULL), group_size 64 (32 and 128 also for
+ * quantize/dequantize), bits 4 or 8 (2 also for quantize/dequantize).
+ */
+#ifndef MLXR_MOE_H
+#define MLXR_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mlxr_moe_stream; /* hipStream_t */
+
+enum { MLXR_MOE_FLOAT32 = 0, MLXR_MOE_BFLOAT16 = 1 };
+
+/* mlx_optional_int (crates/mlxr/src/ops/quantization.rs:16-21) */
+typedef struct {
+  int32_t value;
+  int32_t has_value;
+} mlxr_moe_optional_int;
+
+/* Last error of the calling thread ("" if none).  Replaces the error-handler
+ * slot read by get_and_clear_last_mlx_error (crates/mlxr/src/error.rs:
+ * 275-290); the string stays valid until the thread's next failing call. */
+const char* mlxr_moe_last_error(void);
+
+/* ABI version (major * 10000 + minor * 100 + patch). */
+int mlxr_moe_version(void);
+
+/* Quantise w [rows, cols] (f32 or bf16) to packed codes wq [rows,
+ * cols*bits/32] and scales/biases [rows, cols/group_size] in w's dtype.
+ * Replaces mlx_quantize as called by quantize_device
+ * (crates/mlxr/src/ops/quantization.rs:47-70); defaults g64 / 4-bit
+ * (quantization.rs:11-13). */
+int mlxr_moe_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
+                      mlxr_moe_optional_int group_size,
+                      mlxr_moe_optional_int bits, const char* mode,
+                      uint32_t* wq, void* scales, void* biases,
+                      mlxr_moe_stream stream);
+
+/* out [rows, cols] (out_dtype) = code * scale + bias, evaluated as one fused
+ * multiply-add rounded once.  Replaces mlx_dequantize as called by
+ * dequantize_device (crates/mlxr/src/ops/quantization.rs:118-146).
+ * biases are required for mode "affine". */
+int mlxr_moe_dequantize(const uint32_t* wq, const void* scales,
+                        const void* biases, int sb_dtype, int64_t rows,
+                        int64_t cols, mlxr_moe_optional_int group_size,
+                        mlxr_moe_optional_int bits, const char* mode,
+                        void* out, int out_dtype, mlxr_moe_stream stream);
+
+/* gather_qmm with transpose = true.  x bf16 [x_batch, M, K]; w [E, N,
+ * K*bits/32]; scales/biases bf16 [E, N, K/group]; rhs_indices uint32 [B];
+ * out bf16 [B, M, N]:
+ *   out[b] = x[xb(b)] @ dequant(w[rhs_indices[b]])^T
+ * xb(b) = lhs_indices[b] when given, else b / (B / x_batch) -- the
+ * broadcast of x [..., T, 1, 1, K] against indices [..., T, top_k] in
+ * SplitSwitchFfn::forward (crates/mlxr-lm/src/nn/switch.rs:417-442).
+ * Replaces mlx_gather_qmm as called by gather_qmm_device
+ * (crates/mlxr/src/ops/quantization.rs:171-221).  `sorted_indices` is the
+ * reference's locality hint; rows are always grouped by expert here.
+ * Requires N % 64 == 0, K % 64 == 0, group 64, bits 4 or 8. */
+size_t mlxr_moe_gather_qmm_workspace_size(int64_t B, int64_t M,
+                                          int64_t num_experts);
+int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
+                        int64_t M, int64_t K, const uint32_t* w,
+                        const void* scales, const void* biases, int sb_dtype,
+                        int64_t num_experts, int64_t N,
+                        const uint32_t* lhs_indices,
+                        const uint32_t* rhs_indices, int64_t B, int transpose,
+                        mlxr_moe_optional_int group_size,
+                        mlxr_moe_optional_int bits, const char* mode,
+                        int sorted_indices, void* out, int out_dtype,
+                        void* workspace, size_t workspace_size,
+                        mlxr_moe_stream stream);
+
+/* Indices that partition each row of a [rows, n] f32 (axis = -1 or 1):
+ * out[.., kth] holds the element of sorted rank kth, smaller before, larger
+ * after (the full ascending order, ties by index, is returned).  kth in
+ * [-n, n).  Replaces mlx_argpartition_axis (crates/mlxr/src/ops/sort.rs:
+ * 211-226); invalid axis or kth fail like sort.rs:262-301 expects. */
+int mlxr_moe_argpartition(const float* a, int64_t rows, int64_t n, int kth,
+                          int axis, uint32_t* out, mlxr_moe_stream stream);
+
+/* Row softmax of a [rows, n] f32 over axis -1, computed in f32 (`precise`
+ * accepted for either value).  Replaces mlx_softmax_axis
+ * (crates/mlxr/src/ops/arithmetic.rs:1298-1311). */
+int mlxr_moe_softmax(const float* a, int64_t rows, int64_t n, int axis,
+                     int precise, float* out, mlxr_moe_stream stream);
+
+/* Router of Qwen35MoeBlock::forward (crates/mlxr-lm/src/qwen3_5/text/
+ * moe.rs:122-138): logits = x @ gate_w^T (f32), softmax, top-K, weights
+ * renormalised to sum 1.  x bf16 [T, d]; gate_w f32 [E, d]; topk_idx int32
+ * [T, K] in descending logit order (ties to the lower id; the reference's
+ * order inside the partition is undefined, sort.rs:188); topk_w f32
+ * [T, K].  Workspace holds the [T, E] logits. */
+size_t mlxr_moe_router_workspace_size(int64_t T, int64_t E);
+int mlxr_moe_router_topk(const void* x, int64_t T, int64_t d,
+                         const float* gate_w, int64_t E, int64_t K,
+                         int32_t* topk_idx, float* topk_w, void* workspace,
+                         size_t workspace_size, mlxr_moe_stream stream);
+
+/* Stable sort of flat expert ids [n] by expert: the permutation of
+ * gather_sort (crates/mlxr-lm/src/nn/switch.rs:499-512), order =
+ * argsort(ids) into `sorted`, inv = argsort(order) into `inv`, plus
+ * per-expert counts [E] and offsets [E+1]. */
+size_t mlxr_moe_dispatch_workspace_size(int64_t n, int64_t E);
+int mlxr_moe_dispatch(const int32_t* ids, int64_t n, int64_t E,
+                      int32_t* counts, int32_t* offsets, int32_t* sorted,
+                      int32_t* inv, void* workspace, size_t workspace_size,
+                      mlxr_moe_stream stream);
+
+/* out f32 [T, d] = sum_k w[t,k] * y[t,k,:] (+ shared_y[t,:] *
+ * sigmoid(shared_logit[t])).  y bf16 [T, K, d]; shared_y bf16 [T, d] or
+ * NULL.  Replaces combine_with_weights (crates/mlxr-lm/src/nn/switch.rs:
+ * 223-234) and the shared branch of moe.rs:117-120,145. */
+int mlxr_moe_combine(const void* y, const float* w, int64_t T, int64_t K,
+                     int64_t d, const void* shared_y,
+                     const float* shared_logit, float* out,
+                     mlxr_moe_stream stream);
+
+/* One QuantizedSwitchLinear (crates/mlxr-lm/src/nn/switch.rs:115-168) or
+ * QuantizedLinear (num_experts = 1; crates/mlxr/src/layers/quantized.rs:
+ * 214-379): weight u32 [E, output_dims, input_dims*bits/32], scales and
+ * biases bf16 [E, output_dims, input_dims/group_size]. */
+typedef struct {
+  const uint32_t* weight;
+  const void* scales;
+  const void* biases;
+  int64_t num_experts;
+  int64_t output_dims;
+  int64_t input_dims;
+  int32_t group_size;
+  int32_t bits;
+} mlxr_moe_qlinear;
+
+/* SplitSwitchFfn<SwigluActivation> (crates/mlxr-lm/src/nn/switch.rs:
+ * 366-491): gate_proj, up_proj [E, f, d], down_proj [E, d, f]. */
+typedef struct {
+  mlxr_moe_qlinear gate_proj;
+  mlxr_moe_qlinear up_proj;
+  mlxr_moe_qlinear down_proj;
+} mlxr_moe_switch_glu;
+
+/* SplitSwitchFfn::forward_with_combine (switch.rs:446-474): x bf16 [T, d],
+ * indices int32 [T, K], weights f32 [T, K] -> out f32 [T, d]. */
+size_t mlxr_moe_switch_glu_workspace_size(const mlxr_moe_switch_glu* ffn,
+                                          int64_t T, int64_t K);
+int mlxr_moe_switch_glu_forward(const mlxr_moe_switch_glu* ffn, const void* x,
+                                int64_t T, const int32_t* indices,
+                                const float* weights, int64_t K, float* out,
+                                void* workspace, size_t workspace_size,
+                                mlxr_moe_stream stream);
+
+/* SplitSwitchFfn::forward (switch.rs:417-442): per-expert outputs
+ * y bf16 [T, K, d] before the combine.  Same workspace size as
+ * mlxr_moe_switch_glu_forward. */
+int mlxr_moe_switch_glu_experts(const mlxr_moe_switch_glu* ffn, const void* x,
+                                int64_t T, const int32_t* indices, int64_t K,
+                                void* y, void* workspace,
+                                size_t workspace_size, mlxr_moe_stream stream);
+
+/* Qwen35MoeBlock (crates/mlxr-lm/src/qwen3_5/text/moe.rs:43-159):
+ * f32 router gate_weight [E, d] with optional f32 gate_bias [E] (Linear
+ * with bias = addmm, crates/mlxr/src/layers/linear.rs:91-95; the Qwen
+ * checkpoints build it without, moe.rs:90-92); switch_mlp; optional shared
+ * expert
+ * (SwigluMlp, crates/mlxr-lm/src/nn/swiglu_mlp.rs:24-75, num_experts = 1)
+ * with f32 shared_expert_gate_weight [1, d].  shared_expert_gate_weight ==
+ * NULL means a plain SwitchGLU block without the shared branch. */
+typedef struct {
+  int64_t hidden_size;
+  int64_t num_experts;
+  int64_t num_experts_per_tok;
+  int64_t moe_intermediate_size;
+  int64_t shared_expert_intermediate_size;
+  const float* gate_weight;
+  const float* gate_bias;
+  mlxr_moe_switch_glu switch_mlp;
+  mlxr_moe_qlinear shared_gate_proj;
+  mlxr_moe_qlinear shared_up_proj;
+  mlxr_moe_qlinear shared_down_proj;
+  const float* shared_expert_gate_weight;
+} mlxr_moe_block;
+
+/* Qwen35MoeBlock::forward (moe.rs:116-146): x bf16 [T, d] -> out f32
+ * [T, d].  topk_idx [T, K] / topk_w [T, K] optionally receive the routing
+ * (NULL to skip). */
+size_t mlxr_moe_block_workspace_size(const mlxr_moe_block* block, int64_t T);
+int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
+                           int64_t T, float* out, int32_t* topk_idx,
+                           float* topk_w, void* workspace,
+                           size_t workspace_size, mlxr_moe_stream stream);
+
+/* Device status word of a workspace used by gather_qmm / dispatch /
+ * switch_glu / block calls: 0 = all indices in range, 1 = some index out of
+ * range.  Synchronises `stream`.  Returns the status or -1 on error. */
+int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,
+                              mlxr_moe_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MLXR_MOE_H */

@@ -1,0 +1,122 @@
+"""ctypes binding of libmlxr_moe.so (declarations in include/mlxr_moe.h).
+
+Loading fails loudly when the library is missing: there is no CPU
+fallback behind these functions.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, Structure, c_char_p, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmlxr_moe.so"
+
+FLOAT32 = 0
+BFLOAT16 = 1
+
+
+class MlxrMoeError(RuntimeError):
+    """An entry point returned a nonzero status (mlxr's Exception)."""
+
+
+class OptionalInt(Structure):
+    _fields_ = [("value", c_int32), ("has_value", c_int32)]
+
+    @classmethod
+    def of(cls, v):
+        return cls(0, 0) if v is None else cls(int(v), 1)
+
+
+class QLinear(Structure):
+    _fields_ = [
+        ("weight", c_void_p),
+        ("scales", c_void_p),
+        ("biases", c_void_p),
+        ("num_experts", c_int64),
+        ("output_dims", c_int64),
+        ("input_dims", c_int64),
+        ("group_size", c_int32),
+        ("bits", c_int32),
+    ]
+
+
+class SwitchGlu(Structure):
+    _fields_ = [("gate_proj", QLinear), ("up_proj", QLinear), ("down_proj", QLinear)]
+
+
+class Block(Structure):
+    _fields_ = [
+        ("hidden_size", c_int64),
+        ("num_experts", c_int64),
+        ("num_experts_per_tok", c_int64),
+        ("moe_intermediate_size", c_int64),
+        ("shared_expert_intermediate_size", c_int64),
+        ("gate_weight", c_void_p),
+        ("gate_bias", c_void_p),
+        ("switch_mlp", SwitchGlu),
+        ("shared_gate_proj", QLinear),
+        ("shared_up_proj", QLinear),
+        ("shared_down_proj", QLinear),
+        ("shared_expert_gate_weight", c_void_p),
+    ]
+
+
+P = c_void_p
+OI = OptionalInt
+# name -> (restype, argtypes); the exact set of symbols include/mlxr_moe.h
+# declares.
+SIGNATURES = {
+    "mlxr_moe_last_error": (c_char_p, []),
+    "mlxr_moe_version": (c_int, []),
+    "mlxr_moe_quantize": (c_int, [P, c_int, c_int64, c_int64, OI, OI, c_char_p, P, P, P, P]),
+    "mlxr_moe_dequantize": (c_int, [P, P, P, c_int, c_int64, c_int64, OI, OI, c_char_p, P, c_int, P]),
+    "mlxr_moe_gather_qmm_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "mlxr_moe_gather_qmm": (
+        c_int,
+        [P, c_int, c_int64, c_int64, c_int64, P, P, P, c_int, c_int64, c_int64, P, P, c_int64,
+         c_int, OI, OI, c_char_p, c_int, P, c_int, P, c_size_t, P],
+    ),
+    "mlxr_moe_argpartition": (c_int, [P, c_int64, c_int64, c_int, c_int, P, P]),
+    "mlxr_moe_softmax": (c_int, [P, c_int64, c_int64, c_int, c_int, P, P]),
+    "mlxr_moe_router_workspace_size": (c_size_t, [c_int64, c_int64]),
+    "mlxr_moe_router_topk": (c_int, [P, c_int64, c_int64, P, c_int64, c_int64, P, P, P, c_size_t, P]),
+    "mlxr_moe_dispatch_workspace_size": (c_size_t, [c_int64, c_int64]),
+    "mlxr_moe_dispatch": (c_int, [P, c_int64, c_int64, P, P, P, P, P, c_size_t, P]),
+    "mlxr_moe_combine": (c_int, [P, P, c_int64, c_int64, c_int64, P, P, P, P]),
+    "mlxr_moe_switch_glu_workspace_size": (c_size_t, [POINTER(SwitchGlu), c_int64, c_int64]),
+    "mlxr_moe_switch_glu_forward": (
+        c_int, [POINTER(SwitchGlu), P, c_int64, P, P, c_int64, P, P, c_size_t, P]),
+    "mlxr_moe_switch_glu_experts": (
+        c_int, [POINTER(SwitchGlu), P, c_int64, P, c_int64, P, P, c_size_t, P]),
+    "mlxr_moe_block_workspace_size": (c_size_t, [POINTER(Block), c_int64]),
+    "mlxr_moe_block_forward": (c_int, [POINTER(Block), P, c_int64, P, P, P, P, c_size_t, P]),
+    "mlxr_moe_workspace_status": (c_int, [P, c_size_t, P]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library with typed entry points (loaded once)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise MlxrMoeError(
+                f"{LIB_PATH} is missing: build it with `python mlx-rs_amd/build.py` "
+                "(or __graft_entry__.build()); there is no fallback implementation")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise MlxrMoeError(lib().mlxr_moe_last_error().decode())
+
+
+def last_error() -> str:
+    return lib().mlxr_moe_last_error().decode()

@@ -1,0 +1,475 @@
+// C ABI of the MI355X sparse-MoE block (declarations and reference
+// citations in include/mlxr_moe.h).  Each entry point validates every
+// host-visible argument, then enqueues kernels on the caller's stream.
+// Errors never cross the ABI as exceptions: they return -1 and leave a
+// thread-local message.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+
+#include "../../include/mlxr_moe.h"
+#include "kernels.hpp"
+#include "nn.hpp"
+
+using namespace mlxr_moe;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const std::string& msg) {
+  g_last_error = msg;
+  return -1;
+}
+
+int finish(const Status& st) { return st.ok ? 0 : fail(st.what); }
+
+hipStream_t as_stream(mlxr_moe_stream s) {
+  return reinterpret_cast<hipStream_t>(s);
+}
+
+bool dtype_ok(int dt) { return dt == MLXR_MOE_FLOAT32 || dt == MLXR_MOE_BFLOAT16; }
+
+// mode, group_size and bits as mlx-c resolves them (defaults from
+// crates/mlxr/src/ops/quantization.rs:11-13).
+Status resolve_quant(const char* mode, mlxr_moe_optional_int gs,
+                     mlxr_moe_optional_int bits, bool kernel_path, int* g_out,
+                     int* b_out) {
+  if (mode && std::strcmp(mode, "affine") != 0)
+    return Status::error(std::string("unsupported quantization mode '") +
+                         mode + "' (only 'affine')");
+  const int g = gs.has_value ? gs.value : 64;
+  const int b = bits.has_value ? bits.value : 4;
+  if (kernel_path) {
+    if (g != 64)
+      return Status::error("group_size must be 64, got " + std::to_string(g));
+    if (b != 4 && b != 8)
+      return Status::error("bits must be 4 or 8, got " + std::to_string(b));
+  } else {
+    if (g != 32 && g != 64 && g != 128)
+      return Status::error("group_size must be 32, 64 or 128, got " +
+                           std::to_string(g));
+    if (b != 2 && b != 4 && b != 8)
+      return Status::error("bits must be 2, 4 or 8, got " + std::to_string(b));
+  }
+  *g_out = g;
+  *b_out = b;
+  return Status{};
+}
+
+bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+Status check_workspace(const Carve& plan, void* ws, size_t ws_size) {
+  if (plan.off > ws_size)
+    return Status::error("workspace too small: need " +
+                         std::to_string(plan.off) + " bytes, got " +
+                         std::to_string(ws_size));
+  if (plan.off && !ws) return Status::error("workspace is NULL");
+  if (ws && !aligned(ws, 256))
+    return Status::error("workspace must be 256-byte aligned");
+  return Status{};
+}
+
+// Workspace plans (the same carving the entry points run).
+void plan_gather(Carve& c, int64_t B, int64_t M, int64_t E) {
+  const int64_t R = B * M;
+  c.take<int32_t>(1);  // status
+  c.take<int32_t>(R);  // ids
+  c.take<int32_t>(R);  // xrow
+  c.take<int32_t>(R);  // xrow_sorted
+  carve_dispatch(c, R, E, nullptr);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mlxr_moe_last_error(void) { return g_last_error.c_str(); }
+
+int mlxr_moe_version(void) { return 100; }
+
+int mlxr_moe_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
+                      mlxr_moe_optional_int group_size,
+                      mlxr_moe_optional_int bits, const char* mode,
+                      uint32_t* wq, void* scales, void* biases,
+                      mlxr_moe_stream stream) {
+  int g, b;
+  Status st = resolve_quant(mode, group_size, bits, false, &g, &b);
+  if (!st.ok) return finish(st);
+  if (!dtype_ok(w_dtype)) return fail("quantize: w dtype must be f32 or bf16");
+  if (rows < 0 || cols <= 0) return fail("quantize: bad shape");
+  if (cols % g)
+    return fail("quantize: last dim " + std::to_string(cols) +
+                " is not a multiple of group_size " + std::to_string(g));
+  if (rows && (!w || !wq || !scales || !biases))
+    return fail("quantize: null array");
+  return finish(from_hip(launch_quantize(w, w_dtype == MLXR_MOE_BFLOAT16, rows,
+                                         cols, g, b, wq, scales, biases,
+                                         as_stream(stream)),
+                         "quantize"));
+}
+
+int mlxr_moe_dequantize(const uint32_t* wq, const void* scales,
+                        const void* biases, int sb_dtype, int64_t rows,
+                        int64_t cols, mlxr_moe_optional_int group_size,
+                        mlxr_moe_optional_int bits, const char* mode,
+                        void* out, int out_dtype, mlxr_moe_stream stream) {
+  int g, b;
+  Status st = resolve_quant(mode, group_size, bits, false, &g, &b);
+  if (!st.ok) return finish(st);
+  if (!dtype_ok(sb_dtype) || !dtype_ok(out_dtype))
+    return fail("dequantize: dtypes must be f32 or bf16");
+  if (rows < 0 || cols <= 0 || cols % g) return fail("dequantize: bad shape");
+  if (!biases) return fail("dequantize: biases are required for affine mode");
+  if (rows && (!wq || !scales || !out)) return fail("dequantize: null array");
+  return finish(from_hip(
+      launch_dequantize(wq, scales, biases, sb_dtype == MLXR_MOE_BFLOAT16, rows,
+                        cols, g, b, out, out_dtype == MLXR_MOE_BFLOAT16,
+                        as_stream(stream)),
+      "dequantize"));
+}
+
+size_t mlxr_moe_gather_qmm_workspace_size(int64_t B, int64_t M,
+                                          int64_t num_experts) {
+  Carve c(nullptr);
+  plan_gather(c, B, M, num_experts);
+  return c.off;
+}
+
+int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
+                        int64_t M, int64_t K, const uint32_t* w,
+                        const void* scales, const void* biases, int sb_dtype,
+                        int64_t E, int64_t N, const uint32_t* lhs_indices,
+                        const uint32_t* rhs_indices, int64_t B, int transpose,
+                        mlxr_moe_optional_int group_size,
+                        mlxr_moe_optional_int bits, const char* mode,
+                        int sorted_indices, void* out, int out_dtype,
+                        void* workspace, size_t workspace_size,
+                        mlxr_moe_stream stream) {
+  (void)sorted_indices;
+  int g, b;
+  Status st = resolve_quant(mode, group_size, bits, true, &g, &b);
+  if (!st.ok) return finish(st);
+  if (!transpose)
+    return fail("gather_qmm: only transpose=true (the [E, N, K] layout of "
+                "QuantizedSwitchLinear) is supported");
+  if (x_dtype != MLXR_MOE_BFLOAT16 || sb_dtype != MLXR_MOE_BFLOAT16 ||
+      out_dtype != MLXR_MOE_BFLOAT16)
+    return fail("gather_qmm: x, scales/biases and out must be bf16");
+  if (!biases) return fail("gather_qmm: biases are required for affine mode");
+  if (!rhs_indices) return fail("gather_qmm: rhs_indices are required");
+  if (E <= 0 || E > kMaxExperts)
+    return fail("gather_qmm: num_experts must be in [1, " +
+                std::to_string(kMaxExperts) + "]");
+  if (M <= 0 || K <= 0 || N <= 0 || B < 0 || x_batch <= 0)
+    return fail("gather_qmm: bad shape");
+  if (K % 64 || N % 64)
+    return fail("gather_qmm: K and N must be multiples of 64");
+  if (!lhs_indices && B % x_batch)
+    return fail("gather_qmm: x batch " + std::to_string(x_batch) +
+                " does not broadcast against " + std::to_string(B) +
+                " indices");
+  if (B * M > INT32_MAX / 2) return fail("gather_qmm: too many rows");
+  if (!x || !w || !scales || !out) return fail("gather_qmm: null array");
+  if (!aligned(x, 16) || !aligned(w, 16))
+    return fail("gather_qmm: x and w must be 16-byte aligned");
+  Carve plan(nullptr);
+  plan_gather(plan, B, M, E);
+  st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  if (B == 0) return 0;
+
+  hipStream_t s = as_stream(stream);
+  const int64_t R = B * M;
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  int32_t* ids = c.take<int32_t>(R);
+  int32_t* xrow = c.take<int32_t>(R);
+  int32_t* xrow_sorted = c.take<int32_t>(R);
+  const DispatchBuffers db = carve_dispatch(c, R, E, status);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  st = from_hip(launch_gather_prep(lhs_indices, rhs_indices, B, M, x_batch, E,
+                                   N, ids, xrow, o, status, s),
+                "gather_qmm prep");
+  if (st.ok)
+    st = from_hip(launch_dispatch(ids, R, E, kPrefillTileRows, db, false, s),
+                  "gather_qmm dispatch");
+  if (st.ok)
+    st = from_hip(launch_gather_permute(xrow, db.sorted, db.offsets, E, R,
+                                        xrow_sorted, s),
+                  "gather_qmm permute");
+  if (!st.ok) return finish(st);
+  QGemmArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_ld = K;
+  a.row_map = xrow_sorted;
+  a.row_div = 1;
+  a.offsets = db.offsets;
+  a.active = db.active;
+  a.num_active = db.num_active;
+  a.tiles = db.tiles;
+  a.num_tiles = db.num_tiles;
+  a.w0 = QWeights{w, static_cast<const uint16_t*>(scales),
+                  static_cast<const uint16_t*>(biases)};
+  a.E = (int32_t)E;
+  a.N = (int32_t)N;
+  a.K = (int32_t)K;
+  a.bits = b;
+  a.out = o;
+  a.out_ld = N;
+  a.out_map = db.sorted;
+  a.gated = false;
+  return finish(from_hip(launch_qgemm(a, R, std::min<int64_t>(E, R),
+                                      nn::use_prefill_path(R, E), s),
+                         "gather_qmm"));
+}
+
+int mlxr_moe_argpartition(const float* a, int64_t rows, int64_t n, int kth,
+                          int axis, uint32_t* out, mlxr_moe_stream stream) {
+  if (axis != -1 && axis != 1)
+    return fail("argpartition: axis " + std::to_string(axis) +
+                " is out of bounds for a 2-d array [rows, n] (use -1 or 1)");
+  if (rows < 0 || n <= 0) return fail("argpartition: bad shape");
+  if (kth < -n || kth >= n)
+    return fail("argpartition: kth " + std::to_string(kth) +
+                " is out of bounds for axis of size " + std::to_string(n));
+  if (n > 4096) return fail("argpartition: rows longer than 4096");
+  if (rows && (!a || !out)) return fail("argpartition: null array");
+  return finish(from_hip(launch_argsort_rows(a, rows, n, out,
+                                             as_stream(stream)),
+                         "argpartition"));
+}
+
+int mlxr_moe_softmax(const float* a, int64_t rows, int64_t n, int axis,
+                     int precise, float* out, mlxr_moe_stream stream) {
+  (void)precise;
+  if (axis != -1 && axis != 1)
+    return fail("softmax: axis " + std::to_string(axis) +
+                " is out of bounds for a 2-d array");
+  if (rows < 0 || n <= 0) return fail("softmax: bad shape");
+  if (rows && (!a || !out)) return fail("softmax: null array");
+  return finish(from_hip(launch_softmax_rows(a, rows, n, out,
+                                             as_stream(stream)),
+                         "softmax"));
+}
+
+size_t mlxr_moe_router_workspace_size(int64_t T, int64_t E) {
+  Carve c(nullptr);
+  c.take<float>(T * E);
+  return c.off;
+}
+
+int mlxr_moe_router_topk(const void* x, int64_t T, int64_t d,
+                         const float* gate_w, int64_t E, int64_t K,
+                         int32_t* topk_idx, float* topk_w, void* workspace,
+                         size_t workspace_size, mlxr_moe_stream stream) {
+  if (T < 0 || d <= 0 || E <= 0) return fail("router_topk: bad shape");
+  if (d % 4) return fail("router_topk: hidden size must be a multiple of 4");
+  if (E > kMaxExperts)
+    return fail("router_topk: at most " + std::to_string(kMaxExperts) +
+                " experts");
+  if (K < 1 || K > E || K > 64)
+    return fail("router_topk: k must be in [1, min(E, 64)], got " +
+                std::to_string(K));
+  if (T && (!x || !gate_w || !topk_idx || !topk_w))
+    return fail("router_topk: null array");
+  if (!aligned(gate_w, 16) || !aligned(x, 8))
+    return fail("router_topk: gate_w must be 16-byte and x 8-byte aligned");
+  Carve plan(nullptr);
+  plan.take<float>(T * E);
+  Status st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  Carve c(workspace);
+  float* logits = c.take<float>(T * E);
+  hipStream_t s = as_stream(stream);
+  st = from_hip(launch_router_logits(static_cast<const uint16_t*>(x), T, d,
+                                     gate_w, nullptr, E, nullptr, logits, E,
+                                     s),
+                "router logits");
+  if (st.ok)
+    st = from_hip(launch_router_topk(logits, E, T, E, K, topk_idx, topk_w, s),
+                  "router top-k");
+  return finish(st);
+}
+
+size_t mlxr_moe_dispatch_workspace_size(int64_t n, int64_t E) {
+  Carve c(nullptr);
+  c.take<int32_t>(1);
+  carve_dispatch(c, n, E, nullptr);
+  return c.off;
+}
+
+int mlxr_moe_dispatch(const int32_t* ids, int64_t n, int64_t E,
+                      int32_t* counts, int32_t* offsets, int32_t* sorted,
+                      int32_t* inv, void* workspace, size_t workspace_size,
+                      mlxr_moe_stream stream) {
+  if (n < 0 || E <= 0 || E > kMaxExperts) return fail("dispatch: bad shape");
+  if (n > INT32_MAX / 2) return fail("dispatch: too many ids");
+  if (!counts || !offsets || (n && (!ids || !sorted || !inv)))
+    return fail("dispatch: null array");
+  Carve plan(nullptr);
+  plan.take<int32_t>(1);
+  carve_dispatch(plan, n, E, nullptr);
+  Status st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  DispatchBuffers db = carve_dispatch(c, n, E, status);
+  db.counts = counts;
+  db.offsets = offsets;
+  db.sorted = sorted;
+  db.inv = inv;
+  return finish(from_hip(launch_dispatch(ids, n, E, kPrefillTileRows, db, true,
+                                         as_stream(stream)),
+                         "dispatch"));
+}
+
+int mlxr_moe_combine(const void* y, const float* w, int64_t T, int64_t K,
+                     int64_t d, const void* shared_y,
+                     const float* shared_logit, float* out,
+                     mlxr_moe_stream stream) {
+  if (T < 0 || K < 1 || d <= 0) return fail("combine: bad shape");
+  if (d % 8) return fail("combine: d must be a multiple of 8");
+  if (T && (!y || !w || !out)) return fail("combine: null array");
+  if ((shared_y == nullptr) != (shared_logit == nullptr))
+    return fail("combine: shared_y and shared_logit go together");
+  if (!aligned(y, 16) || !aligned(out, 16) ||
+      (shared_y && !aligned(shared_y, 16)))
+    return fail("combine: y, shared_y and out must be 16-byte aligned");
+  return finish(from_hip(
+      launch_combine(static_cast<const uint16_t*>(y), w, T, K, d,
+                     static_cast<const uint16_t*>(shared_y), shared_logit, 1,
+                     out, as_stream(stream)),
+      "combine"));
+}
+
+size_t mlxr_moe_switch_glu_workspace_size(const mlxr_moe_switch_glu* ffn,
+                                          int64_t T, int64_t K) {
+  if (!ffn) return 0;
+  Carve c(nullptr);
+  c.take<int32_t>(1);
+  nn::SplitSwitchFfn::plan(c, T, K, ffn->gate_proj.input_dims,
+                           ffn->gate_proj.output_dims,
+                           ffn->gate_proj.num_experts);
+  return c.off;
+}
+
+int mlxr_moe_switch_glu_forward(const mlxr_moe_switch_glu* ffn, const void* x,
+                                int64_t T, const int32_t* indices,
+                                const float* weights, int64_t K, float* out,
+                                void* workspace, size_t workspace_size,
+                                mlxr_moe_stream stream) {
+  if (!ffn) return fail("switch_glu: null module");
+  const int64_t d = ffn->gate_proj.input_dims, f = ffn->gate_proj.output_dims;
+  const int64_t E = ffn->gate_proj.num_experts;
+  nn::SplitSwitchFfn m(*ffn);
+  Status st = m.validate(d, f, E);
+  if (!st.ok) return finish(st);
+  if (T < 0 || K < 1 || K > E) return fail("switch_glu: bad T or K");
+  if (T && (!x || !indices || !weights || !out))
+    return fail("switch_glu: null array");
+  if (!aligned(x, 16) || !aligned(out, 16))
+    return fail("switch_glu: x and out must be 16-byte aligned");
+  Carve plan(nullptr);
+  plan.take<int32_t>(1);
+  nn::SplitSwitchFfn::plan(plan, T, K, d, f, E);
+  st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  if (T == 0) return 0;
+  hipStream_t s = as_stream(stream);
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  st = from_hip(launch_zero_status(status, s), "switch_glu status");
+  if (st.ok)
+    st = m.forward_with_combine(static_cast<const uint16_t*>(x), T, indices,
+                                weights, K, out, nullptr, nullptr, 0, c,
+                                status, s);
+  return finish(st);
+}
+
+int mlxr_moe_switch_glu_experts(const mlxr_moe_switch_glu* ffn, const void* x,
+                                int64_t T, const int32_t* indices, int64_t K,
+                                void* y, void* workspace,
+                                size_t workspace_size, mlxr_moe_stream stream) {
+  if (!ffn) return fail("switch_glu: null module");
+  const int64_t d = ffn->gate_proj.input_dims, f = ffn->gate_proj.output_dims;
+  const int64_t E = ffn->gate_proj.num_experts;
+  nn::SplitSwitchFfn m(*ffn);
+  Status st = m.validate(d, f, E);
+  if (!st.ok) return finish(st);
+  if (T < 0 || K < 1 || K > E) return fail("switch_glu: bad T or K");
+  if (T && (!x || !indices || !y)) return fail("switch_glu: null array");
+  if (!aligned(x, 16)) return fail("switch_glu: x must be 16-byte aligned");
+  Carve plan(nullptr);
+  plan.take<int32_t>(1);
+  nn::SplitSwitchFfn::plan(plan, T, K, d, f, E);
+  st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  if (T == 0) return 0;
+  hipStream_t s = as_stream(stream);
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  c.take<uint16_t>(T * K * d);  // the combine's y slot, unused here
+  st = from_hip(launch_zero_status(status, s), "switch_glu status");
+  if (st.ok)
+    st = m.forward(static_cast<const uint16_t*>(x), T, indices, K,
+                   static_cast<uint16_t*>(y), c, status, s);
+  return finish(st);
+}
+
+size_t mlxr_moe_block_workspace_size(const mlxr_moe_block* block, int64_t T) {
+  if (!block) return 0;
+  Carve c(nullptr);
+  c.take<int32_t>(1);
+  nn::Qwen35MoeBlock::plan(c, *block, T);
+  return c.off;
+}
+
+int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
+                           int64_t T, float* out, int32_t* topk_idx,
+                           float* topk_w, void* workspace,
+                           size_t workspace_size, mlxr_moe_stream stream) {
+  if (!block) return fail("block: null module");
+  nn::Qwen35MoeBlock m(*block);
+  Status st = m.validate();
+  if (!st.ok) return finish(st);
+  if (T < 0) return fail("block: bad T");
+  if (T && (!x || !out)) return fail("block: null array");
+  if (!aligned(x, 16) || !aligned(out, 16) ||
+      !aligned(block->gate_weight, 16) ||
+      (block->shared_expert_gate_weight &&
+       !aligned(block->shared_expert_gate_weight, 16)))
+    return fail("block: x, out and router weights must be 16-byte aligned");
+  Carve plan(nullptr);
+  plan.take<int32_t>(1);
+  nn::Qwen35MoeBlock::plan(plan, *block, T);
+  st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  if (T == 0) return 0;
+  hipStream_t s = as_stream(stream);
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  st = from_hip(launch_zero_status(status, s), "block status");
+  if (st.ok)
+    st = m.forward(static_cast<const uint16_t*>(x), T, out, topk_idx, topk_w,
+                   c, s);
+  return finish(st);
+}
+
+int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,
+                              mlxr_moe_stream stream) {
+  if (!workspace || workspace_size < sizeof(int32_t))
+    return fail("workspace_status: no workspace");
+  int32_t v = -1;
+  hipStream_t s = as_stream(stream);
+  hipError_t e = hipMemcpyAsync(&v, workspace, sizeof(v),
+                                hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return finish(from_hip(e, "workspace_status"));
+  return v;
+}
+
+}  // extern "C"

@@ -1,0 +1,72 @@
+// Weighted combine of the routed expert rows, plus the sigmoid-gated shared
+// expert, on gfx950.
+//
+// Replaces combine_with_weights (crates/mlxr-lm/src/nn/switch.rs:223-234):
+// (w * y) with w f32 [T,K,1] and y bf16 [T,K,d] promotes to f32, then a sum
+// over K; and, from Qwen35MoeBlock::forward (moe.rs:117-120, 145),
+// shared * sigmoid(shared_gate(x)) + routed.  Each product is rounded to f32
+// before the k-ordered sum, as in the reference's two-op sequence.
+// HBM-bound elementwise pass: 8 outputs per thread, 16 B loads of y.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxr_moe {
+namespace {
+
+__global__ __launch_bounds__(256) void combine_kernel(
+    const uint16_t* __restrict__ y, const float* __restrict__ w, int T, int K,
+    int d, const uint16_t* __restrict__ shared_y,
+    const float* __restrict__ shared_logit, int64_t shared_ld,
+    float* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int n0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (t >= T || n0 >= d) return;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const float wk = w[(int64_t)t * K + k];
+    const u32x4_t v =
+        *reinterpret_cast<const u32x4_t*>(y + ((int64_t)t * K + k) * d + n0);
+    const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = __fmul_rn(wk, __uint_as_float(pk[j] << 16));
+      const float hi = __fmul_rn(wk, __uint_as_float(pk[j] & 0xffff0000u));
+      acc[2 * j] = __fadd_rn(acc[2 * j], lo);
+      acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], hi);
+    }
+  }
+  if (shared_y) {
+    const float gate = 1.0f / (1.0f + expf(-shared_logit[t * shared_ld]));
+    const u32x4_t v =
+        *reinterpret_cast<const u32x4_t*>(shared_y + (int64_t)t * d + n0);
+    const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] = __fadd_rn(__fmul_rn(__uint_as_float(pk[j] << 16), gate),
+                             acc[2 * j]);
+      acc[2 * j + 1] = __fadd_rn(
+          __fmul_rn(__uint_as_float(pk[j] & 0xffff0000u), gate),
+          acc[2 * j + 1]);
+    }
+  }
+  float4* o = reinterpret_cast<float4*>(out + (int64_t)t * d + n0);
+  o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
+}  // namespace
+
+hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,
+                          int64_t K, int64_t d, const uint16_t* shared_y,
+                          const float* shared_logit, int64_t shared_ld,
+                          float* out, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const dim3 grid((unsigned)((d / 8 + 255) / 256), (unsigned)T);
+  combine_kernel<<<grid, 256, 0, s>>>(y, w, (int)T, (int)K, (int)d, shared_y,
+                                      shared_logit, shared_ld, out);
+  return hipGetLastError();
+}
+
+}  // namespace mlxr_moe

@@ -1,0 +1,243 @@
+// Token -> expert dispatch on gfx950: a stable counting sort of the flat
+// (token, k) expert ids into per-expert contiguous row blocks.
+//
+// Replaces gather_sort / scatter_unsort
+// (crates/mlxr-lm/src/nn/switch.rs:499-517): order = argsort(flat ids),
+// inv = argsort(order).  Because the sort is stable the permutation equals
+// that argsort exactly.  Two kernels:
+//   rank  (one 1024-thread workgroup per 1024 ids): per-wave match masks from
+//         ballots over the id bits give each id its rank among equal ids of
+//         its wave; an LDS table of per-wave counts turns that into a rank
+//         within the workgroup and a per-workgroup histogram.
+//   scan  (one workgroup): per-expert prefix over workgroups, exclusive scan
+//         over experts (offsets), the list of experts with rows, the M-tile
+//         list for the prefill GEMM, and the scatter into sorted/inv.
+// Ids outside [0, E) are left out of every expert and flagged in *status.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxr_moe {
+namespace {
+
+constexpr int kWaves = kDispatchBlock / 64;
+
+__global__ __launch_bounds__(kDispatchBlock) void dispatch_rank_kernel(
+    const int32_t* __restrict__ ids, int n, int E,
+    int32_t* __restrict__ block_hist, int32_t* __restrict__ rank,
+    int32_t* __restrict__ status) {
+  extern __shared__ uint16_t tab[];  // [kWaves][E]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < kWaves * E; i += kDispatchBlock) tab[i] = 0;
+  __syncthreads();
+  const int64_t gi = (int64_t)blockIdx.x * kDispatchBlock + tid;
+  const bool valid = gi < n;
+  const int id = valid ? ids[gi] : -1;
+  const bool ok = valid && id >= 0 && id < E;
+  if (valid && !ok && id != -1) *status = 1;
+  uint64_t match = __ballot(ok);
+  const int id_bits = E > 1 ? 32 - __clz(E - 1) : 0;
+  for (int b = 0; b < id_bits; ++b) {
+    const bool bit = ok && ((id >> b) & 1);
+    const uint64_t bal = __ballot(bit);
+    match &= bit ? bal : ~bal;
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int r = __popcll(match & below);
+  if (ok && r == 0) tab[wave * E + id] = (uint16_t)__popcll(match);
+  __syncthreads();
+  for (int e = tid; e < E; e += kDispatchBlock) {
+    int run = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      const int c = tab[w * E + e];
+      tab[w * E + e] = (uint16_t)run;
+      run += c;
+    }
+    block_hist[(int64_t)blockIdx.x * E + e] = run;
+  }
+  __syncthreads();
+  if (ok) rank[gi] = tab[wave * E + id] + r;
+}
+
+// Exclusive scan of one int per thread over the 1024-thread block.
+__device__ int block_exclusive_scan(int v, int* total, int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += u;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      const int c = wsum[w];
+      wsum[w] = run;
+      run += c;
+    }
+    wsum[kWaves] = run;
+  }
+  __syncthreads();
+  const int ex = wsum[wave] + inc - v;
+  *total = wsum[kWaves];
+  __syncthreads();
+  return ex;
+}
+
+__global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
+    const int32_t* __restrict__ ids, int n, int E, int nb, int tile_rows,
+    DispatchBuffers b) {
+  __shared__ int s_off[kMaxExperts];
+  __shared__ int wsum[kWaves + 1];
+  const int tid = threadIdx.x;
+  int cnt = 0;
+  if (tid < E) {
+    for (int blk = 0; blk < nb; ++blk) {
+      const int c = b.block_hist[(int64_t)blk * E + tid];
+      b.block_hist[(int64_t)blk * E + tid] = cnt;
+      cnt += c;
+    }
+  }
+  int total;
+  const int off = block_exclusive_scan(cnt, &total, wsum);
+  if (tid < E) {
+    b.counts[tid] = cnt;
+    b.offsets[tid] = off;
+    s_off[tid] = off;
+  }
+  if (tid == 0) b.offsets[E] = total;
+
+  const int has = (tid < E && cnt > 0) ? 1 : 0;
+  int n_active;
+  const int apos = block_exclusive_scan(has, &n_active, wsum);
+  if (has) b.active[apos] = tid;
+  if (tid == 0) *b.num_active = n_active;
+
+  const int nt = (tid < E) ? (cnt + tile_rows - 1) / tile_rows : 0;
+  int n_tiles;
+  const int tpos = block_exclusive_scan(nt, &n_tiles, wsum);
+  for (int j = 0; j < nt; ++j) {
+    b.tiles[2 * (tpos + j)] = tid;
+    b.tiles[2 * (tpos + j) + 1] = off + j * tile_rows;
+  }
+  if (tid == 0) *b.num_tiles = n_tiles;
+  __syncthreads();
+
+  for (int i = tid; i < n; i += kDispatchBlock) {
+    const int e = ids[i];
+    if (e < 0 || e >= E) continue;
+    const int pos = s_off[e] +
+                    b.block_hist[(int64_t)(i / kDispatchBlock) * E + e] +
+                    b.rank[i];
+    b.sorted[pos] = i;
+    b.inv[i] = pos;
+  }
+}
+
+__global__ __launch_bounds__(256) void dispatch_identity_kernel(
+    int n, int tile_rows, DispatchBuffers b) {
+  const int tid = threadIdx.x;
+  const int n_tiles = (n + tile_rows - 1) / tile_rows;
+  if (tid == 0) {
+    b.counts[0] = n;
+    b.offsets[0] = 0;
+    b.offsets[1] = n;
+    b.active[0] = 0;
+    *b.num_active = n > 0 ? 1 : 0;
+    *b.num_tiles = n_tiles;
+  }
+  for (int j = tid; j < n_tiles; j += 256) {
+    b.tiles[2 * j] = 0;
+    b.tiles[2 * j + 1] = j * tile_rows;
+  }
+}
+
+__global__ void zero_status_kernel(int32_t* status) { *status = 0; }
+
+// gather_qmm row preparation: flat row r = b * M + m takes expert
+// rhs[b] and x row xb(b) * M + m; rows with an index out of range get
+// expert -1 (left out by the dispatch), a zero output row and *status = 1.
+__global__ __launch_bounds__(256) void gather_prep_kernel(
+    const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs,
+    int64_t B, int64_t M, int64_t x_batch, int64_t E, int64_t N,
+    int32_t* __restrict__ ids, int32_t* __restrict__ xrow,
+    uint16_t* __restrict__ out, int32_t* __restrict__ status) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= B * M) return;
+  const int64_t b = r / M, m = r % M;
+  const int64_t xb = lhs ? (int64_t)lhs[b] : b / (B / x_batch);
+  const uint32_t e = rhs[b];
+  if (e >= (uint64_t)E || xb >= x_batch) {
+    ids[r] = -1;
+    xrow[r] = 0;
+    *status = 1;
+    for (int64_t n = 0; n < N; ++n) out[r * N + n] = 0;
+    return;
+  }
+  ids[r] = (int32_t)e;
+  xrow[r] = (int32_t)(xb * M + m);
+}
+
+__global__ __launch_bounds__(256) void gather_permute_kernel(
+    const int32_t* __restrict__ xrow, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ offsets, int64_t E, int64_t R,
+    int32_t* __restrict__ xrow_sorted) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= R || p >= offsets[E]) return;
+  xrow_sorted[p] = xrow[sorted[p]];
+}
+
+}  // namespace
+
+hipError_t launch_zero_status(int32_t* status, hipStream_t s) {
+  zero_status_kernel<<<1, 1, 0, s>>>(status);
+  return hipGetLastError();
+}
+
+int64_t dispatch_max_tiles(int64_t n, int64_t E, int tile_rows) {
+  return (n + tile_rows - 1) / tile_rows + (E < n ? E : n);
+}
+
+hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
+                           int tile_rows, const DispatchBuffers& b,
+                           bool reset_status, hipStream_t s) {
+  const int nb = (int)((n + kDispatchBlock - 1) / kDispatchBlock);
+  if (reset_status) zero_status_kernel<<<1, 1, 0, s>>>(b.status);
+  if (nb > 0)
+    dispatch_rank_kernel<<<nb, kDispatchBlock,
+                           (size_t)kWaves * E * sizeof(uint16_t), s>>>(
+        ids, (int)n, (int)E, b.block_hist, b.rank, b.status);
+  dispatch_scan_kernel<<<1, kDispatchBlock, 0, s>>>(ids, (int)n, (int)E, nb,
+                                                    tile_rows, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_prep(const uint32_t* lhs, const uint32_t* rhs,
+                              int64_t B, int64_t M, int64_t x_batch, int64_t E,
+                              int64_t N, int32_t* ids, int32_t* xrow,
+                              uint16_t* out, int32_t* status, hipStream_t s) {
+  const int64_t R = B * M;
+  zero_status_kernel<<<1, 1, 0, s>>>(status);
+  if (R > 0)
+    gather_prep_kernel<<<(unsigned)((R + 255) / 256), 256, 0, s>>>(
+        lhs, rhs, B, M, x_batch, E, N, ids, xrow, out, status);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_permute(const int32_t* xrow, const int32_t* sorted,
+                                 const int32_t* offsets, int64_t E, int64_t R,
+                                 int32_t* xrow_sorted, hipStream_t s) {
+  if (R > 0)
+    gather_permute_kernel<<<(unsigned)((R + 255) / 256), 256, 0, s>>>(
+        xrow, sorted, offsets, E, R, xrow_sorted);
+  return hipGetLastError();
+}
+
+hipError_t launch_dispatch_identity(int64_t n, int tile_rows,
+                                    const DispatchBuffers& b, hipStream_t s) {
+  dispatch_identity_kernel<<<1, 256, 0, s>>>((int)n, tile_rows, b);
+  return hipGetLastError();
+}
+
+}  // namespace mlxr_moe

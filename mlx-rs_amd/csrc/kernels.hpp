@@ -1,0 +1,112 @@
+// Host-side launchers for the MoE kernels.  Every launcher enqueues on the
+// given stream and returns the launch status; none synchronises.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mlxr_moe {
+
+// ---------------------------------------------------------------- quant.hip
+hipError_t launch_quantize(const void* w, bool w_bf16, int64_t rows,
+                           int64_t cols, int group_size, int bits, uint32_t* wq,
+                           void* scales, void* biases, hipStream_t s);
+hipError_t launch_dequantize(const uint32_t* wq, const void* scales,
+                             const void* biases, bool sb_bf16, int64_t rows,
+                             int64_t cols, int group_size, int bits, void* out,
+                             bool out_bf16, hipStream_t s);
+
+// --------------------------------------------------------------- router.hip
+// logits[t, e] for e < E from w [E, d] (+ bias[e] when given); column E
+// from w_extra [1, d] when given (the shared-expert gate).  ld = row stride
+// of logits.
+hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
+                                const float* w, const float* bias, int64_t E,
+                                const float* w_extra, float* logits,
+                                int64_t ld, hipStream_t s);
+hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
+                              int64_t E, int64_t K, int32_t* idx, float* wts,
+                              hipStream_t s);
+hipError_t launch_argsort_rows(const float* a, int64_t rows, int64_t n,
+                               uint32_t* out, hipStream_t s);
+hipError_t launch_softmax_rows(const float* a, int64_t rows, int64_t n,
+                               float* out, hipStream_t s);
+
+// ------------------------------------------------------------- dispatch.hip
+// Stable counting sort of ids [n] (values in [0, E)) by expert.
+struct DispatchBuffers {
+  int32_t* counts;      // [E]
+  int32_t* offsets;     // [E + 1]
+  int32_t* sorted;      // [n]  flat index per sorted slot
+  int32_t* inv;         // [n]  sorted slot per flat index
+  int32_t* active;      // [E]  experts with rows, ascending
+  int32_t* num_active;  // [1]
+  int32_t* tiles;       // [max_tiles] packed (expert, first row) of M-tiles
+  int32_t* num_tiles;   // [1]
+  int32_t* block_hist;  // [ceil(n/1024), E] scratch
+  int32_t* rank;        // [n] scratch
+  int32_t* status;      // [1] 0 ok, 1 id out of range
+};
+constexpr int kDispatchBlock = 1024;
+constexpr int kMaxExperts = 1024;
+int64_t dispatch_max_tiles(int64_t n, int64_t E, int tile_rows);
+// Clears a workspace status word with a one-thread kernel (no memset node,
+// so the call stays valid under stream capture).
+hipError_t launch_zero_status(int32_t* status, hipStream_t s);
+// Ids equal to -1 are left out silently (rows excluded by the caller);
+// other ids outside [0, E) are left out and set *status = 1.
+hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
+                           int tile_rows, const DispatchBuffers& b,
+                           bool reset_status, hipStream_t s);
+// gather_qmm helpers: per flat row r = b*M + m the expert id and x row, and
+// the x row of each sorted slot.
+hipError_t launch_gather_prep(const uint32_t* lhs, const uint32_t* rhs,
+                              int64_t B, int64_t M, int64_t x_batch, int64_t E,
+                              int64_t N, int32_t* ids, int32_t* xrow,
+                              uint16_t* out, int32_t* status, hipStream_t s);
+hipError_t launch_gather_permute(const int32_t* xrow, const int32_t* sorted,
+                                 const int32_t* offsets, int64_t E, int64_t R,
+                                 int32_t* xrow_sorted, hipStream_t s);
+// Identity dispatch for a dense (always-on) expert: one expert, n rows.
+hipError_t launch_dispatch_identity(int64_t n, int tile_rows,
+                                    const DispatchBuffers& b, hipStream_t s);
+
+// ---------------------------------------------------------------- qgemm.hip
+struct QWeights {
+  const uint32_t* w;       // [E, N, K*bits/32]
+  const uint16_t* scales;  // [E, N, K/64] bf16
+  const uint16_t* biases;  // [E, N, K/64] bf16
+};
+struct QGemmArgs {
+  const uint16_t* x;       // activations (bf16)
+  int64_t x_ld;            // row stride of x in elements
+  const int32_t* row_map;  // x row of slot p = row_map[p] / row_div (null: p)
+  int32_t row_div;
+  const int32_t* offsets;  // [E+1] slot range of each expert
+  const int32_t* active;   // [E] experts with rows
+  const int32_t* num_active;
+  const int32_t* tiles;    // M-tile list (prefill path)
+  const int32_t* num_tiles;
+  QWeights w0;             // gate (or the only projection)
+  QWeights w1;             // up (gated mode only)
+  int32_t E, N, K, bits;
+  uint16_t* out;           // bf16
+  int64_t out_ld;
+  const int32_t* out_map;  // out row of slot p = out_map[p] (null: p)
+  bool gated;              // out = swiglu(x.w0, x.w1)
+};
+// Rows per M-tile of the prefill kernel; the dispatch builds its tile list.
+constexpr int kPrefillTileRows = 128;
+// max_rows_per_expert bounds the grid of the decode kernel; max_active
+// bounds the number of experts with rows.
+hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
+                        int64_t max_active, bool prefill, hipStream_t s);
+
+// -------------------------------------------------------------- combine.hip
+hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,
+                          int64_t K, int64_t d, const uint16_t* shared_y,
+                          const float* shared_logit, int64_t shared_ld,
+                          float* out, hipStream_t s);
+
+}  // namespace mlxr_moe

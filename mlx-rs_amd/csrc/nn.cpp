@@ -1,0 +1,311 @@
+// C++ host mirror of mlxr-lm's MoE modules (see nn.hpp for the reference
+// mapping).  Orchestration only: every array op is a kernel launch on the
+// caller's stream.
+#include "nn.hpp"
+
+#include <algorithm>
+
+namespace mlxr_moe {
+
+Status from_hip(hipError_t e, const char* where) {
+  if (e == hipSuccess) return Status{};
+  return Status::error(std::string(where) + ": " + hipGetErrorString(e));
+}
+
+Status check_qlinear(const mlxr_moe_qlinear& q, int64_t experts, int64_t out,
+                     int64_t in, const char* name) {
+  const std::string n(name);
+  if (!q.weight || !q.scales || !q.biases)
+    return Status::error(n + ": weight, scales and biases are required "
+                             "(affine mode)");
+  if (q.bits != 4 && q.bits != 8)
+    return Status::error(n + ": bits must be 4 or 8, got " +
+                         std::to_string(q.bits));
+  if (q.group_size != 64)
+    return Status::error(n + ": group_size must be 64, got " +
+                         std::to_string(q.group_size));
+  if (q.num_experts != experts || q.output_dims != out || q.input_dims != in)
+    return Status::error(
+        n + ": shape [" + std::to_string(q.num_experts) + ", " +
+        std::to_string(q.output_dims) + ", " + std::to_string(q.input_dims) +
+        "] does not match the expected [" + std::to_string(experts) + ", " +
+        std::to_string(out) + ", " + std::to_string(in) + "]");
+  if (out % 64 || in % 64)
+    return Status::error(n + ": input and output dims must be multiples of "
+                             "64");
+  if ((reinterpret_cast<uintptr_t>(q.weight) & 15) ||
+      (reinterpret_cast<uintptr_t>(q.scales) & 1) ||
+      (reinterpret_cast<uintptr_t>(q.biases) & 1))
+    return Status::error(n + ": weight must be 16-byte aligned");
+  return Status{};
+}
+
+DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
+                               int32_t* status) {
+  DispatchBuffers b{};
+  const int64_t nb = (n + kDispatchBlock - 1) / kDispatchBlock;
+  b.counts = c.take<int32_t>(E);
+  b.offsets = c.take<int32_t>(E + 1);
+  b.sorted = c.take<int32_t>(n);
+  b.inv = c.take<int32_t>(n);
+  b.active = c.take<int32_t>(E);
+  b.num_active = c.take<int32_t>(1);
+  b.tiles = c.take<int32_t>(2 * dispatch_max_tiles(n, E, kPrefillTileRows));
+  b.num_tiles = c.take<int32_t>(1);
+  b.block_hist = c.take<int32_t>(nb * E);
+  b.rank = c.take<int32_t>(n);
+  b.status = status;
+  return b;
+}
+
+namespace nn {
+
+bool use_prefill_path(int64_t rows, int64_t experts) {
+  (void)rows;
+  (void)experts;
+  return false;
+}
+
+namespace {
+
+QWeights qw(const mlxr_moe_qlinear& q) {
+  return QWeights{q.weight, static_cast<const uint16_t*>(q.scales),
+                  static_cast<const uint16_t*>(q.biases)};
+}
+
+}  // namespace
+
+// ------------------------------------------------------------- SwigluMlp
+Status SwigluMlp::validate(int64_t d, int64_t f) const {
+  Status st = check_qlinear(gate_, 1, f, d, "shared_expert.gate_proj");
+  if (st.ok) st = check_qlinear(up_, 1, f, d, "shared_expert.up_proj");
+  if (st.ok) st = check_qlinear(down_, 1, d, f, "shared_expert.down_proj");
+  if (st.ok && (gate_.bits != up_.bits || gate_.bits != down_.bits))
+    st = Status::error("shared_expert: projections must share bits");
+  return st;
+}
+
+void SwigluMlp::plan(Carve& ws, int64_t T, int64_t d, int64_t f) {
+  (void)d;
+  carve_dispatch(ws, T, 1, nullptr);
+  ws.take<uint16_t>(T * f);
+}
+
+// SwigluMlp::forward (swiglu_mlp.rs:63-70): down(swiglu(gate(x), up(x))).
+// The dense MLP runs through the grouped kernels as one expert that every
+// token selects.
+Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
+                          Carve& ws, int32_t* status, hipStream_t s) const {
+  const int64_t d = gate_.input_dims, f = gate_.output_dims;
+  const DispatchBuffers db = carve_dispatch(ws, T, 1, status);
+  uint16_t* act = ws.take<uint16_t>(T * f);
+  Status st = from_hip(launch_dispatch_identity(T, kPrefillTileRows, db, s),
+                       "shared_expert dispatch");
+  if (!st.ok) return st;
+  const bool prefill = use_prefill_path(T, 1);
+  QGemmArgs g{};
+  g.x = x;
+  g.x_ld = d;
+  g.row_map = nullptr;
+  g.row_div = 1;
+  g.offsets = db.offsets;
+  g.active = db.active;
+  g.num_active = db.num_active;
+  g.tiles = db.tiles;
+  g.num_tiles = db.num_tiles;
+  g.w0 = qw(gate_);
+  g.w1 = qw(up_);
+  g.E = 1;
+  g.N = (int32_t)f;
+  g.K = (int32_t)d;
+  g.bits = gate_.bits;
+  g.out = act;
+  g.out_ld = f;
+  g.out_map = nullptr;
+  g.gated = true;
+  st = from_hip(launch_qgemm(g, T, 1, prefill, s), "shared_expert gate/up");
+  if (!st.ok) return st;
+  QGemmArgs h = g;
+  h.x = act;
+  h.x_ld = f;
+  h.w0 = qw(down_);
+  h.w1 = QWeights{};
+  h.N = (int32_t)d;
+  h.K = (int32_t)f;
+  h.out = y;
+  h.out_ld = d;
+  h.gated = false;
+  return from_hip(launch_qgemm(h, T, 1, prefill, s), "shared_expert down");
+}
+
+// -------------------------------------------------------- SplitSwitchFfn
+Status SplitSwitchFfn::validate(int64_t d, int64_t f, int64_t E) const {
+  Status st = check_qlinear(w_.gate_proj, E, f, d, "switch_mlp.gate_proj");
+  if (st.ok) st = check_qlinear(w_.up_proj, E, f, d, "switch_mlp.up_proj");
+  if (st.ok)
+    st = check_qlinear(w_.down_proj, E, d, f, "switch_mlp.down_proj");
+  if (st.ok && (w_.gate_proj.bits != w_.up_proj.bits ||
+                w_.gate_proj.bits != w_.down_proj.bits))
+    st = Status::error("switch_mlp: projections must share bits");
+  if (st.ok && E > kMaxExperts)
+    st = Status::error("switch_mlp: at most " + std::to_string(kMaxExperts) +
+                       " experts");
+  return st;
+}
+
+void SplitSwitchFfn::plan(Carve& ws, int64_t T, int64_t K, int64_t d,
+                          int64_t f, int64_t E) {
+  ws.take<uint16_t>(T * K * d);  // y (forward_with_combine)
+  carve_dispatch(ws, T * K, E, nullptr);
+  ws.take<uint16_t>(T * K * f);
+}
+
+// SplitSwitchFfn::forward (switch.rs:417-442) on the sorted path: dispatch
+// (gather_sort), gate and up gather_qmm fused with swiglu, down gather_qmm
+// whose rows land at their flat (t, k) position (scatter_unsort).
+Status SplitSwitchFfn::forward(const uint16_t* x, int64_t T,
+                               const int32_t* indices, int64_t K, uint16_t* y,
+                               Carve& ws, int32_t* status,
+                               hipStream_t s) const {
+  const int64_t d = w_.gate_proj.input_dims, f = w_.gate_proj.output_dims;
+  const int64_t E = w_.gate_proj.num_experts;
+  const int64_t n = T * K;
+  const DispatchBuffers db = carve_dispatch(ws, n, E, status);
+  uint16_t* act = ws.take<uint16_t>(n * f);
+  Status st = from_hip(
+      launch_dispatch(indices, n, E, kPrefillTileRows, db, false, s),
+      "switch_mlp dispatch");
+  if (!st.ok) return st;
+  const int64_t max_active = std::min(E, n);
+  const bool prefill = use_prefill_path(n, E);
+  QGemmArgs g{};
+  g.x = x;
+  g.x_ld = d;
+  g.row_map = db.sorted;
+  g.row_div = (int32_t)K;
+  g.offsets = db.offsets;
+  g.active = db.active;
+  g.num_active = db.num_active;
+  g.tiles = db.tiles;
+  g.num_tiles = db.num_tiles;
+  g.w0 = qw(w_.gate_proj);
+  g.w1 = qw(w_.up_proj);
+  g.E = (int32_t)E;
+  g.N = (int32_t)f;
+  g.K = (int32_t)d;
+  g.bits = w_.gate_proj.bits;
+  g.out = act;
+  g.out_ld = f;
+  g.out_map = nullptr;
+  g.gated = true;
+  st = from_hip(launch_qgemm(g, n, max_active, prefill, s),
+                "switch_mlp gate/up");
+  if (!st.ok) return st;
+  QGemmArgs h = g;
+  h.x = act;
+  h.x_ld = f;
+  h.row_map = nullptr;
+  h.row_div = 1;
+  h.w0 = qw(w_.down_proj);
+  h.w1 = QWeights{};
+  h.N = (int32_t)d;
+  h.K = (int32_t)f;
+  h.out = y;
+  h.out_ld = d;
+  h.out_map = db.sorted;
+  h.gated = false;
+  return from_hip(launch_qgemm(h, n, max_active, prefill, s),
+                  "switch_mlp down");
+}
+
+// forward_with_combine (switch.rs:446-474) + combine_with_weights
+// (switch.rs:223-234); the block's shared branch is added in the same pass.
+Status SplitSwitchFfn::forward_with_combine(
+    const uint16_t* x, int64_t T, const int32_t* indices, const float* weights,
+    int64_t K, float* out, const uint16_t* shared_y, const float* shared_logit,
+    int64_t shared_ld, Carve& ws, int32_t* status, hipStream_t s) const {
+  const int64_t d = w_.gate_proj.input_dims;
+  uint16_t* y = ws.take<uint16_t>(T * K * d);
+  Status st = forward(x, T, indices, K, y, ws, status, s);
+  if (!st.ok) return st;
+  return from_hip(launch_combine(y, weights, T, K, d, shared_y, shared_logit,
+                                 shared_ld, out, s),
+                  "combine");
+}
+
+// -------------------------------------------------------- Qwen35MoeBlock
+Status Qwen35MoeBlock::validate() const {
+  const int64_t d = b_.hidden_size, E = b_.num_experts;
+  const int64_t K = b_.num_experts_per_tok, f = b_.moe_intermediate_size;
+  if (d <= 0 || E <= 0 || f <= 0)
+    return Status::error("block: hidden_size, num_experts and "
+                         "moe_intermediate_size must be positive");
+  if (K < 1 || K > E || K > 64)
+    return Status::error("block: num_experts_per_tok must be in [1, "
+                         "min(num_experts, 64)], got " + std::to_string(K));
+  if (d % 64)
+    return Status::error("block: hidden_size must be a multiple of 64");
+  if (!b_.gate_weight) return Status::error("block: gate_weight is required");
+  Status st = SplitSwitchFfn(b_.switch_mlp).validate(d, f, E);
+  if (st.ok && has_shared()) {
+    const int64_t fs = b_.shared_expert_intermediate_size;
+    st = SwigluMlp(b_.shared_gate_proj, b_.shared_up_proj,
+                   b_.shared_down_proj)
+             .validate(d, fs);
+  }
+  return st;
+}
+
+void Qwen35MoeBlock::plan(Carve& ws, const mlxr_moe_block& b, int64_t T) {
+  const int64_t d = b.hidden_size, E = b.num_experts;
+  const int64_t K = b.num_experts_per_tok, f = b.moe_intermediate_size;
+  const bool shared = b.shared_expert_gate_weight != nullptr;
+  ws.take<float>(T * (E + (shared ? 1 : 0)));
+  ws.take<int32_t>(T * K);
+  ws.take<float>(T * K);
+  if (shared) {
+    ws.take<uint16_t>(T * d);
+    SwigluMlp::plan(ws, T, d, b.shared_expert_intermediate_size);
+  }
+  SplitSwitchFfn::plan(ws, T, K, d, f, E);
+}
+
+// Qwen35MoeBlock::forward (moe.rs:116-146).
+Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
+                               int32_t* topk_idx, float* topk_w, Carve& ws,
+                               hipStream_t s) const {
+  const int64_t d = b_.hidden_size, E = b_.num_experts;
+  const int64_t K = b_.num_experts_per_tok;
+  const bool shared = has_shared();
+  const int64_t ld = E + (shared ? 1 : 0);
+  int32_t* status = reinterpret_cast<int32_t*>(ws.base);
+  float* logits = ws.take<float>(T * ld);
+  int32_t* idx = ws.take<int32_t>(T * K);
+  float* wts = ws.take<float>(T * K);
+  if (topk_idx) idx = topk_idx;
+  if (topk_w) wts = topk_w;
+  // gate.forward + shared_expert_gate.forward (moe.rs:118,123) in one pass.
+  Status st = from_hip(
+      launch_router_logits(x, T, d, b_.gate_weight, b_.gate_bias, E,
+                           shared ? b_.shared_expert_gate_weight : nullptr,
+                           logits, ld, s),
+      "router logits");
+  if (!st.ok) return st;
+  st = from_hip(launch_router_topk(logits, ld, T, E, K, idx, wts, s),
+                "router top-k");
+  if (!st.ok) return st;
+  uint16_t* sy = nullptr;
+  if (shared) {
+    sy = ws.take<uint16_t>(T * d);
+    st = SwigluMlp(b_.shared_gate_proj, b_.shared_up_proj,
+                   b_.shared_down_proj)
+             .forward(x, T, sy, ws, status, s);
+    if (!st.ok) return st;
+  }
+  return SplitSwitchFfn(b_.switch_mlp)
+      .forward_with_combine(x, T, idx, wts, K, out, sy,
+                            shared ? logits + E : nullptr, ld, ws, status, s);
+}
+
+}  // namespace nn
+}  // namespace mlxr_moe

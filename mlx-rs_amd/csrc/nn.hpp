@@ -1,0 +1,111 @@
+// C++ host mirror of mlxr-lm's MoE modules over the gfx950 kernels.
+//
+//   SwigluMlp        crates/mlxr-lm/src/nn/swiglu_mlp.rs:24-75
+//   SplitSwitchFfn   crates/mlxr-lm/src/nn/switch.rs:366-491
+//   Qwen35MoeBlock   crates/mlxr-lm/src/qwen3_5/text/moe.rs:43-159
+//
+// Modules hold non-owning views of caller-owned device weights (the
+// mlxr_moe_* descriptors of the C ABI).  forward() enqueues on a stream and
+// takes scratch from a caller-provided workspace; the sizes come from the
+// same carving code run without a base pointer, so plan and execution
+// cannot disagree.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/mlxr_moe.h"
+#include "kernels.hpp"
+
+namespace mlxr_moe {
+
+// Bump allocator over a workspace; with base == nullptr it only measures.
+struct Carve {
+  char* base;
+  size_t off = 0;
+  explicit Carve(void* b) : base(static_cast<char*>(b)) {}
+  template <class T>
+  T* take(int64_t count) {
+    off = (off + 255) & ~size_t(255);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += size_t(count > 0 ? count : 0) * sizeof(T);
+    return p;
+  }
+};
+
+// Failure inside a module: a message for mlxr_moe_last_error().
+struct Status {
+  bool ok = true;
+  std::string what;
+  static Status error(std::string m) { return Status{false, std::move(m)}; }
+};
+
+Status check_qlinear(const mlxr_moe_qlinear& q, int64_t experts, int64_t out,
+                     int64_t in, const char* name);
+Status from_hip(hipError_t e, const char* where);
+
+// Dispatch buffers for n flat rows over E experts, carved from a workspace.
+DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
+                               int32_t* status);
+
+namespace nn {
+
+// Rows per expert above which the MFMA tile kernel with LDS-dequantised
+// weights runs instead of the register-dequant kernel (the reference
+// switches to its sorted path at T*K >= SORT_THRESHOLD = 2048, switch.rs:40;
+// here the choice is about GEMM shape, not sorting, which always happens).
+bool use_prefill_path(int64_t rows, int64_t experts);
+
+class SwigluMlp {
+ public:
+  SwigluMlp(const mlxr_moe_qlinear& gate, const mlxr_moe_qlinear& up,
+            const mlxr_moe_qlinear& down)
+      : gate_(gate), up_(up), down_(down) {}
+  Status validate(int64_t d, int64_t f) const;
+  // y bf16 [T, d] = down(silu(gate(x)) * up(x))
+  Status forward(const uint16_t* x, int64_t T, uint16_t* y, Carve& ws,
+                 int32_t* status, hipStream_t s) const;
+  static void plan(Carve& ws, int64_t T, int64_t d, int64_t f);
+
+ private:
+  mlxr_moe_qlinear gate_, up_, down_;
+};
+
+class SplitSwitchFfn {
+ public:
+  explicit SplitSwitchFfn(const mlxr_moe_switch_glu& w) : w_(w) {}
+  Status validate(int64_t d, int64_t f, int64_t E) const;
+  // SplitSwitchFfn::forward: y bf16 [T, K, d] per-expert outputs.
+  Status forward(const uint16_t* x, int64_t T, const int32_t* indices,
+                 int64_t K, uint16_t* y, Carve& ws, int32_t* status,
+                 hipStream_t s) const;
+  // forward_with_combine: out f32 [T, d] = sum_k w * y (+ shared branch).
+  Status forward_with_combine(const uint16_t* x, int64_t T,
+                              const int32_t* indices, const float* weights,
+                              int64_t K, float* out, const uint16_t* shared_y,
+                              const float* shared_logit, int64_t shared_ld,
+                              Carve& ws, int32_t* status,
+                              hipStream_t s) const;
+  static void plan(Carve& ws, int64_t T, int64_t K, int64_t d, int64_t f,
+                   int64_t E);
+
+ private:
+  mlxr_moe_switch_glu w_;
+};
+
+class Qwen35MoeBlock {
+ public:
+  explicit Qwen35MoeBlock(const mlxr_moe_block& b) : b_(b) {}
+  Status validate() const;
+  bool has_shared() const { return b_.shared_expert_gate_weight != nullptr; }
+  Status forward(const uint16_t* x, int64_t T, float* out, int32_t* topk_idx,
+                 float* topk_w, Carve& ws, hipStream_t s) const;
+  static void plan(Carve& ws, const mlxr_moe_block& b, int64_t T);
+
+ private:
+  mlxr_moe_block b_;
+};
+
+}  // namespace nn
+}  // namespace mlxr_moe

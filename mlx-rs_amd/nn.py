@@ -1,0 +1,238 @@
+"""mlxr-lm MoE modules over the gfx950 C ABI.
+
+    QuantizedSwitchLinear  crates/mlxr-lm/src/nn/switch.rs:115-168
+    QuantizedLinear        crates/mlxr/src/layers/quantized.rs:214-379
+    SwigluMlp              crates/mlxr-lm/src/nn/swiglu_mlp.rs:24-75
+    SplitSwitchFfn         crates/mlxr-lm/src/nn/switch.rs:366-491
+    Qwen35MoeBlock         crates/mlxr-lm/src/qwen3_5/text/moe.rs:43-159
+
+Each module keeps its device tensors (torch, for memory) and the C
+descriptor that points at them; forward() is one C-ABI call whose kernels
+run on the current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _capi as C
+from . import ops
+from ._capi import MlxrMoeError
+
+
+class QuantizedSwitchLinear:
+    """Expert-stacked quantised linear: weight [E, out, in*bits/32] (int32
+    storage of uint32 words), scales/biases bf16 [E, out, in/group]."""
+
+    def __init__(self, weight, scales, biases, group_size=64, bits=4):
+        if weight.ndim != 3:
+            raise MlxrMoeError("QuantizedSwitchLinear weight must be [E, out, packed_in]")
+        self.weight = weight.contiguous()
+        self.scales = scales.contiguous()
+        self.biases = biases.contiguous()
+        self.group_size = group_size
+        self.bits = bits
+
+    @classmethod
+    def try_from_switch_linear(cls, weight, group_size=64, bits=4):
+        """QuantizedSwitchLinear::try_from_switch_linear (switch.rs:129-145)."""
+        wq, s, b = ops.quantize(weight, group_size, bits)
+        return cls(wq, s, b, group_size, bits)
+
+    @property
+    def num_experts(self):
+        return self.weight.shape[0]
+
+    @property
+    def output_dims(self):
+        return self.weight.shape[1]
+
+    @property
+    def input_dims(self):
+        return self.weight.shape[2] * 32 // self.bits
+
+    def apply(self, x, indices, sorted=False):
+        """QuantizedSwitchLinear::apply (switch.rs:148-167)."""
+        return ops.gather_qmm(x, self.weight, self.scales, self.biases, None, indices, True,
+                              self.group_size, self.bits, sorted)
+
+    def descriptor(self) -> C.QLinear:
+        return C.QLinear(self.weight.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(),
+                         self.num_experts, self.output_dims, self.input_dims,
+                         self.group_size, self.bits)
+
+
+class QuantizedLinear(QuantizedSwitchLinear):
+    """A single quantised linear (weight [out, in*bits/32]) seen as one
+    expert."""
+
+    def __init__(self, weight, scales, biases, group_size=64, bits=4):
+        super().__init__(weight.reshape((1,) + tuple(weight.shape)),
+                         scales.reshape((1,) + tuple(scales.shape)),
+                         biases.reshape((1,) + tuple(biases.shape)), group_size, bits)
+
+    @classmethod
+    def try_from_linear(cls, weight, group_size=64, bits=4):
+        """QuantizedLinear::try_from_linear (layers/quantized.rs:249-273)."""
+        wq, s, b = ops.quantize(weight, group_size, bits)
+        return cls(wq, s, b, group_size, bits)
+
+    def forward(self, x):
+        """quantized_matmul(x, w, transpose=true) (layers/quantized.rs:356-373)."""
+        lead = tuple(x.shape[:-1])
+        x2 = x.reshape(-1, 1, x.shape[-1])
+        idx = torch.zeros(x2.shape[0], dtype=torch.int32, device=x.device)
+        y = ops.gather_qmm(x2, self.weight, self.scales, self.biases, None, idx, True,
+                           self.group_size, self.bits)
+        return y.reshape(lead + (self.output_dims,))
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+class SplitSwitchFfn:
+    """SplitSwitchFfn<SwigluActivation>: gate_proj, up_proj [E, f, d],
+    down_proj [E, d, f]."""
+
+    def __init__(self, gate_proj: QuantizedSwitchLinear, up_proj: QuantizedSwitchLinear,
+                 down_proj: QuantizedSwitchLinear):
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+        self._desc = C.SwitchGlu(gate_proj.descriptor(), up_proj.descriptor(),
+                                 down_proj.descriptor())
+
+    @classmethod
+    def from_dense(cls, gate_w, up_w, down_w, group_size=64, bits=4):
+        """Quantise dense expert weights, as try_into_quantized does
+        (switch.rs:478-491)."""
+        q = QuantizedSwitchLinear.try_from_switch_linear
+        return cls(q(gate_w, group_size, bits), q(up_w, group_size, bits),
+                   q(down_w, group_size, bits))
+
+    def descriptor(self) -> C.SwitchGlu:
+        return self._desc
+
+    def _prep(self, x, indices):
+        d = self.gate_proj.input_dims
+        x2 = x.reshape(-1, d).contiguous()
+        K = indices.shape[-1]
+        idx = indices.reshape(-1, K).to(torch.int32).contiguous()
+        if idx.shape[0] != x2.shape[0]:
+            raise MlxrMoeError("SplitSwitchFfn: indices must be [..., T, K] over x [..., T, d]")
+        return x2, idx, K
+
+    def forward(self, x, indices):
+        """Per-expert outputs [..., K, d] (switch.rs:417-442)."""
+        x2, idx, K = self._prep(x, indices)
+        T, d = x2.shape
+        y = torch.empty((T, K, d), dtype=torch.bfloat16, device=x.device)
+        lib = C.lib()
+        ws = ops.workspace(lib.mlxr_moe_switch_glu_workspace_size(ctypes.byref(self._desc), T, K),
+                           x.device)
+        C.check(lib.mlxr_moe_switch_glu_experts(
+            ctypes.byref(self._desc), _ptr(x2), T, _ptr(idx), K, _ptr(y), _ptr(ws), ws.numel(),
+            ops._stream(x)))
+        self.last_workspace = ws
+        return y.reshape(tuple(indices.shape) + (d,))
+
+    def forward_with_combine(self, x, indices, weights):
+        """sum_k weights * expert_k(x) -> f32 [..., d] (switch.rs:446-474)."""
+        x2, idx, K = self._prep(x, indices)
+        T, d = x2.shape
+        w = weights.reshape(-1, K).to(torch.float32).contiguous()
+        out = torch.empty((T, d), dtype=torch.float32, device=x.device)
+        lib = C.lib()
+        ws = ops.workspace(lib.mlxr_moe_switch_glu_workspace_size(ctypes.byref(self._desc), T, K),
+                           x.device)
+        C.check(lib.mlxr_moe_switch_glu_forward(
+            ctypes.byref(self._desc), _ptr(x2), T, _ptr(idx), _ptr(w), K, _ptr(out), _ptr(ws),
+            ws.numel(), ops._stream(x)))
+        self.last_workspace = ws
+        return out.reshape(tuple(x.shape[:-1]) + (d,))
+
+
+class SwigluMlp:
+    """down(silu(gate(x)) * up(x)) with QuantizedLinear projections."""
+
+    def __init__(self, gate_proj: QuantizedLinear, up_proj: QuantizedLinear,
+                 down_proj: QuantizedLinear):
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+
+    def forward(self, x):
+        """SwigluMlp::forward (swiglu_mlp.rs:63-70); bf16 output.  Runs as
+        a one-expert SplitSwitchFfn with routing weight 1 (exact)."""
+        ffn = SplitSwitchFfn(self.gate_proj, self.up_proj, self.down_proj)
+        lead = tuple(x.shape[:-1])
+        T = x.numel() // x.shape[-1]
+        idx = torch.zeros((T, 1), dtype=torch.int32, device=x.device)
+        return ffn.forward(x.reshape(T, -1), idx).reshape(lead + (-1,))
+
+
+class Qwen35MoeBlock:
+    """Router (f32 Linear [E, d]) -> softmax -> top-k -> renormalise ->
+    SplitSwitchFfn, plus an optional sigmoid-gated shared SwigluMlp."""
+
+    def __init__(self, gate_weight, switch_mlp: SplitSwitchFfn, num_experts_per_tok: int,
+                 shared_expert: SwigluMlp | None = None, shared_expert_gate_weight=None,
+                 gate_bias=None):
+        if (shared_expert is None) != (shared_expert_gate_weight is None):
+            raise MlxrMoeError("shared_expert and shared_expert_gate_weight go together")
+        self.gate_weight = gate_weight.to(torch.float32).contiguous()
+        self.gate_bias = None if gate_bias is None else gate_bias.to(torch.float32).contiguous()
+        self.switch_mlp = switch_mlp
+        self.shared_expert = shared_expert
+        self.shared_expert_gate_weight = (
+            None if shared_expert_gate_weight is None
+            else shared_expert_gate_weight.to(torch.float32).contiguous())
+        self.num_experts_per_tok = num_experts_per_tok
+        E, d = self.gate_weight.shape
+        f = switch_mlp.gate_proj.output_dims
+        z = C.QLinear()
+        se = shared_expert
+        self._desc = C.Block(
+            d, E, num_experts_per_tok, f,
+            0 if se is None else se.gate_proj.output_dims,
+            self.gate_weight.data_ptr(), _ptr(self.gate_bias), switch_mlp.descriptor(),
+            z if se is None else se.gate_proj.descriptor(),
+            z if se is None else se.up_proj.descriptor(),
+            z if se is None else se.down_proj.descriptor(),
+            _ptr(self.shared_expert_gate_weight))
+        self._ws = None
+        self.last_indices = None
+        self.last_weights = None
+
+    def descriptor(self) -> C.Block:
+        return self._desc
+
+    def workspace_size(self, T: int) -> int:
+        return C.lib().mlxr_moe_block_workspace_size(ctypes.byref(self._desc), T)
+
+    def forward(self, x, out=None, workspace=None, keep_routing=True):
+        """Qwen35MoeBlock::forward (moe.rs:116-146): x bf16 [..., d] ->
+        f32 [..., d]."""
+        d = x.shape[-1]
+        x2 = x.reshape(-1, d)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        T = x2.shape[0]
+        K = self.num_experts_per_tok
+        if out is None:
+            out = torch.empty((T, d), dtype=torch.float32, device=x.device)
+        if workspace is None:
+            need = self.workspace_size(T)
+            if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
+                self._ws = ops.workspace(need, x.device)
+            workspace = self._ws
+        idx = wts = None
+        if keep_routing:
+            idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
+            wts = torch.empty((T, K), dtype=torch.float32, device=x.device)
+        C.check(C.lib().mlxr_moe_block_forward(
+            ctypes.byref(self._desc), _ptr(x2), T, _ptr(out), _ptr(idx), _ptr(wts),
+            _ptr(workspace), workspace.numel(), ops._stream(x)))
+        self.last_indices, self.last_weights = idx, wts
+        self.last_workspace = workspace
+        return out.reshape(tuple(x.shape[:-1]) + (d,))
+
+    __call__ = forward

@@ -1,0 +1,154 @@
+"""MoE block configurations and seeded synthetic weights/inputs.
+
+The five shapes the block is measured and tested on (c1 small CPU case,
+c2 Qwen3-30B-A3B-shaped decode, c3 the same shape at prefill with Zipf
+routing skew, c4 high-expert-count with shared expert, c5 wide 8-bit).
+Weights are drawn N(0, 0.02) in f32, rounded to bf16 and affine-quantised
+on the device by this library's quantize kernel; x ~ N(0, 1) in bf16;
+router weights N(0, 0.02) in f32 (unquantised).  No checkpoint is read:
+everything is synthetic, from torch generators seeded per tensor.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import nn, ops
+
+
+@dataclass(frozen=True)
+class MoEConfig:
+    name: str
+    d: int                 # hidden size
+    E: int                 # routed experts
+    K: int                 # experts per token
+    f: int                 # expert intermediate size
+    fs: int = 0            # shared-expert intermediate size (0: none)
+    bits: int = 4
+    group_size: int = 64
+    zipf_alpha: float | None = None   # routing skew via per-expert logit bias
+    tokens: tuple = field(default_factory=tuple)
+    seed: int = 0
+
+
+CONFIGS = {
+    "c1": MoEConfig("c1_small_cpu", d=512, E=8, K=2, f=256, tokens=(16,)),
+    "c2": MoEConfig("c2_qwen3_30b_a3b_decode", d=2048, E=128, K=8, f=768,
+                    tokens=(1, 8, 32, 64)),
+    "c3": MoEConfig("c3_qwen3_30b_a3b_prefill_zipf", d=2048, E=128, K=8, f=768,
+                    zipf_alpha=1.1, tokens=(512, 2048, 4096)),
+    "c4": MoEConfig("c4_e512_top10_shared", d=2048, E=512, K=10, f=512, fs=512,
+                    tokens=(1, 64, 2048)),
+    "c5": MoEConfig("c5_wide_8bit_zipf", d=4096, E=128, K=8, f=1536, bits=8,
+                    zipf_alpha=1.1, tokens=(32, 512)),
+}
+
+
+def _gen(device, seed: int, stream: int) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed * 1000003 + stream)
+    return g
+
+
+def _normal(shape, std, device, seed, stream):
+    return torch.randn(shape, generator=_gen(device, seed, stream), device=device,
+                       dtype=torch.float32) * std
+
+
+def make_x(cfg: MoEConfig, T: int, device, seed: int | None = None) -> torch.Tensor:
+    seed = cfg.seed if seed is None else seed
+    return _normal((T, cfg.d), 1.0, device, seed, 1).to(torch.bfloat16)
+
+
+def zipf_bias(cfg: MoEConfig, gate_w: torch.Tensor, device, iters: int = 20,
+              n_cal: int = 4096) -> torch.Tensor:
+    """Per-expert router bias giving a Zipf(alpha) top-K load over a seeded
+    permutation of experts, calibrated by fixed-point iterations
+    b += log p - log p_hat on a separate calibration batch (seed 1)."""
+    E, K = cfg.E, cfg.K
+    perm = torch.randperm(E, generator=_gen("cpu", cfg.seed, 7))
+    rank = torch.empty(E)
+    rank[perm] = torch.arange(1, E + 1, dtype=torch.float32)
+    p = rank.pow(-cfg.zipf_alpha)
+    p = (p / p.sum()).to(device)
+    b = p.log()
+    xc = _normal((n_cal, cfg.d), 1.0, device, 1, 11).to(torch.bfloat16).float()
+    base = xc @ gate_w.t()
+    for _ in range(iters):
+        top = (base + b).topk(K, dim=-1).indices
+        load = torch.bincount(top.reshape(-1), minlength=E).float() / (n_cal * K)
+        if (load - p).abs().sum() < 0.05:
+            break
+        b = b + (p.log() - (load + 1e-6).log()) * 0.5
+    return b.float()
+
+
+@dataclass
+class BlockWeights:
+    cfg: MoEConfig
+    gate_w: torch.Tensor
+    gate_b: torch.Tensor | None
+    switch_mlp: nn.SplitSwitchFfn
+    shared_expert: nn.SwigluMlp | None
+    shared_gate_w: torch.Tensor | None
+
+    def block(self) -> nn.Qwen35MoeBlock:
+        return nn.Qwen35MoeBlock(self.gate_w, self.switch_mlp, self.cfg.K, self.shared_expert,
+                                 self.shared_gate_w, self.gate_b)
+
+
+def make_weights(cfg: MoEConfig, device) -> BlockWeights:
+    """Seeded weights for `cfg`, quantised on `device` by this library."""
+    s = cfg.seed
+    gate_w = _normal((cfg.E, cfg.d), 0.02, device, s, 2)
+    gate_b = zipf_bias(cfg, gate_w, device) if cfg.zipf_alpha else None
+
+    def qbank(shape, stream):
+        w = _normal(shape, 0.02, device, s, stream).to(torch.bfloat16)
+        return nn.QuantizedSwitchLinear.try_from_switch_linear(w, cfg.group_size, cfg.bits)
+
+    mlp = nn.SplitSwitchFfn(qbank((cfg.E, cfg.f, cfg.d), 3), qbank((cfg.E, cfg.f, cfg.d), 4),
+                            qbank((cfg.E, cfg.d, cfg.f), 5))
+    shared = sgw = None
+    if cfg.fs:
+        def qlin(shape, stream):
+            w = _normal(shape, 0.02, device, s, stream).to(torch.bfloat16)
+            return nn.QuantizedLinear.try_from_linear(w, cfg.group_size, cfg.bits)
+        shared = nn.SwigluMlp(qlin((cfg.fs, cfg.d), 8), qlin((cfg.fs, cfg.d), 9),
+                              qlin((cfg.d, cfg.fs), 10))
+        sgw = _normal((1, cfg.d), 0.02, device, s, 12)
+    return BlockWeights(cfg, gate_w, gate_b, mlp, shared, sgw)
+
+
+def algorithmic_bytes(cfg: MoEConfig, T: int, distinct_experts: int) -> int:
+    """HBM bytes one block forward must move at decode: the packed weights,
+    scales and biases of the distinct selected experts (3 projections), the
+    f32 router weights, x in, f32 out, and the routing (idx + weight)."""
+    per_w = cfg.bits / 8 + 4 / cfg.group_size
+    b = distinct_experts * 3 * cfg.f * cfg.d * per_w + cfg.E * cfg.d * 4
+    if cfg.fs:
+        b += 3 * cfg.fs * cfg.d * per_w + cfg.d * 4
+    b += T * cfg.d * 2 + T * cfg.d * 4 + T * cfg.K * 8
+    return int(b)
+
+
+def algorithmic_flops(cfg: MoEConfig, T: int) -> int:
+    """Expert matmul FLOPs of one forward: 6*T*K*f*d (+ shared expert)."""
+    fl = 6 * T * cfg.K * cfg.f * cfg.d
+    if cfg.fs:
+        fl += 6 * T * cfg.fs * cfg.d + 2 * T * cfg.d
+    return int(fl)
+
+
+def distinct(indices: torch.Tensor) -> int:
+    return int(torch.unique(indices.reshape(-1)).numel())
+
+
+def expert_bytes_per_row(cfg: MoEConfig, K_dim: int) -> float:
+    return K_dim * (cfg.bits / 8 + 4 / cfg.group_size)
+
+
+__all__ = ["MoEConfig", "CONFIGS", "make_x", "make_weights", "BlockWeights", "zipf_bias",
+           "algorithmic_bytes", "algorithmic_flops", "distinct", "math", "ops"]

@@ -1,0 +1,464 @@
+/*
+ * moe_oracle.c -- CPU restatement of mlxr-lm's sparse-MoE block.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker for the HIP path and the
+ * "port" CPU baseline.  Never linked into the product library.
+ *
+ * Reference op sequence (paths relative to /root/reference):
+ *   Qwen35MoeBlock::forward      crates/mlxr-lm/src/qwen3_5/text/moe.rs:116-146
+ *   SplitSwitchFfn::forward*     crates/mlxr-lm/src/nn/switch.rs:417-474
+ *   combine_with_weights         crates/mlxr-lm/src/nn/switch.rs:223-234
+ *   gather_sort / scatter_unsort crates/mlxr-lm/src/nn/switch.rs:499-517
+ *   QuantizedSwitchLinear::apply crates/mlxr-lm/src/nn/switch.rs:148-167
+ *   SwigluMlp::forward           crates/mlxr-lm/src/nn/swiglu_mlp.rs:63-70
+ *   swiglu / silu                crates/mlxr-lm/src/activations.rs:187-200,
+ *                                crates/mlxr/src/layers/activation.rs:869-873
+ *   quantize/dequantize/gather_qmm crates/mlxr/src/ops/quantization.rs:47-221
+ *   argpartition_axis            crates/mlxr/src/ops/sort.rs:186-226
+ *   packed layout + dequant      crates/mlxr-lm/src/attention/kernel_source.rs:30-35,96-107
+ *   host scalar dequant mirror   crates/mlxr-lm/src/cache/fused_quantized_sdpa.rs:448-530
+ *
+ * What pins each function (tests/test_oracle.py):
+ *   orc_quantize      reference test quantization.rs:299-315 (max error
+ *                     bound at bits 2/4/8), closed forms (constant group,
+ *                     exact code ladders), brute-force optimality of codes.
+ *                     The fp32 scale/bias recipe itself is MLX v0.31.2's
+ *                     affine quantiser restated from its published source;
+ *                     no reference-held vector pins its last bits.
+ *   orc_dequantize    closed form code*scale+bias; round trip with
+ *                     orc_quantize; slot layout of kernel_source.rs:101-104.
+ *   orc_router_logits fp64 dot products (rounding bound), permutation of
+ *                     experts, one-hot inputs.
+ *   orc_router_topk   full sort on small E, softmax sums to 1, renorm.
+ *   orc_dispatch      equals a stable argsort (switch.rs:499-512), inverse.
+ *   orc_gather_qmm    equals gather_mm(x, dequant(w)^T) in fp64
+ *                     (quantization.rs:344-421), lhs/rhs index cases.
+ *   orc_swiglu        reference test activations.rs:341-351.
+ *   orc_block_forward sorted and unsorted dispatch give identical outputs
+ *                     (switch.rs:446-474); K=1 reduces to one expert;
+ *                     linearity in the routing weights.
+ */
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ bf16 */
+
+float orc_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0; /* NaN */
+  u += 0x7fffu + ((u >> 16) & 1u);                      /* RNE */
+  return (uint16_t)(u >> 16);
+}
+
+static inline float load_val(const void* p, int dtype, int64_t i) {
+  return dtype == ORC_BF16 ? orc_bf16_to_f32(((const uint16_t*)p)[i])
+                           : ((const float*)p)[i];
+}
+
+static inline void store_val(void* p, int dtype, int64_t i, float v) {
+  if (dtype == ORC_BF16)
+    ((uint16_t*)p)[i] = orc_f32_to_bf16(v);
+  else
+    ((float*)p)[i] = v;
+}
+
+static inline float round_to(int dtype, float v) {
+  return dtype == ORC_BF16 ? orc_bf16_to_f32(orc_f32_to_bf16(v)) : v;
+}
+
+static int valid_quant(int group_size, int bits) {
+  return (bits == 2 || bits == 4 || bits == 8) &&
+         (group_size == 32 || group_size == 64 || group_size == 128);
+}
+
+/* -------------------------------------------------------------- quantize */
+/* MLX affine quantiser (mlx v0.31.2, called via mlx_quantize from
+ * crates/mlxr/src/ops/quantization.rs:47-70).  Per group of group_size
+ * consecutive elements of a row, in fp32:
+ *   n_bins = 2^bits - 1
+ *   scale  = max((max - min) / n_bins, 1e-7), negated unless |min| > |max|
+ *   edge   = |min| > |max| ? min : max
+ *   q0     = rint(edge / scale); if q0 != 0: scale = edge / q0, bias = edge
+ *   code   = clamp(rint((w - bias) / scale), 0, n_bins)   (unrounded s, b)
+ * scale and bias are stored rounded to w's dtype.  Codes pack little-end
+ * first: element k of a word sits at bits [k*bits, (k+1)*bits). */
+int orc_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
+                 int group_size, int bits, uint32_t* wq, void* scales,
+                 void* biases) {
+  if (!valid_quant(group_size, bits) || cols % group_size) return -1;
+  const float n_bins = (float)((1 << bits) - 1);
+  const int per_word = 32 / bits;
+  const int64_t groups = cols / group_size;
+  const int64_t words_per_row = cols / per_word;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t g = 0; g < groups; ++g) {
+      const int64_t base = r * cols + g * group_size;
+      float wmax = -INFINITY, wmin = INFINITY;
+      for (int j = 0; j < group_size; ++j) {
+        float v = load_val(w, w_dtype, base + j);
+        wmax = fmaxf(wmax, v);
+        wmin = fminf(wmin, v);
+      }
+      const int neg_edge = fabsf(wmin) > fabsf(wmax);
+      float scale = fmaxf((wmax - wmin) / n_bins, 1e-7f);
+      scale = neg_edge ? scale : -scale;
+      const float edge = neg_edge ? wmin : wmax;
+      const float q0 = rintf(edge / scale);
+      float bias = 0.0f;
+      if (q0 != 0.0f) {
+        scale = edge / q0;
+        bias = edge;
+      }
+      for (int wi = 0; wi < group_size / per_word; ++wi) {
+        uint32_t word = 0;
+        for (int k = 0; k < per_word; ++k) {
+          float v = load_val(w, w_dtype, base + wi * per_word + k);
+          float q = rintf((v - bias) / scale);
+          q = fminf(fmaxf(q, 0.0f), n_bins);
+          word |= (uint32_t)q << (k * bits);
+        }
+        wq[r * words_per_row + (g * group_size) / per_word + wi] = word;
+      }
+      store_val(scales, w_dtype, r * groups + g, scale);
+      store_val(biases, w_dtype, r * groups + g, bias);
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------ dequantize */
+/* w = code * scale + bias  (kernel_source.rs:96-107; the host mirror at
+ * fused_quantized_sdpa.rs:471-480 does the same in f32), evaluated as one
+ * fused multiply-add and rounded once to out_dtype. */
+int orc_dequantize(const uint32_t* wq, const void* scales, const void* biases,
+                   int sb_dtype, int64_t rows, int64_t cols, int group_size,
+                   int bits, void* out, int out_dtype) {
+  if (!valid_quant(group_size, bits) || cols % group_size) return -1;
+  const int per_word = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  const int64_t groups = cols / group_size;
+  const int64_t words_per_row = cols / per_word;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < cols; ++c) {
+      const uint32_t word = wq[r * words_per_row + c / per_word];
+      const uint32_t code = (word >> ((c % per_word) * bits)) & mask;
+      const float s = load_val(scales, sb_dtype, r * groups + c / group_size);
+      const float b = load_val(biases, sb_dtype, r * groups + c / group_size);
+      store_val(out, out_dtype, r * cols + c, fmaf((float)code, s, b));
+    }
+  }
+  return 0;
+}
+
+/* --------------------------------------------------------------- router */
+/* Router projection (moe.rs:123 -> Linear::forward, linear.rs:91-95:
+ * matmul(x, W^T) with x bf16 promoted to f32).  Summation order, shared
+ * with the HIP kernel: 64 lanes; lane l owns elements j = 4l + 256i + c
+ * (c = 0..3), accumulates fmaf(x_j, w_j, acc) over i then c; lanes are then
+ * combined by the butterfly v += v[l ^ m] for m = 32, 16, 8, 4, 2, 1. */
+static float lane_dot(const uint16_t* xrow, const float* wrow, int64_t d) {
+  float lane[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int64_t i = 0; 4 * l + 256 * i < d; ++i) {
+      for (int c = 0; c < 4; ++c) {
+        int64_t j = 4 * l + 256 * i + c;
+        if (j < d) acc = fmaf(orc_bf16_to_f32(xrow[j]), wrow[j], acc);
+      }
+    }
+    lane[l] = acc;
+  }
+  for (int m = 32; m >= 1; m >>= 1) {
+    float nxt[64];
+    for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ m];
+    memcpy(lane, nxt, sizeof(lane));
+  }
+  return lane[0];
+}
+
+void orc_router_logits(const uint16_t* x, const float* w, int64_t T,
+                       int64_t d, int64_t E, float* logits) {
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t e = 0; e < E; ++e)
+      logits[t * E + e] = lane_dot(x + t * d, w + e * d, d);
+}
+
+/* softmax_axis(precise) + argpartition(-K) + take_along_axis + sum + divide
+ * (moe.rs:124-138).  Selection on logits, descending, ties to the lower id.
+ * Softmax: m = max, S = sum exp(l - m) accumulated per lane (lane l holds
+ * experts l, l+64, ...) then the same butterfly as above; p = exp(l - m)/S;
+ * weights = p_k / (p_0 + ... + p_{K-1}) summed in k order. */
+void orc_router_topk(const float* logits, int64_t T, int64_t E, int64_t K,
+                     int32_t* idx, float* weights) {
+  char* taken = (char*)malloc((size_t)E);
+  float* p = (float*)malloc(sizeof(float) * (size_t)K);
+  for (int64_t t = 0; t < T; ++t) {
+    const float* l = logits + t * E;
+    memset(taken, 0, (size_t)E);
+    for (int64_t k = 0; k < K; ++k) {
+      int64_t best = -1;
+      for (int64_t e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        if (best < 0 || l[e] > l[best]) best = e;
+      }
+      taken[best] = 1;
+      idx[t * K + k] = (int32_t)best;
+    }
+    const float m = l[idx[t * K]];
+    float lane[64];
+    for (int ln = 0; ln < 64; ++ln) {
+      float acc = 0.0f;
+      for (int64_t e = ln; e < E; e += 64) acc += expf(l[e] - m);
+      lane[ln] = acc;
+    }
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+      float nxt[64];
+      for (int ln = 0; ln < 64; ++ln) nxt[ln] = lane[ln] + lane[ln ^ msk];
+      memcpy(lane, nxt, sizeof(lane));
+    }
+    const float S = lane[0];
+    float psum = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      p[k] = expf(l[idx[t * K + k]] - m) / S;
+      psum += p[k];
+    }
+    for (int64_t k = 0; k < K; ++k) weights[t * K + k] = p[k] / psum;
+  }
+  free(p);
+  free(taken);
+}
+
+/* ------------------------------------------------------------- dispatch */
+/* gather_sort (switch.rs:499-512): order = argsort(flat ids) (stable),
+ * inv = argsort(order).  Counting sort gives the same permutation. */
+int orc_dispatch(const int32_t* ids, int64_t n, int64_t E, int32_t* counts,
+                 int32_t* offsets, int32_t* sorted, int32_t* inv) {
+  memset(counts, 0, sizeof(int32_t) * (size_t)E);
+  for (int64_t i = 0; i < n; ++i) {
+    if (ids[i] < 0 || ids[i] >= E) return -1;
+    counts[ids[i]]++;
+  }
+  offsets[0] = 0;
+  for (int64_t e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+  int32_t* fill = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+  memcpy(fill, offsets, sizeof(int32_t) * (size_t)E);
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t pos = fill[ids[i]]++;
+    sorted[pos] = (int32_t)i;
+    inv[i] = pos;
+  }
+  free(fill);
+  return 0;
+}
+
+/* ----------------------------------------------------------- gather_qmm */
+/* One output element: x (already f32) . dequant(weight row), f32
+ * accumulation in 8 interleaved partial sums. */
+static float qdot(const float* xf, const uint32_t* wrow, const uint16_t* srow,
+                  const uint16_t* brow, int64_t Kd, int gs, int bits) {
+  const int per_word = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t g = 0; g < Kd / gs; ++g) {
+    const float s = orc_bf16_to_f32(srow[g]);
+    const float b = orc_bf16_to_f32(brow[g]);
+    const uint32_t* wg = wrow + g * gs / per_word;
+    const float* xg = xf + g * gs;
+    for (int wi = 0; wi < gs / per_word; ++wi) {
+      uint32_t word = wg[wi];
+      for (int k = 0; k < per_word; ++k) {
+        const float wv = fmaf((float)((word >> (k * bits)) & mask), s, b);
+        part[k & 7] = fmaf(xg[wi * per_word + k], wv, part[k & 7]);
+      }
+    }
+  }
+  return ((part[0] + part[1]) + (part[2] + part[3])) +
+         ((part[4] + part[5]) + (part[6] + part[7]));
+}
+
+/* y[n] = bf16(x . dequant(W[e, n])) for n in [0, N) */
+static void qmv(const float* xf, const orc_qlinear* q, int64_t e, int64_t N,
+                int64_t Kd, int gs, int bits, uint16_t* y) {
+  const int64_t wpr = Kd * bits / 32, gpr = Kd / gs;
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t row = e * N + n;
+    y[n] = orc_f32_to_bf16(qdot(xf, q->w + row * wpr, q->scales + row * gpr,
+                                q->biases + row * gpr, Kd, gs, bits));
+  }
+}
+
+int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
+                   const uint32_t* w, const uint16_t* scales,
+                   const uint16_t* biases, int64_t E, int64_t N,
+                   const int32_t* lhs, const int32_t* rhs, int64_t B,
+                   int group_size, int bits, uint16_t* out, int nthreads) {
+  if (!valid_quant(group_size, bits) || Kd % group_size) return -1;
+  if (!lhs && (x_batch <= 0 || B % x_batch)) return -1;
+  for (int64_t b = 0; b < B; ++b) {
+    if (rhs[b] < 0 || rhs[b] >= E) return -1;
+    if (lhs && (lhs[b] < 0 || lhs[b] >= x_batch)) return -1;
+  }
+  orc_qlinear q = {w, scales, biases};
+  const int64_t rep = lhs ? 1 : B / x_batch;
+  if (nthreads <= 0) nthreads = 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+  for (int64_t bm = 0; bm < B * M; ++bm) {
+    const int64_t b = bm / M, m = bm % M;
+    const int64_t xb = lhs ? lhs[b] : b / rep;
+    float* xf = (float*)malloc(sizeof(float) * (size_t)Kd);
+    for (int64_t j = 0; j < Kd; ++j)
+      xf[j] = orc_bf16_to_f32(x[(xb * M + m) * Kd + j]);
+    qmv(xf, &q, rhs[b], N, Kd, group_size, bits, out + bm * N);
+    free(xf);
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------- swiglu */
+/* silu(g) * u (activations.rs:187-200) with silu = g * sigmoid(g)
+ * (activation.rs:869-873).  MLX evaluates the compiled graph in the
+ * arrays' dtype, so every op result is rounded to bf16. */
+static inline float swiglu1(float g, float u) {
+  const float sg = orc_bf16_to_f32(orc_f32_to_bf16(1.0f / (1.0f + expf(-g))));
+  const float h = orc_bf16_to_f32(orc_f32_to_bf16(g * sg));
+  return h * u;
+}
+
+void orc_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
+                uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = orc_f32_to_bf16(
+        swiglu1(orc_bf16_to_f32(g[i]), orc_bf16_to_f32(u[i])));
+}
+
+/* ------------------------------------------------------------- combine */
+/* combine_with_weights (switch.rs:223-234): (w * y) rounded to f32, then
+ * summed over k in order.  Shared branch (moe.rs:117-120,145):
+ * shared = y_s * sigmoid(sg); out = shared + routed. */
+void orc_combine(const uint16_t* y, const float* w, int64_t T, int64_t K,
+                 int64_t d, const uint16_t* shared_y, const float* shared_logit,
+                 float* out) {
+  for (int64_t t = 0; t < T; ++t) {
+    float gate = 0.0f;
+    if (shared_y) gate = 1.0f / (1.0f + expf(-shared_logit[t]));
+    for (int64_t n = 0; n < d; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const float prod = w[t * K + k] * orc_bf16_to_f32(y[(t * K + k) * d + n]);
+        acc += prod;
+      }
+      if (shared_y) {
+        const float sh = orc_bf16_to_f32(shared_y[t * d + n]) * gate;
+        acc = sh + acc;
+      }
+      out[t * d + n] = acc;
+    }
+  }
+}
+
+/* --------------------------------------------------------------- block */
+/* One expert FFN on one token: y = down(swiglu(gate(x), up(x))). */
+static void expert_ffn(const float* xf, const orc_qlinear* g,
+                       const orc_qlinear* u, const orc_qlinear* dn, int64_t e,
+                       int64_t d, int64_t f, int gs, int bits, uint16_t* y,
+                       uint16_t* gb, uint16_t* ub, float* af) {
+  qmv(xf, g, e, f, d, gs, bits, gb);
+  qmv(xf, u, e, f, d, gs, bits, ub);
+  for (int64_t n = 0; n < f; ++n) {
+    uint16_t a = orc_f32_to_bf16(
+        swiglu1(orc_bf16_to_f32(gb[n]), orc_bf16_to_f32(ub[n])));
+    af[n] = orc_bf16_to_f32(a);
+  }
+  qmv(af, dn, e, d, f, gs, bits, y);
+}
+
+int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
+                      float* out, int32_t* idx_out, float* w_out,
+                      int nthreads) {
+  const int64_t d = blk->hidden, E = blk->num_experts, K = blk->top_k;
+  const int64_t f = blk->intermediate, fs = blk->shared_intermediate;
+  const int gs = blk->group_size, bits = blk->bits;
+  if (!valid_quant(gs, bits) || d % gs || f % gs || (fs && fs % gs) ||
+      K < 1 || K > E || K > 64)
+    return -1;
+  if (nthreads <= 0) nthreads = 1;
+
+  float* logits = (float*)malloc(sizeof(float) * (size_t)(T * E));
+  int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * (size_t)(T * K));
+  float* wts = (float*)malloc(sizeof(float) * (size_t)(T * K));
+  uint16_t* y = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * K * d));
+  uint16_t* sy = fs ? (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * d)) : NULL;
+  float* sg = fs ? (float*)malloc(sizeof(float) * (size_t)T) : NULL;
+
+  /* router */
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+  for (int64_t t = 0; t < T; ++t) {
+    for (int64_t e = 0; e < E; ++e) {
+      float v = lane_dot(x + t * d, blk->router_w + e * d, d);
+      if (blk->router_b) v += blk->router_b[e];
+      logits[t * E + e] = v;
+    }
+    if (fs) sg[t] = lane_dot(x + t * d, blk->shared_gate_w, d);
+  }
+  orc_router_topk(logits, T, E, K, idx, wts);
+
+  /* routed experts, one (token, k) pair at a time (gather_qmm's
+   * unsorted path; the sorted path gives identical rows) */
+  const int64_t fmax = fs > f ? fs : f;
+#pragma omp parallel num_threads(nthreads)
+  {
+    float* xf = (float*)malloc(sizeof(float) * (size_t)d);
+    float* af = (float*)malloc(sizeof(float) * (size_t)fmax);
+    uint16_t* gb = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)fmax);
+    uint16_t* ub = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)fmax);
+    int64_t last_t = -1;
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t tk = 0; tk < T * K; ++tk) {
+      const int64_t t = tk / K;
+      if (t != last_t) {
+        for (int64_t j = 0; j < d; ++j) xf[j] = orc_bf16_to_f32(x[t * d + j]);
+        last_t = t;
+      }
+      expert_ffn(xf, &blk->gate_proj, &blk->up_proj, &blk->down_proj,
+                 idx[tk], d, f, gs, bits, y + tk * d, gb, ub, af);
+    }
+    if (fs) {
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t t = 0; t < T; ++t) {
+        for (int64_t j = 0; j < d; ++j) xf[j] = orc_bf16_to_f32(x[t * d + j]);
+        expert_ffn(xf, &blk->shared_gate, &blk->shared_up, &blk->shared_down,
+                   0, d, fs, gs, bits, sy + t * d, gb, ub, af);
+      }
+    }
+    free(xf);
+    free(af);
+    free(gb);
+    free(ub);
+  }
+
+  orc_combine(y, wts, T, K, d, sy, sg, out);
+  if (idx_out) memcpy(idx_out, idx, sizeof(int32_t) * (size_t)(T * K));
+  if (w_out) memcpy(w_out, wts, sizeof(float) * (size_t)(T * K));
+  free(logits);
+  free(idx);
+  free(wts);
+  free(y);
+  free(sy);
+  free(sg);
+  return 0;
+}

@@ -1,0 +1,121 @@
+/*
+ * moe_oracle.h -- CPU restatement of mlxr-lm's sparse-MoE block.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the parity checker for the HIP path
+ * and the "port" CPU baseline timed by bench.py.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The product library (libmlxr_moe.so) never links or calls it.
+ *
+ * The reference (flukejones/mlx-rs) binds MLX C++ v0.31.2 through mlx-c.
+ * Neither is present in /root/reference, so every function below restates
+ * the reference's op sequence from its Rust call sites (cited per function)
+ * and fixes the numerics MLX leaves unspecified.  The choices are the same
+ * on CPU and GPU:
+ *   - bf16 conversion is round-to-nearest-even; NaN -> 0x7FC0.
+ *   - dequantised weight = round(fmaf(code, scale, bias)) to the scales'
+ *     dtype (one rounding).
+ *   - router logits use a fixed 64-lane summation order (see
+ *     orc_router_logits), so expert selection is bit-reproducible.
+ *   - top-k selects on logits (softmax is monotone), descending, ties to
+ *     the lower expert id.
+ *
+ * Parity status (what pins each function) is listed in the header of
+ * moe_oracle.c and checked by tests/test_oracle.py.
+ */
+#ifndef MLXR_MOE_ORACLE_H
+#define MLXR_MOE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype tags shared with the product C-ABI */
+#define ORC_F32 0
+#define ORC_BF16 1
+
+float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);
+
+/* MLX affine quantisation of w [rows, cols] (cols % group_size == 0).
+ * bits in {2,4,8}; group_size in {32,64,128}.  wq [rows, cols*bits/32],
+ * scales/biases [rows, cols/group_size] in w's dtype.  Returns 0 or -1. */
+int orc_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
+                 int group_size, int bits, uint32_t* wq, void* scales,
+                 void* biases);
+
+/* Inverse: out [rows, cols] in out_dtype.  Returns 0 or -1. */
+int orc_dequantize(const uint32_t* wq, const void* scales, const void* biases,
+                   int sb_dtype, int64_t rows, int64_t cols, int group_size,
+                   int bits, void* out, int out_dtype);
+
+/* logits[t, e] = x[t, :] . w[e, :]  (x bf16 [T,d], w f32 [E,d]) in the
+ * fixed lane order described in moe_oracle.c. */
+void orc_router_logits(const uint16_t* x, const float* w, int64_t T,
+                       int64_t d, int64_t E, float* logits);
+
+/* softmax(precise) -> top-K -> renormalise, per row of logits [T, E].
+ * idx [T, K] (descending logit, ties -> lower id), weights [T, K]. */
+void orc_router_topk(const float* logits, int64_t T, int64_t E, int64_t K,
+                     int32_t* idx, float* weights);
+
+/* Stable counting sort of ids [n] by expert (== argsort(flat ids)).
+ * counts [E], offsets [E+1], sorted [n] (flat index per sorted slot),
+ * inv [n] (sorted slot per flat index).  Returns 0 or -1 (id out of range). */
+int orc_dispatch(const int32_t* ids, int64_t n, int64_t E, int32_t* counts,
+                 int32_t* offsets, int32_t* sorted, int32_t* inv);
+
+/* gather_qmm with transpose=true:
+ *   out[b, m, :] = x[xb(b), m, :] . dequant(w[rhs[b]])^T
+ * x bf16 [x_batch, M, Kd]; w u32 [E, N, Kd*bits/32]; scales/biases bf16
+ * [E, N, Kd/group]; xb(b) = lhs[b] if lhs else b / (B / x_batch).
+ * fp32 accumulation, bf16 output [B, M, N].  Returns 0 or -1. */
+int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
+                   const uint32_t* w, const uint16_t* scales,
+                   const uint16_t* biases, int64_t E, int64_t N,
+                   const int32_t* lhs, const int32_t* rhs, int64_t B,
+                   int group_size, int bits, uint16_t* out, int nthreads);
+
+/* act = silu(g) * u with MLX's per-op bf16 rounding. */
+void orc_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
+                uint16_t* out);
+
+/* out[t, :] = sum_k w[t,k] * y[t,k,:]  (+ shared[t,:] * sigmoid(sg[t])). */
+void orc_combine(const uint16_t* y, const float* w, int64_t T, int64_t K,
+                 int64_t d, const uint16_t* shared_y, const float* shared_logit,
+                 float* out);
+
+/* One quantised linear bank: w [E, out, in*bits/32], scales/biases bf16. */
+typedef struct {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+} orc_qlinear;
+
+typedef struct {
+  int64_t hidden;           /* d */
+  int64_t num_experts;      /* E */
+  int64_t top_k;            /* K */
+  int64_t intermediate;     /* f */
+  int64_t shared_intermediate; /* f_s, 0 = no shared expert */
+  int32_t bits;
+  int32_t group_size;
+  const float* router_w;    /* [E, d] f32 */
+  const float* router_b;    /* [E] f32 or NULL (addmm: dot + bias) */
+  orc_qlinear gate_proj, up_proj, down_proj;      /* switch_mlp */
+  orc_qlinear shared_gate, shared_up, shared_down; /* E = 1 */
+  const float* shared_gate_w; /* [1, d] f32 */
+} orc_block;
+
+/* Qwen35MoeBlock::forward on x bf16 [T, d] -> out f32 [T, d].
+ * idx_out/w_out (optional) receive the routing.  nthreads <= 0 means 1. */
+int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
+                      float* out, int32_t* idx_out, float* w_out,
+                      int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

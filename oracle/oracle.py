@@ -1,0 +1,259 @@
+"""numpy view of the CPU oracle (liboracle.so built from moe_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the parity checker and the "port" CPU baseline.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module.  bf16 arrays are numpy uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_uint16, c_uint32, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+F32, BF16 = 0, 1
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB))
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(c_void_p)
+
+
+# ----------------------------------------------------------------- bf16
+def f32_to_bf16(a) -> np.ndarray:
+    """Round-to-nearest-even f32 -> bf16 bits (NaN -> 0x7FC0)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r[nan] = 0x7FC0
+    return r
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+# ------------------------------------------------------------- wrappers
+def quantize(w: np.ndarray, group_size=64, bits=4, bf16=True):
+    """w: uint16 bf16 bits (bf16=True) or float32 [rows, cols]."""
+    w = np.ascontiguousarray(w)
+    rows, cols = int(np.prod(w.shape[:-1])), w.shape[-1]
+    wq = np.zeros(w.shape[:-1] + (cols * bits // 32,), np.uint32)
+    sdt = np.uint16 if bf16 else np.float32
+    sc = np.zeros(w.shape[:-1] + (cols // group_size,), sdt)
+    bi = np.zeros_like(sc)
+    rc = lib().orc_quantize(_p(w), c_int(BF16 if bf16 else F32), c_int64(rows), c_int64(cols),
+                            c_int(group_size), c_int(bits), _p(wq), _p(sc), _p(bi))
+    if rc:
+        raise ValueError("orc_quantize rejected the arguments")
+    return wq, sc, bi
+
+
+def dequantize(wq, scales, biases, group_size=64, bits=4, out_bf16=True):
+    wq = np.ascontiguousarray(wq, np.uint32)
+    sb_bf16 = scales.dtype == np.uint16
+    cols = wq.shape[-1] * 32 // bits
+    rows = int(np.prod(wq.shape[:-1]))
+    out = np.zeros(wq.shape[:-1] + (cols,), np.uint16 if out_bf16 else np.float32)
+    rc = lib().orc_dequantize(_p(wq), _p(np.ascontiguousarray(scales)),
+                              _p(np.ascontiguousarray(biases)), c_int(BF16 if sb_bf16 else F32),
+                              c_int64(rows), c_int64(cols), c_int(group_size), c_int(bits),
+                              _p(out), c_int(BF16 if out_bf16 else F32))
+    if rc:
+        raise ValueError("orc_dequantize rejected the arguments")
+    return out
+
+
+def router_logits(x_bf16, w_f32):
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    w = np.ascontiguousarray(w_f32, np.float32)
+    T, d = x.shape
+    E = w.shape[0]
+    out = np.zeros((T, E), np.float32)
+    lib().orc_router_logits(_p(x), _p(w), c_int64(T), c_int64(d), c_int64(E), _p(out))
+    return out
+
+
+def router_topk(logits, K):
+    lg = np.ascontiguousarray(logits, np.float32)
+    T, E = lg.shape
+    idx = np.zeros((T, K), np.int32)
+    w = np.zeros((T, K), np.float32)
+    lib().orc_router_topk(_p(lg), c_int64(T), c_int64(E), c_int64(K), _p(idx), _p(w))
+    return idx, w
+
+
+def dispatch(ids, E):
+    ids = np.ascontiguousarray(ids, np.int32).reshape(-1)
+    n = ids.size
+    counts = np.zeros(E, np.int32)
+    offsets = np.zeros(E + 1, np.int32)
+    srt = np.zeros(n, np.int32)
+    inv = np.zeros(n, np.int32)
+    rc = lib().orc_dispatch(_p(ids), c_int64(n), c_int64(E), _p(counts), _p(offsets), _p(srt),
+                            _p(inv))
+    if rc:
+        raise ValueError("orc_dispatch: id out of range")
+    return counts, offsets, srt, inv
+
+
+def gather_qmm(x, wq, scales, biases, rhs, lhs=None, group_size=64, bits=4, nthreads=1):
+    """x uint16 [x_batch, M, K]; wq uint32 [E, N, K*bits/32]; scales/biases
+    uint16 [E, N, K/g]; rhs [B] -> out uint16 [B, M, N]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    xb, M, Kd = x.shape
+    E, N = wq.shape[0], wq.shape[1]
+    rhs = np.ascontiguousarray(rhs, np.int32).reshape(-1)
+    lhs_a = None if lhs is None else np.ascontiguousarray(lhs, np.int32).reshape(-1)
+    B = rhs.size
+    out = np.zeros((B, M, N), np.uint16)
+    rc = lib().orc_gather_qmm(_p(x), c_int64(xb), c_int64(M), c_int64(Kd),
+                              _p(np.ascontiguousarray(wq, np.uint32)),
+                              _p(np.ascontiguousarray(scales, np.uint16)),
+                              _p(np.ascontiguousarray(biases, np.uint16)), c_int64(E),
+                              c_int64(N), _p(lhs_a), _p(rhs), c_int64(B), c_int(group_size),
+                              c_int(bits), _p(out), c_int(nthreads))
+    if rc:
+        raise ValueError("orc_gather_qmm rejected the arguments")
+    return out
+
+
+def swiglu(g, u):
+    g = np.ascontiguousarray(g, np.uint16)
+    u = np.ascontiguousarray(u, np.uint16)
+    out = np.zeros_like(g)
+    lib().orc_swiglu(_p(g), _p(u), c_int64(g.size), _p(out))
+    return out
+
+
+def combine(y, w, shared_y=None, shared_logit=None):
+    y = np.ascontiguousarray(y, np.uint16)
+    T, K, d = y.shape
+    out = np.zeros((T, d), np.float32)
+    lib().orc_combine(_p(y), _p(np.ascontiguousarray(w, np.float32)), c_int64(T), c_int64(K),
+                      c_int64(d),
+                      _p(None if shared_y is None else np.ascontiguousarray(shared_y, np.uint16)),
+                      _p(None if shared_logit is None
+                         else np.ascontiguousarray(shared_logit, np.float32)),
+                      _p(out))
+    return out
+
+
+class _QL(Structure):
+    _fields_ = [("w", c_void_p), ("scales", c_void_p), ("biases", c_void_p)]
+
+
+class _Block(Structure):
+    _fields_ = [
+        ("hidden", c_int64), ("num_experts", c_int64), ("top_k", c_int64),
+        ("intermediate", c_int64), ("shared_intermediate", c_int64), ("bits", c_int32),
+        ("group_size", c_int32), ("router_w", c_void_p), ("router_b", c_void_p),
+        ("gate_proj", _QL), ("up_proj", _QL), ("down_proj", _QL),
+        ("shared_gate", _QL), ("shared_up", _QL), ("shared_down", _QL),
+        ("shared_gate_w", c_void_p),
+    ]
+
+
+def _ql(t):
+    if t is None:
+        return _QL()
+    return _QL(t[0].ctypes.data, t[1].ctypes.data, t[2].ctypes.data)
+
+
+def block_forward(p: dict, x, nthreads=1):
+    """p: numpy block parameters -- d, E, K, f, fs, bits, group_size,
+    router_w, router_b (or None), gate/up/down = (wq, scales, biases),
+    shared_gate/shared_up/shared_down, shared_gate_w (None when fs == 0).
+    Returns (out f32 [T, d], idx [T, K], weights [T, K])."""
+    keep = []
+
+    def c(a, dt):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dt)
+        keep.append(a)
+        return a
+
+    def q(t):
+        if t is None:
+            return None
+        return (c(t[0], np.uint32), c(t[1], np.uint16), c(t[2], np.uint16))
+
+    x = c(x, np.uint16)
+    T = x.shape[0]
+    rw, rb = c(p["router_w"], np.float32), c(p.get("router_b"), np.float32)
+    sgw = c(p.get("shared_gate_w"), np.float32)
+    blk = _Block(p["d"], p["E"], p["K"], p["f"], p.get("fs", 0), p["bits"], p["group_size"],
+                 rw.ctypes.data, None if rb is None else rb.ctypes.data,
+                 _ql(q(p["gate"])), _ql(q(p["up"])), _ql(q(p["down"])),
+                 _ql(q(p.get("shared_gate"))), _ql(q(p.get("shared_up"))),
+                 _ql(q(p.get("shared_down"))), None if sgw is None else sgw.ctypes.data)
+    out = np.zeros((T, p["d"]), np.float32)
+    idx = np.zeros((T, p["K"]), np.int32)
+    w = np.zeros((T, p["K"]), np.float32)
+    rc = lib().orc_block_forward(ctypes.byref(blk), _p(x), c_int64(T), _p(out), _p(idx), _p(w),
+                                 c_int(nthreads))
+    if rc:
+        raise ValueError("orc_block_forward rejected the arguments")
+    return out, idx, w
+
+
+__all__ = ["build", "lib", "f32_to_bf16", "bf16_to_f32", "quantize", "dequantize",
+           "router_logits", "router_topk", "dispatch", "gather_qmm", "swiglu", "combine",
+           "block_forward", "POINTER", "c_float", "c_uint16", "c_uint32"]
+
+
+# ------------------------------------------------------- torch adapters
+def to_np(t):
+    """Device tensor -> numpy with bf16 as uint16 bits and packed int32
+    words as uint32."""
+    import torch
+
+    t = t.detach()
+    if t.dtype == torch.bfloat16:
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    if t.dtype == torch.int32:
+        return t.contiguous().cpu().numpy().view(np.uint32)
+    return t.contiguous().cpu().numpy()
+
+
+def block_params(bw) -> dict:
+    """Numpy parameters for block_forward from a workloads.BlockWeights."""
+    cfg = bw.cfg
+
+    def q(lin):
+        return (to_np(lin.weight).reshape(lin.weight.shape[0], lin.weight.shape[1], -1),
+                to_np(lin.scales), to_np(lin.biases))
+
+    m = bw.switch_mlp
+    p = dict(d=cfg.d, E=cfg.E, K=cfg.K, f=cfg.f, fs=cfg.fs, bits=cfg.bits,
+             group_size=cfg.group_size, router_w=to_np(bw.gate_w),
+             router_b=None if bw.gate_b is None else to_np(bw.gate_b),
+             gate=q(m.gate_proj), up=q(m.up_proj), down=q(m.down_proj))
+    if cfg.fs:
+        s = bw.shared_expert
+        p.update(shared_gate=q(s.gate_proj), shared_up=q(s.up_proj), shared_down=q(s.down_proj),
+                 shared_gate_w=to_np(bw.shared_gate_w))
+    return p

@@ -1,0 +1,117 @@
+"""The C-ABI library loads and exports every declared symbol, and rejects
+bad arguments on the host with an mlxr-style error (no GPU needed: every
+call here fails validation before touching the device)."""
+import ctypes
+import re
+import threading
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mlxr_moe.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mlxr_moe_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    for s in ["mlxr_moe_gather_qmm", "mlxr_moe_quantize", "mlxr_moe_dequantize",
+              "mlxr_moe_argpartition", "mlxr_moe_router_topk", "mlxr_moe_dispatch",
+              "mlxr_moe_combine", "mlxr_moe_switch_glu_forward", "mlxr_moe_block_forward",
+              "mlxr_moe_last_error"]:
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = ctypes.CDLL(str(pkg.LIB_PATH))
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing
+    assert sorted(pkg._capi.SIGNATURES) == declared_symbols()
+    assert pkg._capi.lib().mlxr_moe_version() >= 100
+
+
+def _err(pkg):
+    return pkg._capi.last_error()
+
+
+def test_quantize_rejects_bad_bits_group_mode(pkg):
+    lib, C = pkg._capi.lib(), pkg._capi
+    OI = C.OptionalInt
+    assert lib.mlxr_moe_quantize(None, C.BFLOAT16, 4, 64, OI.of(64), OI.of(3), b"affine",
+                                 None, None, None, None) == -1
+    assert "bits" in _err(pkg)
+    assert lib.mlxr_moe_quantize(None, C.BFLOAT16, 4, 64, OI.of(48), OI.of(4), b"affine",
+                                 None, None, None, None) == -1
+    assert "group_size" in _err(pkg)
+    assert lib.mlxr_moe_quantize(None, C.BFLOAT16, 4, 100, OI.of(None), OI.of(None), None,
+                                 None, None, None, None) == -1
+    assert "multiple of group_size 64" in _err(pkg)
+    assert lib.mlxr_moe_quantize(None, C.BFLOAT16, 4, 64, OI.of(64), OI.of(4), b"mxfp4",
+                                 None, None, None, None) == -1
+    assert "mode" in _err(pkg)
+
+
+def test_gather_qmm_rejects_unsupported(pkg):
+    lib, C = pkg._capi.lib(), pkg._capi
+    OI = C.OptionalInt
+    args = lambda gs, bits, transpose: (  # noqa: E731
+        None, C.BFLOAT16, 1, 1, 128, None, None, None, C.BFLOAT16, 4, 64, None, None, 1,
+        transpose, OI.of(gs), OI.of(bits), b"affine", 0, None, C.BFLOAT16, None, 0, None)
+    assert lib.mlxr_moe_gather_qmm(*args(32, 4, 1)) == -1
+    assert "group_size must be 64" in _err(pkg)
+    assert lib.mlxr_moe_gather_qmm(*args(64, 2, 1)) == -1
+    assert "bits must be 4 or 8" in _err(pkg)
+    assert lib.mlxr_moe_gather_qmm(*args(64, 4, 0)) == -1
+    assert "transpose" in _err(pkg)
+
+
+def test_argpartition_invalid_axis_and_kth(pkg):
+    """crates/mlxr/src/ops/sort.rs:262-301: invalid axis / kth must error."""
+    lib = pkg._capi.lib()
+    assert lib.mlxr_moe_argpartition(None, 1, 5, 2, 2, None, None) == -1
+    assert "axis" in _err(pkg)
+    assert lib.mlxr_moe_argpartition(None, 1, 5, 5, 0 - 1, None, None) == -1
+    assert "kth" in _err(pkg)
+    assert lib.mlxr_moe_argpartition(None, 1, 5, -6, -1, None, None) == -1
+
+
+def test_block_validation(pkg):
+    C = pkg._capi
+    lib = C.lib()
+    blk = C.Block()
+    blk.hidden_size, blk.num_experts, blk.num_experts_per_tok = 2048, 128, 0
+    blk.moe_intermediate_size = 768
+    assert lib.mlxr_moe_block_forward(ctypes.byref(blk), None, 1, None, None, None, None, 0,
+                                      None) == -1
+    assert "num_experts_per_tok" in _err(pkg)
+    blk.num_experts_per_tok = 8
+    assert lib.mlxr_moe_block_forward(ctypes.byref(blk), None, 1, None, None, None, None, 0,
+                                      None) == -1
+    assert "gate_weight" in _err(pkg)
+
+
+def test_last_error_is_thread_local(pkg):
+    lib = pkg._capi.lib()
+    assert lib.mlxr_moe_argpartition(None, 1, 5, 2, 7, None, None) == -1
+    seen = {}
+
+    def other():
+        seen["msg"] = pkg._capi.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "axis" in _err(pkg)
+
+
+def test_python_mirror_axis_errors_without_gpu(pkg):
+    torch = pytest.importorskip("torch")
+    a = torch.zeros(5)
+    with pytest.raises(pkg.MlxrMoeError):
+        pkg.ops.argpartition_axis(a, 2, 1)

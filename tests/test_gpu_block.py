@@ -1,0 +1,122 @@
+"""GPU parity of the whole MoE block (Qwen35MoeBlock::forward) and of
+SplitSwitchFfn against the CPU oracle on the benchmark configurations.
+
+Bar: routing indices bit-exact; routing weights to 2e-6 relative;
+max |out - oracle| <= 2e-2 * RMS(oracle) with f32 accumulation."""
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+
+_WEIGHTS = {}
+
+
+def weights(pkg, cfg_name, dev):
+    if cfg_name not in _WEIGHTS:
+        _WEIGHTS.clear()  # keep one config resident at a time
+        torch.cuda.empty_cache()
+        _WEIGHTS[cfg_name] = pkg.workloads.make_weights(pkg.workloads.CONFIGS[cfg_name], dev)
+    return _WEIGHTS[cfg_name]
+
+
+def check_block(pkg, orc, bw, x, nthreads=16):
+    block = bw.block()
+    out = block(x)
+    torch.cuda.synchronize()
+    print(f"  block {bw.cfg.name} T={x.shape[0]}", flush=True)
+    ref, ridx, rw = orc.block_forward(orc.block_params(bw), orc.to_np(x), nthreads=nthreads)
+    idx = block.last_indices.cpu().numpy()
+    assert np.array_equal(idx, ridx), "routing indices differ"
+    assert np.allclose(block.last_weights.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+    got = out.cpu().numpy().astype(np.float64)
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    err = np.abs(got - ref).max()
+    print(f"  max|err| {err:.3e}  rms {rms:.3e}  ratio {err / rms:.2e}", flush=True)
+    assert err <= 2e-2 * rms
+    assert pkg.ops.workspace_status(block.last_workspace) == 0
+    return out, block
+
+
+def test_c1_golden_fixture(pkg, orc, dev):
+    """The committed c1 fixture (tests/golden/c1_block.npz), inputs rebuilt
+    from numpy's seed-0 stream and uploaded as-is (no GPU quantisation)."""
+    from make_golden import c1_inputs, digest
+    z = np.load(Path(__file__).resolve().parent / "golden" / "c1_block.npz")
+    x, p, dense = c1_inputs()
+    assert digest(x) == str(z["x_sha"])
+    assert digest(*p["gate"], *p["up"], *p["down"]) == str(z["packed_sha"])
+    t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(dev)  # noqa: E731
+
+    def bank(q):
+        return pkg.nn.QuantizedSwitchLinear(t(q[0], np.int32), t(q[1], np.int16).view(torch.bfloat16),
+                                            t(q[2], np.int16).view(torch.bfloat16), 64, 4)
+
+    mlp = pkg.nn.SplitSwitchFfn(bank(p["gate"]), bank(p["up"]), bank(p["down"]))
+    block = pkg.nn.Qwen35MoeBlock(t(p["router_w"], np.float32), mlp, 2)
+    xt = t(x, np.int16).view(torch.bfloat16)
+    out = block(xt).cpu().numpy()
+    assert np.array_equal(block.last_indices.cpu().numpy(), z["idx"])
+    assert np.allclose(block.last_weights.cpu().numpy(), z["weights"], rtol=2e-6)
+    rms = np.sqrt(np.mean(z["out"].astype(np.float64) ** 2))
+    assert np.abs(out - z["out"]).max() <= 2e-2 * rms
+    # and the GPU quantiser reproduces the fixture's packed weights
+    for name in ("gate", "up", "down"):
+        wq, sc, bi = pkg.ops.quantize(t(dense[name], np.int16).view(torch.bfloat16), 64, 4)
+        assert np.array_equal(orc.to_np(wq), p[name][0])
+        assert np.array_equal(orc.to_np(sc), p[name][1])
+
+
+@pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 8), ("c2", 64), ("c5", 32),
+                                   ("c4", 1), ("c4", 64), ("c3", 512)])
+def test_block_parity(pkg, orc, dev, cfg, T):
+    bw = weights(pkg, cfg, dev)
+    x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
+    check_block(pkg, orc, bw, x)
+
+
+def test_block_token_permutation_equivariance(pkg, dev):
+    """At full c2 size: permuting tokens permutes output rows bit for bit,
+    and repeated runs are bit-identical (size-independent properties)."""
+    bw = weights(pkg, "c2", dev)
+    T = 64
+    x = pkg.workloads.make_x(bw.cfg, T, dev, seed=99)
+    block = bw.block()
+    a = block(x).clone()
+    b = block(x).clone()
+    assert torch.equal(a, b)
+    perm = torch.randperm(T, generator=torch.Generator().manual_seed(0)).to(dev)
+    c = block(x[perm])
+    assert torch.equal(c, a[perm])
+
+
+def test_switch_glu_forward_matches_composition(pkg, orc, dev):
+    """SplitSwitchFfn::forward (per-expert rows) and forward_with_combine
+    against the oracle composition of gather_qmm / swiglu / combine."""
+    bw = weights(pkg, "c2", dev)
+    cfg = bw.cfg
+    T = 24
+    x = pkg.workloads.make_x(cfg, T, dev, seed=5)
+    g = torch.Generator().manual_seed(3)
+    idx = torch.stack([torch.randperm(cfg.E, generator=g)[:cfg.K] for _ in range(T)]).int().to(dev)
+    w = torch.rand((T, cfg.K), generator=g).to(dev)
+    mlp = bw.switch_mlp
+    y = mlp.forward(x, idx)
+    out = mlp.forward_with_combine(x, idx, w)
+    p = orc.block_params(bw)
+    xs = orc.to_np(x)[:, None, :]
+    ids = idx.cpu().numpy().reshape(-1)
+    ga = orc.gather_qmm(xs, *p["gate"], ids, nthreads=16)
+    ua = orc.gather_qmm(xs, *p["up"], ids, nthreads=16)
+    ya = orc.gather_qmm(orc.swiglu(ga, ua), *p["down"], ids, nthreads=16).reshape(T, cfg.K, -1)
+    yf = orc.bf16_to_f32(ya).astype(np.float64)
+    rms = np.sqrt(np.mean(yf ** 2))
+    assert np.abs(orc.bf16_to_f32(orc.to_np(y)) - yf).max() <= 2e-2 * rms
+    ref = orc.combine(ya, w.cpu().numpy())
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    assert np.abs(out.cpu().numpy() - ref).max() <= 2e-2 * rms

@@ -1,0 +1,208 @@
+"""GPU parity of the op-level entry points against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(orc, a, dev):
+    return torch.from_numpy(orc.f32_to_bf16(a).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def _np(orc, t):
+    return orc.to_np(t)
+
+
+# ------------------------------------------------------- quantize
+@pytest.mark.parametrize("shape,gs,bits", [
+    ((8, 256), 64, 4), ((8, 256), 64, 8), ((8, 256), 64, 2), ((16, 512), 128, 4),
+    ((16, 512), 32, 8), ((3, 64, 128), 64, 4)])
+def test_quantize_bit_exact_bf16(pkg, orc, dev, shape, gs, bits):
+    rng = np.random.default_rng(abs(hash((shape, gs, bits))) % 2 ** 32)
+    w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    w[..., :64] *= 50  # a wide group next to narrow ones
+    wt = _bf16(orc, w, dev)
+    wq, sc, bi = pkg.ops.quantize(wt, gs, bits)
+    rq, rs, rb = orc.quantize(_np(orc, wt), gs, bits, bf16=True)
+    assert np.array_equal(_np(orc, wq).reshape(rq.shape), rq)
+    assert np.array_equal(_np(orc, sc), rs)
+    assert np.array_equal(_np(orc, bi), rb)
+    deq = pkg.ops.dequantize(wq, sc, bi, gs, bits)
+    assert np.array_equal(_np(orc, deq), orc.dequantize(rq, rs, rb, gs, bits))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_quantize_reference_arange_f32(pkg, orc, dev, bits):
+    """quantization.rs:299-315 on the GPU, f32 in, f32 scales."""
+    x = torch.arange(0, 512, dtype=torch.float32, device=dev).expand(128, 512).contiguous()
+    wq, sc, bi = pkg.ops.quantize(x, 128, bits)
+    assert tuple(wq.shape) == (128, 512 // (32 // bits)) and tuple(sc.shape) == (128, 4)
+    xh = pkg.ops.dequantize(wq, sc, bi, 128, bits)
+    assert float((x - xh).abs().max()) <= 127.0 / (1 << bits)
+    rq, rs, rb = orc.quantize(x.cpu().numpy(), 128, bits, bf16=False)
+    assert np.array_equal(_np(orc, wq), rq)
+    assert np.array_equal(sc.cpu().numpy(), rs) and np.array_equal(bi.cpu().numpy(), rb)
+
+
+def test_quantize_full_expert_bank_bit_exact(pkg, orc, dev):
+    """c2 gate_proj [128, 768, 2048] at 4 bits and a c5-sized 8-bit slice."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    for shape, bits in [((128, 768, 2048), 4), ((16, 1536, 4096), 8)]:
+        w = (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        wq, sc, bi = pkg.ops.quantize(w, 64, bits)
+        rq, rs, rb = orc.quantize(_np(orc, w), 64, bits, bf16=True)
+        assert np.array_equal(_np(orc, wq), rq)
+        assert np.array_equal(_np(orc, sc), rs) and np.array_equal(_np(orc, bi), rb)
+        del w, wq, sc, bi
+
+
+# --------------------------------------------------------- router
+@pytest.mark.parametrize("T,d,E,K", [(16, 512, 8, 2), (1, 2048, 128, 8), (64, 2048, 128, 8),
+                                     (64, 2048, 512, 10), (300, 4096, 128, 8)])
+def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
+    rng = np.random.default_rng(T * 7 + E)
+    x = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev)
+    w = torch.from_numpy((rng.standard_normal((E, d)) * 0.02).astype(np.float32)).to(dev)
+    idx, wts = pkg.ops.router_topk(x, w, K)
+    lg = orc.router_logits(_np(orc, x), w.cpu().numpy())
+    ridx, rw = orc.router_topk(lg, K)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+
+
+def test_router_ties_pick_lower_ids(pkg, dev):
+    x = torch.zeros((4, 512), dtype=torch.bfloat16, device=dev)
+    w = torch.randn((64, 512), device=dev)
+    idx, wts = pkg.ops.router_topk(x, w, 4)
+    assert idx.cpu().tolist() == [[0, 1, 2, 3]] * 4
+    assert torch.allclose(wts, torch.full_like(wts, 0.25))
+
+
+# ------------------------------------------------------- dispatch
+@pytest.mark.parametrize("n,E", [(0, 8), (1, 1), (5, 3), (512, 128), (1000, 7), (4096, 128),
+                                 (20480, 512), (32768, 128), (33000, 1024)])
+def test_dispatch_is_stable_argsort(pkg, orc, dev, n, E):
+    rng = np.random.default_rng(n + E)
+    ids = rng.integers(0, E, n).astype(np.int32)
+    if n > 100:
+        ids[: n // 3] = E - 1  # a heavy expert spanning several workgroups
+    counts, offsets, order, inv = pkg.ops.dispatch(torch.from_numpy(ids).to(dev), E)
+    rc, ro, rs, ri = orc.dispatch(ids, E)
+    assert np.array_equal(counts.cpu().numpy(), rc)
+    assert np.array_equal(offsets.cpu().numpy(), ro)
+    assert np.array_equal(order.cpu().numpy(), rs)
+    assert np.array_equal(inv.cpu().numpy(), ri)
+    assert pkg.ops.workspace_status(order._mlxr_workspace) == 0
+
+
+def test_dispatch_flags_out_of_range(pkg, dev):
+    ids = torch.tensor([0, 3, 9, 1], dtype=torch.int32, device=dev)
+    counts, offsets, order, inv = pkg.ops.dispatch(ids, 4)
+    assert pkg.ops.workspace_status(order._mlxr_workspace) == 1
+    assert counts.cpu().tolist() == [1, 1, 0, 1]
+    assert offsets.cpu().tolist()[-1] == 3
+
+
+# ----------------------------------------------------- gather_qmm
+def _qbank(pkg, orc, E, N, K, bits, dev, seed):
+    rng = np.random.default_rng(seed)
+    w = _bf16(orc, (rng.standard_normal((E, N, K)) * 0.02).astype(np.float32), dev)
+    return pkg.ops.quantize(w, 64, bits)
+
+
+def _close(got, want, what=""):
+    got = got.astype(np.float64)
+    want = want.astype(np.float64)
+    rms = np.sqrt(np.mean(want ** 2)) + 1e-30
+    err = np.abs(got - want)
+    # bf16 outputs from two fp32 accumulation orders: a couple of ulps
+    assert np.all(err <= 2 ** -7 * np.abs(want) + 1e-2 * rms), (what, err.max(), rms)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_reference_cases(pkg, orc, dev, bits):
+    """quantization.rs:344-421 shapes: M=32, N=64, K=64; (lhs=(0,), rhs=(2,1))
+    and (x batch 5, lhs=(0,2), rhs=(2,1))."""
+    wq, sc, bi = _qbank(pkg, orc, 3, 64, 64, bits, dev, 11)
+    rng = np.random.default_rng(12)
+    for xb, lhs in [(1, [0, 0]), (5, [0, 2])]:
+        x = _bf16(orc, rng.standard_normal((xb, 32, 64)).astype(np.float32), dev)
+        l_t = torch.tensor(lhs, dtype=torch.int32, device=dev)
+        r_t = torch.tensor([2, 1], dtype=torch.int32, device=dev)
+        got = pkg.ops.gather_qmm(x, wq, sc, bi, l_t, r_t, True, 64, bits)
+        assert tuple(got.shape) == (2, 32, 64)
+        want = orc.gather_qmm(_np(orc, x), _np(orc, wq), _np(orc, sc), _np(orc, bi), [2, 1],
+                              lhs, bits=bits)
+        _close(orc.bf16_to_f32(_np(orc, got)), orc.bf16_to_f32(want), (xb, bits))
+        # gather_mm of the dequantised weights (fp64) as a second reference
+        wd = orc.bf16_to_f32(_np(orc, pkg.ops.dequantize(wq, sc, bi, 64, bits))).astype(np.float64)
+        xf = orc.bf16_to_f32(_np(orc, x)).astype(np.float64)
+        mm = np.stack([xf[lhs[i]] @ wd[[2, 1][i]].T for i in range(2)])
+        _close(orc.bf16_to_f32(_np(orc, got)), mm, "gather_mm")
+
+
+@pytest.mark.parametrize("T,K,E,N,Kd,bits", [
+    (1, 8, 128, 768, 2048, 4), (64, 8, 128, 768, 2048, 4), (64, 8, 128, 2048, 768, 4),
+    (16, 2, 8, 256, 512, 4), (32, 8, 128, 1536, 4096, 8), (7, 10, 512, 512, 2048, 4),
+    (300, 8, 16, 128, 256, 4), (40, 1, 2, 64, 64, 8)])
+def test_gather_qmm_moe_unsorted_shapes(pkg, orc, dev, T, K, E, N, Kd, bits):
+    """x [T, 1, 1, Kd] against indices [T, K] -> [T, K, 1, N]."""
+    wq, sc, bi = _qbank(pkg, orc, E, N, Kd, bits, dev, T + E)
+    rng = np.random.default_rng(T * 3 + K)
+    x = _bf16(orc, rng.standard_normal((T, 1, 1, Kd)).astype(np.float32), dev)
+    idx = rng.integers(0, E, (T, K)).astype(np.int32)
+    if T > 4:
+        idx[: T // 2, 0] = 3 % E  # one expert with many rows
+    got = pkg.ops.gather_qmm(x, wq, sc, bi, None, torch.from_numpy(idx).to(dev), True, 64, bits)
+    assert tuple(got.shape) == (T, K, 1, N)
+    want = orc.gather_qmm(_np(orc, x).reshape(T, 1, Kd), _np(orc, wq), _np(orc, sc),
+                          _np(orc, bi), idx.reshape(-1), bits=bits, nthreads=16)
+    _close(orc.bf16_to_f32(_np(orc, got)).reshape(T * K, N),
+           orc.bf16_to_f32(want).reshape(T * K, N), (T, K, E, N, Kd, bits))
+
+
+def test_gather_qmm_out_of_range_index(pkg, orc, dev):
+    wq, sc, bi = _qbank(pkg, orc, 4, 64, 64, 4, dev, 3)
+    x = torch.ones((3, 1, 64), dtype=torch.bfloat16, device=dev)
+    idx = torch.tensor([1, 7, 2], dtype=torch.int32, device=dev)
+    got = pkg.ops.gather_qmm(x, wq, sc, bi, None, idx)
+    assert pkg.ops.workspace_status(got._mlxr_workspace) == 1
+    assert torch.all(got[1] == 0)
+    ok = pkg.ops.gather_qmm(x[[0, 2]], wq, sc, bi, None, idx[[0, 2]])
+    assert torch.equal(got[[0, 2]], ok)
+
+
+# -------------------------------------------------------- combine
+def test_combine_bit_exact(pkg, orc, dev):
+    rng = np.random.default_rng(13)
+    T, K, d = 33, 8, 2048
+    y = _bf16(orc, rng.standard_normal((T, K, d)).astype(np.float32), dev)
+    w = torch.from_numpy(rng.random((T, K)).astype(np.float32)).to(dev)
+    got = pkg.ops.combine(y, w).cpu().numpy()
+    assert np.array_equal(got, orc.combine(_np(orc, y), w.cpu().numpy()))
+    sy = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev)
+    sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(dev)
+    got = pkg.ops.combine(y, w, sy, sl).cpu().numpy()
+    want = orc.combine(_np(orc, y), w.cpu().numpy(), _np(orc, sy), sl.cpu().numpy())
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------- argpartition / softmax
+def test_argpartition_and_softmax(pkg, dev):
+    a = torch.randn((37, 128), device=dev)
+    a[0, 5] = a[0, 9]  # a tie
+    for kth in (-8, 0, 64, 127):
+        p = pkg.ops.argpartition_axis(a, kth, -1).long()
+        vals = torch.gather(a, 1, p)
+        k = kth % 128
+        assert torch.all(vals[:, :k] <= vals[:, k:k + 1])
+        assert torch.all(vals[:, k + 1:] >= vals[:, k:k + 1])
+        assert torch.equal(p.sort(1).values, torch.arange(128, device=dev).expand(37, 128))
+    pt = pkg.ops.argpartition_axis(a.t().contiguous(), 3, 0)
+    assert pt.shape == (128, 37)
+    s = pkg.ops.softmax_axis(a, -1, True)
+    assert torch.allclose(s, torch.softmax(a, -1), rtol=1e-5, atol=1e-7)
+    with pytest.raises(pkg.MlxrMoeError):
+        pkg.ops.argpartition_axis(a, 128, -1)

@@ -1,0 +1,296 @@
+"""Pins of the CPU oracle: reference-held tests restated, closed forms,
+brute force and invariants.  CPU only."""
+import numpy as np
+import pytest
+
+
+# ------------------------------------------------------------ quantize
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_quantize_dequantize_reference_bound(orc, bits):
+    """crates/mlxr/src/ops/quantization.rs:299-315: rows arange(0, 512) at
+    group 128; shapes, and max |x - x_hat| <= 127 / 2^bits."""
+    x = np.broadcast_to(np.arange(0, 512, dtype=np.float32), (128, 512)).copy()
+    wq, sc, bi = orc.quantize(x, group_size=128, bits=bits, bf16=False)
+    assert wq.shape == (128, 512 // (32 // bits))
+    assert sc.shape == (128, 4) and bi.shape == (128, 4)
+    xh = orc.dequantize(wq, sc, bi, group_size=128, bits=bits, out_bf16=False)
+    assert np.abs(x - xh).max() <= 127.0 / (1 << bits)
+
+
+def test_quantize_constant_group_is_exact(orc):
+    w = np.full((3, 64), 0.5, np.float32)
+    w[1] = -2.25
+    w[2] = 0.0
+    wq, sc, bi = orc.quantize(w, 64, 4, bf16=False)
+    assert np.array_equal(orc.dequantize(wq, sc, bi, 64, 4, out_bf16=False), w)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_quantize_exact_ladder(orc, bits, sign):
+    """A group that is exactly bias + k * step for every code k is
+    reconstructed exactly (edge snapping: the larger-magnitude end is
+    code 0)."""
+    n = 1 << bits
+    step = 0.25
+    rng = np.random.default_rng(bits)
+    codes = np.concatenate([[0, n - 1], rng.integers(0, n, 62)]).astype(np.float32)
+    w = (sign * (codes * step - 1.0)).astype(np.float32)[None, :]
+    wq, sc, bi = orc.quantize(w, 64, bits, bf16=False)
+    assert np.array_equal(orc.dequantize(wq, sc, bi, 64, bits, out_bf16=False), w)
+    edge = w[0, np.argmax(np.abs(w[0]))]
+    assert bi[0, 0] == edge
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_quantize_codes_are_nearest(orc, bits):
+    """Brute force over all codes: each code minimises |w - (q*s + b)| for
+    the group's (f32-stored, so unrounded) scale and bias."""
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((16, 128)) * 0.02).astype(np.float32)
+    wq, sc, bi = orc.quantize(w, 64, bits, bf16=False)
+    per = 32 // bits
+    codes = ((wq[:, :, None] >> (np.arange(per, dtype=np.uint32) * bits)) & ((1 << bits) - 1))
+    codes = codes.reshape(16, 128).astype(np.float64)
+    s = np.repeat(sc.astype(np.float64), 64, axis=1)
+    b = np.repeat(bi.astype(np.float64), 64, axis=1)
+    err = np.abs(w - (codes * s + b))
+    allq = np.arange(1 << bits, dtype=np.float64)
+    best = np.abs(w[:, :, None] - (allq * s[:, :, None] + b[:, :, None])).min(-1)
+    assert np.all(err <= best + 1e-6 * np.abs(s))
+    # edge snapping: the bias is the group's larger-magnitude end and sits
+    # an integer number of scales from zero
+    g = w.reshape(16, 2, 64)
+    edge = np.take_along_axis(g, np.abs(g).argmax(-1)[..., None], -1)[..., 0]
+    assert np.array_equal(bi, edge)
+    q0 = bi.astype(np.float64) / sc.astype(np.float64)
+    assert np.all(np.abs(q0 - np.rint(q0)) <= 1e-5 * np.abs(q0))
+    assert np.all((q0 <= 0) & (np.abs(q0) <= (1 << bits) - 1 + 0.5))
+
+
+def test_dequantize_slot_layout(orc):
+    """kernel_source.rs:101-104: slot j of a word holds bits [j*b, (j+1)*b);
+    dequant = code * scale + bias (one rounding)."""
+    rng = np.random.default_rng(2)
+    for bits in (2, 4, 8):
+        per = 32 // bits
+        codes = rng.integers(0, 1 << bits, size=(4, 64), dtype=np.uint32)
+        words = np.zeros((4, 64 // per), np.uint32)
+        for j in range(per):
+            words |= codes[:, j::per] << np.uint32(j * bits)
+        sc = orc.f32_to_bf16(rng.standard_normal((4, 1)).astype(np.float32) * 0.01)
+        bi = orc.f32_to_bf16(rng.standard_normal((4, 1)).astype(np.float32) * 0.1)
+        got = orc.dequantize(words, sc, bi, 64, bits, out_bf16=True)
+        exact = codes.astype(np.float64) * orc.bf16_to_f32(sc).astype(np.float64) + \
+            orc.bf16_to_f32(bi).astype(np.float64)
+        want = orc.f32_to_bf16(exact.astype(np.float32))
+        assert np.array_equal(got, want), bits
+
+
+def test_quantize_bf16_storage_round_trip(orc):
+    rng = np.random.default_rng(3)
+    w = orc.f32_to_bf16((rng.standard_normal((8, 256)) * 0.02).astype(np.float32))
+    wq, sc, bi = orc.quantize(w, 64, 4, bf16=True)
+    wh = orc.bf16_to_f32(orc.dequantize(wq, sc, bi, 64, 4))
+    wf = orc.bf16_to_f32(w)
+    s = np.abs(np.repeat(orc.bf16_to_f32(sc), 64, axis=1))
+    b = np.abs(np.repeat(orc.bf16_to_f32(bi), 64, axis=1))
+    # Snapping the edge to an exact code stretches the grid by at most
+    # 0.5/|q0| (|q0| >= 7.5 at 4 bits), so the far end can overshoot the
+    # last code by up to one step; plus the bf16 rounding of the scale
+    # (times the code, at most 15), of the bias and of the result.
+    bound = 1.0 * s + (15 * s + b + np.abs(wh)) * 2.0 ** -8
+    assert np.all(np.abs(wh - wf) <= bound)
+
+
+def test_quantize_rejects_bad_args(orc):
+    with pytest.raises(ValueError):
+        orc.quantize(np.zeros((2, 64), np.float32), 64, 3, bf16=False)
+    with pytest.raises(ValueError):
+        orc.quantize(np.zeros((2, 96), np.float32), 64, 4, bf16=False)
+
+
+# -------------------------------------------------------------- router
+def test_router_logits_rounding_bound(orc):
+    rng = np.random.default_rng(4)
+    T, d, E = 5, 2048, 16
+    x = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    w = (rng.standard_normal((E, d)) * 0.02).astype(np.float32)
+    got = orc.router_logits(x, w).astype(np.float64)
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    exact = xf @ w.astype(np.float64).T
+    bound = d * 2.0 ** -23 * (np.abs(xf) @ np.abs(w.astype(np.float64)).T)
+    assert np.all(np.abs(got - exact) <= bound)
+    # experts are independent: permuting rows permutes columns bit-exactly
+    perm = rng.permutation(E)
+    assert np.array_equal(orc.router_logits(x, w[perm]), got.astype(np.float32)[:, perm])
+
+
+def test_router_logits_one_hot(orc):
+    d, E = 512, 8
+    w = np.random.default_rng(5).standard_normal((E, d)).astype(np.float32)
+    for j in (0, 3, 255, 511):
+        x = np.zeros((1, d), np.float32)
+        x[0, j] = 1.0
+        assert np.array_equal(orc.router_logits(orc.f32_to_bf16(x), w)[0], w[:, j])
+
+
+def test_router_topk_matches_full_sort(orc):
+    rng = np.random.default_rng(6)
+    T, E, K = 64, 8, 2
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[0, :] = 0.25  # all tied: lowest ids win
+    lg[1, 5] = lg[1, 2] = lg[1].max() + 1.0
+    idx, w = orc.router_topk(lg, K)
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-float(lg[t, e]), e))
+        assert list(idx[t]) == order[:K]
+    p = np.exp(lg.astype(np.float64) - lg.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    pk = np.take_along_axis(p, idx, 1)
+    assert np.allclose(w, pk / pk.sum(1, keepdims=True), rtol=1e-6, atol=1e-7)
+    assert np.allclose(w.sum(1), 1.0, atol=1e-6)
+    assert list(idx[0]) == [0, 1]
+    assert list(idx[1]) == [2, 5]
+
+
+# ------------------------------------------------------------ dispatch
+def test_dispatch_is_stable_argsort(orc):
+    rng = np.random.default_rng(7)
+    for n, E in [(1, 1), (37, 4), (4096, 128), (20480, 512)]:
+        ids = rng.integers(0, E, n).astype(np.int32)
+        counts, offsets, srt, inv = orc.dispatch(ids, E)
+        order = np.argsort(ids, kind="stable")
+        assert np.array_equal(srt, order)
+        assert np.array_equal(inv, np.argsort(order, kind="stable"))
+        assert np.array_equal(counts, np.bincount(ids, minlength=E))
+        assert offsets[0] == 0 and np.array_equal(np.diff(offsets), counts)
+    with pytest.raises(ValueError):
+        orc.dispatch(np.array([0, 4], np.int32), 4)
+
+
+# ---------------------------------------------------------- gather_qmm
+def _dense(orc, wq, sc, bi, bits):
+    return orc.dequantize(wq, sc, bi, 64, bits, out_bf16=False).astype(np.float64)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_equals_gather_mm_of_dequant(orc, bits):
+    """quantization.rs:344-421: gather_qmm == gather_mm(x, dequant(w)^T)
+    for (lhs=(0,), rhs=(2,1)) and (x batch 5, lhs=(0,2), rhs=(2,1))."""
+    rng = np.random.default_rng(8)
+    M, N, K = 32, 64, 64
+    wf = orc.f32_to_bf16(rng.standard_normal((3, N, K)).astype(np.float32))
+    wq, sc, bi = orc.quantize(wf, 64, bits)
+    wd = _dense(orc, wq, sc, bi, bits)
+    for xb, lhs in [(1, [0]), (5, [0, 2])]:
+        x = orc.f32_to_bf16(rng.standard_normal((xb, M, K)).astype(np.float32))
+        rhs = [2, 1]
+        lhs_use = lhs if len(lhs) == 2 else [0, 0]
+        got = orc.bf16_to_f32(orc.gather_qmm(x, wq, sc, bi, rhs, lhs_use, bits=bits))
+        xf = orc.bf16_to_f32(x).astype(np.float64)
+        want = np.stack([xf[lhs_use[i]] @ wd[rhs[i]].T for i in range(2)])
+        assert np.allclose(got, want, rtol=2 ** -7, atol=1e-3 * np.abs(want).max())
+
+
+def test_gather_qmm_broadcast_x_over_topk(orc):
+    """x [T, 1, K] against indices [T, k]: out row (t, j) uses x[t]."""
+    rng = np.random.default_rng(9)
+    T, k, E, N, K = 6, 3, 5, 64, 128
+    wq, sc, bi = orc.quantize(orc.f32_to_bf16(rng.standard_normal((E, N, K)).astype(np.float32)))
+    x = orc.f32_to_bf16(rng.standard_normal((T, 1, K)).astype(np.float32))
+    idx = rng.integers(0, E, (T, k)).astype(np.int32)
+    got = orc.gather_qmm(x, wq, sc, bi, idx.reshape(-1))
+    lhs = np.repeat(np.arange(T), k)
+    assert np.array_equal(got, orc.gather_qmm(x, wq, sc, bi, idx.reshape(-1), lhs))
+
+
+# -------------------------------------------------------------- swiglu
+def test_swiglu_reference_values(orc):
+    """activations.rs:341-351 inputs: silu(g) * u vs the manual formula."""
+    g = np.array([1.0, -1.0, 0.5, 2.0], np.float32)
+    u = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    got = orc.bf16_to_f32(orc.swiglu(orc.f32_to_bf16(g), orc.f32_to_bf16(u)))
+    want = g / (1 + np.exp(-g.astype(np.float64))) * u
+    assert np.allclose(got, want, rtol=3 * 2 ** -8)
+
+
+# --------------------------------------------------------------- block
+def _c1_params(orc, seed=0, K=2, E=8, fs=0, bits=4, bias=False):
+    rng = np.random.default_rng(seed)
+    d, f = 512, 256
+
+    def q(shape):
+        w = orc.f32_to_bf16((rng.standard_normal(shape) * 0.02).astype(np.float32))
+        return orc.quantize(w, 64, bits)
+
+    p = dict(d=d, E=E, K=K, f=f, fs=fs, bits=bits, group_size=64,
+             router_w=(rng.standard_normal((E, d)) * 0.02).astype(np.float32),
+             router_b=(rng.standard_normal(E).astype(np.float32) if bias else None),
+             gate=q((E, f, d)), up=q((E, f, d)), down=q((E, d, f)))
+    if fs:
+        p.update(shared_gate=q((1, fs, d)), shared_up=q((1, fs, d)), shared_down=q((1, d, fs)),
+                 shared_gate_w=(rng.standard_normal((1, d)) * 0.02).astype(np.float32))
+    x = orc.f32_to_bf16(rng.standard_normal((16, d)).astype(np.float32))
+    return p, x
+
+
+@pytest.mark.parametrize("fs,bias", [(0, False), (256, False), (0, True)])
+def test_block_equals_sorted_composition(orc, fs, bias):
+    """switch.rs:446-474: the sorted path (gather_sort -> gather_qmm ->
+    swiglu -> gather_qmm -> scatter_unsort -> combine) and the block's
+    per-(t, k) path give identical bits."""
+    p, x = _c1_params(orc, fs=fs, bias=bias)
+    out, idx, w = orc.block_forward(p, x)
+    T, K, d, f = x.shape[0], p["K"], p["d"], p["f"]
+    lg = orc.router_logits(x, p["router_w"])
+    if bias:
+        lg = (lg + p["router_b"]).astype(np.float32)
+    idx2, w2 = orc.router_topk(lg, K)
+    assert np.array_equal(idx, idx2) and np.array_equal(w, w2)
+    _, _, order, inv = orc.dispatch(idx, p["E"])
+    rows = order // K
+    xs = x[rows][:, None, :]
+    ids = idx.reshape(-1)[order]
+    g = orc.gather_qmm(xs, *p["gate"], ids)
+    u = orc.gather_qmm(xs, *p["up"], ids)
+    a = orc.swiglu(g, u)
+    y = orc.gather_qmm(a, *p["down"], ids)[inv].reshape(T, K, d)
+    sy = sl = None
+    if fs:
+        x1 = x[:, None, :]
+        zeros = np.zeros(T, np.int32)
+        sa = orc.swiglu(orc.gather_qmm(x1, *p["shared_gate"], zeros),
+                        orc.gather_qmm(x1, *p["shared_up"], zeros))
+        sy = orc.gather_qmm(sa, *p["shared_down"], zeros).reshape(T, d)
+        sl = orc.router_logits(x, p["shared_gate_w"])[:, 0]
+    assert np.array_equal(out, orc.combine(y, w, sy, sl))
+
+
+def test_block_top1_is_single_expert(orc):
+    p, x = _c1_params(orc, K=1)
+    out, idx, w = orc.block_forward(p, x)
+    assert np.all(w == 1.0)
+    e = idx[:, 0]
+    g = orc.gather_qmm(x[:, None, :], *p["gate"], e)
+    u = orc.gather_qmm(x[:, None, :], *p["up"], e)
+    y = orc.gather_qmm(orc.swiglu(g, u), *p["down"], e).reshape(16, -1)
+    assert np.array_equal(out, orc.bf16_to_f32(y))
+
+
+def test_block_zero_input(orc):
+    p, x = _c1_params(orc)
+    out, idx, w = orc.block_forward(p, np.zeros_like(x))
+    assert np.all(idx == [0, 1]) and np.allclose(w, 0.5)
+    # biases of the quantised weights make gate(0) = 0 exactly (x = 0)
+    assert np.all(out == 0.0)
+
+
+def test_combine_linear_in_weights(orc):
+    rng = np.random.default_rng(10)
+    y = orc.f32_to_bf16(rng.standard_normal((4, 3, 64)).astype(np.float32))
+    w1 = rng.random((4, 3)).astype(np.float32)
+    w2 = rng.random((4, 3)).astype(np.float32)
+    lhs = orc.combine(y, w1 + w2)
+    rhs = orc.combine(y, w1) + orc.combine(y, w2)
+    assert np.allclose(lhs, rhs, rtol=1e-5, atol=1e-6)
