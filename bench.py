@@ -1,0 +1,262 @@
+"""MoE-block throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--tokens 64]
+
+One step is one Qwen35MoeBlock forward (router -> dispatch -> grouped
+quantised expert GEMMs -> combine) over T synthetic tokens, weights and
+inputs already resident in HBM.  Prints ONE JSON line: tokens/s through the
+block, the dominant kernel's roofline (algorithmic bytes or FLOPs per launch
+over its average launch time, from HIP events recorded on the stream it runs
+on) and the CPU oracle timed on this host's cores on a bounded sample.
+
+Only one GPU is used; --gpus N with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+import __graft_entry__ as entry
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2", help="c1..c5 (default c2, the decode block)")
+    ap.add_argument("--tokens", type=int, default=64, help="T of the headline line")
+    ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
+                    help="replay one captured HIP graph per step, or launch eagerly")
+    ap.add_argument("--sweep", default="c2:1,c2:8,c2:32,c3:4096",
+                    help="extra cfg:T points timed after the headline ('' for none)")
+    ap.add_argument("--sweep-steps", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bound of the CPU-baseline sample (0 skips it)")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0: the host cores, up to 16")
+    return ap.parse_args()
+
+
+def host_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+class Runner:
+    """One block at one T: eager or graph-replay steps on the current stream."""
+
+    def __init__(self, pkg, bw, T, dev, launch):
+        import torch
+        self.torch = torch
+        self.T = T
+        self.block = bw.block()
+        self.x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
+        self.out = torch.empty((T, bw.cfg.d), dtype=torch.float32, device=dev)
+        self.ws = pkg.ops.workspace(self.block.workspace_size(T), dev)
+        # one routed run: distinct experts for the byte count
+        self.block(self.x, out=self.out, workspace=self.ws, keep_routing=True)
+        torch.cuda.synchronize()
+        self.idx = self.block.last_indices.clone()
+        self.ref = self.out.clone()
+        self.graph = None
+        if launch == "graph":
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for _ in range(2):
+                    self.eager()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.eager()
+            torch.cuda.synchronize()
+            self.graph = g
+            for _ in range(3):  # every replay reproduces the eager result
+                g.replay()
+                torch.cuda.synchronize()
+                if not torch.equal(self.out, self.ref):
+                    raise RuntimeError("graph replay differs from the eager forward")
+                self.eager()
+                torch.cuda.synchronize()
+
+    def eager(self):
+        self.block(self.x, out=self.out, workspace=self.ws, keep_routing=False)
+
+    def step(self):
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.eager()
+
+    def timed(self, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            self.step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    def kernel_time(self, pkg, kernel, steps):
+        """Average duration (s) of `kernel` over `steps` eager forwards, from
+        HIP events the library records around each launch on its stream."""
+        import ctypes
+        C = pkg._capi
+        lib = C.lib()
+        self.torch.cuda.synchronize()
+        C.check(lib.mlxr_moe_profile_start(kernel.encode()))
+        for _ in range(steps):
+            self.eager()
+        n = ctypes.c_int64()
+        tot, mn, mx = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        C.check(lib.mlxr_moe_profile_stop(ctypes.byref(n), ctypes.byref(tot), ctypes.byref(mn),
+                                          ctypes.byref(mx)))
+        if n.value == 0:
+            raise RuntimeError(f"kernel {kernel} was not launched")
+        return tot.value / n.value / 1e3, n.value, mn.value / 1e3, mx.value / 1e3
+
+
+def gated_bytes(cfg, T, U):
+    """Algorithmic HBM bytes of one gate/up launch: the packed words plus
+    bf16 scales and biases of the U distinct selected experts' gate and up
+    rows (2*f*d weights each), x read once (T*d bf16) and the activations
+    written (T*K*f bf16)."""
+    per_w = cfg.bits / 8 + 4 / cfg.group_size
+    return int(U * 2 * cfg.f * cfg.d * per_w + T * cfg.d * 2 + T * cfg.K * cfg.f * 2)
+
+
+def gated_flops(cfg, T):
+    return 4 * T * cfg.K * cfg.f * cfg.d
+
+
+def cpu_baseline(pkg, orc, bw, T, seconds, threads):
+    """The oracle (plain C, OpenMP) on this host: whole block forwards of the
+    same c-config at T tokens until `seconds` have passed (at least one)."""
+    import torch
+    p = orc.block_params(bw)
+    x = orc.to_np(pkg.workloads.make_x(bw.cfg, T, torch.device("cuda:0"), seed=T))
+    orc.block_forward(p, x[:1], nthreads=threads)  # page in
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        orc.block_forward(p, x, nthreads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return dict(value=round(n * T / el, 2), unit="tokens/s", cores=threads, kind="port",
+                sample=f"{n} block forwards of {bw.cfg.name} at T={T} "
+                       f"({el:.1f} s, oracle/moe_oracle.c, {threads} OpenMP threads)")
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one MI355X only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the MoE block is not sharded across GPUs here.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = entry.load_package()
+    dev = torch.device("cuda:0")
+    W = pkg.workloads
+    cfg = W.CONFIGS[args.config]
+    T = args.tokens
+    print(f"bench: {cfg.name} T={T} on {torch.cuda.get_device_name(dev)}", file=sys.stderr,
+          flush=True)
+    bw = W.make_weights(cfg, dev)
+    r = Runner(pkg, bw, T, dev, args.launch)
+    U = W.distinct(r.idx)
+    sec = r.timed(args.steps, args.warmup)
+    tok_s = T / sec
+    block_bytes = W.algorithmic_bytes(cfg, T, U)
+    print(f"bench: {sec * 1e6:.1f} us/step, {tok_s:.0f} tokens/s", file=sys.stderr, flush=True)
+
+    # dominant kernel: the fused gate/up gather_qmm
+    kt, kn, kmin, kmax = r.kernel_time(pkg, "qgemm_gated", args.steps)
+    decode = T * cfg.K < 2048
+    if decode:
+        traffic_alg = gated_bytes(cfg, T, U)
+        achieved = traffic_alg / kt / 1e9
+        roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None)
+    else:
+        achieved = gated_flops(cfg, T) / kt / 1e12
+        roof = dict(bound="mfma", achieved=round(achieved, 2), peak=BF16_PEAK_TFLOPS,
+                    unit="TFLOP/s", frac=round(achieved / BF16_PEAK_TFLOPS, 4), traffic=None)
+    roof.update(kernel="qgemm_gated", kernel_us=round(kt * 1e6, 2), launches=kn,
+                kernel_us_min=round(kmin * 1e6, 2), kernel_us_max=round(kmax * 1e6, 2))
+    print(f"bench: qgemm_gated {kt * 1e6:.2f} us avg over {kn} launches", file=sys.stderr,
+          flush=True)
+
+    sweep = []
+    banks = {cfg.name: bw}
+    for item in [s for s in args.sweep.split(",") if s]:
+        cname, tt = item.split(":")
+        tt = int(tt)
+        c2 = W.CONFIGS[cname]
+        if c2.name not in banks:
+            banks[c2.name] = W.make_weights(c2, dev)
+        r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch)
+        s2 = r2.timed(args.sweep_steps, 5)
+        U2 = W.distinct(r2.idx)
+        ent = dict(config=c2.name, T=tt, tokens_per_s=round(tt / s2, 1),
+                   us_per_step=round(s2 * 1e6, 2), distinct_experts=U2)
+        if tt * c2.K < 2048:
+            ent["block_hbm_gbs"] = round(W.algorithmic_bytes(c2, tt, U2) / s2 / 1e9, 1)
+        else:
+            ent["block_tflops"] = round(W.algorithmic_flops(c2, tt) / s2 / 1e12, 2)
+        sweep.append(ent)
+        print(f"bench: sweep {ent}", file=sys.stderr, flush=True)
+        del r2
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        orc = entry.load_oracle()
+        threads = args.cpu_threads or host_cores()
+        cpu = cpu_baseline(pkg, orc, bw, T, args.cpu_seconds, threads)
+        print(f"bench: cpu baseline {cpu}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "MoE-block tokens/sec (Qwen3-30B-A3B-shaped 4-bit block, decode)",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x, N(0,0.02) weights affine-quantised on the GPU)",
+        "config": {"workload": f"{cfg.name} T={T}", "tokens": T, "d": cfg.d, "E": cfg.E,
+                   "K": cfg.K, "f": cfg.f, "bits": cfg.bits, "group_size": cfg.group_size,
+                   "distinct_experts": U, "launch": args.launch,
+                   "block_algorithmic_bytes": block_bytes,
+                   "block_hbm_gbs": round(block_bytes / sec / 1e9, 1)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

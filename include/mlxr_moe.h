@@ -227,6 +227,18 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
 int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,
                               mlxr_moe_stream stream);
 
+/* Kernel timing (no counterpart in the reference, whose benches time whole
+ * models with criterion, crates/mlxr-lm/benches/lm_decode.rs): while
+ * `kernel` is armed, each launch of that kernel is bracketed by HIP events
+ * on the stream it is launched on.  Names: "router_logits", "router_topk",
+ * "dispatch", "qgemm_gated", "qgemm_down", "combine".  NULL disarms.  Not
+ * for use while the stream is being captured into a graph. */
+int mlxr_moe_profile_start(const char* kernel);
+/* Waits for the armed kernel's last launch, returns the number of launches
+ * and their elapsed time (total / min / max, milliseconds), and disarms. */
+int mlxr_moe_profile_stop(int64_t* launches, double* total_ms, double* min_ms,
+                          double* max_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,7 +6,7 @@ fallback behind these functions.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, Structure, c_char_p, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlxr_moe.so"
@@ -91,6 +91,9 @@ SIGNATURES = {
     "mlxr_moe_block_workspace_size": (c_size_t, [POINTER(Block), c_int64]),
     "mlxr_moe_block_forward": (c_int, [POINTER(Block), P, c_int64, P, P, P, P, c_size_t, P]),
     "mlxr_moe_workspace_status": (c_int, [P, c_size_t, P]),
+    "mlxr_moe_profile_start": (c_int, [c_char_p]),
+    "mlxr_moe_profile_stop": (c_int, [POINTER(c_int64), POINTER(c_double), POINTER(c_double),
+                                      POINTER(c_double)]),
 }
 
 _lib = None

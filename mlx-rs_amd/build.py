@@ -30,6 +30,7 @@ SOURCES = [
     "qgemm.hip",
     "combine.hip",
     "nn.cpp",
+    "profile.cpp",
     "capi.cpp",
 ]
 
@@ -40,6 +41,10 @@ COMMON = [
     f"--offload-arch={ARCH}",
     # packed fp32 VALU ops stay off on this hardware pool
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # every multiply and add rounds separately unless the source calls fmaf
+    # (hipcc's default would fuse them): the combine and softmax then match
+    # a plain C evaluation of the same expressions bit for bit
+    "-ffp-contract=off",
     "-Wall",
     "-Wno-unused-function",
 ]

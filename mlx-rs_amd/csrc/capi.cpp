@@ -459,6 +459,28 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
   return finish(st);
 }
 
+int mlxr_moe_profile_start(const char* kernel) {
+  static const char* const kNames[] = {"router_logits", "router_topk",
+                                       "dispatch",      "qgemm_gated",
+                                       "qgemm_down",    "combine"};
+  if (kernel && *kernel) {
+    bool known = false;
+    for (const char* n : kNames) known = known || std::strcmp(n, kernel) == 0;
+    if (!known)
+      return fail(std::string("profile_start: unknown kernel '") + kernel +
+                  "'");
+  }
+  return profile_arm(kernel);
+}
+
+int mlxr_moe_profile_stop(int64_t* launches, double* total_ms, double* min_ms,
+                          double* max_ms) {
+  std::string err;
+  if (profile_collect(launches, total_ms, min_ms, max_ms, &err) != 0)
+    return fail(err);
+  return 0;
+}
+
 int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,
                               mlxr_moe_stream stream) {
   if (!workspace || workspace_size < sizeof(int32_t))

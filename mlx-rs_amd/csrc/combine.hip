@@ -64,6 +64,7 @@ hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,
                           float* out, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const dim3 grid((unsigned)((d / 8 + 255) / 256), (unsigned)T);
+  ProfileScope prof("combine", s);
   combine_kernel<<<grid, 256, 0, s>>>(y, w, (int)T, (int)K, (int)d, shared_y,
                                       shared_logit, shared_ld, out);
   return hipGetLastError();

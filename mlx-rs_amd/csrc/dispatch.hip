@@ -203,6 +203,7 @@ hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
                            int tile_rows, const DispatchBuffers& b,
                            bool reset_status, hipStream_t s) {
   const int nb = (int)((n + kDispatchBlock - 1) / kDispatchBlock);
+  ProfileScope prof("dispatch", s);
   if (reset_status) zero_status_kernel<<<1, 1, 0, s>>>(b.status);
   if (nb > 0)
     dispatch_rank_kernel<<<nb, kDispatchBlock,

@@ -6,7 +6,30 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace mlxr_moe {
+
+// ------------------------------------------------------------- profile.cpp
+// Brackets one kernel launch with HIP events on its stream when that
+// kernel's name is armed (profile_arm); a no-op otherwise.
+class ProfileScope {
+ public:
+  ProfileScope(const char* kernel, hipStream_t s);
+  ~ProfileScope();
+  ProfileScope(const ProfileScope&) = delete;
+  ProfileScope& operator=(const ProfileScope&) = delete;
+
+ private:
+  hipEvent_t stop_ = nullptr;
+  hipStream_t stream_ = nullptr;
+};
+// kernel == nullptr or "" disarms.  Re-arming drops unread launches.
+int profile_arm(const char* kernel);
+// Launch count and elapsed milliseconds (total, min, max) of the armed
+// kernel since profile_arm; waits for the last launch; disarms.
+int profile_collect(int64_t* launches, double* total_ms, double* min_ms,
+                    double* max_ms, std::string* err);
 
 // ---------------------------------------------------------------- quant.hip
 hipError_t launch_quantize(const void* w, bool w_bf16, int64_t rows,

@@ -14,9 +14,14 @@
 // v_mfma_f32_16x16x32_bf16 with tokens as the M side and output channels
 // as the N side.  Per quantisation group g the MFMA yields
 //   P = sum x * c'   and   X = sum x
-// where c' is the code (8-bit) or 128 + code (4-bit: the code is OR-ed into
-// the mantissa of bf16 128.0, one v_and_or per two codes), and the group's
-// contribution is scale * P + (bias - 128 * scale) * X in fp32.
+// where c' is the code (8-bit, converted exactly) or 1 + code/16 (4-bit: the
+// code is OR-ed into the top four mantissa bits of bf16 1.0, one shift and
+// one v_and_or per two codes), and the group's contribution in fp32 is
+//   8-bit: scale * P + bias * X
+//   4-bit: 16 * scale * P + (bias - 16 * scale) * X.
+// Keeping the code in the top mantissa bits keeps P within about 2x of the
+// code term it carries, so the offset cancels with little loss (with the code
+// in the low bits, 128 + code, the fp32 error of P grows ~8x).
 // K (the input dim) is split over 1, 2 or 4 waves when few experts are
 // active, so that small T still spreads over all CUs.
 #include <type_traits>
@@ -38,14 +43,15 @@ __device__ __forceinline__ u32x4_t perm4(u32x4_t v) {
   return r;
 }
 
-// 8 nibbles -> bf16 (128 + code), pairs (n0,n4) (n1,n5) (n2,n6) (n3,n7).
+// 8 nibbles -> bf16 (1 + code/16): nibble k moves to mantissa bits 6..3 of
+// its half; pairs (n0,n4) (n1,n5) (n2,n6) (n3,n7).
 __device__ __forceinline__ u32x4_t unpack4(uint32_t w) {
-  const uint32_t m = 0x000F000Fu, mg = 0x43004300u;
+  const uint32_t m = 0x00780078u, one = 0x3F803F80u;
   u32x4_t r;
-  r.x = (w & m) | mg;
-  r.y = ((w >> 4) & m) | mg;
-  r.z = ((w >> 8) & m) | mg;
-  r.w = ((w >> 12) & m) | mg;
+  r.x = ((w << 3) & m) | one;
+  r.y = ((w >> 1) & m) | one;
+  r.z = ((w >> 5) & m) | one;
+  r.w = ((w >> 9) & m) | one;
   return r;
 }
 
@@ -164,19 +170,20 @@ __global__ __launch_bounds__(256) void qgemm_decode_kernel(QGemmArgs a,
         X = mfma16x16x32(A1, as_bf16x8(ones), X);
         f32x4_t P0 = mfma16x16x32(A0, as_bf16x8(q0[u].step(0)), zero);
         P0 = mfma16x16x32(A1, as_bf16x8(q0[u].step(1)), P0);
-        const float sc0 = bf16_to_f32(s0[u]);
+        const float s0f = bf16_to_f32(s0[u]);
         const float bi0 = bf16_to_f32(b0[u]);
-        const float c0 = BITS == 4 ? __builtin_fmaf(-128.0f, sc0, bi0) : bi0;
+        const float sc0 = BITS == 4 ? 16.0f * s0f : s0f;
+        const float c0 = BITS == 4 ? __builtin_fmaf(-16.0f, s0f, bi0) : bi0;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           acc0[r] = __builtin_fmaf(sc0, P0[r], __builtin_fmaf(c0, X[r], acc0[r]));
         if constexpr (GATED) {
           f32x4_t P1 = mfma16x16x32(A0, as_bf16x8(q1[u].step(0)), zero);
           P1 = mfma16x16x32(A1, as_bf16x8(q1[u].step(1)), P1);
-          const float sc1 = bf16_to_f32(s1[u]);
+          const float s1f = bf16_to_f32(s1[u]);
           const float bi1 = bf16_to_f32(b1[u]);
-          const float c1 =
-              BITS == 4 ? __builtin_fmaf(-128.0f, sc1, bi1) : bi1;
+          const float sc1 = BITS == 4 ? 16.0f * s1f : s1f;
+          const float c1 = BITS == 4 ? __builtin_fmaf(-16.0f, s1f, bi1) : bi1;
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             acc1[r] =
@@ -236,6 +243,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   if (wg1 * 2 < 1024 && groups % 4 == 0 && a.N % 16 == 0) ks = 4;
   const int cw = 4 / ks;
   const dim3 grid((unsigned)(a.N / (16 * cw)), (unsigned)max_active);
+  ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
 #define MLXR_QG(B, G) qgemm_decode_kernel<B, G><<<grid, 256, 0, s>>>(a, ks)
   if (a.bits == 4)
     a.gated ? MLXR_QG(4, true) : MLXR_QG(4, false);

@@ -222,6 +222,7 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
   // Few tokens: one logit column per wave so the 4*d*E bytes of router
   // weights spread over E/4 workgroups.  Many tokens: 4 columns x 16
   // tokens per wave for register reuse of both operands.
+  ProfileScope prof("router_logits", s);
   if (T <= 16) {
     const dim3 grid((unsigned)((e_tot + 3) / 4), 1);
     router_logits_kernel<1, 16><<<grid, 256, 0, s>>>(
@@ -238,6 +239,7 @@ hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
                               int64_t E, int64_t K, int32_t* idx, float* wts,
                               hipStream_t s) {
   if (T == 0) return hipSuccess;
+  ProfileScope prof("router_topk", s);
   const dim3 grid((unsigned)((T + 3) / 4));
   const int slots = (int)((E + 63) / 64);
 #define MLXR_TOPK(S)                                                     \
