@@ -42,7 +42,21 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound of the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: the host cores, up to 16")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB, 20 times (the "
+                         "known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def copy_calibration(mib: int) -> None:
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 20}), flush=True)
 
 
 def host_cores() -> int:
@@ -172,6 +186,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
+        return
     import torch
     pkg = entry.load_package()
     dev = torch.device("cuda:0")

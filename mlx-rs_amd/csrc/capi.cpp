@@ -168,6 +168,9 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
     return fail("gather_qmm: bad shape");
   if (K % 64 || N % 64)
     return fail("gather_qmm: K and N must be multiples of 64");
+  if (K > kMaxInputDims)
+    return fail("gather_qmm: K above " + std::to_string(kMaxInputDims) +
+                " is not supported");
   if (!lhs_indices && B % x_batch)
     return fail("gather_qmm: x batch " + std::to_string(x_batch) +
                 " does not broadcast against " + std::to_string(B) +
@@ -210,6 +213,7 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   a.offsets = db.offsets;
   a.active = db.active;
   a.num_active = db.num_active;
+  a.work = db.work;
   a.tiles = db.tiles;
   a.num_tiles = db.num_tiles;
   a.w0 = QWeights{w, static_cast<const uint16_t*>(scales),
@@ -290,7 +294,8 @@ int mlxr_moe_router_topk(const void* x, int64_t T, int64_t d,
                                      s),
                 "router logits");
   if (st.ok)
-    st = from_hip(launch_router_topk(logits, E, T, E, K, topk_idx, topk_w, s),
+    st = from_hip(launch_router_topk(logits, E, T, E, K, topk_idx, topk_w,
+                                     nullptr, s),
                   "router top-k");
   return finish(st);
 }
@@ -451,12 +456,9 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
   if (T == 0) return 0;
   hipStream_t s = as_stream(stream);
   Carve c(workspace);
-  int32_t* status = c.take<int32_t>(1);
-  st = from_hip(launch_zero_status(status, s), "block status");
-  if (st.ok)
-    st = m.forward(static_cast<const uint16_t*>(x), T, out, topk_idx, topk_w,
-                   c, s);
-  return finish(st);
+  c.take<int32_t>(1);  // status word, cleared by the routing kernel
+  return finish(m.forward(static_cast<const uint16_t*>(x), T, out, topk_idx,
+                          topk_w, c, s));
 }
 
 int mlxr_moe_profile_start(const char* kernel) {

@@ -15,6 +15,7 @@
 // Ids outside [0, E) are left out of every expert and flagged in *status.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "route.hpp"
 
 namespace mlxr_moe {
 namespace {
@@ -58,33 +59,6 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_rank_kernel(
   if (ok) rank[gi] = tab[wave * E + id] + r;
 }
 
-// Exclusive scan of one int per thread over the 1024-thread block.
-__device__ int block_exclusive_scan(int v, int* total, int* wsum) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += u;
-  }
-  if (lane == 63) wsum[wave] = inc;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < kWaves; ++w) {
-      const int c = wsum[w];
-      wsum[w] = run;
-      run += c;
-    }
-    wsum[kWaves] = run;
-  }
-  __syncthreads();
-  const int ex = wsum[wave] + inc - v;
-  *total = wsum[kWaves];
-  __syncthreads();
-  return ex;
-}
-
 __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
     const int32_t* __restrict__ ids, int n, int E, int nb, int tile_rows,
     DispatchBuffers b) {
@@ -111,7 +85,13 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
   const int has = (tid < E && cnt > 0) ? 1 : 0;
   int n_active;
   const int apos = block_exclusive_scan(has, &n_active, wsum);
-  if (has) b.active[apos] = tid;
+  if (has) {
+    b.active[apos] = tid;
+    b.work[4 * apos] = tid;
+    b.work[4 * apos + 1] = off;
+    b.work[4 * apos + 2] = cnt;
+    b.work[4 * apos + 3] = 0;
+  }
   if (tid == 0) *b.num_active = n_active;
 
   const int nt = (tid < E) ? (cnt + tile_rows - 1) / tile_rows : 0;
@@ -135,6 +115,46 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
   }
 }
 
+// n <= 1024 ids: the whole sort in one workgroup.
+__global__ __launch_bounds__(kDispatchBlock) void dispatch_small_kernel(
+    const int32_t* __restrict__ ids, int n, int E, int tile_rows,
+    DispatchBuffers b, int reset_status) {
+  __shared__ DispatchScratch ls;
+  if (reset_status && threadIdx.x == 0) *b.status = 0;
+  __syncthreads();
+  const int id = (int)threadIdx.x < n ? ids[threadIdx.x] : -1;
+  block_dispatch(id, n, E, tile_rows, b, &ls);
+}
+
+// Decode routing in one workgroup (T * K <= 1024): top-K of every token
+// (16 waves over the tokens), the renormalised weights, the status reset and
+// the counting sort of the T * K expert ids.
+template <int SLOTS>
+__global__ __launch_bounds__(kDispatchBlock) void route_small_kernel(
+    const float* __restrict__ logits, int64_t ld, int T, int E, int K,
+    int32_t* __restrict__ idx, float* __restrict__ wts, int tile_rows,
+    DispatchBuffers b) {
+  __shared__ DispatchScratch ls;
+  __shared__ TopkScratch sc[kDispatchBlock / 64];
+  __shared__ int ids[kDispatchBlock];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) *b.status = 0;
+  for (int t = wave; t < T; t += kDispatchBlock / 64) {
+    int id;
+    float wt;
+    wave_topk<SLOTS>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
+    if (lane < K) {
+      idx[(int64_t)t * K + lane] = id;
+      wts[(int64_t)t * K + lane] = wt;
+      ids[t * K + lane] = id;
+    }
+  }
+  __syncthreads();
+  const int n = T * K;
+  block_dispatch((int)threadIdx.x < n ? ids[threadIdx.x] : -1, n, E,
+                 tile_rows, b, &ls);
+}
+
 __global__ __launch_bounds__(256) void dispatch_identity_kernel(
     int n, int tile_rows, DispatchBuffers b) {
   const int tid = threadIdx.x;
@@ -144,6 +164,10 @@ __global__ __launch_bounds__(256) void dispatch_identity_kernel(
     b.offsets[0] = 0;
     b.offsets[1] = n;
     b.active[0] = 0;
+    b.work[0] = 0;
+    b.work[1] = 0;
+    b.work[2] = n;
+    b.work[3] = 0;
     *b.num_active = n > 0 ? 1 : 0;
     *b.num_tiles = n_tiles;
   }
@@ -202,15 +226,49 @@ int64_t dispatch_max_tiles(int64_t n, int64_t E, int tile_rows) {
 hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
                            int tile_rows, const DispatchBuffers& b,
                            bool reset_status, hipStream_t s) {
-  const int nb = (int)((n + kDispatchBlock - 1) / kDispatchBlock);
   ProfileScope prof("dispatch", s);
+  if (n <= kDispatchBlock) {
+    dispatch_small_kernel<<<1, kDispatchBlock, 0, s>>>(
+        ids, (int)n, (int)E, tile_rows, b, reset_status ? 1 : 0);
+    return hipGetLastError();
+  }
+  const int nb = (int)((n + kDispatchBlock - 1) / kDispatchBlock);
   if (reset_status) zero_status_kernel<<<1, 1, 0, s>>>(b.status);
-  if (nb > 0)
-    dispatch_rank_kernel<<<nb, kDispatchBlock,
-                           (size_t)kWaves * E * sizeof(uint16_t), s>>>(
-        ids, (int)n, (int)E, b.block_hist, b.rank, b.status);
+  dispatch_rank_kernel<<<nb, kDispatchBlock,
+                         (size_t)kWaves * E * sizeof(uint16_t), s>>>(
+      ids, (int)n, (int)E, b.block_hist, b.rank, b.status);
   dispatch_scan_kernel<<<1, kDispatchBlock, 0, s>>>(ids, (int)n, (int)E, nb,
                                                     tile_rows, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
+                        int64_t K, int32_t* idx, float* wts, int tile_rows,
+                        const DispatchBuffers& b, hipStream_t s) {
+  if (T == 0) return launch_zero_status(b.status, s);
+  // one workgroup while each of its 16 waves has one token; beyond that the
+  // top-k spreads over the GPU (a wave per token) before the sort
+  if (T > kDispatchBlock / 64 || T * K > kDispatchBlock) {
+    hipError_t e = launch_router_topk(logits, ld, T, E, K, idx, wts, b.status, s);
+    if (e != hipSuccess) return e;
+    return launch_dispatch(idx, T * K, E, tile_rows, b, false, s);
+  }
+  ProfileScope prof("router_topk", s);
+  const int slots = (int)((E + 63) / 64);
+#define MLXR_RS(S)                                                         \
+  route_small_kernel<S><<<1, kDispatchBlock, 0, s>>>(                      \
+      logits, ld, (int)T, (int)E, (int)K, idx, wts, tile_rows, b)
+  if (slots <= 1)
+    MLXR_RS(1);
+  else if (slots <= 2)
+    MLXR_RS(2);
+  else if (slots <= 4)
+    MLXR_RS(4);
+  else if (slots <= 8)
+    MLXR_RS(8);
+  else
+    MLXR_RS(16);
+#undef MLXR_RS
   return hipGetLastError();
 }
 

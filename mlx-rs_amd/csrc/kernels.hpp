@@ -48,9 +48,10 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 const float* w, const float* bias, int64_t E,
                                 const float* w_extra, float* logits,
                                 int64_t ld, hipStream_t s);
+// One wave per token; clears *status first when status != nullptr.
 hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
                               int64_t E, int64_t K, int32_t* idx, float* wts,
-                              hipStream_t s);
+                              int32_t* status, hipStream_t s);
 hipError_t launch_argsort_rows(const float* a, int64_t rows, int64_t n,
                                uint32_t* out, hipStream_t s);
 hipError_t launch_softmax_rows(const float* a, int64_t rows, int64_t n,
@@ -65,6 +66,7 @@ struct DispatchBuffers {
   int32_t* inv;         // [n]  sorted slot per flat index
   int32_t* active;      // [E]  experts with rows, ascending
   int32_t* num_active;  // [1]
+  int32_t* work;        // [E][4] (expert, first slot, rows, 0) per active
   int32_t* tiles;       // [max_tiles] packed (expert, first row) of M-tiles
   int32_t* num_tiles;   // [1]
   int32_t* block_hist;  // [ceil(n/1024), E] scratch
@@ -82,6 +84,12 @@ hipError_t launch_zero_status(int32_t* status, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
                            int tile_rows, const DispatchBuffers& b,
                            bool reset_status, hipStream_t s);
+// Top-K + renormalised weights of every token from its logits, then the
+// counting sort of the T*K ids, clearing *b.status first.  T <= 16 runs as
+// one workgroup; larger T as the top-k kernel plus launch_dispatch.
+hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
+                        int64_t K, int32_t* idx, float* wts, int tile_rows,
+                        const DispatchBuffers& b, hipStream_t s);
 // gather_qmm helpers: per flat row r = b*M + m the expert id and x row, and
 // the x row of each sorted slot.
 hipError_t launch_gather_prep(const uint32_t* lhs, const uint32_t* rhs,
@@ -109,6 +117,7 @@ struct QGemmArgs {
   const int32_t* offsets;  // [E+1] slot range of each expert
   const int32_t* active;   // [E] experts with rows
   const int32_t* num_active;
+  const int32_t* work;     // [E][4] (expert, first slot, rows, 0) per active
   const int32_t* tiles;    // M-tile list (prefill path)
   const int32_t* num_tiles;
   QWeights w0;             // gate (or the only projection)
@@ -119,6 +128,8 @@ struct QGemmArgs {
   const int32_t* out_map;  // out row of slot p = out_map[p] (null: p)
   bool gated;              // out = swiglu(x.w0, x.w1)
 };
+// Largest input dim (K) of a projection: 8 waves x 8 groups of 64.
+constexpr int kMaxInputDims = 4096;
 // Rows per M-tile of the prefill kernel; the dispatch builds its tile list.
 constexpr int kPrefillTileRows = 128;
 // max_rows_per_expert bounds the grid of the decode kernel; max_active

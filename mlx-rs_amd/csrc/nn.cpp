@@ -33,6 +33,9 @@ Status check_qlinear(const mlxr_moe_qlinear& q, int64_t experts, int64_t out,
   if (out % 64 || in % 64)
     return Status::error(n + ": input and output dims must be multiples of "
                              "64");
+  if (in > kMaxInputDims)
+    return Status::error(n + ": input dims above " +
+                         std::to_string(kMaxInputDims) + " are not supported");
   if ((reinterpret_cast<uintptr_t>(q.weight) & 15) ||
       (reinterpret_cast<uintptr_t>(q.scales) & 1) ||
       (reinterpret_cast<uintptr_t>(q.biases) & 1))
@@ -50,6 +53,7 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
   b.inv = c.take<int32_t>(n);
   b.active = c.take<int32_t>(E);
   b.num_active = c.take<int32_t>(1);
+  b.work = c.take<int32_t>(4 * E);
   b.tiles = c.take<int32_t>(2 * dispatch_max_tiles(n, E, kPrefillTileRows));
   b.num_tiles = c.take<int32_t>(1);
   b.block_hist = c.take<int32_t>(nb * E);
@@ -111,6 +115,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.offsets = db.offsets;
   g.active = db.active;
   g.num_active = db.num_active;
+  g.work = db.work;
   g.tiles = db.tiles;
   g.num_tiles = db.num_tiles;
   g.w0 = qw(gate_);
@@ -161,21 +166,31 @@ void SplitSwitchFfn::plan(Carve& ws, int64_t T, int64_t K, int64_t d,
 }
 
 // SplitSwitchFfn::forward (switch.rs:417-442) on the sorted path: dispatch
-// (gather_sort), gate and up gather_qmm fused with swiglu, down gather_qmm
-// whose rows land at their flat (t, k) position (scatter_unsort).
+// (gather_sort), then the expert products.
 Status SplitSwitchFfn::forward(const uint16_t* x, int64_t T,
                                const int32_t* indices, int64_t K, uint16_t* y,
                                Carve& ws, int32_t* status,
                                hipStream_t s) const {
-  const int64_t d = w_.gate_proj.input_dims, f = w_.gate_proj.output_dims;
   const int64_t E = w_.gate_proj.num_experts;
   const int64_t n = T * K;
   const DispatchBuffers db = carve_dispatch(ws, n, E, status);
-  uint16_t* act = ws.take<uint16_t>(n * f);
   Status st = from_hip(
       launch_dispatch(indices, n, E, kPrefillTileRows, db, false, s),
       "switch_mlp dispatch");
   if (!st.ok) return st;
+  return experts(x, T, K, db, y, ws, s);
+}
+
+// The expert products of SplitSwitchFfn::forward given the dispatch: gate and
+// up gather_qmm fused with swiglu (switch.rs:432-434), down gather_qmm whose
+// rows land at their flat (t, k) position (scatter_unsort, switch.rs:437-439).
+Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
+                               const DispatchBuffers& db, uint16_t* y,
+                               Carve& ws, hipStream_t s) const {
+  const int64_t d = w_.gate_proj.input_dims, f = w_.gate_proj.output_dims;
+  const int64_t E = w_.gate_proj.num_experts;
+  const int64_t n = T * K;
+  uint16_t* act = ws.take<uint16_t>(n * f);
   const int64_t max_active = std::min(E, n);
   const bool prefill = use_prefill_path(n, E);
   QGemmArgs g{};
@@ -186,6 +201,7 @@ Status SplitSwitchFfn::forward(const uint16_t* x, int64_t T,
   g.offsets = db.offsets;
   g.active = db.active;
   g.num_active = db.num_active;
+  g.work = db.work;
   g.tiles = db.tiles;
   g.num_tiles = db.num_tiles;
   g.w0 = qw(w_.gate_proj);
@@ -198,8 +214,8 @@ Status SplitSwitchFfn::forward(const uint16_t* x, int64_t T,
   g.out_ld = f;
   g.out_map = nullptr;
   g.gated = true;
-  st = from_hip(launch_qgemm(g, n, max_active, prefill, s),
-                "switch_mlp gate/up");
+  Status st = from_hip(launch_qgemm(g, n, max_active, prefill, s),
+                       "switch_mlp gate/up");
   if (!st.ok) return st;
   QGemmArgs h = g;
   h.x = act;
@@ -270,7 +286,9 @@ void Qwen35MoeBlock::plan(Carve& ws, const mlxr_moe_block& b, int64_t T) {
   SplitSwitchFfn::plan(ws, T, K, d, f, E);
 }
 
-// Qwen35MoeBlock::forward (moe.rs:116-146).
+// Qwen35MoeBlock::forward (moe.rs:116-146).  Kernels: router logits (with
+// the shared-expert gate as one more column), routing (top-k, weights and
+// the expert dispatch), [shared expert], gate/up, down, combine.
 Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
                                int32_t* topk_idx, float* topk_w, Carve& ws,
                                hipStream_t s) const {
@@ -284,6 +302,11 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
   float* wts = ws.take<float>(T * K);
   if (topk_idx) idx = topk_idx;
   if (topk_w) wts = topk_w;
+  uint16_t* sy = shared ? ws.take<uint16_t>(T * d) : nullptr;
+  Carve shared_ws = ws;  // the shared expert's scratch (plan order)
+  if (shared) SwigluMlp::plan(ws, T, d, b_.shared_expert_intermediate_size);
+  uint16_t* y = ws.take<uint16_t>(T * K * d);
+  const DispatchBuffers db = carve_dispatch(ws, T * K, E, status);
   // gate.forward + shared_expert_gate.forward (moe.rs:118,123) in one pass.
   Status st = from_hip(
       launch_router_logits(x, T, d, b_.gate_weight, b_.gate_bias, E,
@@ -291,20 +314,23 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
                            logits, ld, s),
       "router logits");
   if (!st.ok) return st;
-  st = from_hip(launch_router_topk(logits, ld, T, E, K, idx, wts, s),
-                "router top-k");
+  // softmax, argpartition top-k, renormalise (moe.rs:124-138) + gather_sort
+  st = from_hip(
+      launch_route(logits, ld, T, E, K, idx, wts, kPrefillTileRows, db, s),
+      "router top-k / dispatch");
   if (!st.ok) return st;
-  uint16_t* sy = nullptr;
   if (shared) {
-    sy = ws.take<uint16_t>(T * d);
     st = SwigluMlp(b_.shared_gate_proj, b_.shared_up_proj,
                    b_.shared_down_proj)
-             .forward(x, T, sy, ws, status, s);
+             .forward(x, T, sy, shared_ws, status, s);
     if (!st.ok) return st;
   }
-  return SplitSwitchFfn(b_.switch_mlp)
-      .forward_with_combine(x, T, idx, wts, K, out, sy,
-                            shared ? logits + E : nullptr, ld, ws, status, s);
+  const SplitSwitchFfn mlp(b_.switch_mlp);
+  st = mlp.experts(x, T, K, db, y, ws, s);
+  if (!st.ok) return st;
+  return from_hip(launch_combine(y, wts, T, K, d, sy,
+                                 shared ? logits + E : nullptr, ld, out, s),
+                  "combine");
 }
 
 }  // namespace nn

@@ -80,6 +80,10 @@ class SplitSwitchFfn {
   Status forward(const uint16_t* x, int64_t T, const int32_t* indices,
                  int64_t K, uint16_t* y, Carve& ws, int32_t* status,
                  hipStream_t s) const;
+  // The expert products given a dispatch of the T*K flat ids.
+  Status experts(const uint16_t* x, int64_t T, int64_t K,
+                 const DispatchBuffers& db, uint16_t* y, Carve& ws,
+                 hipStream_t s) const;
   // forward_with_combine: out f32 [T, d] = sum_k w * y (+ shared branch).
   Status forward_with_combine(const uint16_t* x, int64_t T,
                               const int32_t* indices, const float* weights,

@@ -9,10 +9,10 @@
 // workgroup tile, however many tokens chose it.
 //
 // Decode kernel (few rows per expert): HBM-bound.  Weights are never
-// dequantised to memory.  Each lane loads its packed words (8 B per group
-// for 4-bit, 16 B for 8-bit), expands codes into bf16 registers and feeds
-// v_mfma_f32_16x16x32_bf16 with tokens as the M side and output channels
-// as the N side.  Per quantisation group g the MFMA yields
+// dequantised to memory: every lane loads 16 contiguous bytes of its row per
+// step (the width that streams at full HBM rate), expands the codes into bf16
+// registers and feeds v_mfma_f32_16x16x32_bf16 with tokens as the M side and
+// output channels as the N side.  Per quantisation group g the MFMAs yield
 //   P = sum x * c'   and   X = sum x
 // where c' is the code (8-bit, converted exactly) or 1 + code/16 (4-bit: the
 // code is OR-ed into the top four mantissa bits of bf16 1.0, one shift and
@@ -22,15 +22,19 @@
 // Keeping the code in the top mantissa bits keeps P within about 2x of the
 // code term it carries, so the offset cancels with little loss (with the code
 // in the low bits, 128 + code, the fp32 error of P grows ~8x).
-// K (the input dim) is split over 1, 2 or 4 waves when few experts are
-// active, so that small T still spreads over all CUs.
-#include <type_traits>
+// The input dim is split over the waves of a workgroup (two groups per wave
+// per pass) so each wave keeps its x slice in registers and re-reads only
+// weights; the partial sums meet in LDS.
+#include <algorithm>
 
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace mlxr_moe {
 namespace {
+
+// (experts x 16-channel blocks) from which the streaming kernel runs
+constexpr int64_t kStreamMinBlocks = 2048;
 
 // Reorder 8 consecutive bf16 x values to the code order that unpack4 emits:
 // element j of the fragment holds x[perm(j)], perm = 0,4,1,5,2,6,3,7.
@@ -70,162 +74,469 @@ __device__ __forceinline__ u32x4_t unpack8(uint32_t w0, uint32_t w1) {
   return r;
 }
 
-template <int BITS>
-struct GroupWords;
-template <>
-struct GroupWords<4> {
-  u32x2_t v;
-  __device__ __forceinline__ void load(const uint32_t* p, int g4) {
-    v = *reinterpret_cast<const u32x2_t*>(p + 2 * g4);
-  }
-  __device__ __forceinline__ u32x4_t step(int s) const {
-    return unpack4(s == 0 ? v.x : v.y);
-  }
-};
-template <>
-struct GroupWords<8> {
-  u32x4_t v;
-  __device__ __forceinline__ void load(const uint32_t* p, int g4) {
-    v = *reinterpret_cast<const u32x4_t*>(p + 4 * g4);
-  }
-  __device__ __forceinline__ u32x4_t step(int s) const {
-    return s == 0 ? unpack8(v.x, v.y) : unpack8(v.z, v.w);
-  }
+// One "step" of a wave is one 16-byte load per lane per row: at 4-bit two
+// adjacent quantisation groups (64 B of the row; lanes q = 0,1 hold the two
+// halves of the first group, q = 2,3 of the second), at 8-bit one group
+// (64 B; lane q holds bytes 16q..16q+15).  Each MFMA sum must cover a single
+// group (its own scale and bias), so at 4-bit the x operand exists twice per
+// step, zero on the lanes of the other group: xa feeds the first group's
+// sums, xb the second's, and the weight operand is shared.
+template <int NM, int SPW>
+struct StepBuf {
+  u32x4_t w[NM][SPW];
+  uint32_t s[NM][SPW];  // bf16 scales: 4-bit (first | second << 16), 8-bit g
+  uint32_t b[NM][SPW];  // bf16 biases, same packing
 };
 
-template <int BITS, bool GATED>
-__global__ __launch_bounds__(256) void qgemm_decode_kernel(QGemmArgs a,
-                                                           int ks) {
-  __shared__ f32x4_t red[4][2][64];
+// Scale or bias bits of one step: both groups at 4-bit (one u32 when
+// 4-byte aligned), the one group at 8-bit.
+__device__ __forceinline__ uint32_t load_sb(const uint16_t* p, bool pair,
+                                            bool two) {
+  if (pair) return *reinterpret_cast<const uint32_t*>(p);
+  return (uint32_t)p[0] | (two ? (uint32_t)p[1] << 16 : 0u);
+}
+
+// Loads of one 16-channel block: row `wrow` (this lane's channel), groups
+// [G0, G0 + mg) of this wave.  Nothing past the row's last group is read.
+template <int BITS, int NM, int SPW>
+__device__ __forceinline__ void load_steps(StepBuf<NM, SPW>& bb,
+                                           const QGemmArgs& a, int64_t wrow,
+                                           int groups, int G0, int mg, int q,
+                                           bool sb_pairs) {
+  constexpr int GPS = BITS == 4 ? 2 : 1;
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const QWeights& W = m == 0 ? a.w0 : a.w1;
+    const uint32_t* wr = W.w + wrow * groups * (2 * BITS);
+    const uint16_t* sr = W.scales + wrow * groups;
+    const uint16_t* br = W.biases + wrow * groups;
+#pragma unroll
+    for (int st = 0; st < SPW; ++st) {
+      const int g0 = G0 + GPS * st;  // first group of the step
+      bb.w[m][st] = u32x4_t{0u, 0u, 0u, 0u};
+      bb.s[m][st] = 0u;
+      bb.b[m][st] = 0u;
+      if (GPS * st < mg) {
+        if constexpr (BITS == 4) {
+          const int gl = g0 + (q >> 1);  // this lane's group
+          if (gl < G0 + mg)
+            bb.w[m][st] = *reinterpret_cast<const u32x4_t*>(
+                wr + gl * 8 + 4 * (q & 1));
+          const bool two = g0 + 1 < G0 + mg;
+          bb.s[m][st] = load_sb(sr + g0, sb_pairs && two, two);
+          bb.b[m][st] = load_sb(br + g0, sb_pairs && two, two);
+        } else {
+          bb.w[m][st] =
+              *reinterpret_cast<const u32x4_t*>(wr + g0 * 16 + 4 * q);
+          bb.s[m][st] = sr[g0];
+          bb.b[m][st] = br[g0];
+        }
+      }
+    }
+  }
+}
+
+// sc * P + cb * X terms of one group from its bf16 scale and bias bits.
+template <int BITS>
+__device__ __forceinline__ void group_terms(uint32_t s16, uint32_t b16,
+                                            float& sc, float& cb) {
+  const float sf = __uint_as_float(s16 << 16);
+  const float bf = __uint_as_float(b16 << 16);
+  if constexpr (BITS == 4) {
+    sc = 16.0f * sf;
+    cb = __builtin_fmaf(-16.0f, sf, bf);
+  } else {
+    sc = sf;
+    cb = bf;
+  }
+}
+
+// Decode grouped GEMM.  One workgroup = kw waves = one (active expert, tile
+// of CB*16 output channels).  Wave w owns SPW steps of the input dim per
+// pass; passes repeat until the kw waves have covered it.  Per 16-token chunk
+// of the expert's rows a wave issues the weight loads of the tile's first
+// block, loads its slice of x into registers (MFMA A operand) with the
+// per-group token sums X, then multiplies block i while the loads of block
+// i+1 are in flight.  The kw partial sums of each block meet in LDS and one
+// wave writes the block.  Lane l: token / channel l%16, quarter l/16.
+template <int BITS, bool GATED, int SPW, int CB>
+__global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
+                                                            int tiles_n) {
+  extern __shared__ f32x4_t red[];  // [kw][CB][NM][64]
+  constexpr int NM = GATED ? 2 : 1;
+  constexpr int GPS = BITS == 4 ? 2 : 1;
+  constexpr int GW = SPW * GPS;          // groups per wave per pass
+  constexpr int NX = BITS == 4 ? 4 : 2;  // x fragments per step
+  const int kw = blockDim.x >> 6;
+  const int item = blockIdx.x;
+  const int ai = item / tiles_n, tile = item - ai * tiles_n;
   const int n_act = *a.num_active;
-  if ((int)blockIdx.y >= n_act) return;
-  const int e = a.active[blockIdx.y];
-  const int row0 = a.offsets[e];
-  const int rows = a.offsets[e + 1] - row0;
+  const int4 wk = reinterpret_cast<const int4*>(a.work)[ai];
+  if (ai >= n_act) return;
+  const int e = wk.x, row0 = wk.y, rows = wk.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int cw = 4 / ks;
-  const int ct = wave / ks, kslice = wave - ct * ks;
-  const int ch = (blockIdx.x * cw + ct) * 16 + (lane & 15);
-  const int g4 = lane >> 4;
+  const int c = lane & 15, q = lane >> 4;
   const int groups = a.K >> 6;
-  const int gps = groups / ks;
-  const int G0 = kslice * gps, G1 = G0 + gps;
-  constexpr int WPG = 2 * BITS;  // packed words per row per group
-  const int64_t wrow = (int64_t)e * a.N + ch;
-  const uint32_t* wp0 = a.w0.w + wrow * groups * WPG;
-  const uint16_t* sp0 = a.w0.scales + wrow * groups;
-  const uint16_t* bp0 = a.w0.biases + wrow * groups;
-  const uint32_t* wp1 = GATED ? a.w1.w + wrow * groups * WPG : nullptr;
-  const uint16_t* sp1 = GATED ? a.w1.scales + wrow * groups : nullptr;
-  const uint16_t* bp1 = GATED ? a.w1.biases + wrow * groups : nullptr;
+  const int per_pass = kw * GW;
+  const int passes = (groups + per_pass - 1) / per_pass;
+  const bool sb_pairs = (groups & 1) == 0;  // steps start on even groups
   const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  const u32x4_t zq = {0u, 0u, 0u, 0u};
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  const int64_t wrow0 = (int64_t)e * a.N + (int64_t)tile * CB * 16 + c;
 
   for (int tt = 0; tt < rows; tt += 16) {
-    const int tok = tt + (lane & 15);
+    const int tok = tt + c;
     const bool tv = tok < rows;
     int64_t xrow = 0;
     if (tv) {
       const int slot = row0 + tok;
       xrow = a.row_map ? a.row_map[slot] / a.row_div : slot;
     }
-    const uint16_t* xr = a.x + xrow * a.x_ld + 16 * g4;
-    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f};
-    f32x4_t acc1 = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[CB][NM];
+#pragma unroll
+    for (int bi = 0; bi < CB; ++bi)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[bi][m] = zero;
 
-    auto run = [&](auto U_tag, int G) {
-      constexpr int U = decltype(U_tag)::value;
-      u32x4_t xa[U][2];
-      GroupWords<BITS> q0[U], q1[U];
-      uint16_t s0[U], b0[U], s1[U], b1[U];
+    for (int pass = 0; pass < passes; ++pass) {
+      const int G0 = pass * per_pass + wave * GW;
+      const int mg = max(0, min(GW, groups - G0));
+      StepBuf<NM, SPW> buf[CB > 1 ? 2 : 1];
+      load_steps<BITS, NM, SPW>(buf[0], a, wrow0, groups, G0, mg, q,
+                                sb_pairs);
+      // x slice (A operand) and the per-group sums X
+      bf16x8_t xa[SPW][NX], xb[SPW][NX];
+      f32x4_t XA[SPW], XB[SPW];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        q0[u].load(wp0 + (G + u) * WPG, g4);
-        s0[u] = sp0[G + u];
-        b0[u] = bp0[G + u];
-        if constexpr (GATED) {
-          q1[u].load(wp1 + (G + u) * WPG, g4);
-          s1[u] = sp1[G + u];
-          b1[u] = bp1[G + u];
-        }
-        if (tv) {
-          xa[u][0] = *reinterpret_cast<const u32x4_t*>(xr + 64 * (G + u));
-          xa[u][1] = *reinterpret_cast<const u32x4_t*>(xr + 64 * (G + u) + 8);
-        } else {
-          xa[u][0] = u32x4_t{0u, 0u, 0u, 0u};
-          xa[u][1] = u32x4_t{0u, 0u, 0u, 0u};
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        bf16x8_t A0, A1;
+      for (int st = 0; st < SPW; ++st) {
+        const int g0 = G0 + GPS * st;
         if constexpr (BITS == 4) {
-          A0 = as_bf16x8(perm4(xa[u][0]));
-          A1 = as_bf16x8(perm4(xa[u][1]));
+          const int gl = g0 + (q >> 1);
+          const bool in = tv && GPS * st < mg && gl < G0 + mg;
+          const uint16_t* xr = a.x + xrow * a.x_ld + 64 * gl + 32 * (q & 1);
+#pragma unroll
+          for (int i = 0; i < NX; ++i) {
+            u32x4_t v = zq;
+            if (in) v = *reinterpret_cast<const u32x4_t*>(xr + 8 * i);
+            v = perm4(v);
+            xa[st][i] = as_bf16x8((q >> 1) ? zq : v);
+            xb[st][i] = as_bf16x8((q >> 1) ? v : zq);
+          }
         } else {
-          A0 = as_bf16x8(xa[u][0]);
-          A1 = as_bf16x8(xa[u][1]);
-        }
-        const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-        f32x4_t X = mfma16x16x32(A0, as_bf16x8(ones), zero);
-        X = mfma16x16x32(A1, as_bf16x8(ones), X);
-        f32x4_t P0 = mfma16x16x32(A0, as_bf16x8(q0[u].step(0)), zero);
-        P0 = mfma16x16x32(A1, as_bf16x8(q0[u].step(1)), P0);
-        const float s0f = bf16_to_f32(s0[u]);
-        const float bi0 = bf16_to_f32(b0[u]);
-        const float sc0 = BITS == 4 ? 16.0f * s0f : s0f;
-        const float c0 = BITS == 4 ? __builtin_fmaf(-16.0f, s0f, bi0) : bi0;
+          const bool in = tv && st < mg;
+          const uint16_t* xr = a.x + xrow * a.x_ld + 64 * g0 + 16 * q;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc0[r] = __builtin_fmaf(sc0, P0[r], __builtin_fmaf(c0, X[r], acc0[r]));
-        if constexpr (GATED) {
-          f32x4_t P1 = mfma16x16x32(A0, as_bf16x8(q1[u].step(0)), zero);
-          P1 = mfma16x16x32(A1, as_bf16x8(q1[u].step(1)), P1);
-          const float s1f = bf16_to_f32(s1[u]);
-          const float bi1 = bf16_to_f32(b1[u]);
-          const float sc1 = BITS == 4 ? 16.0f * s1f : s1f;
-          const float c1 = BITS == 4 ? __builtin_fmaf(-16.0f, s1f, bi1) : bi1;
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc1[r] =
-                __builtin_fmaf(sc1, P1[r], __builtin_fmaf(c1, X[r], acc1[r]));
+          for (int i = 0; i < NX; ++i) {
+            u32x4_t v = zq;
+            if (in) v = *reinterpret_cast<const u32x4_t*>(xr + 8 * i);
+            xa[st][i] = as_bf16x8(v);
+          }
         }
       }
-    };
-    int G = G0;
-    for (; G + 4 <= G1; G += 4)
-      run(std::integral_constant<int, 4>{}, G);
-    for (; G < G1; ++G) run(std::integral_constant<int, 1>{}, G);
-
-    if (ks > 1) {
-      red[wave][0][lane] = acc0;
-      if constexpr (GATED) red[wave][1][lane] = acc1;
-      __syncthreads();
-      if (kslice == 0) {
-        for (int q = 1; q < ks; ++q) {
-          acc0 += red[wave + q][0][lane];
-          if constexpr (GATED) acc1 += red[wave + q][1][lane];
+#pragma unroll
+      for (int st = 0; st < SPW; ++st) {
+        XA[st] = zero;
+        XB[st] = zero;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+          XA[st] = mfma16x16x32(xa[st][i], as_bf16x8(ones), XA[st]);
+          if constexpr (BITS == 4)
+            XB[st] = mfma16x16x32(xb[st][i], as_bf16x8(ones), XB[st]);
         }
       }
-      __syncthreads();
+#pragma unroll
+      for (int bi = 0; bi < CB; ++bi) {
+        if (bi + 1 < CB)
+          load_steps<BITS, NM, SPW>(buf[(bi + 1) & 1], a,
+                                    wrow0 + (bi + 1) * 16, groups, G0, mg, q,
+                                    sb_pairs);
+        const StepBuf<NM, SPW>& cur = buf[bi & 1];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          f32x4_t ac = acc[bi][m];
+#pragma unroll
+          for (int st = 0; st < SPW; ++st) {
+            if (GPS * st < mg) {
+              const u32x4_t wv = cur.w[m][st];
+              if constexpr (BITS == 4) {
+                f32x4_t PA = zero, PB = zero;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                  const bf16x8_t u = as_bf16x8(unpack4(wv[i]));
+                  PA = mfma16x16x32(xa[st][i], u, PA);
+                  PB = mfma16x16x32(xb[st][i], u, PB);
+                }
+                float sA, cA, sB, cB;
+                group_terms<4>(cur.s[m][st] & 0xffffu,
+                               cur.b[m][st] & 0xffffu, sA, cA);
+                group_terms<4>(cur.s[m][st] >> 16, cur.b[m][st] >> 16, sB,
+                               cB);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  ac[r] = __builtin_fmaf(
+                      sA, PA[r], __builtin_fmaf(cA, XA[st][r], ac[r]));
+                  ac[r] = __builtin_fmaf(
+                      sB, PB[r], __builtin_fmaf(cB, XB[st][r], ac[r]));
+                }
+              } else {
+                f32x4_t P = mfma16x16x32(
+                    xa[st][0], as_bf16x8(unpack8(wv.x, wv.y)), zero);
+                P = mfma16x16x32(xa[st][1], as_bf16x8(unpack8(wv.z, wv.w)),
+                                 P);
+                float sc, cb;
+                group_terms<8>(cur.s[m][st], cur.b[m][st], sc, cb);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  ac[r] = __builtin_fmaf(
+                      sc, P[r], __builtin_fmaf(cb, XA[st][r], ac[r]));
+              }
+            }
+          }
+          acc[bi][m] = ac;
+        }
+      }
     }
-    if (kslice == 0) {
+#pragma unroll
+    for (int bi = 0; bi < CB; ++bi)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+        red[((wave * CB + bi) * NM + m) * 64 + lane] = acc[bi][m];
+    __syncthreads();
+    // block bi is summed and written by wave bi % kw
+    for (int bi = wave; bi < CB; bi += kw) {
+      f32x4_t s0 = zero, s1 = zero;
+      for (int w = 0; w < kw; ++w) {
+        s0 += red[((w * CB + bi) * NM) * 64 + lane];
+        if constexpr (GATED) s1 += red[((w * CB + bi) * NM + 1) * 64 + lane];
+      }
+      const int ch = (tile * CB + bi) * 16 + c;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = tt + 4 * g4 + r;
+        const int t = tt + 4 * q + r;
         if (t < rows) {
           const int slot = row0 + t;
           if constexpr (GATED) {
-            const uint16_t v =
-                swiglu_bf16(bf16_round(acc0[r]), bf16_round(acc1[r]));
-            a.out[(int64_t)slot * a.out_ld + ch] = v;
+            a.out[(int64_t)slot * a.out_ld + ch] =
+                swiglu_bf16(bf16_round(s0[r]), bf16_round(s1[r]));
           } else {
             const int64_t orow = a.out_map ? a.out_map[slot] : slot;
-            a.out[orow * a.out_ld + ch] = f32_to_bf16(acc0[r]);
+            a.out[orow * a.out_ld + ch] = f32_to_bf16(s0[r]);
           }
         }
       }
     }
+    __syncthreads();
   }
+}
+
+// Streaming decode GEMM for many (expert, row-tile) items.  One workgroup =
+// `waves` waves = one (active expert, tile of waves*16 output channels); wave
+// w owns one 16-channel block over the whole input dim, so no partial sums
+// cross waves.  Per chunk of up to TT of the expert's tokens the workgroup
+// stages x (bf16, in the MFMA operand order) and the per-group token sums X
+// in LDS once; each wave then streams its block's packed weights with D
+// super-steps of loads in flight (a register ring) and reads x from LDS.
+//
+// Block-diagonal MFMA: the 16 rows of the A operand are TT tokens x GG
+// groups (GG = 16 / TT).  Lane quarter q (l/16) supplies the codes of group
+// q*GG/4 of the super-step, and the x operand row (group j, token t) is
+// non-zero only on the lanes of group j, so one v_mfma_f32_16x16x32_bf16
+// yields the partial sums of GG groups at once and every lane applies the
+// scale and bias of a single group.  A super-step covers GG groups; each
+// lane loads 16*GG codes of its group (16 B per load).  Lanes that feed
+// zeros read a zero block in LDS.  The GG partial sums of a token meet by
+// cross-lane adds at the end.
+template <int BITS, bool GATED, int TT, int D>
+__device__ __forceinline__ void stream_body(const QGemmArgs& a, int tiles_n,
+                                            char* smem) {
+  constexpr int NM = GATED ? 2 : 1;
+  constexpr int GG = 16 / TT;               // groups per MFMA
+  constexpr int LPG = 4 / GG;               // lane quarters per group
+  constexpr int CPL = 64 / LPG;             // codes per lane per super-step
+  constexpr int NL = CPL * BITS / 128;      // 16-byte loads per lane
+  constexpr int NMF = CPL / 8;              // MFMAs per super-step
+  const int waves = blockDim.x >> 6;
+  const int item = blockIdx.x;
+  const int ai = item / tiles_n, tile = item - ai * tiles_n;
+  const int n_act = *a.num_active;
+  const int4 wk = reinterpret_cast<const int4*>(a.work)[ai];
+  if (ai >= n_act) return;
+  const int e = wk.x, row0 = wk.y, rows = wk.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, q = lane >> 4;
+  const int gq = q / LPG, sq = q % LPG;     // this lane's group, its part
+  const int K = a.K, groups = K >> 6;
+  const int ssteps = (groups + GG - 1) / GG;
+  // LDS: x chunk [TT][K + 8] bf16 (rows padded 16 B), 16 B zero block,
+  // X [groups][TT] f32
+  const int xs = K + 8;
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);
+  char* zero_blk = smem + (size_t)TT * xs * 2;
+  float* Xl = reinterpret_cast<float*>(zero_blk + 16);
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  const int64_t wrow = (int64_t)e * a.N + ((int64_t)tile * waves + wave) * 16 + n;
+  const int ch = (tile * waves + wave) * 16 + n;
+  // A operand row of this lane: (group m / TT, token m % TT), m = l % 16
+  const int arow_g = n / TT, arow_t = n % TT;
+
+  struct Ring {
+    u32x4_t w[NM][NL];
+    uint32_t s[NM], b[NM];
+  };
+  auto load = [&](Ring& r, int ss) {
+    const int g = ss * GG + gq;  // this lane's group
+    const bool ok = g < groups;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const QWeights& W = m == 0 ? a.w0 : a.w1;
+      const uint32_t* wp = W.w + wrow * groups * (2 * BITS) + g * (2 * BITS) +
+                           sq * (CPL * BITS / 32);
+#pragma unroll
+      for (int i = 0; i < NL; ++i)
+        r.w[m][i] = ok ? reinterpret_cast<const u32x4_t*>(wp)[i]
+                       : u32x4_t{0u, 0u, 0u, 0u};
+      r.s[m] = ok ? W.scales[wrow * groups + g] : 0u;
+      r.b[m] = ok ? W.biases[wrow * groups + g] : 0u;
+    }
+  };
+
+  for (int tt = 0; tt < rows; tt += TT) {
+    const int nt = min(TT, rows - tt);
+    Ring ring[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      if (j < ssteps) load(ring[j], j);
+    // stage x: 8 elements (16 B) per thread and iteration
+    const int per_row = K >> 3;
+    for (int i = threadIdx.x; i < TT * per_row; i += blockDim.x) {
+      const int t = i / per_row, k8 = i - t * per_row;
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (t < nt) {
+        const int slot = row0 + tt + t;
+        const int64_t xrow = a.row_map ? a.row_map[slot] / a.row_div : slot;
+        v = *reinterpret_cast<const u32x4_t*>(a.x + xrow * a.x_ld + 8 * k8);
+        if constexpr (BITS == 4) v = perm4(v);
+      }
+      *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = v;
+    }
+    if (threadIdx.x == 0)
+      *reinterpret_cast<u32x4_t*>(zero_blk) = u32x4_t{0u, 0u, 0u, 0u};
+    __syncthreads();
+    for (int i = threadIdx.x; i < groups * TT; i += blockDim.x) {
+      const int g = i / TT, t = i - g * TT;
+      float sx = 0.0f;
+      const uint16_t* xp = xl + (size_t)t * xs + 64 * g;
+      for (int k = 0; k < 64; k += 2) {
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(xp + k);
+        sx += __uint_as_float(u << 16) + __uint_as_float(u & 0xffff0000u);
+      }
+      Xl[g * TT + t] = sx;
+    }
+    __syncthreads();
+
+    f32x4_t acc[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) acc[m] = zero;
+    // x operand source of this lane: its row's token chunk in its group's
+    // codes, or the zero block off the diagonal / past the tokens
+    const bool diag = arow_g == gq && arow_t < nt;
+    const char* xsrc = smem + ((size_t)arow_t * xs + sq * CPL) * 2;
+    for (int ss0 = 0; ss0 < ssteps; ss0 += D) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        const int ss = ss0 + j;
+        if (ss < ssteps) {
+          const Ring cur = ring[j];
+          if (ss + D < ssteps) load(ring[j], ss + D);
+          const int g = ss * GG + gq;
+          const bool on = diag && g < groups;
+          const char* xp = on ? xsrc + (size_t)(64 * g) * 2 : zero_blk;
+          const int xstep = on ? 16 : 0;
+          bf16x8_t xa[NMF];
+#pragma unroll
+          for (int i = 0; i < NMF; ++i)
+            xa[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xp + xstep * i));
+          // X of this lane's output rows: group (4q+r)/TT, tokens (4q+r)%TT
+          const int og = ss * GG + (4 * q) / TT;
+          const f32x4_t X = og < groups
+              ? *reinterpret_cast<const f32x4_t*>(Xl + og * TT + (4 * q) % TT)
+              : zero;
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            f32x4_t P = zero;
+#pragma unroll
+            for (int i = 0; i < NMF; ++i) {
+              u32x4_t u;
+              if constexpr (BITS == 4) {
+                u = unpack4(cur.w[m][i / 4][i % 4]);
+              } else {
+                const u32x4_t wv = cur.w[m][i / 2];
+                u = (i & 1) ? unpack8(wv.z, wv.w) : unpack8(wv.x, wv.y);
+              }
+              P = mfma16x16x32(xa[i], as_bf16x8(u), P);
+            }
+            // scale/bias of this lane's output group (4q)/TT, loaded by the
+            // first lane quarter of that group
+            uint32_t sb = cur.s[m], bb = cur.b[m];
+            if constexpr (TT != 4) {
+              const int src_lane = (((4 * q) / TT) * LPG) * 16 + n;
+              sb = (uint32_t)__shfl((int)sb, src_lane, 64);
+              bb = (uint32_t)__shfl((int)bb, src_lane, 64);
+            }
+            float sc, cb;
+            group_terms<BITS>(sb, bb, sc, cb);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[m][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(cb, X[r], acc[m][r]));
+          }
+        }
+      }
+    }
+    // the GG group partials of a token sit on lanes 16*(TT/4) apart
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = acc[m][r];
+        if constexpr (TT == 4) v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        acc[m][r] = v;
+      }
+    }
+    // lanes q < TT/4 hold tokens 4q..4q+3
+    if (q < TT / 4) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 4 * q + r;
+        if (t < nt) {
+          const int slot = row0 + tt + t;
+          if constexpr (GATED) {
+            a.out[(int64_t)slot * a.out_ld + ch] =
+                swiglu_bf16(bf16_round(acc[0][r]), bf16_round(acc[1][r]));
+          } else {
+            const int64_t orow = a.out_map ? a.out_map[slot] : slot;
+            a.out[orow * a.out_ld + ch] = f32_to_bf16(acc[0][r]);
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next chunk overwrites the LDS tiles
+  }
+}
+
+// Tokens per pass follow the expert's row count: 4 (one pass for up to 4
+// rows, GG = 4) or 8 (GG = 2).  LDS is sized for 8.
+template <int BITS, bool GATED, int D>
+__global__ __launch_bounds__(256) void qgemm_stream_kernel(QGemmArgs a,
+                                                           int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int ai = blockIdx.x / tiles_n;
+  const int rows = reinterpret_cast<const int4*>(a.work)[ai].z;
+  if (rows <= 4)
+    stream_body<BITS, GATED, 4, D>(a, tiles_n, smem);
+  else
+    stream_body<BITS, GATED, 8, D>(a, tiles_n, smem);
 }
 
 }  // namespace
@@ -236,19 +547,77 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   (void)total_rows;
   if (max_active <= 0) return hipSuccess;
   const int groups = a.K / 64;
-  // Workgroups at ks = 1: one per (active expert, 64 output channels).
-  const int64_t wg1 = max_active * (a.N / 64);
-  int ks = 1;
-  if (wg1 < 1024 && groups % 2 == 0 && a.N % 32 == 0) ks = 2;
-  if (wg1 * 2 < 1024 && groups % 4 == 0 && a.N % 16 == 0) ks = 4;
-  const int cw = 4 / ks;
-  const dim3 grid((unsigned)(a.N / (16 * cw)), (unsigned)max_active);
+  // Many (expert, block) items: the streaming kernel (one block per wave,
+  // x in LDS, a ring of weight loads).  Few: the split-K kernel below, which
+  // spreads each block over up to 16 waves.
+  if (max_active * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0) {
+    constexpr int kWaves = 4, kMaxTT = 8;
+    const int tiles_n = a.N / (16 * kWaves);
+    const size_t lds = (size_t)kMaxTT * (a.K + 8) * 2 + 16 +
+                       (size_t)groups * kMaxTT * sizeof(float);
+    const dim3 grid((unsigned)(max_active * tiles_n));
+    ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
+#define MLXR_QS(B, G, D) \
+  qgemm_stream_kernel<B, G, D><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n)
+    if (a.bits == 4) {
+      if (a.gated)
+        MLXR_QS(4, true, 3);
+      else
+        MLXR_QS(4, false, 3);
+    } else {
+      if (a.gated)
+        MLXR_QS(8, true, 2);
+      else
+        MLXR_QS(8, false, 2);
+    }
+#undef MLXR_QS
+    return hipGetLastError();
+  }
+  // waves along the input dim: two groups each per pass (one step at 4-bit,
+  // two at 8-bit), up to 16 waves; more groups take several passes
+  constexpr int kGroupsPerWave = 2;
+  const int kw = std::min(16, (groups + kGroupsPerWave - 1) / kGroupsPerWave);
+  // channel blocks per workgroup: as many as keep >= ~1024 workgroups, with
+  // the partial sums of the blocks within 64 KB of LDS
+  const int nm = a.gated ? 2 : 1;
+  const int nblk = a.N / 16;
+  int cb = 1;
+  // (the gated kernel keeps one block: two would spill under the 128-VGPR
+  // budget of 16-wave workgroups)
+  for (int c = 4; c > 1 && !a.gated; c >>= 1)
+    if (nblk % c == 0 && max_active * (nblk / c) >= 1024 &&
+        kw * c * nm <= 64) {
+      cb = c;
+      break;
+    }
+  const int tiles_n = nblk / cb;
+  const size_t lds = (size_t)kw * cb * nm * 64 * sizeof(f32x4_t);
+  const dim3 grid((unsigned)(max_active * tiles_n));
+  const dim3 block((unsigned)(64 * kw));
   ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
-#define MLXR_QG(B, G) qgemm_decode_kernel<B, G><<<grid, 256, 0, s>>>(a, ks)
-  if (a.bits == 4)
-    a.gated ? MLXR_QG(4, true) : MLXR_QG(4, false);
-  else
-    a.gated ? MLXR_QG(8, true) : MLXR_QG(8, false);
+#define MLXR_QG(B, G, SPW)                                                  \
+  do {                                                                      \
+    if (cb == 4)                                                            \
+      qgemm_decode_kernel<B, G, SPW, 4>                                     \
+          <<<grid, block, lds, s>>>(a, tiles_n);                            \
+    else if (cb == 2)                                                       \
+      qgemm_decode_kernel<B, G, SPW, 2>                                     \
+          <<<grid, block, lds, s>>>(a, tiles_n);                            \
+    else                                                                    \
+      qgemm_decode_kernel<B, G, SPW, 1>                                     \
+          <<<grid, block, lds, s>>>(a, tiles_n);                            \
+  } while (0)
+  if (a.bits == 4) {
+    if (a.gated)
+      qgemm_decode_kernel<4, true, 1, 1><<<grid, block, lds, s>>>(a, tiles_n);
+    else
+      MLXR_QG(4, false, 1);
+  } else {
+    if (a.gated)
+      qgemm_decode_kernel<8, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n);
+    else
+      MLXR_QG(8, false, 2);
+  }
 #undef MLXR_QG
   return hipGetLastError();
 }

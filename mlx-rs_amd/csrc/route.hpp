@@ -1,0 +1,217 @@
+// Device routines shared by the router and the dispatch kernels:
+//   wave_topk       top-K of one token's logits on one wave (radix select on
+//                   order-preserving keys, ballots only), softmax and the
+//                   renormalised top-K weights;
+//   block_dispatch  stable counting sort of up to 1024 expert ids held in
+//                   LDS by one 1024-thread workgroup.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxr_moe {
+
+// Order-preserving key of a float: larger float, larger key; -0 == +0.
+__device__ __forceinline__ uint32_t float_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) == 0u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Per-wave scratch for wave_topk: the K selected (key, id) pairs.
+struct TopkScratch {
+  uint32_t key[64];
+  int32_t id[64];
+};
+
+// Top-K of logits[e], e < E, for one token, selected on the logits (softmax
+// is monotone): descending, ties to the lower expert id -- the selection of
+// argpartition(-K) plus a deterministic order inside the partition
+// (crates/mlxr/src/ops/sort.rs:186-226, whose order is undefined).  Then
+// softmax over all E (max-subtracted, lane sums in expert order e = l + 64s,
+// butterfly across lanes) and w_k = p_k / sum_k p_k (k in order).
+// Returns on lane k < K its expert id (*out_id) and weight (*out_w).
+template <int SLOTS>
+__device__ void wave_topk(const float* __restrict__ logits, int E, int K,
+                          TopkScratch* sc, int* out_id, float* out_w) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = (1ull << lane) - 1ull;
+  float v[SLOTS];
+  uint32_t key[SLOTS];
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const int e = lane + 64 * s;
+    v[s] = e < E ? logits[e] : 0.0f;
+    key[s] = e < E ? float_key(v[s]) : 0u;  // 0: below every real key
+  }
+  // theta = largest key with at least K keys >= theta (the K-th largest)
+  uint32_t theta = 0u;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = theta | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) cnt += __popcll(__ballot(key[s] >= cand));
+    if (cnt >= K) theta = cand;
+  }
+  // keys above theta, then the lowest-id keys equal to theta
+  int left = K;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) left -= __popcll(__ballot(key[s] > theta));
+  int base = 0;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const uint64_t eq = __ballot(key[s] == theta);
+    const int take = min(__popcll(eq), left);
+    left -= take;
+    const bool sel =
+        key[s] > theta || (key[s] == theta && __popcll(eq & below) < take);
+    const uint64_t sm = __ballot(sel);
+    if (sel) {
+      const int pos = base + __popcll(sm & below);
+      sc->key[pos] = key[s];
+      sc->id[pos] = lane + 64 * s;
+    }
+    base += __popcll(sm);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // rank of each selected pair: larger key first, then lower id
+  int my_id = 0, rank = 0;
+  uint32_t my_key = 0u;
+  if (lane < K) {
+    my_key = sc->key[lane];
+    my_id = sc->id[lane];
+    for (int j = 0; j < K; ++j) {
+      const uint32_t kj = sc->key[j];
+      const int ij = sc->id[j];
+      rank += (kj > my_key || (kj == my_key && ij < my_id)) ? 1 : 0;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < K) sc->id[rank] = my_id;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int id = lane < K ? sc->id[lane] : 0;
+  const float m = logits[sc->id[0]];
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s)
+    if (lane + 64 * s < E) acc += expf(v[s] - m);
+  const float S = wave_sum_butterfly(acc);
+  const float p = lane < K ? expf(logits[id] - m) / S : 0.0f;
+  float psum = 0.0f;
+  for (int k = 0; k < K; ++k) psum += __shfl(p, k, 64);
+  *out_id = id;
+  *out_w = p / psum;
+}
+
+// LDS of block_dispatch: per-wave match counts, scan scratch, offsets.
+struct DispatchScratch {
+  uint16_t tab[kDispatchBlock / 64][kMaxExperts];
+  int wsum[kDispatchBlock / 64 + 1];
+  int off[kMaxExperts];
+};
+
+// Exclusive scan of one int per thread over a 1024-thread workgroup.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* total,
+                                                    int* wsum) {
+  constexpr int kWaves = kDispatchBlock / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += u;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      const int c = wsum[w];
+      wsum[w] = run;
+      run += c;
+    }
+    wsum[kWaves] = run;
+  }
+  __syncthreads();
+  const int ex = wsum[wave] + inc - v;
+  *total = wsum[kWaves];
+  __syncthreads();
+  return ex;
+}
+
+// Stable counting sort of ids[0..n) (n <= 1024, read by thread i) by expert
+// in [0, E): counts, offsets, the active-expert list, the M-tile list and
+// sorted/inv, exactly the permutation of a stable argsort.  Ids of -1 are
+// left out silently; other ids outside [0, E) are left out and flag
+// *status.  Every thread of the 1024-thread workgroup must call it.
+__device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
+                               const DispatchBuffers& b, DispatchScratch* ls) {
+  constexpr int kWaves = kDispatchBlock / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < kWaves * E; i += kDispatchBlock)
+    ls->tab[i / E][i % E] = 0;
+  __syncthreads();
+  const bool valid = tid < n;
+  const int id = valid ? id_in : -1;
+  const bool ok = valid && id >= 0 && id < E;
+  if (valid && !ok && id != -1) *b.status = 1;
+  uint64_t match = __ballot(ok);
+  const int id_bits = E > 1 ? 32 - __clz(E - 1) : 0;
+  for (int bit = 0; bit < id_bits; ++bit) {
+    const bool on = ok && ((id >> bit) & 1);
+    const uint64_t bal = __ballot(on);
+    match &= on ? bal : ~bal;
+  }
+  const int r = __popcll(match & ((1ull << lane) - 1ull));
+  if (ok && r == 0) ls->tab[wave][id] = (uint16_t)__popcll(match);
+  __syncthreads();
+  int cnt = 0;
+  if (tid < E) {
+    for (int w = 0; w < kWaves; ++w) {
+      const int c = ls->tab[w][tid];
+      ls->tab[w][tid] = (uint16_t)cnt;
+      cnt += c;
+    }
+  }
+  int total;
+  const int off = block_exclusive_scan(cnt, &total, ls->wsum);
+  if (tid < E) {
+    b.counts[tid] = cnt;
+    b.offsets[tid] = off;
+    ls->off[tid] = off;
+  }
+  if (tid == 0) b.offsets[E] = total;
+  const int has = (tid < E && cnt > 0) ? 1 : 0;
+  int n_active;
+  const int apos = block_exclusive_scan(has, &n_active, ls->wsum);
+  if (has) {
+    b.active[apos] = tid;
+    b.work[4 * apos] = tid;
+    b.work[4 * apos + 1] = off;
+    b.work[4 * apos + 2] = cnt;
+    b.work[4 * apos + 3] = 0;
+  }
+  if (tid == 0) *b.num_active = n_active;
+  const int nt = tid < E ? (cnt + tile_rows - 1) / tile_rows : 0;
+  int n_tiles;
+  const int tpos = block_exclusive_scan(nt, &n_tiles, ls->wsum);
+  for (int j = 0; j < nt; ++j) {
+    b.tiles[2 * (tpos + j)] = tid;
+    b.tiles[2 * (tpos + j) + 1] = off + j * tile_rows;
+  }
+  if (tid == 0) *b.num_tiles = n_tiles;
+  __syncthreads();
+  if (ok) {
+    const int pos = ls->off[id] + ls->tab[wave][id] + r;
+    b.sorted[pos] = tid;
+    b.inv[tid] = pos;
+  }
+}
+
+}  // namespace mlxr_moe

@@ -16,13 +16,15 @@
 // ties to the lower expert id.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "route.hpp"
 
 namespace mlxr_moe {
 namespace {
 
 // One wave computes EB logit columns for up to TB tokens of a token block.
-// Router weights stream as float4 (16 B per lane), x as 4 bf16 (8 B).
-template <int EB, int TB>
+// Router weights stream as float4 (16 B per lane), x as 4 bf16 (8 B); the
+// loads of U consecutive 256-wide steps are issued before their FMAs.
+template <int EB, int TB, int U>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, int T, int d, const float* __restrict__ w,
     const float* __restrict__ bias, int E, const float* __restrict__ w_extra,
@@ -41,34 +43,49 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     const int e = e0 + q;
     wrow[q] = e < E ? w + (int64_t)e * d : (e == E ? w_extra : nullptr);
   }
+  const uint16_t* xrow[TB];
+#pragma unroll
+  for (int tt = 0; tt < TB; ++tt)
+    xrow[tt] = x + (int64_t)(t0 + (tt < nt ? tt : 0)) * d;
   float acc[EB][TB];
 #pragma unroll
   for (int q = 0; q < EB; ++q)
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt) acc[q][tt] = 0.0f;
 
-  for (int j = 4 * lane; j < d; j += 256) {
-    float4 wv[EB];
+  const int steps = (d + 255) / 256;
+  for (int i0 = 0; i0 < steps; i0 += U) {
+    float4 wv[U][EB];
+    uint2 xv[U][TB];
 #pragma unroll
-    for (int q = 0; q < EB; ++q)
-      wv[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + j)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < U; ++u) {
+      const int j = 4 * lane + 256 * (i0 + u);
+      const bool in = j < d;
 #pragma unroll
-    for (int tt = 0; tt < TB; ++tt) {
-      if (tt < nt) {
-        const uint2 xv = *reinterpret_cast<const uint2*>(
-            x + (int64_t)(t0 + tt) * d + j);
-        const float x0 = __uint_as_float(xv.x << 16);
-        const float x1 = __uint_as_float(xv.x & 0xffff0000u);
-        const float x2 = __uint_as_float(xv.y << 16);
-        const float x3 = __uint_as_float(xv.y & 0xffff0000u);
+      for (int q = 0; q < EB; ++q)
+        wv[u][q] = (in && wrow[q]) ? *reinterpret_cast<const float4*>(wrow[q] + j)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int tt = 0; tt < TB; ++tt)
+        xv[u][tt] = in ? *reinterpret_cast<const uint2*>(xrow[tt] + j)
+                       : make_uint2(0u, 0u);
+    }
+    // elements past d contribute fmaf(0, 0, acc) = acc exactly
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int tt = 0; tt < TB; ++tt) {
+        const float x0 = __uint_as_float(xv[u][tt].x << 16);
+        const float x1 = __uint_as_float(xv[u][tt].x & 0xffff0000u);
+        const float x2 = __uint_as_float(xv[u][tt].y << 16);
+        const float x3 = __uint_as_float(xv[u][tt].y & 0xffff0000u);
 #pragma unroll
         for (int q = 0; q < EB; ++q) {
           float a = acc[q][tt];
-          a = __builtin_fmaf(x0, wv[q].x, a);
-          a = __builtin_fmaf(x1, wv[q].y, a);
-          a = __builtin_fmaf(x2, wv[q].z, a);
-          a = __builtin_fmaf(x3, wv[q].w, a);
+          a = __builtin_fmaf(x0, wv[u][q].x, a);
+          a = __builtin_fmaf(x1, wv[u][q].y, a);
+          a = __builtin_fmaf(x2, wv[u][q].z, a);
+          a = __builtin_fmaf(x3, wv[u][q].w, a);
           acc[q][tt] = a;
         }
       }
@@ -78,74 +95,31 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   for (int q = 0; q < EB; ++q) {
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt) {
-      if (tt < nt) {
-        float v = wave_sum_butterfly(acc[q][tt]);
-        if (bias && e0 + q < E) v += bias[e0 + q];
-        if (lane == 0 && e0 + q < e_tot)
-          logits[(int64_t)(t0 + tt) * ld + e0 + q] = v;
-      }
+      float v = wave_sum_butterfly(acc[q][tt]);
+      if (bias && e0 + q < E) v += bias[e0 + q];
+      if (lane == 0 && e0 + q < e_tot && tt < nt)
+        logits[(int64_t)(t0 + tt) * ld + e0 + q] = v;
     }
   }
 }
 
-// One wave per token.  Lane l holds experts l + 64s.  Result k lives in
-// lane k until it is written.
+// One wave per token: top-K, softmax and renormalised weights (wave_topk).
+// Workgroup 0 also clears the workspace status word when given.
 template <int SLOTS>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, int64_t ld, int T, int E, int K,
-    int32_t* __restrict__ idx, float* __restrict__ wts) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* status) {
+  __shared__ TopkScratch sc[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (status && blockIdx.x == 0 && threadIdx.x == 0) *status = 0;
+  const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
-  float v[SLOTS];
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    const int e = lane + 64 * s;
-    v[s] = e < E ? logits[(int64_t)t * ld + e] : -INFINITY;
-  }
-  uint32_t taken = 0;
-  int my_idx = 0;
-  float my_val = 0.0f, m = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const int e = lane + 64 * s;
-      if (e < E && !((taken >> s) & 1u)) {
-        if (v[s] > bv || (v[s] == bv && e < bi)) {
-          bv = v[s];
-          bi = e;
-        }
-      }
-    }
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) {
-      const float ov = __shfl_xor(bv, msk, 64);
-      const int oi = __shfl_xor(bi, msk, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    if (lane == k) {
-      my_idx = bi;
-      my_val = bv;
-    }
-    if (k == 0) m = bv;
-  }
-  float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s)
-    if (lane + 64 * s < E) acc += expf(v[s] - m);
-  const float S = wave_sum_butterfly(acc);
-  const float p = lane < K ? expf(my_val - m) / S : 0.0f;
-  float psum = 0.0f;
-  for (int k = 0; k < K; ++k) psum += __shfl(p, k, 64);
+  int id;
+  float wt;
+  wave_topk<SLOTS>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
   if (lane < K) {
-    idx[(int64_t)t * K + lane] = my_idx;
-    wts[(int64_t)t * K + lane] = p / psum;
+    idx[(int64_t)t * K + lane] = id;
+    wts[(int64_t)t * K + lane] = wt;
   }
 }
 
@@ -219,32 +193,36 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 int64_t ld, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const int64_t e_tot = E + (w_extra ? 1 : 0);
-  // Few tokens: one logit column per wave so the 4*d*E bytes of router
-  // weights spread over E/4 workgroups.  Many tokens: 4 columns x 16
-  // tokens per wave for register reuse of both operands.
   ProfileScope prof("router_logits", s);
-  if (T <= 16) {
-    const dim3 grid((unsigned)((e_tot + 3) / 4), 1);
-    router_logits_kernel<1, 16><<<grid, 256, 0, s>>>(
-        x, (int)T, (int)d, w, bias, (int)E, w_extra, logits, ld);
-  } else {
-    const dim3 grid((unsigned)((e_tot + 15) / 16), (unsigned)((T + 15) / 16));
-    router_logits_kernel<4, 16><<<grid, 256, 0, s>>>(
-        x, (int)T, (int)d, w, bias, (int)E, w_extra, logits, ld);
-  }
+  // Enough waves to have every CU pulling router weights at small T, and
+  // register reuse of both operands (EB experts x TB tokens) at large T.
+#define MLXR_RL(EB, TB, U)                                                   \
+  router_logits_kernel<EB, TB, U>                                            \
+      <<<dim3((unsigned)((e_tot + 4 * EB - 1) / (4 * EB)),                   \
+              (unsigned)((T + TB - 1) / TB)),                                \
+         256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, w_extra, logits, ld)
+  if (T <= 2)
+    MLXR_RL(1, 1, 8);
+  else if (T <= 16)
+    MLXR_RL(1, 2, 8);
+  else if (T <= 256)
+    MLXR_RL(2, 4, 4);
+  else
+    MLXR_RL(4, 8, 2);
+#undef MLXR_RL
   return hipGetLastError();
 }
 
 hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
                               int64_t E, int64_t K, int32_t* idx, float* wts,
-                              hipStream_t s) {
+                              int32_t* status, hipStream_t s) {
   if (T == 0) return hipSuccess;
   ProfileScope prof("router_topk", s);
   const dim3 grid((unsigned)((T + 3) / 4));
   const int slots = (int)((E + 63) / 64);
 #define MLXR_TOPK(S)                                                     \
   router_topk_kernel<S><<<grid, 256, 0, s>>>(logits, ld, (int)T, (int)E, \
-                                             (int)K, idx, wts)
+                                             (int)K, idx, wts, status)
   if (slots <= 1)
     MLXR_TOPK(1);
   else if (slots <= 2)
