@@ -214,6 +214,7 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   a.active = db.active;
   a.num_active = db.num_active;
   a.work = db.work;
+  a.num_work = db.num_work;
   a.tiles = db.tiles;
   a.num_tiles = db.num_tiles;
   a.w0 = QWeights{w, static_cast<const uint16_t*>(scales),
@@ -226,7 +227,7 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   a.out_ld = N;
   a.out_map = db.sorted;
   a.gated = false;
-  return finish(from_hip(launch_qgemm(a, R, std::min<int64_t>(E, R),
+  return finish(from_hip(launch_qgemm(a, R, dispatch_max_work(R, E),
                                       nn::use_prefill_path(R, E), s),
                          "gather_qmm"));
 }

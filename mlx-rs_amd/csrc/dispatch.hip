@@ -85,14 +85,19 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
   const int has = (tid < E && cnt > 0) ? 1 : 0;
   int n_active;
   const int apos = block_exclusive_scan(has, &n_active, wsum);
-  if (has) {
-    b.active[apos] = tid;
-    b.work[4 * apos] = tid;
-    b.work[4 * apos + 1] = off;
-    b.work[4 * apos + 2] = cnt;
-    b.work[4 * apos + 3] = 0;
-  }
+  if (has) b.active[apos] = tid;
   if (tid == 0) *b.num_active = n_active;
+  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
+  int n_work;
+  const int wpos = block_exclusive_scan(nw, &n_work, wsum);
+  for (int j = 0; j < nw; ++j) {
+    int32_t* w = b.work + 4 * (wpos + j);
+    w[0] = tid;
+    w[1] = off + j * kWorkRows;
+    w[2] = min(kWorkRows, cnt - j * kWorkRows);
+    w[3] = cnt;
+  }
+  if (tid == 0) *b.num_work = n_work;
 
   const int nt = (tid < E) ? (cnt + tile_rows - 1) / tile_rows : 0;
   int n_tiles;
@@ -164,16 +169,19 @@ __global__ __launch_bounds__(256) void dispatch_identity_kernel(
     b.offsets[0] = 0;
     b.offsets[1] = n;
     b.active[0] = 0;
-    b.work[0] = 0;
-    b.work[1] = 0;
-    b.work[2] = n;
-    b.work[3] = 0;
     *b.num_active = n > 0 ? 1 : 0;
+    *b.num_work = (n + kWorkRows - 1) / kWorkRows;
     *b.num_tiles = n_tiles;
   }
   for (int j = tid; j < n_tiles; j += 256) {
     b.tiles[2 * j] = 0;
     b.tiles[2 * j + 1] = j * tile_rows;
+  }
+  for (int j = tid; j * kWorkRows < n; j += 256) {
+    b.work[4 * j] = 0;
+    b.work[4 * j + 1] = j * kWorkRows;
+    b.work[4 * j + 2] = min(kWorkRows, n - j * kWorkRows);
+    b.work[4 * j + 3] = n;
   }
 }
 

@@ -66,7 +66,10 @@ struct DispatchBuffers {
   int32_t* inv;         // [n]  sorted slot per flat index
   int32_t* active;      // [E]  experts with rows, ascending
   int32_t* num_active;  // [1]
-  int32_t* work;        // [E][4] (expert, first slot, rows, 0) per active
+  int32_t* work;        // [max_work][4] (expert, first slot, rows, expert
+                        // rows): each expert's rows in chunks of at most
+                        // kWorkRows
+  int32_t* num_work;    // [1]
   int32_t* tiles;       // [max_tiles] packed (expert, first row) of M-tiles
   int32_t* num_tiles;   // [1]
   int32_t* block_hist;  // [ceil(n/1024), E] scratch
@@ -75,7 +78,14 @@ struct DispatchBuffers {
 };
 constexpr int kDispatchBlock = 1024;
 constexpr int kMaxExperts = 1024;
+// Rows per decode work item: an expert with more rows becomes several items,
+// so the decode GEMM's work items stay small and alike.
+constexpr int kWorkRows = 8;
 int64_t dispatch_max_tiles(int64_t n, int64_t E, int tile_rows);
+// Bound on the work items of n flat rows over E experts.
+inline int64_t dispatch_max_work(int64_t n, int64_t E) {
+  return (E < n ? E : n) + n / kWorkRows;
+}
 // Clears a workspace status word with a one-thread kernel (no memset node,
 // so the call stays valid under stream capture).
 hipError_t launch_zero_status(int32_t* status, hipStream_t s);
@@ -117,7 +127,9 @@ struct QGemmArgs {
   const int32_t* offsets;  // [E+1] slot range of each expert
   const int32_t* active;   // [E] experts with rows
   const int32_t* num_active;
-  const int32_t* work;     // [E][4] (expert, first slot, rows, 0) per active
+  const int32_t* work;     // work items (expert, first slot, rows <= 8,
+                           // rows of the expert)
+  const int32_t* num_work;
   const int32_t* tiles;    // M-tile list (prefill path)
   const int32_t* num_tiles;
   QWeights w0;             // gate (or the only projection)
@@ -132,10 +144,9 @@ struct QGemmArgs {
 constexpr int kMaxInputDims = 4096;
 // Rows per M-tile of the prefill kernel; the dispatch builds its tile list.
 constexpr int kPrefillTileRows = 128;
-// max_rows_per_expert bounds the grid of the decode kernel; max_active
-// bounds the number of experts with rows.
+// max_items bounds the number of work items (dispatch_max_work).
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
-                        int64_t max_active, bool prefill, hipStream_t s);
+                        int64_t max_items, bool prefill, hipStream_t s);
 
 // -------------------------------------------------------------- combine.hip
 hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,

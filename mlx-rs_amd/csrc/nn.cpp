@@ -53,7 +53,8 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
   b.inv = c.take<int32_t>(n);
   b.active = c.take<int32_t>(E);
   b.num_active = c.take<int32_t>(1);
-  b.work = c.take<int32_t>(4 * E);
+  b.work = c.take<int32_t>(4 * dispatch_max_work(n, E));
+  b.num_work = c.take<int32_t>(1);
   b.tiles = c.take<int32_t>(2 * dispatch_max_tiles(n, E, kPrefillTileRows));
   b.num_tiles = c.take<int32_t>(1);
   b.block_hist = c.take<int32_t>(nb * E);
@@ -116,6 +117,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.active = db.active;
   g.num_active = db.num_active;
   g.work = db.work;
+  g.num_work = db.num_work;
   g.tiles = db.tiles;
   g.num_tiles = db.num_tiles;
   g.w0 = qw(gate_);
@@ -128,7 +130,8 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.out_ld = f;
   g.out_map = nullptr;
   g.gated = true;
-  st = from_hip(launch_qgemm(g, T, 1, prefill, s), "shared_expert gate/up");
+  const int64_t items = dispatch_max_work(T, 1);
+  st = from_hip(launch_qgemm(g, T, items, prefill, s), "shared_expert gate/up");
   if (!st.ok) return st;
   QGemmArgs h = g;
   h.x = act;
@@ -140,7 +143,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   h.out = y;
   h.out_ld = d;
   h.gated = false;
-  return from_hip(launch_qgemm(h, T, 1, prefill, s), "shared_expert down");
+  return from_hip(launch_qgemm(h, T, items, prefill, s), "shared_expert down");
 }
 
 // -------------------------------------------------------- SplitSwitchFfn
@@ -191,7 +194,7 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   const int64_t E = w_.gate_proj.num_experts;
   const int64_t n = T * K;
   uint16_t* act = ws.take<uint16_t>(n * f);
-  const int64_t max_active = std::min(E, n);
+  const int64_t max_items = dispatch_max_work(n, E);
   const bool prefill = use_prefill_path(n, E);
   QGemmArgs g{};
   g.x = x;
@@ -202,6 +205,7 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   g.active = db.active;
   g.num_active = db.num_active;
   g.work = db.work;
+  g.num_work = db.num_work;
   g.tiles = db.tiles;
   g.num_tiles = db.num_tiles;
   g.w0 = qw(w_.gate_proj);
@@ -214,7 +218,7 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   g.out_ld = f;
   g.out_map = nullptr;
   g.gated = true;
-  Status st = from_hip(launch_qgemm(g, n, max_active, prefill, s),
+  Status st = from_hip(launch_qgemm(g, n, max_items, prefill, s),
                        "switch_mlp gate/up");
   if (!st.ok) return st;
   QGemmArgs h = g;
@@ -230,7 +234,7 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   h.out_ld = d;
   h.out_map = db.sorted;
   h.gated = false;
-  return from_hip(launch_qgemm(h, n, max_active, prefill, s),
+  return from_hip(launch_qgemm(h, n, max_items, prefill, s),
                   "switch_mlp down");
 }
 

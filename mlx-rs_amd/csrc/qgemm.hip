@@ -33,8 +33,42 @@
 namespace mlxr_moe {
 namespace {
 
-// (experts x 16-channel blocks) from which the streaming kernel runs
-constexpr int64_t kStreamMinBlocks = 2048;
+// Launch shape of the streaming kernel: (experts x 16-channel blocks) from
+// which it runs, waves per workgroup, super-steps of loads in flight at 4-
+// and 8-bit.
+#ifndef MLXR_STREAM_MIN_BLOCKS
+#define MLXR_STREAM_MIN_BLOCKS 2048
+#endif
+#ifndef MLXR_STREAM_WAVES
+#define MLXR_STREAM_WAVES 4
+#endif
+#ifndef MLXR_STREAM_DEPTH4
+#define MLXR_STREAM_DEPTH4 1
+#endif
+#ifndef MLXR_STREAM_DEPTH8
+#define MLXR_STREAM_DEPTH8 1
+#endif
+#ifndef MLXR_SCHED_BARRIER
+#define MLXR_SCHED_BARRIER() __builtin_amdgcn_sched_barrier(0)
+#endif
+// experts with at most this many rows use the 4-token MFMA form
+#ifndef MLXR_STREAM_TT4_ROWS
+#define MLXR_STREAM_TT4_ROWS 4
+#endif
+constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
+// 16-channel blocks per wave, at most (gate/up, down): the gated kernel
+// moves twice the bytes per step and does best with one
+#ifndef MLXR_STREAM_MAX_NB_GATED
+#define MLXR_STREAM_MAX_NB_GATED 1
+#endif
+#ifndef MLXR_STREAM_MAX_NB
+#define MLXR_STREAM_MAX_NB 2
+#endif
+#ifndef MLXR_STREAM_SLOTS
+#define MLXR_STREAM_SLOTS 512
+#endif
+// workgroups resident at once (2 per CU on 256 CUs)
+constexpr int64_t kStreamSlots = MLXR_STREAM_SLOTS;
 
 // Reorder 8 consecutive bf16 x values to the code order that unpack4 emits:
 // element j of the fragment holds x[perm(j)], perm = 0,4,1,5,2,6,3,7.
@@ -48,15 +82,26 @@ __device__ __forceinline__ u32x4_t perm4(u32x4_t v) {
 }
 
 // 8 nibbles -> bf16 (1 + code/16): nibble k moves to mantissa bits 6..3 of
-// its half; pairs (n0,n4) (n1,n5) (n2,n6) (n3,n7).
-__device__ __forceinline__ u32x4_t unpack4(uint32_t w) {
-  const uint32_t m = 0x00780078u, one = 0x3F803F80u;
-  u32x4_t r;
-  r.x = ((w << 3) & m) | one;
-  r.y = ((w >> 1) & m) | one;
-  r.z = ((w >> 5) & m) | one;
-  r.w = ((w >> 9) & m) | one;
+// its half; pairs (n0,n4) (n1,n5) (n2,n6) (n3,n7).  Written as one shift and
+// one v_and_or_b32 per output: a VOP3 op takes one scalar operand here, so
+// the mask rides in an SGPR and the bf16 1.0 pair in a VGPR (`one`).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m,
+                                           uint32_t one) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(one));
   return r;
+}
+__device__ __forceinline__ u32x4_t unpack4(uint32_t w, uint32_t one) {
+  const uint32_t m = 0x00780078u;
+  u32x4_t r;
+  r.x = and_or(w << 3, m, one);
+  r.y = and_or(w >> 1, m, one);
+  r.z = and_or(w >> 5, m, one);
+  r.w = and_or(w >> 9, m, one);
+  return r;
+}
+__device__ __forceinline__ u32x4_t unpack4(uint32_t w) {
+  return unpack4(w, 0x3F803F80u);
 }
 
 // 8 bytes (two words) -> bf16 codes in natural order.  Integers <= 255 are
@@ -170,7 +215,7 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
   const int kw = blockDim.x >> 6;
   const int item = blockIdx.x;
   const int ai = item / tiles_n, tile = item - ai * tiles_n;
-  const int n_act = *a.num_active;
+  const int n_act = *a.num_work;
   const int4 wk = reinterpret_cast<const int4*>(a.work)[ai];
   if (ai >= n_act) return;
   const int e = wk.x, row0 = wk.y, rows = wk.z;
@@ -349,92 +394,140 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
 // cross-lane adds at the end.
 template <int BITS, bool GATED, int TT, int D>
 __device__ __forceinline__ void stream_body(const QGemmArgs& a, int tiles_n,
-                                            char* smem) {
+                                            int nb, char* smem) {
   constexpr int NM = GATED ? 2 : 1;
-  constexpr int GG = 16 / TT;               // groups per MFMA
-  constexpr int LPG = 4 / GG;               // lane quarters per group
-  constexpr int CPL = 64 / LPG;             // codes per lane per super-step
-  constexpr int NL = CPL * BITS / 128;      // 16-byte loads per lane
-  constexpr int NMF = CPL / 8;              // MFMAs per super-step
+  constexpr int GG = 16 / TT;           // groups per MFMA
+  constexpr int LPG = 4 / GG;           // lane quarters per group
+  constexpr int CPL = 64 / LPG;         // codes per lane per super-step
+  constexpr int NL = CPL * BITS / 128;  // 16-byte loads per lane
+  constexpr int NMF = CPL / 8;          // MFMAs per super-step
+  constexpr int WPG = 2 * BITS;         // packed words per row and group
   const int waves = blockDim.x >> 6;
   const int item = blockIdx.x;
   const int ai = item / tiles_n, tile = item - ai * tiles_n;
-  const int n_act = *a.num_active;
+  const int n_act = *a.num_work;
   const int4 wk = reinterpret_cast<const int4*>(a.work)[ai];
   if (ai >= n_act) return;
   const int e = wk.x, row0 = wk.y, rows = wk.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, q = lane >> 4;
-  const int gq = q / LPG, sq = q % LPG;     // this lane's group, its part
+  const int gq = q / LPG, sq = q % LPG;  // this lane's group, its part
   const int K = a.K, groups = K >> 6;
-  const int ssteps = (groups + GG - 1) / GG;
+  const int ssteps = groups / GG;  // the host runs this kernel when GG | groups
+  const int total = nb * ssteps;   // super-steps of this wave, all blocks
   // LDS: x chunk [TT][K + 8] bf16 (rows padded 16 B), 16 B zero block,
   // X [groups][TT] f32
   const int xs = K + 8;
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem);
   char* zero_blk = smem + (size_t)TT * xs * 2;
   float* Xl = reinterpret_cast<float*>(zero_blk + 16);
+  // per-block partial sums [waves][nb][NM][64] after X (16-byte aligned)
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(
+      smem + (((size_t)TT * xs * 2 + 16 + (size_t)groups * TT * 4 + 15) & ~size_t(15)));
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  const int64_t wrow = (int64_t)e * a.N + ((int64_t)tile * waves + wave) * 16 + n;
-  const int ch = (tile * waves + wave) * 16 + n;
+  // this wave's blocks: nb consecutive 16-channel blocks from ch0
+  const int ch0 = ((tile * waves + wave) * nb) * 16 + n;
+  const int64_t wrow0 = (int64_t)e * a.N + ch0;
   // A operand row of this lane: (group m / TT, token m % TT), m = l % 16
   const int arow_g = n / TT, arow_t = n % TT;
 
+  // ring of R = D + 1 slots: global super-step gs lives in slot gs % R; the
+  // load for gs + D goes into the slot that gs - 1 freed, so nothing is
+  // copied, and the ring runs on across block boundaries
+  constexpr int R = D + 1;
   struct Ring {
     u32x4_t w[NM][NL];
-    uint32_t s[NM], b[NM];
   };
-  auto load = [&](Ring& r, int ss) {
-    const int g = ss * GG + gq;  // this lane's group
-    const bool ok = g < groups;
+  const uint32_t* wb[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const QWeights& W = m == 0 ? a.w0 : a.w1;
+    wb[m] = W.w + (wrow0 * groups + gq) * WPG + sq * (CPL * BITS / 32);
+  }
+  const int64_t blk_rows = (int64_t)16 * groups;  // row stride of a block
+  auto load = [&](Ring& r, int gs) {
+    const int bi = gs / ssteps, ss = gs - bi * ssteps;
+    const int64_t go = bi * blk_rows + ss * GG;  // group offset
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const QWeights& W = m == 0 ? a.w0 : a.w1;
-      const uint32_t* wp = W.w + wrow * groups * (2 * BITS) + g * (2 * BITS) +
-                           sq * (CPL * BITS / 32);
+      const u32x4_t* wp = reinterpret_cast<const u32x4_t*>(wb[m] + go * WPG);
 #pragma unroll
-      for (int i = 0; i < NL; ++i)
-        r.w[m][i] = ok ? reinterpret_cast<const u32x4_t*>(wp)[i]
-                       : u32x4_t{0u, 0u, 0u, 0u};
-      r.s[m] = ok ? W.scales[wrow * groups + g] : 0u;
-      r.b[m] = ok ? W.biases[wrow * groups + g] : 0u;
+      for (int i = 0; i < NL; ++i) r.w[m][i] = wp[i];
     }
   };
+  // Scales and biases of this wave's blocks: 16 rows x groups bf16 per
+  // block and array, contiguous in memory.  They are copied to LDS once with
+  // 16-byte loads (the hot loop then reads its two values per step from
+  // LDS): a per-step 2-byte load per lane would touch 16 cache lines for
+  // 128 useful bytes.
+  const int sbn = nb * 16 * groups;  // bf16 per array
+  uint16_t* sbl = reinterpret_cast<uint16_t*>(
+      reinterpret_cast<char*>(red) + (size_t)waves * nb * NM * 64 * sizeof(f32x4_t)) +
+      (size_t)wave * NM * 2 * sbn;
+  const uint32_t one_v = 0x3F803F80u;
 
   for (int tt = 0; tt < rows; tt += TT) {
     const int nt = min(TT, rows - tt);
-    Ring ring[D];
-#pragma unroll
-    for (int j = 0; j < D; ++j)
-      if (j < ssteps) load(ring[j], j);
-    // stage x: 8 elements (16 B) per thread and iteration
+    // x first (the compute waits on it), then the first D weight steps
     const int per_row = K >> 3;
-    for (int i = threadIdx.x; i < TT * per_row; i += blockDim.x) {
-      const int t = i / per_row, k8 = i - t * per_row;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (t < nt) {
-        const int slot = row0 + tt + t;
-        const int64_t xrow = a.row_map ? a.row_map[slot] / a.row_div : slot;
-        v = *reinterpret_cast<const u32x4_t*>(a.x + xrow * a.x_ld + 8 * k8);
-        if constexpr (BITS == 4) v = perm4(v);
-      }
-      *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = v;
+    int64_t xr[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const int slot = row0 + tt + t;
+      xr[t] = t < nt ? (a.row_map ? a.row_map[slot] / a.row_div : slot) : 0;
     }
+    // stage x: thread k8 holds elements 8*k8..8*k8+7 of every token of the
+    // chunk; the token sums X of each 64-wide group come from the 8 threads
+    // sharing it
+    for (int k8 = threadIdx.x; k8 < per_row; k8 += blockDim.x) {
+      u32x4_t v[TT];
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        v[t] = u32x4_t{0u, 0u, 0u, 0u};
+        if (t < nt)
+          v[t] = *reinterpret_cast<const u32x4_t*>(a.x + xr[t] * a.x_ld + 8 * k8);
+      }
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        float sx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sx += __uint_as_float(v[t][j] << 16) + __uint_as_float(v[t][j] & 0xffff0000u);
+        sx += __shfl_xor(sx, 1, 64);
+        sx += __shfl_xor(sx, 2, 64);
+        sx += __shfl_xor(sx, 4, 64);
+        if ((k8 & 7) == 0) Xl[(k8 >> 3) * TT + t] = sx;
+        u32x4_t w = v[t];
+        if constexpr (BITS == 4) w = perm4(w);
+        *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = w;
+      }
+    }
+    if (tt == 0) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        const QWeights& W = m == 0 ? a.w0 : a.w1;
+        const uint16_t* s0 = W.scales + (wrow0 - n) * groups;
+        const uint16_t* b0 = W.biases + (wrow0 - n) * groups;
+        for (int i = lane; i < sbn / 8; i += 64) {
+          *reinterpret_cast<u32x4_t*>(sbl + (m * 2) * sbn + 8 * i) =
+              *reinterpret_cast<const u32x4_t*>(s0 + 8 * i);
+          *reinterpret_cast<u32x4_t*>(sbl + (m * 2 + 1) * sbn + 8 * i) =
+              *reinterpret_cast<const u32x4_t*>(b0 + 8 * i);
+        }
+      }
+    }
+    Ring ring[R];
+#pragma unroll
+    for (int j = 0; j < D; ++j) load(ring[j], min(j, total - 1));
     if (threadIdx.x == 0)
       *reinterpret_cast<u32x4_t*>(zero_blk) = u32x4_t{0u, 0u, 0u, 0u};
     __syncthreads();
-    for (int i = threadIdx.x; i < groups * TT; i += blockDim.x) {
-      const int g = i / TT, t = i - g * TT;
-      float sx = 0.0f;
-      const uint16_t* xp = xl + (size_t)t * xs + 64 * g;
-      for (int k = 0; k < 64; k += 2) {
-        const uint32_t u = *reinterpret_cast<const uint32_t*>(xp + k);
-        sx += __uint_as_float(u << 16) + __uint_as_float(u & 0xffff0000u);
-      }
-      Xl[g * TT + t] = sx;
-    }
-    __syncthreads();
 
+    // The loop issues the same loads every super-step (past the end they
+    // repeat the last step, a cache hit) and holds no stores, so the
+    // compiler can wait for exactly the oldest ring slot.  Steps past the
+    // end multiply zeros.  Each block's partial sums go to LDS (red) and
+    // are combined after the loop.
     f32x4_t acc[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) acc[m] = zero;
@@ -442,81 +535,87 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a, int tiles_n,
     // codes, or the zero block off the diagonal / past the tokens
     const bool diag = arow_g == gq && arow_t < nt;
     const char* xsrc = smem + ((size_t)arow_t * xs + sq * CPL) * 2;
-    for (int ss0 = 0; ss0 < ssteps; ss0 += D) {
+    for (int gs0 = 0; gs0 < total; gs0 += R) {
 #pragma unroll
-      for (int j = 0; j < D; ++j) {
-        const int ss = ss0 + j;
-        if (ss < ssteps) {
-          const Ring cur = ring[j];
-          if (ss + D < ssteps) load(ring[j], ss + D);
-          const int g = ss * GG + gq;
-          const bool on = diag && g < groups;
-          const char* xp = on ? xsrc + (size_t)(64 * g) * 2 : zero_blk;
-          const int xstep = on ? 16 : 0;
-          bf16x8_t xa[NMF];
+      for (int j = 0; j < R; ++j) {
+        const int gs = gs0 + j;
+        load(ring[(j + D) % R], min(gs + D, total - 1));
+        const Ring& cur = ring[j];
+        const bool live = gs < total;
+        const int bi = gs / ssteps, ss = gs - bi * ssteps;
+        const int g = ss * GG + gq;
+        const bool on = diag && live;
+        const char* xp = on ? xsrc + (size_t)(64 * g) * 2 : zero_blk;
+        const int xstep = on ? 16 : 0;
+        // all x fragments of the step are read before the first MFMA, so
+        // the MFMA chain waits on LDS once per step, not once per MFMA
+        bf16x8_t xa[NMF];
 #pragma unroll
-          for (int i = 0; i < NMF; ++i)
-            xa[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xp + xstep * i));
-          // X of this lane's output rows: group (4q+r)/TT, tokens (4q+r)%TT
-          const int og = ss * GG + (4 * q) / TT;
-          const f32x4_t X = og < groups
-              ? *reinterpret_cast<const f32x4_t*>(Xl + og * TT + (4 * q) % TT)
-              : zero;
+        for (int i = 0; i < NMF; ++i)
+          xa[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xp + xstep * i));
+        // X of this lane's output rows: group (4q+r)/TT, tokens (4q+r)%TT
+        const int og = ss * GG + (4 * q) / TT;
+        f32x4_t X = *reinterpret_cast<const f32x4_t*>(Xl + og * TT + (4 * q) % TT);
+        if (!live) X = zero;
+        MLXR_SCHED_BARRIER();
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          f32x4_t P = zero;
+#pragma unroll
+          for (int i = 0; i < NMF; ++i) {
+            u32x4_t u;
+            if constexpr (BITS == 4) {
+              u = unpack4(cur.w[m][i / 4][i % 4], one_v);
+            } else {
+              const u32x4_t wv = cur.w[m][i / 2];
+              u = (i & 1) ? unpack8(wv.z, wv.w) : unpack8(wv.x, wv.y);
+            }
+            P = mfma16x16x32(xa[i], as_bf16x8(u), P);
+          }
+          // scale/bias of this lane's output group og (channel n)
+          const int si = ((live ? bi : 0) * 16 + n) * groups + min(og, groups - 1);
+          const uint32_t sv = sbl[(m * 2) * sbn + si];
+          const uint32_t bv = sbl[(m * 2 + 1) * sbn + si];
+          float sc, cb;
+          group_terms<BITS>(sv, bv, sc, cb);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[m][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(cb, X[r], acc[m][r]));
+        }
+        if (live && ss == ssteps - 1) {
 #pragma unroll
           for (int m = 0; m < NM; ++m) {
-            f32x4_t P = zero;
-#pragma unroll
-            for (int i = 0; i < NMF; ++i) {
-              u32x4_t u;
-              if constexpr (BITS == 4) {
-                u = unpack4(cur.w[m][i / 4][i % 4]);
-              } else {
-                const u32x4_t wv = cur.w[m][i / 2];
-                u = (i & 1) ? unpack8(wv.z, wv.w) : unpack8(wv.x, wv.y);
-              }
-              P = mfma16x16x32(xa[i], as_bf16x8(u), P);
-            }
-            // scale/bias of this lane's output group (4q)/TT, loaded by the
-            // first lane quarter of that group
-            uint32_t sb = cur.s[m], bb = cur.b[m];
-            if constexpr (TT != 4) {
-              const int src_lane = (((4 * q) / TT) * LPG) * 16 + n;
-              sb = (uint32_t)__shfl((int)sb, src_lane, 64);
-              bb = (uint32_t)__shfl((int)bb, src_lane, 64);
-            }
-            float sc, cb;
-            group_terms<BITS>(sb, bb, sc, cb);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[m][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(cb, X[r], acc[m][r]));
+            red[((wave * nb + bi) * NM + m) * 64 + lane] = acc[m];
+            acc[m] = zero;
           }
         }
       }
     }
-    // the GG group partials of a token sit on lanes 16*(TT/4) apart
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = acc[m][r];
-        if constexpr (TT == 4) v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        acc[m][r] = v;
-      }
-    }
-    // lanes q < TT/4 hold tokens 4q..4q+3
+    // Each token's GG group partials sit on lanes 16*(TT/4) apart; lanes
+    // q < TT/4 add them up and write tokens 4q..4q+3 of channel n.
     if (q < TT / 4) {
+      for (int bi = 0; bi < nb; ++bi) {
+        f32x4_t tot[NM];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 4 * q + r;
-        if (t < nt) {
-          const int slot = row0 + tt + t;
-          if constexpr (GATED) {
-            a.out[(int64_t)slot * a.out_ld + ch] =
-                swiglu_bf16(bf16_round(acc[0][r]), bf16_round(acc[1][r]));
-          } else {
-            const int64_t orow = a.out_map ? a.out_map[slot] : slot;
-            a.out[orow * a.out_ld + ch] = f32_to_bf16(acc[0][r]);
+        for (int m = 0; m < NM; ++m) {
+          const f32x4_t* rp = red + ((wave * nb + bi) * NM + m) * 64 + n;
+          tot[m] = zero;
+#pragma unroll
+          for (int qq = q; qq < 4; qq += TT / 4) tot[m] += rp[16 * qq];
+        }
+        const int ch = ch0 + bi * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 4 * q + r;
+          if (t < nt) {
+            const int slot = row0 + tt + t;
+            if constexpr (GATED) {
+              a.out[(int64_t)slot * a.out_ld + ch] =
+                  swiglu_bf16(bf16_round(tot[0][r]), bf16_round(tot[1][r]));
+            } else {
+              const int64_t orow = a.out_map ? a.out_map[slot] : slot;
+              a.out[orow * a.out_ld + ch] = f32_to_bf16(tot[0][r]);
+            }
           }
         }
       }
@@ -528,47 +627,69 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a, int tiles_n,
 // Tokens per pass follow the expert's row count: 4 (one pass for up to 4
 // rows, GG = 4) or 8 (GG = 2).  LDS is sized for 8.
 template <int BITS, bool GATED, int D>
-__global__ __launch_bounds__(256) void qgemm_stream_kernel(QGemmArgs a,
-                                                           int tiles_n) {
+__global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
+    QGemmArgs a, int tiles_n, int nb) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int ai = blockIdx.x / tiles_n;
-  const int rows = reinterpret_cast<const int4*>(a.work)[ai].z;
-  if (rows <= 4)
-    stream_body<BITS, GATED, 4, D>(a, tiles_n, smem);
+  // The MFMA form follows the expert's row count (not the item's), so every
+  // token of an expert is summed in the same order, wherever its item
+  // boundaries fall.  The 8-token form moves half the bytes per super-step:
+  // twice the depth.
+  const int expert_rows = reinterpret_cast<const int4*>(a.work)[ai].w;
+  if (expert_rows <= MLXR_STREAM_TT4_ROWS)
+    stream_body<BITS, GATED, 4, D>(a, tiles_n, nb, smem);
   else
-    stream_body<BITS, GATED, 8, D>(a, tiles_n, smem);
+    stream_body<BITS, GATED, 8, 2 * D>(a, tiles_n, nb, smem);
 }
 
 }  // namespace
 
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
-                        int64_t max_active, bool prefill, hipStream_t s) {
+                        int64_t max_items, bool prefill, hipStream_t s) {
   (void)prefill;
   (void)total_rows;
-  if (max_active <= 0) return hipSuccess;
+  if (max_items <= 0) return hipSuccess;
   const int groups = a.K / 64;
   // Many (expert, block) items: the streaming kernel (one block per wave,
   // x in LDS, a ring of weight loads).  Few: the split-K kernel below, which
   // spreads each block over up to 16 waves.
-  if (max_active * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0) {
-    constexpr int kWaves = 4, kMaxTT = 8;
-    const int tiles_n = a.N / (16 * kWaves);
-    const size_t lds = (size_t)kMaxTT * (a.K + 8) * 2 + 16 +
-                       (size_t)groups * kMaxTT * sizeof(float);
-    const dim3 grid((unsigned)(max_active * tiles_n));
+  const auto a16 = [](const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+  };
+  const bool sb16 = a16(a.w0.scales) && a16(a.w0.biases) &&
+                    (!a.gated || (a16(a.w1.scales) && a16(a.w1.biases)));
+  if (max_items * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0 &&
+      groups % 4 == 0 && sb16) {
+    constexpr int kWaves = MLXR_STREAM_WAVES, kMaxTT = 8;
+    // blocks per wave: about one workgroup per slot (two per CU), so x is
+    // staged as few times as the GPU allows
+    const int64_t per_tile = a.N / (16 * kWaves);
+    int nb = 1;
+    for (int c = a.gated ? MLXR_STREAM_MAX_NB_GATED : MLXR_STREAM_MAX_NB; c > 1; --c)
+      if (per_tile % c == 0 && max_items * (per_tile / c) >= kStreamSlots) {
+        nb = c;
+        break;
+      }
+    const int tiles_n = (int)(per_tile / nb);
+    const size_t lds =
+        (((size_t)kMaxTT * (a.K + 8) * 2 + 16 + (size_t)groups * kMaxTT * 4 + 15) &
+         ~size_t(15)) +
+        (size_t)kWaves * nb * (a.gated ? 2 : 1) * 64 * sizeof(f32x4_t) +
+        (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
+    const dim3 grid((unsigned)(max_items * tiles_n));
     ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
 #define MLXR_QS(B, G, D) \
-  qgemm_stream_kernel<B, G, D><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n)
+  qgemm_stream_kernel<B, G, D><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, nb)
     if (a.bits == 4) {
       if (a.gated)
-        MLXR_QS(4, true, 3);
+        MLXR_QS(4, true, MLXR_STREAM_DEPTH4);
       else
-        MLXR_QS(4, false, 3);
+        MLXR_QS(4, false, MLXR_STREAM_DEPTH4);
     } else {
       if (a.gated)
-        MLXR_QS(8, true, 2);
+        MLXR_QS(8, true, MLXR_STREAM_DEPTH8);
       else
-        MLXR_QS(8, false, 2);
+        MLXR_QS(8, false, MLXR_STREAM_DEPTH8);
     }
 #undef MLXR_QS
     return hipGetLastError();
@@ -585,14 +706,14 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   // (the gated kernel keeps one block: two would spill under the 128-VGPR
   // budget of 16-wave workgroups)
   for (int c = 4; c > 1 && !a.gated; c >>= 1)
-    if (nblk % c == 0 && max_active * (nblk / c) >= 1024 &&
+    if (nblk % c == 0 && max_items * (nblk / c) >= 1024 &&
         kw * c * nm <= 64) {
       cb = c;
       break;
     }
   const int tiles_n = nblk / cb;
   const size_t lds = (size_t)kw * cb * nm * 64 * sizeof(f32x4_t);
-  const dim3 grid((unsigned)(max_active * tiles_n));
+  const dim3 grid((unsigned)(max_items * tiles_n));
   const dim3 block((unsigned)(64 * kw));
   ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
 #define MLXR_QG(B, G, SPW)                                                  \

@@ -190,14 +190,19 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
   const int has = (tid < E && cnt > 0) ? 1 : 0;
   int n_active;
   const int apos = block_exclusive_scan(has, &n_active, ls->wsum);
-  if (has) {
-    b.active[apos] = tid;
-    b.work[4 * apos] = tid;
-    b.work[4 * apos + 1] = off;
-    b.work[4 * apos + 2] = cnt;
-    b.work[4 * apos + 3] = 0;
-  }
+  if (has) b.active[apos] = tid;
   if (tid == 0) *b.num_active = n_active;
+  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
+  int n_work;
+  const int wpos = block_exclusive_scan(nw, &n_work, ls->wsum);
+  for (int j = 0; j < nw; ++j) {
+    int32_t* w = b.work + 4 * (wpos + j);
+    w[0] = tid;
+    w[1] = off + j * kWorkRows;
+    w[2] = min(kWorkRows, cnt - j * kWorkRows);
+    w[3] = cnt;
+  }
+  if (tid == 0) *b.num_work = n_work;
   const int nt = tid < E ? (cnt + tile_rows - 1) / tile_rows : 0;
   int n_tiles;
   const int tpos = block_exclusive_scan(nt, &n_tiles, ls->wsum);
