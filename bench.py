@@ -157,6 +157,22 @@ def gated_flops(cfg, T):
     return 4 * T * cfg.K * cfg.f * cfg.d
 
 
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by a plain copy of known
+    size), when it covers this workload; None otherwise."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "qgemm_decode_c2_T64_traffic.json")
+    try:
+        with open(path) as fh:
+            data = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    if data.get("workload") != workload:
+        return None
+    return data.get("kernels", {}).get(kernel, {}).get("traffic_bytes")
+
+
 def cpu_baseline(pkg, orc, bw, T, seconds, threads):
     """The oracle (plain C, OpenMP) on this host: whole block forwards of the
     same c-config at T tokens until `seconds` have passed (at least one)."""
@@ -212,7 +228,9 @@ def main():
         traffic_alg = gated_bytes(cfg, T, U)
         achieved = traffic_alg / kt / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None)
+                    frac=round(achieved / HBM_PEAK_GBS, 4),
+                    traffic=measured_traffic(f"{cfg.name} T={T}", "qgemm_gated"),
+                    algorithmic_bytes=traffic_alg)
     else:
         achieved = gated_flops(cfg, T) / kt / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 2), peak=BF16_PEAK_TFLOPS,
