@@ -79,7 +79,6 @@ void plan_gather(Carve& c, int64_t B, int64_t M, int64_t E) {
   c.take<int32_t>(1);  // status
   c.take<int32_t>(R);  // ids
   c.take<int32_t>(R);  // xrow
-  c.take<int32_t>(R);  // xrow_sorted
   carve_dispatch(c, R, E, nullptr);
 }
 
@@ -191,7 +190,6 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   int32_t* status = c.take<int32_t>(1);
   int32_t* ids = c.take<int32_t>(R);
   int32_t* xrow = c.take<int32_t>(R);
-  int32_t* xrow_sorted = c.take<int32_t>(R);
   const DispatchBuffers db = carve_dispatch(c, R, E, status);
   uint16_t* o = static_cast<uint16_t*>(out);
   st = from_hip(launch_gather_prep(lhs_indices, rhs_indices, B, M, x_batch, E,
@@ -200,16 +198,13 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   if (st.ok)
     st = from_hip(launch_dispatch(ids, R, E, kPrefillTileRows, db, false, s),
                   "gather_qmm dispatch");
-  if (st.ok)
-    st = from_hip(launch_gather_permute(xrow, db.sorted, db.offsets, E, R,
-                                        xrow_sorted, s),
-                  "gather_qmm permute");
   if (!st.ok) return finish(st);
   QGemmArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.x_ld = K;
-  a.row_map = xrow_sorted;
+  a.row_map = xrow;
   a.row_div = 1;
+  a.x_by_slot = false;
   a.offsets = db.offsets;
   a.active = db.active;
   a.num_active = db.num_active;
@@ -225,7 +220,7 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   a.bits = b;
   a.out = o;
   a.out_ld = N;
-  a.out_map = db.sorted;
+  a.out_by_flat = true;
   a.gated = false;
   return finish(from_hip(launch_qgemm(a, R, dispatch_max_work(R, E),
                                       nn::use_prefill_path(R, E), s),

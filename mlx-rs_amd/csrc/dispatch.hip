@@ -10,8 +10,9 @@
 //         its wave; an LDS table of per-wave counts turns that into a rank
 //         within the workgroup and a per-workgroup histogram.
 //   scan  (one workgroup): per-expert prefix over workgroups, exclusive scan
-//         over experts (offsets), the list of experts with rows, the M-tile
-//         list for the prefill GEMM, and the scatter into sorted/inv.
+//         over experts (offsets), the list of experts with rows, the work
+//         item records and M-tile list for the GEMMs, and the scatter into
+//         sorted/inv (and the flat rows of the work records).
 // Ids outside [0, E) are left out of every expert and flagged in *status.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -63,6 +64,7 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
     const int32_t* __restrict__ ids, int n, int E, int nb, int tile_rows,
     DispatchBuffers b) {
   __shared__ int s_off[kMaxExperts];
+  __shared__ int s_wpos[kMaxExperts];
   __shared__ int wsum[kWaves + 1];
   const int tid = threadIdx.x;
   int cnt = 0;
@@ -90,8 +92,9 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
   const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
   int n_work;
   const int wpos = block_exclusive_scan(nw, &n_work, wsum);
+  if (tid < E) s_wpos[tid] = wpos;
   for (int j = 0; j < nw; ++j) {
-    int32_t* w = b.work + 4 * (wpos + j);
+    int32_t* w = b.work + kWorkInts * (wpos + j);
     w[0] = tid;
     w[1] = off + j * kWorkRows;
     w[2] = min(kWorkRows, cnt - j * kWorkRows);
@@ -117,6 +120,8 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
                     b.rank[i];
     b.sorted[pos] = i;
     b.inv[i] = pos;
+    const int r = pos - s_off[e];
+    b.work[kWorkInts * (s_wpos[e] + r / kWorkRows) + 4 + r % kWorkRows] = i;
   }
 }
 
@@ -178,10 +183,12 @@ __global__ __launch_bounds__(256) void dispatch_identity_kernel(
     b.tiles[2 * j + 1] = j * tile_rows;
   }
   for (int j = tid; j * kWorkRows < n; j += 256) {
-    b.work[4 * j] = 0;
-    b.work[4 * j + 1] = j * kWorkRows;
-    b.work[4 * j + 2] = min(kWorkRows, n - j * kWorkRows);
-    b.work[4 * j + 3] = n;
+    int32_t* w = b.work + kWorkInts * j;
+    w[0] = 0;
+    w[1] = j * kWorkRows;
+    w[2] = min(kWorkRows, n - j * kWorkRows);
+    w[3] = n;
+    for (int i = 0; i < kWorkRows; ++i) w[4 + i] = j * kWorkRows + i;
   }
 }
 
@@ -209,15 +216,6 @@ __global__ __launch_bounds__(256) void gather_prep_kernel(
   }
   ids[r] = (int32_t)e;
   xrow[r] = (int32_t)(xb * M + m);
-}
-
-__global__ __launch_bounds__(256) void gather_permute_kernel(
-    const int32_t* __restrict__ xrow, const int32_t* __restrict__ sorted,
-    const int32_t* __restrict__ offsets, int64_t E, int64_t R,
-    int32_t* __restrict__ xrow_sorted) {
-  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (p >= R || p >= offsets[E]) return;
-  xrow_sorted[p] = xrow[sorted[p]];
 }
 
 }  // namespace
@@ -289,15 +287,6 @@ hipError_t launch_gather_prep(const uint32_t* lhs, const uint32_t* rhs,
   if (R > 0)
     gather_prep_kernel<<<(unsigned)((R + 255) / 256), 256, 0, s>>>(
         lhs, rhs, B, M, x_batch, E, N, ids, xrow, out, status);
-  return hipGetLastError();
-}
-
-hipError_t launch_gather_permute(const int32_t* xrow, const int32_t* sorted,
-                                 const int32_t* offsets, int64_t E, int64_t R,
-                                 int32_t* xrow_sorted, hipStream_t s) {
-  if (R > 0)
-    gather_permute_kernel<<<(unsigned)((R + 255) / 256), 256, 0, s>>>(
-        xrow, sorted, offsets, E, R, xrow_sorted);
   return hipGetLastError();
 }
 

@@ -66,9 +66,8 @@ struct DispatchBuffers {
   int32_t* inv;         // [n]  sorted slot per flat index
   int32_t* active;      // [E]  experts with rows, ascending
   int32_t* num_active;  // [1]
-  int32_t* work;        // [max_work][4] (expert, first slot, rows, expert
-                        // rows): each expert's rows in chunks of at most
-                        // kWorkRows
+  int32_t* work;        // [max_work][kWorkInts] work item records: each
+                        // expert's rows in chunks of at most kWorkRows
   int32_t* num_work;    // [1]
   int32_t* tiles;       // [max_tiles] packed (expert, first row) of M-tiles
   int32_t* num_tiles;   // [1]
@@ -81,6 +80,11 @@ constexpr int kMaxExperts = 1024;
 // Rows per decode work item: an expert with more rows becomes several items,
 // so the decode GEMM's work items stay small and alike.
 constexpr int kWorkRows = 8;
+// Work item record: expert, first sorted slot, rows (<= kWorkRows), rows of
+// the whole expert, then the flat row index (sorted[slot]) of each of the
+// item's slots (unset past rows).  A GEMM workgroup learns its task, and
+// where its x rows live, from these 48 bytes without a dependent load.
+constexpr int kWorkInts = 4 + kWorkRows;
 int64_t dispatch_max_tiles(int64_t n, int64_t E, int tile_rows);
 // Bound on the work items of n flat rows over E experts.
 inline int64_t dispatch_max_work(int64_t n, int64_t E) {
@@ -100,15 +104,11 @@ hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
 hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
                         int64_t K, int32_t* idx, float* wts, int tile_rows,
                         const DispatchBuffers& b, hipStream_t s);
-// gather_qmm helpers: per flat row r = b*M + m the expert id and x row, and
-// the x row of each sorted slot.
+// gather_qmm helper: per flat row r = b*M + m the expert id and x row.
 hipError_t launch_gather_prep(const uint32_t* lhs, const uint32_t* rhs,
                               int64_t B, int64_t M, int64_t x_batch, int64_t E,
                               int64_t N, int32_t* ids, int32_t* xrow,
                               uint16_t* out, int32_t* status, hipStream_t s);
-hipError_t launch_gather_permute(const int32_t* xrow, const int32_t* sorted,
-                                 const int32_t* offsets, int64_t E, int64_t R,
-                                 int32_t* xrow_sorted, hipStream_t s);
 // Identity dispatch for a dense (always-on) expert: one expert, n rows.
 hipError_t launch_dispatch_identity(int64_t n, int tile_rows,
                                     const DispatchBuffers& b, hipStream_t s);
@@ -122,13 +122,16 @@ struct QWeights {
 struct QGemmArgs {
   const uint16_t* x;       // activations (bf16)
   int64_t x_ld;            // row stride of x in elements
-  const int32_t* row_map;  // x row of slot p = row_map[p] / row_div (null: p)
+  // x row of sorted slot p: p when x_by_slot; else, with f the flat row of
+  // p (from the work record), row_map[f] when row_map is given, f / row_div
+  // otherwise
+  const int32_t* row_map;
   int32_t row_div;
+  bool x_by_slot;
   const int32_t* offsets;  // [E+1] slot range of each expert
   const int32_t* active;   // [E] experts with rows
   const int32_t* num_active;
-  const int32_t* work;     // work items (expert, first slot, rows <= 8,
-                           // rows of the expert)
+  const int32_t* work;     // work item records (kWorkInts each)
   const int32_t* num_work;
   const int32_t* tiles;    // M-tile list (prefill path)
   const int32_t* num_tiles;
@@ -137,7 +140,7 @@ struct QGemmArgs {
   int32_t E, N, K, bits;
   uint16_t* out;           // bf16
   int64_t out_ld;
-  const int32_t* out_map;  // out row of slot p = out_map[p] (null: p)
+  bool out_by_flat;        // out row of slot p = its flat row (else p)
   bool gated;              // out = swiglu(x.w0, x.w1)
 };
 // Largest input dim (K) of a projection: 8 waves x 8 groups of 64.

@@ -53,7 +53,7 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
   b.inv = c.take<int32_t>(n);
   b.active = c.take<int32_t>(E);
   b.num_active = c.take<int32_t>(1);
-  b.work = c.take<int32_t>(4 * dispatch_max_work(n, E));
+  b.work = c.take<int32_t>(kWorkInts * dispatch_max_work(n, E));
   b.num_work = c.take<int32_t>(1);
   b.tiles = c.take<int32_t>(2 * dispatch_max_tiles(n, E, kPrefillTileRows));
   b.num_tiles = c.take<int32_t>(1);
@@ -113,6 +113,8 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.x_ld = d;
   g.row_map = nullptr;
   g.row_div = 1;
+  g.x_by_slot = false;
+  g.out_by_flat = false;
   g.offsets = db.offsets;
   g.active = db.active;
   g.num_active = db.num_active;
@@ -128,7 +130,6 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.bits = gate_.bits;
   g.out = act;
   g.out_ld = f;
-  g.out_map = nullptr;
   g.gated = true;
   const int64_t items = dispatch_max_work(T, 1);
   st = from_hip(launch_qgemm(g, T, items, prefill, s), "shared_expert gate/up");
@@ -136,6 +137,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   QGemmArgs h = g;
   h.x = act;
   h.x_ld = f;
+  h.x_by_slot = true;
   h.w0 = qw(down_);
   h.w1 = QWeights{};
   h.N = (int32_t)d;
@@ -199,8 +201,10 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   QGemmArgs g{};
   g.x = x;
   g.x_ld = d;
-  g.row_map = db.sorted;
+  g.row_map = nullptr;
   g.row_div = (int32_t)K;
+  g.x_by_slot = false;
+  g.out_by_flat = false;
   g.offsets = db.offsets;
   g.active = db.active;
   g.num_active = db.num_active;
@@ -216,7 +220,6 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   g.bits = w_.gate_proj.bits;
   g.out = act;
   g.out_ld = f;
-  g.out_map = nullptr;
   g.gated = true;
   Status st = from_hip(launch_qgemm(g, n, max_items, prefill, s),
                        "switch_mlp gate/up");
@@ -224,15 +227,14 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   QGemmArgs h = g;
   h.x = act;
   h.x_ld = f;
-  h.row_map = nullptr;
-  h.row_div = 1;
+  h.x_by_slot = true;
   h.w0 = qw(w_.down_proj);
   h.w1 = QWeights{};
   h.N = (int32_t)d;
   h.K = (int32_t)f;
   h.out = y;
   h.out_ld = d;
-  h.out_map = db.sorted;
+  h.out_by_flat = true;
   h.gated = false;
   return from_hip(launch_qgemm(h, n, max_items, prefill, s),
                   "switch_mlp down");

@@ -56,11 +56,8 @@ namespace {
 #define MLXR_STREAM_TT4_ROWS 4
 #endif
 constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
-// 16-channel blocks per wave, at most (gate/up, down): the gated kernel
-// moves twice the bytes per step and does best with one
-#ifndef MLXR_STREAM_MAX_NB_GATED
-#define MLXR_STREAM_MAX_NB_GATED 1
-#endif
+// 16-channel blocks per wave of the down kernel, at most (1 or 2); the
+// gated kernel moves twice the bytes per step and keeps one
 #ifndef MLXR_STREAM_MAX_NB
 #define MLXR_STREAM_MAX_NB 2
 #endif
@@ -216,7 +213,8 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
   const int item = blockIdx.x;
   const int ai = item / tiles_n, tile = item - ai * tiles_n;
   const int n_act = *a.num_work;
-  const int4 wk = reinterpret_cast<const int4*>(a.work)[ai];
+  const int32_t* rec = a.work + (int64_t)kWorkInts * ai;
+  const int4 wk = *reinterpret_cast<const int4*>(rec);
   if (ai >= n_act) return;
   const int e = wk.x, row0 = wk.y, rows = wk.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -236,7 +234,8 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
     int64_t xrow = 0;
     if (tv) {
       const int slot = row0 + tok;
-      xrow = a.row_map ? a.row_map[slot] / a.row_div : slot;
+      const int flat = rec[4 + tok];
+      xrow = a.x_by_slot ? slot : (a.row_map ? a.row_map[flat] : flat / a.row_div);
     }
     f32x4_t acc[CB][NM];
 #pragma unroll
@@ -365,7 +364,7 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
             a.out[(int64_t)slot * a.out_ld + ch] =
                 swiglu_bf16(bf16_round(s0[r]), bf16_round(s1[r]));
           } else {
-            const int64_t orow = a.out_map ? a.out_map[slot] : slot;
+            const int64_t orow = a.out_by_flat ? rec[4 + t] : slot;
             a.out[orow * a.out_ld + ch] = f32_to_bf16(s0[r]);
           }
         }
@@ -375,13 +374,20 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
   }
 }
 
-// Streaming decode GEMM for many (expert, row-tile) items.  One workgroup =
-// `waves` waves = one (active expert, tile of waves*16 output channels); wave
-// w owns one 16-channel block over the whole input dim, so no partial sums
-// cross waves.  Per chunk of up to TT of the expert's tokens the workgroup
-// stages x (bf16, in the MFMA operand order) and the per-group token sums X
-// in LDS once; each wave then streams its block's packed weights with D
-// super-steps of loads in flight (a register ring) and reads x from LDS.
+// Streaming decode GEMM for many (work item, channel tile) units.  One
+// workgroup = `waves` waves = one work item (at most 8 rows of one expert)
+// x one tile of waves*nb*16 output channels; wave w owns nb 16-channel
+// blocks over the whole input dim, so no partial sums cross waves.  The
+// workgroup stages the item's x rows (bf16, in the MFMA operand order) and
+// the per-group token sums X in LDS once; each wave then streams its
+// blocks' packed weights with D super-steps of loads in flight (a register
+// ring) and reads x from LDS.
+//
+// Prologue order: the work record (one scalar load: the expert and the flat
+// row of each slot, so the x rows need no further lookup), then the first D
+// weight super-steps, the wave's scales and biases and the x rows are all
+// issued before the first LDS store, so the weight stream starts one memory
+// round trip after the workgroup does.
 //
 // Block-diagonal MFMA: the 16 rows of the A operand are TT tokens x GG
 // groups (GG = 16 / TT).  Lane quarter q (l/16) supplies the codes of group
@@ -392,10 +398,14 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
 // lane loads 16*GG codes of its group (16 B per load).  Lanes that feed
 // zeros read a zero block in LDS.  The GG partial sums of a token meet by
 // cross-lane adds at the end.
-template <int BITS, bool GATED, int TT, int D>
-__device__ __forceinline__ void stream_body(const QGemmArgs& a, int tiles_n,
-                                            int nb, char* smem) {
+template <int BITS, bool GATED, int TT, int D, int NB>
+__device__ __forceinline__ void stream_body(const QGemmArgs& a,
+                                            const int32_t* rec, int4 wk,
+                                            int tile, char* smem) {
+  constexpr int nb = NB;
+  static_assert(kWorkRows <= 8, "an item of a >4-row expert fits TT = 8");
   constexpr int NM = GATED ? 2 : 1;
+  constexpr int NA = 2 * NM;            // scale and bias arrays
   constexpr int GG = 16 / TT;           // groups per MFMA
   constexpr int LPG = 4 / GG;           // lane quarters per group
   constexpr int CPL = 64 / LPG;         // codes per lane per super-step
@@ -403,28 +413,25 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a, int tiles_n,
   constexpr int NMF = CPL / 8;          // MFMAs per super-step
   constexpr int WPG = 2 * BITS;         // packed words per row and group
   const int waves = blockDim.x >> 6;
-  const int item = blockIdx.x;
-  const int ai = item / tiles_n, tile = item - ai * tiles_n;
-  const int n_act = *a.num_work;
-  const int4 wk = reinterpret_cast<const int4*>(a.work)[ai];
-  if (ai >= n_act) return;
-  const int e = wk.x, row0 = wk.y, rows = wk.z;
+  // items of experts with at most 4 rows run with TT = 4, the others with
+  // TT = 8 >= kWorkRows: an item is always one pass
+  const int e = wk.x, row0 = wk.y, nt = min(wk.z, TT);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, q = lane >> 4;
   const int gq = q / LPG, sq = q % LPG;  // this lane's group, its part
   const int K = a.K, groups = K >> 6;
   const int ssteps = groups / GG;  // the host runs this kernel when GG | groups
   const int total = nb * ssteps;   // super-steps of this wave, all blocks
-  // LDS: x chunk [TT][K + 8] bf16 (rows padded 16 B), 16 B zero block,
-  // X [groups][TT] f32
+  // LDS: x [TT][K + 8] bf16 (rows padded 16 B), 16 B zero block,
+  // X [groups][TT] f32, then per wave its scales and biases
   const int xs = K + 8;
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem);
   char* zero_blk = smem + (size_t)TT * xs * 2;
   float* Xl = reinterpret_cast<float*>(zero_blk + 16);
-  // per-block partial sums [waves][nb][NM][64] after X (16-byte aligned)
-  f32x4_t* red = reinterpret_cast<f32x4_t*>(
-      smem + (((size_t)TT * xs * 2 + 16 + (size_t)groups * TT * 4 + 15) & ~size_t(15)));
+  char* sb_base =
+      smem + (((size_t)TT * xs * 2 + 16 + (size_t)groups * TT * 4 + 15) & ~size_t(15));
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  const u32x4_t zq = {0u, 0u, 0u, 0u};
   // this wave's blocks: nb consecutive 16-channel blocks from ch0
   const int ch0 = ((tile * waves + wave) * nb) * 16 + n;
   const int64_t wrow0 = (int64_t)e * a.N + ch0;
@@ -455,191 +462,224 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a, int tiles_n,
       for (int i = 0; i < NL; ++i) r.w[m][i] = wp[i];
     }
   };
-  // Scales and biases of this wave's blocks: 16 rows x groups bf16 per
-  // block and array, contiguous in memory.  They are copied to LDS once with
-  // 16-byte loads (the hot loop then reads its two values per step from
-  // LDS): a per-step 2-byte load per lane would touch 16 cache lines for
-  // 128 useful bytes.
-  const int sbn = nb * 16 * groups;  // bf16 per array
-  uint16_t* sbl = reinterpret_cast<uint16_t*>(
-      reinterpret_cast<char*>(red) + (size_t)waves * nb * NM * 64 * sizeof(f32x4_t)) +
-      (size_t)wave * NM * 2 * sbn;
-  const uint32_t one_v = 0x3F803F80u;
+  Ring ring[R];
+#pragma unroll
+  for (int j = 0; j < D; ++j) load(ring[j], min(j, total - 1));
 
-  for (int tt = 0; tt < rows; tt += TT) {
-    const int nt = min(TT, rows - tt);
-    // x first (the compute waits on it), then the first D weight steps
-    const int per_row = K >> 3;
-    int64_t xr[TT];
+  // Scales and biases of this wave's blocks: 16 rows x groups bf16 per
+  // block and array, contiguous in memory, copied to LDS with 16-byte loads
+  // (the hot loop then reads its two values per step from LDS): a per-step
+  // 2-byte load per lane would touch 16 cache lines for 128 useful bytes.
+  const int sbn = nb * 16 * groups;  // bf16 per array
+  const int sbv = sbn >> 3;          // 16-byte vectors per array
+  uint16_t* sbl = reinterpret_cast<uint16_t*>(sb_base) + (size_t)wave * NA * sbn;
+  const uint16_t* sbsrc[NA];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const QWeights& W = m == 0 ? a.w0 : a.w1;
+    sbsrc[2 * m] = W.scales + (wrow0 - n) * groups;
+    sbsrc[2 * m + 1] = W.biases + (wrow0 - n) * groups;
+  }
+  u32x4_t sv[NA];
+  const bool s_in = lane < sbv;
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+    sv[i] = s_in ? *reinterpret_cast<const u32x4_t*>(sbsrc[i] + 8 * lane) : zq;
+
+  // x rows of the item's tokens, from the record
+  int64_t xr[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    int64_t r = 0;
+    if (t < nt) {
+      const int slot = row0 + t;
+      const int flat = rec[4 + t];
+      r = a.x_by_slot ? slot : (a.row_map ? a.row_map[flat] : flat / a.row_div);
+    }
+    xr[t] = r;
+  }
+  // thread k8 holds elements 8*k8..8*k8+7 of every token; the token sums X
+  // of each 64-wide group come from the 8 threads sharing it
+  const int per_row = K >> 3;
+  auto load_x = [&](int k8, u32x4_t (&v)[TT]) {
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      const int slot = row0 + tt + t;
-      xr[t] = t < nt ? (a.row_map ? a.row_map[slot] / a.row_div : slot) : 0;
+      v[t] = zq;
+      if (t < nt)
+        v[t] = *reinterpret_cast<const u32x4_t*>(a.x + xr[t] * a.x_ld + 8 * k8);
     }
-    // stage x: thread k8 holds elements 8*k8..8*k8+7 of every token of the
-    // chunk; the token sums X of each 64-wide group come from the 8 threads
-    // sharing it
-    for (int k8 = threadIdx.x; k8 < per_row; k8 += blockDim.x) {
-      u32x4_t v[TT];
+  };
+  auto stage_x = [&](int k8, const u32x4_t (&v)[TT]) {
 #pragma unroll
-      for (int t = 0; t < TT; ++t) {
-        v[t] = u32x4_t{0u, 0u, 0u, 0u};
-        if (t < nt)
-          v[t] = *reinterpret_cast<const u32x4_t*>(a.x + xr[t] * a.x_ld + 8 * k8);
-      }
+    for (int t = 0; t < TT; ++t) {
+      float sx = 0.0f;
 #pragma unroll
-      for (int t = 0; t < TT; ++t) {
-        float sx = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          sx += __uint_as_float(v[t][j] << 16) + __uint_as_float(v[t][j] & 0xffff0000u);
-        sx += __shfl_xor(sx, 1, 64);
-        sx += __shfl_xor(sx, 2, 64);
-        sx += __shfl_xor(sx, 4, 64);
-        if ((k8 & 7) == 0) Xl[(k8 >> 3) * TT + t] = sx;
-        u32x4_t w = v[t];
-        if constexpr (BITS == 4) w = perm4(w);
-        *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = w;
-      }
+      for (int j = 0; j < 4; ++j)
+        sx += __uint_as_float(v[t][j] << 16) + __uint_as_float(v[t][j] & 0xffff0000u);
+      sx += __shfl_xor(sx, 1, 64);
+      sx += __shfl_xor(sx, 2, 64);
+      sx += __shfl_xor(sx, 4, 64);
+      if ((k8 & 7) == 0) Xl[(k8 >> 3) * TT + t] = sx;
+      u32x4_t w = v[t];
+      if constexpr (BITS == 4) w = perm4(w);
+      *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = w;
     }
-    if (tt == 0) {
+  };
+  {
+    // first chunk: every load above is in flight before the first store
+    const int k8 = threadIdx.x;
+    u32x4_t v[TT];
+    const bool x_in = k8 < per_row;
+    if (x_in) load_x(k8, v);
+    if (s_in) {
+#pragma unroll
+      for (int i = 0; i < NA; ++i)
+        *reinterpret_cast<u32x4_t*>(sbl + i * sbn + 8 * lane) = sv[i];
+    }
+    if (x_in) stage_x(k8, v);  // per_row is a multiple of 8: whole octets
+  }
+  // the rest (input dims above 64 * 8 * waves, or long scale rows)
+  for (int i = lane + 64; i < sbv; i += 64) {
+#pragma unroll
+    for (int j = 0; j < NA; ++j)
+      *reinterpret_cast<u32x4_t*>(sbl + j * sbn + 8 * i) =
+          *reinterpret_cast<const u32x4_t*>(sbsrc[j] + 8 * i);
+  }
+  for (int k8 = threadIdx.x + blockDim.x; k8 < per_row; k8 += blockDim.x) {
+    u32x4_t v[TT];
+    load_x(k8, v);
+    stage_x(k8, v);
+  }
+  if (threadIdx.x == 0) *reinterpret_cast<u32x4_t*>(zero_blk) = zq;
+  __syncthreads();
+
+  // The loop issues the same loads every super-step (past the end they
+  // repeat the last step, a cache hit) and holds no stores, so the
+  // compiler can wait for exactly the oldest ring slot.  Steps past the
+  // end multiply zeros.  With two blocks per wave the first block's sums
+  // move to `first` when its last step is done.
+  f32x4_t acc[NM], first[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) acc[m] = first[m] = zero;
+  const uint32_t one_v = 0x3F803F80u;
+  // x operand source of this lane: its row's token chunk in its group's
+  // codes, or the zero block off the diagonal / past the tokens
+  const bool diag = arow_g == gq && arow_t < nt;
+  const char* xsrc = smem + ((size_t)arow_t * xs + sq * CPL) * 2;
+  for (int gs0 = 0; gs0 < total; gs0 += R) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int gs = gs0 + j;
+      load(ring[(j + D) % R], min(gs + D, total - 1));
+      const Ring& cur = ring[j];
+      const bool live = gs < total;
+      const int bi = gs / ssteps, ss = gs - bi * ssteps;
+      const int g = ss * GG + gq;
+      const bool on = diag && live;
+      const char* xp = on ? xsrc + (size_t)(64 * g) * 2 : zero_blk;
+      const int xstep = on ? 16 : 0;
+      // all x fragments of the step are read before the first MFMA, so
+      // the MFMA chain waits on LDS once per step, not once per MFMA
+      bf16x8_t xa[NMF];
+#pragma unroll
+      for (int i = 0; i < NMF; ++i)
+        xa[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xp + xstep * i));
+      // X of this lane's output rows: group (4q+r)/TT, tokens (4q+r)%TT
+      const int og = ss * GG + (4 * q) / TT;
+      f32x4_t X = *reinterpret_cast<const f32x4_t*>(Xl + og * TT + (4 * q) % TT);
+      if (!live) X = zero;
+      MLXR_SCHED_BARRIER();
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        const QWeights& W = m == 0 ? a.w0 : a.w1;
-        const uint16_t* s0 = W.scales + (wrow0 - n) * groups;
-        const uint16_t* b0 = W.biases + (wrow0 - n) * groups;
-        for (int i = lane; i < sbn / 8; i += 64) {
-          *reinterpret_cast<u32x4_t*>(sbl + (m * 2) * sbn + 8 * i) =
-              *reinterpret_cast<const u32x4_t*>(s0 + 8 * i);
-          *reinterpret_cast<u32x4_t*>(sbl + (m * 2 + 1) * sbn + 8 * i) =
-              *reinterpret_cast<const u32x4_t*>(b0 + 8 * i);
+        f32x4_t P = zero;
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          u32x4_t u;
+          if constexpr (BITS == 4) {
+            u = unpack4(cur.w[m][i / 4][i % 4], one_v);
+          } else {
+            const u32x4_t wv = cur.w[m][i / 2];
+            u = (i & 1) ? unpack8(wv.z, wv.w) : unpack8(wv.x, wv.y);
+          }
+          P = mfma16x16x32(xa[i], as_bf16x8(u), P);
         }
+        // scale/bias of this lane's output group og (channel n)
+        const int si = ((live ? bi : 0) * 16 + n) * groups + min(og, groups - 1);
+        const uint32_t sc_bits = sbl[(m * 2) * sbn + si];
+        const uint32_t bi_bits = sbl[(m * 2 + 1) * sbn + si];
+        float sc, cb;
+        group_terms<BITS>(sc_bits, bi_bits, sc, cb);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[m][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(cb, X[r], acc[m][r]));
+      }
+      if constexpr (NB == 2) {
+        const bool done0 = live && bi == 0 && ss == ssteps - 1;
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            first[m][r] = done0 ? acc[m][r] : first[m][r];
+            acc[m][r] = done0 ? 0.0f : acc[m][r];
+          }
       }
     }
-    Ring ring[R];
+  }
+  // Each token's GG group partials sit on lanes 16*(TT/4) apart: a
+  // butterfly over those lanes sums them, and lanes q < TT/4 write tokens
+  // 4q..4q+3 of channel n.
 #pragma unroll
-    for (int j = 0; j < D; ++j) load(ring[j], min(j, total - 1));
-    if (threadIdx.x == 0)
-      *reinterpret_cast<u32x4_t*>(zero_blk) = u32x4_t{0u, 0u, 0u, 0u};
-    __syncthreads();
-
-    // The loop issues the same loads every super-step (past the end they
-    // repeat the last step, a cache hit) and holds no stores, so the
-    // compiler can wait for exactly the oldest ring slot.  Steps past the
-    // end multiply zeros.  Each block's partial sums go to LDS (red) and
-    // are combined after the loop.
-    f32x4_t acc[NM];
+  for (int bi = 0; bi < NB; ++bi) {
+    f32x4_t tot[NM];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) acc[m] = zero;
-    // x operand source of this lane: its row's token chunk in its group's
-    // codes, or the zero block off the diagonal / past the tokens
-    const bool diag = arow_g == gq && arow_t < nt;
-    const char* xsrc = smem + ((size_t)arow_t * xs + sq * CPL) * 2;
-    for (int gs0 = 0; gs0 < total; gs0 += R) {
+    for (int m = 0; m < NM; ++m) {
+      tot[m] = (NB == 2 && bi == 0) ? first[m] : acc[m];
 #pragma unroll
-      for (int j = 0; j < R; ++j) {
-        const int gs = gs0 + j;
-        load(ring[(j + D) % R], min(gs + D, total - 1));
-        const Ring& cur = ring[j];
-        const bool live = gs < total;
-        const int bi = gs / ssteps, ss = gs - bi * ssteps;
-        const int g = ss * GG + gq;
-        const bool on = diag && live;
-        const char* xp = on ? xsrc + (size_t)(64 * g) * 2 : zero_blk;
-        const int xstep = on ? 16 : 0;
-        // all x fragments of the step are read before the first MFMA, so
-        // the MFMA chain waits on LDS once per step, not once per MFMA
-        bf16x8_t xa[NMF];
-#pragma unroll
-        for (int i = 0; i < NMF; ++i)
-          xa[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xp + xstep * i));
-        // X of this lane's output rows: group (4q+r)/TT, tokens (4q+r)%TT
-        const int og = ss * GG + (4 * q) / TT;
-        f32x4_t X = *reinterpret_cast<const f32x4_t*>(Xl + og * TT + (4 * q) % TT);
-        if (!live) X = zero;
-        MLXR_SCHED_BARRIER();
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          f32x4_t P = zero;
-#pragma unroll
-          for (int i = 0; i < NMF; ++i) {
-            u32x4_t u;
-            if constexpr (BITS == 4) {
-              u = unpack4(cur.w[m][i / 4][i % 4], one_v);
-            } else {
-              const u32x4_t wv = cur.w[m][i / 2];
-              u = (i & 1) ? unpack8(wv.z, wv.w) : unpack8(wv.x, wv.y);
-            }
-            P = mfma16x16x32(xa[i], as_bf16x8(u), P);
-          }
-          // scale/bias of this lane's output group og (channel n)
-          const int si = ((live ? bi : 0) * 16 + n) * groups + min(og, groups - 1);
-          const uint32_t sv = sbl[(m * 2) * sbn + si];
-          const uint32_t bv = sbl[(m * 2 + 1) * sbn + si];
-          float sc, cb;
-          group_terms<BITS>(sv, bv, sc, cb);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[m][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(cb, X[r], acc[m][r]));
-        }
-        if (live && ss == ssteps - 1) {
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            red[((wave * nb + bi) * NM + m) * 64 + lane] = acc[m];
-            acc[m] = zero;
-          }
-        }
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (TT == 4) tot[m][r] += __shfl_xor(tot[m][r], 16, 64);
+        tot[m][r] += __shfl_xor(tot[m][r], 32, 64);
       }
     }
-    // Each token's GG group partials sit on lanes 16*(TT/4) apart; lanes
-    // q < TT/4 add them up and write tokens 4q..4q+3 of channel n.
     if (q < TT / 4) {
-      for (int bi = 0; bi < nb; ++bi) {
-        f32x4_t tot[NM];
+      const int ch = ch0 + bi * 16;
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          const f32x4_t* rp = red + ((wave * nb + bi) * NM + m) * 64 + n;
-          tot[m] = zero;
-#pragma unroll
-          for (int qq = q; qq < 4; qq += TT / 4) tot[m] += rp[16 * qq];
-        }
-        const int ch = ch0 + bi * 16;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 4 * q + r;
-          if (t < nt) {
-            const int slot = row0 + tt + t;
-            if constexpr (GATED) {
-              a.out[(int64_t)slot * a.out_ld + ch] =
-                  swiglu_bf16(bf16_round(tot[0][r]), bf16_round(tot[1][r]));
-            } else {
-              const int64_t orow = a.out_map ? a.out_map[slot] : slot;
-              a.out[orow * a.out_ld + ch] = f32_to_bf16(tot[0][r]);
-            }
+      for (int r = 0; r < 4; ++r) {
+        const int t = 4 * q + r;
+        if (t < nt) {
+          const int slot = row0 + t;
+          if constexpr (GATED) {
+            a.out[(int64_t)slot * a.out_ld + ch] =
+                swiglu_bf16(bf16_round(tot[0][r]), bf16_round(tot[1][r]));
+          } else {
+            const int64_t orow = a.out_by_flat ? rec[4 + t] : slot;
+            a.out[orow * a.out_ld + ch] = f32_to_bf16(tot[0][r]);
           }
         }
       }
     }
-    __syncthreads();  // the next chunk overwrites the LDS tiles
   }
 }
 
-// Tokens per pass follow the expert's row count: 4 (one pass for up to 4
-// rows, GG = 4) or 8 (GG = 2).  LDS is sized for 8.
-template <int BITS, bool GATED, int D>
+// Tokens per pass follow the expert's row count: 4 (GG = 4) for experts
+// with at most MLXR_STREAM_TT4_ROWS rows, else 8 (GG = 2).  LDS is sized
+// for 8.
+template <int BITS, bool GATED, int D, int NB>
 __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
-    QGemmArgs a, int tiles_n, int nb) {
+    QGemmArgs a, int tiles_n) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int ai = blockIdx.x / tiles_n;
+  const int ai = blockIdx.x / tiles_n, tile = blockIdx.x - ai * tiles_n;
+  const int n_act = *a.num_work;
+  const int32_t* rec = a.work + (int64_t)kWorkInts * ai;
+  const int4 wk = *reinterpret_cast<const int4*>(rec);
+  if (ai >= n_act) return;
   // The MFMA form follows the expert's row count (not the item's), so every
   // token of an expert is summed in the same order, wherever its item
   // boundaries fall.  The 8-token form moves half the bytes per super-step:
   // twice the depth.
-  const int expert_rows = reinterpret_cast<const int4*>(a.work)[ai].w;
-  if (expert_rows <= MLXR_STREAM_TT4_ROWS)
-    stream_body<BITS, GATED, 4, D>(a, tiles_n, nb, smem);
+  if (wk.w <= MLXR_STREAM_TT4_ROWS)
+    stream_body<BITS, GATED, 4, D, NB>(a, rec, wk, tile, smem);
   else
-    stream_body<BITS, GATED, 8, 2 * D>(a, tiles_n, nb, smem);
+    stream_body<BITS, GATED, 8, 2 * D, NB>(a, rec, wk, tile, smem);
 }
 
 }  // namespace
@@ -665,7 +705,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     // staged as few times as the GPU allows
     const int64_t per_tile = a.N / (16 * kWaves);
     int nb = 1;
-    for (int c = a.gated ? MLXR_STREAM_MAX_NB_GATED : MLXR_STREAM_MAX_NB; c > 1; --c)
+    for (int c = a.gated ? 1 : MLXR_STREAM_MAX_NB; c > 1; --c)
       if (per_tile % c == 0 && max_items * (per_tile / c) >= kStreamSlots) {
         nb = c;
         break;
@@ -674,22 +714,25 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     const size_t lds =
         (((size_t)kMaxTT * (a.K + 8) * 2 + 16 + (size_t)groups * kMaxTT * 4 + 15) &
          ~size_t(15)) +
-        (size_t)kWaves * nb * (a.gated ? 2 : 1) * 64 * sizeof(f32x4_t) +
         (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
     const dim3 grid((unsigned)(max_items * tiles_n));
     ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
-#define MLXR_QS(B, G, D) \
-  qgemm_stream_kernel<B, G, D><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, nb)
+#define MLXR_QS(B, G, D, NB) \
+  qgemm_stream_kernel<B, G, D, NB><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n)
     if (a.bits == 4) {
       if (a.gated)
-        MLXR_QS(4, true, MLXR_STREAM_DEPTH4);
+        MLXR_QS(4, true, MLXR_STREAM_DEPTH4, 1);
+      else if (nb == 2)
+        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 2);
       else
-        MLXR_QS(4, false, MLXR_STREAM_DEPTH4);
+        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 1);
     } else {
       if (a.gated)
-        MLXR_QS(8, true, MLXR_STREAM_DEPTH8);
+        MLXR_QS(8, true, MLXR_STREAM_DEPTH8, 1);
+      else if (nb == 2)
+        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, 2);
       else
-        MLXR_QS(8, false, MLXR_STREAM_DEPTH8);
+        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, 1);
     }
 #undef MLXR_QS
     return hipGetLastError();

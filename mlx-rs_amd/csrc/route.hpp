@@ -114,6 +114,7 @@ struct DispatchScratch {
   uint16_t tab[kDispatchBlock / 64][kMaxExperts];
   int wsum[kDispatchBlock / 64 + 1];
   int off[kMaxExperts];
+  int wpos[kMaxExperts];
 };
 
 // Exclusive scan of one int per thread over a 1024-thread workgroup.
@@ -146,8 +147,9 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* total,
 }
 
 // Stable counting sort of ids[0..n) (n <= 1024, read by thread i) by expert
-// in [0, E): counts, offsets, the active-expert list, the M-tile list and
-// sorted/inv, exactly the permutation of a stable argsort.  Ids of -1 are
+// in [0, E): counts, offsets, the active-expert list, the work item records,
+// the M-tile list and sorted/inv, exactly the permutation of a stable
+// argsort.  Ids of -1 are
 // left out silently; other ids outside [0, E) are left out and flag
 // *status.  Every thread of the 1024-thread workgroup must call it.
 __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
@@ -195,8 +197,9 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
   const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
   int n_work;
   const int wpos = block_exclusive_scan(nw, &n_work, ls->wsum);
+  if (tid < E) ls->wpos[tid] = wpos;
   for (int j = 0; j < nw; ++j) {
-    int32_t* w = b.work + 4 * (wpos + j);
+    int32_t* w = b.work + kWorkInts * (wpos + j);
     w[0] = tid;
     w[1] = off + j * kWorkRows;
     w[2] = min(kWorkRows, cnt - j * kWorkRows);
@@ -213,9 +216,12 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
   if (tid == 0) *b.num_tiles = n_tiles;
   __syncthreads();
   if (ok) {
-    const int pos = ls->off[id] + ls->tab[wave][id] + r;
+    const int rank = ls->tab[wave][id] + r;
+    const int pos = ls->off[id] + rank;
     b.sorted[pos] = tid;
     b.inv[tid] = pos;
+    b.work[kWorkInts * (ls->wpos[id] + rank / kWorkRows) + 4 +
+           rank % kWorkRows] = tid;
   }
 }
 
