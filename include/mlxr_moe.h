@@ -103,6 +103,16 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
                         void* workspace, size_t workspace_size,
                         mlxr_moe_stream stream);
 
+/* Which numerics a gather_qmm (or a SplitSwitchFfn / shared-expert GEMM) of
+ * `rows` flat rows over `num_experts` experts uses (no counterpart in the
+ * reference, whose MLX backend makes the same kind of choice inside
+ * mlx_gather_qmm): 1 = the M-tiled kernel, whose weight tiles are
+ * dequantised to bf16 -- gather_mm(x, dequantize(w)^T), as the reference's
+ * test states gather_qmm (crates/mlxr/src/ops/quantization.rs:344-421);
+ * 0 = the streaming kernel, which keeps the dequantised weights in f32.
+ * Both accumulate in f32.  Returns -1 for negative sizes. */
+int mlxr_moe_gather_qmm_tiled(int64_t rows, int64_t num_experts);
+
 /* Indices that partition each row of a [rows, n] f32 (axis = -1 or 1):
  * out[.., kth] holds the element of sorted rank kth, smaller before, larger
  * after (the full ascending order, ties by index, is returned).  kth in

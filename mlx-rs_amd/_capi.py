@@ -91,6 +91,7 @@ SIGNATURES = {
     "mlxr_moe_block_workspace_size": (c_size_t, [POINTER(Block), c_int64]),
     "mlxr_moe_block_forward": (c_int, [POINTER(Block), P, c_int64, P, P, P, P, c_size_t, P]),
     "mlxr_moe_workspace_status": (c_int, [P, c_size_t, P]),
+    "mlxr_moe_gather_qmm_tiled": (c_int, [c_int64, c_int64]),
     "mlxr_moe_profile_start": (c_int, [c_char_p]),
     "mlxr_moe_profile_stop": (c_int, [POINTER(c_int64), POINTER(c_double), POINTER(c_double),
                                       POINTER(c_double)]),

@@ -28,6 +28,7 @@ SOURCES = [
     "router.hip",
     "dispatch.hip",
     "qgemm.hip",
+    "prefill.hip",
     "combine.hip",
     "nn.cpp",
     "profile.cpp",

@@ -212,6 +212,7 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   a.num_work = db.num_work;
   a.tiles = db.tiles;
   a.num_tiles = db.num_tiles;
+  a.sorted = db.sorted;
   a.w0 = QWeights{w, static_cast<const uint16_t*>(scales),
                   static_cast<const uint16_t*>(biases)};
   a.E = (int32_t)E;
@@ -225,6 +226,11 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
   return finish(from_hip(launch_qgemm(a, R, dispatch_max_work(R, E),
                                       nn::use_prefill_path(R, E), s),
                          "gather_qmm"));
+}
+
+int mlxr_moe_gather_qmm_tiled(int64_t rows, int64_t num_experts) {
+  if (rows < 0 || num_experts < 0) return -1;
+  return nn::use_prefill_path(rows, num_experts) ? 1 : 0;
 }
 
 int mlxr_moe_argpartition(const float* a, int64_t rows, int64_t n, int kth,

@@ -182,6 +182,10 @@ __global__ __launch_bounds__(256) void dispatch_identity_kernel(
     b.tiles[2 * j] = 0;
     b.tiles[2 * j + 1] = j * tile_rows;
   }
+  for (int i = tid; i < n; i += 256) {
+    b.sorted[i] = i;
+    b.inv[i] = i;
+  }
   for (int j = tid; j * kWorkRows < n; j += 256) {
     int32_t* w = b.work + kWorkInts * j;
     w[0] = 0;

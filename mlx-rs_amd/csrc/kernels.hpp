@@ -135,6 +135,7 @@ struct QGemmArgs {
   const int32_t* num_work;
   const int32_t* tiles;    // M-tile list (prefill path)
   const int32_t* num_tiles;
+  const int32_t* sorted;   // flat row of each sorted slot (prefill path)
   QWeights w0;             // gate (or the only projection)
   QWeights w1;             // up (gated mode only)
   int32_t E, N, K, bits;
@@ -145,11 +146,20 @@ struct QGemmArgs {
 };
 // Largest input dim (K) of a projection: 8 waves x 8 groups of 64.
 constexpr int kMaxInputDims = 4096;
-// Rows per M-tile of the prefill kernel; the dispatch builds its tile list.
+// Rows per M-tile of the prefill kernel (64 per wave along M); the dispatch
+// builds its tile list.  Waves along N: 64 B columns each.
 constexpr int kPrefillTileRows = 128;
-// max_items bounds the number of work items (dispatch_max_work).
+constexpr int kPrefillWavesN = 2;
+// max_items bounds the number of work items (dispatch_max_work); prefill
+// selects the M-tiled kernel (prefill.hip) where it applies.
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s);
+
+// ---------------------------------------------------------------- prefill.hip
+bool prefill_supported(const QGemmArgs& a);
+// max_tiles bounds the M-tile list (dispatch_max_tiles).
+hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t max_tiles,
+                                hipStream_t s);
 
 // -------------------------------------------------------------- combine.hip
 hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,

@@ -66,9 +66,8 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
 namespace nn {
 
 bool use_prefill_path(int64_t rows, int64_t experts) {
-  (void)rows;
-  (void)experts;
-  return false;
+  // the M-tiled kernel pays once the experts average a quarter tile
+  return rows >= (int64_t)(kPrefillTileRows / 4) * experts;
 }
 
 namespace {
@@ -122,6 +121,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.num_work = db.num_work;
   g.tiles = db.tiles;
   g.num_tiles = db.num_tiles;
+  g.sorted = db.sorted;
   g.w0 = qw(gate_);
   g.w1 = qw(up_);
   g.E = 1;
@@ -212,6 +212,7 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   g.num_work = db.num_work;
   g.tiles = db.tiles;
   g.num_tiles = db.num_tiles;
+  g.sorted = db.sorted;
   g.w0 = qw(w_.gate_proj);
   g.w1 = qw(w_.up_proj);
   g.E = (int32_t)E;

@@ -238,6 +238,17 @@ def combine(y: torch.Tensor, weights: torch.Tensor, shared_y=None, shared_logit=
     return out
 
 
+def gather_qmm_tiled(rows: int, num_experts: int) -> bool:
+    """True when a gather_qmm of `rows` flat rows over `num_experts` experts
+    runs the M-tiled kernel (weights dequantised to bf16 tiles, the
+    gather_mm(x, dequantize(w)) numerics), False for the streaming kernel
+    (weights dequantised in f32)."""
+    rc = C.lib().mlxr_moe_gather_qmm_tiled(int(rows), int(num_experts))
+    if rc < 0:
+        raise MlxrMoeError("gather_qmm_tiled: negative size")
+    return bool(rc)
+
+
 def workspace_status(ws: torch.Tensor) -> int:
     """Device status word of a call's workspace (1 = an index was out of
     range).  Synchronises the current stream."""

@@ -32,7 +32,9 @@
  *   orc_router_topk   full sort on small E, softmax sums to 1, renorm.
  *   orc_dispatch      equals a stable argsort (switch.rs:499-512), inverse.
  *   orc_gather_qmm    equals gather_mm(x, dequant(w)^T) in fp64
- *                     (quantization.rs:344-421), lhs/rhs index cases.
+ *                     (quantization.rs:344-421), lhs/rhs index cases;
+ *                     the tiled form bit-for-bit equals that gather_mm on
+ *                     bf16 weights up to f32 accumulation (fp64 bound).
  *   orc_swiglu        reference test activations.rs:341-351.
  *   orc_block_forward sorted and unsorted dispatch give identical outputs
  *                     (switch.rs:446-474); K=1 reduces to one expert;
@@ -267,10 +269,21 @@ int orc_dispatch(const int32_t* ids, int64_t n, int64_t E, int32_t* counts,
 }
 
 /* ----------------------------------------------------------- gather_qmm */
+/* gather_qmm has two numerics, as MLX's has (its matrix-vector kernels for
+ * few rows per expert, its tiled matrix-matrix kernels for many):
+ *   vector form  each weight is fmaf(code, scale, bias) in f32;
+ *   tiled form   each weight is that value rounded to bf16 first -- the
+ *                weight tile is dequantised into the activation dtype, and
+ *                the product is gather_mm(x, dequantize(w)^T), which is how
+ *                the reference's own test defines gather_qmm
+ *                (quantization.rs:344-421).
+ * Both accumulate in f32.  The GPU picks the form per GEMM from the rows per
+ * expert (mlxr_moe_gather_qmm_tiled); the checks pass the same choice. */
 /* One output element: x (already f32) . dequant(weight row), f32
  * accumulation in 8 interleaved partial sums. */
 static float qdot(const float* xf, const uint32_t* wrow, const uint16_t* srow,
-                  const uint16_t* brow, int64_t Kd, int gs, int bits) {
+                  const uint16_t* brow, int64_t Kd, int gs, int bits,
+                  int tiled) {
   const int per_word = 32 / bits;
   const uint32_t mask = (1u << bits) - 1u;
   float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -282,7 +295,8 @@ static float qdot(const float* xf, const uint32_t* wrow, const uint16_t* srow,
     for (int wi = 0; wi < gs / per_word; ++wi) {
       uint32_t word = wg[wi];
       for (int k = 0; k < per_word; ++k) {
-        const float wv = fmaf((float)((word >> (k * bits)) & mask), s, b);
+        float wv = fmaf((float)((word >> (k * bits)) & mask), s, b);
+        if (tiled) wv = orc_bf16_to_f32(orc_f32_to_bf16(wv));
         part[k & 7] = fmaf(xg[wi * per_word + k], wv, part[k & 7]);
       }
     }
@@ -293,12 +307,12 @@ static float qdot(const float* xf, const uint32_t* wrow, const uint16_t* srow,
 
 /* y[n] = bf16(x . dequant(W[e, n])) for n in [0, N) */
 static void qmv(const float* xf, const orc_qlinear* q, int64_t e, int64_t N,
-                int64_t Kd, int gs, int bits, uint16_t* y) {
+                int64_t Kd, int gs, int bits, int tiled, uint16_t* y) {
   const int64_t wpr = Kd * bits / 32, gpr = Kd / gs;
   for (int64_t n = 0; n < N; ++n) {
     const int64_t row = e * N + n;
     y[n] = orc_f32_to_bf16(qdot(xf, q->w + row * wpr, q->scales + row * gpr,
-                                q->biases + row * gpr, Kd, gs, bits));
+                                q->biases + row * gpr, Kd, gs, bits, tiled));
   }
 }
 
@@ -306,7 +320,8 @@ int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
                    const uint32_t* w, const uint16_t* scales,
                    const uint16_t* biases, int64_t E, int64_t N,
                    const int32_t* lhs, const int32_t* rhs, int64_t B,
-                   int group_size, int bits, uint16_t* out, int nthreads) {
+                   int group_size, int bits, int tiled, uint16_t* out,
+                   int nthreads) {
   if (!valid_quant(group_size, bits) || Kd % group_size) return -1;
   if (!lhs && (x_batch <= 0 || B % x_batch)) return -1;
   for (int64_t b = 0; b < B; ++b) {
@@ -323,7 +338,7 @@ int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
     float* xf = (float*)malloc(sizeof(float) * (size_t)Kd);
     for (int64_t j = 0; j < Kd; ++j)
       xf[j] = orc_bf16_to_f32(x[(xb * M + m) * Kd + j]);
-    qmv(xf, &q, rhs[b], N, Kd, group_size, bits, out + bm * N);
+    qmv(xf, &q, rhs[b], N, Kd, group_size, bits, tiled, out + bm * N);
     free(xf);
   }
   return 0;
@@ -375,16 +390,16 @@ void orc_combine(const uint16_t* y, const float* w, int64_t T, int64_t K,
 /* One expert FFN on one token: y = down(swiglu(gate(x), up(x))). */
 static void expert_ffn(const float* xf, const orc_qlinear* g,
                        const orc_qlinear* u, const orc_qlinear* dn, int64_t e,
-                       int64_t d, int64_t f, int gs, int bits, uint16_t* y,
-                       uint16_t* gb, uint16_t* ub, float* af) {
-  qmv(xf, g, e, f, d, gs, bits, gb);
-  qmv(xf, u, e, f, d, gs, bits, ub);
+                       int64_t d, int64_t f, int gs, int bits, int tiled,
+                       uint16_t* y, uint16_t* gb, uint16_t* ub, float* af) {
+  qmv(xf, g, e, f, d, gs, bits, tiled, gb);
+  qmv(xf, u, e, f, d, gs, bits, tiled, ub);
   for (int64_t n = 0; n < f; ++n) {
     uint16_t a = orc_f32_to_bf16(
         swiglu1(orc_bf16_to_f32(gb[n]), orc_bf16_to_f32(ub[n])));
     af[n] = orc_bf16_to_f32(a);
   }
-  qmv(af, dn, e, d, f, gs, bits, y);
+  qmv(af, dn, e, d, f, gs, bits, tiled, y);
 }
 
 int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
@@ -435,14 +450,16 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
         last_t = t;
       }
       expert_ffn(xf, &blk->gate_proj, &blk->up_proj, &blk->down_proj,
-                 idx[tk], d, f, gs, bits, y + tk * d, gb, ub, af);
+                 idx[tk], d, f, gs, bits, blk->switch_tiled, y + tk * d, gb,
+                 ub, af);
     }
     if (fs) {
 #pragma omp for schedule(dynamic, 1)
       for (int64_t t = 0; t < T; ++t) {
         for (int64_t j = 0; j < d; ++j) xf[j] = orc_bf16_to_f32(x[t * d + j]);
         expert_ffn(xf, &blk->shared_gate, &blk->shared_up, &blk->shared_down,
-                   0, d, fs, gs, bits, sy + t * d, gb, ub, af);
+                   0, d, fs, gs, bits, blk->shared_tiled, sy + t * d, gb, ub,
+                   af);
       }
     }
     free(xf);

@@ -71,12 +71,16 @@ int orc_dispatch(const int32_t* ids, int64_t n, int64_t E, int32_t* counts,
  *   out[b, m, :] = x[xb(b), m, :] . dequant(w[rhs[b]])^T
  * x bf16 [x_batch, M, Kd]; w u32 [E, N, Kd*bits/32]; scales/biases bf16
  * [E, N, Kd/group]; xb(b) = lhs[b] if lhs else b / (B / x_batch).
- * fp32 accumulation, bf16 output [B, M, N].  Returns 0 or -1. */
+ * fp32 accumulation, bf16 output [B, M, N].  tiled = 0: weights
+ * dequantised in f32 (vector form); tiled = 1: dequantised weights rounded
+ * to bf16 first (tiled form, gather_mm(x, dequantize(w)^T)).  Returns 0 or
+ * -1. */
 int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
                    const uint32_t* w, const uint16_t* scales,
                    const uint16_t* biases, int64_t E, int64_t N,
                    const int32_t* lhs, const int32_t* rhs, int64_t B,
-                   int group_size, int bits, uint16_t* out, int nthreads);
+                   int group_size, int bits, int tiled, uint16_t* out,
+                   int nthreads);
 
 /* act = silu(g) * u with MLX's per-op bf16 rounding. */
 void orc_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
@@ -107,6 +111,8 @@ typedef struct {
   orc_qlinear gate_proj, up_proj, down_proj;      /* switch_mlp */
   orc_qlinear shared_gate, shared_up, shared_down; /* E = 1 */
   const float* shared_gate_w; /* [1, d] f32 */
+  int32_t switch_tiled;     /* gather_qmm form of the routed experts */
+  int32_t shared_tiled;     /* and of the shared expert (see orc_gather_qmm) */
 } orc_block;
 
 /* Qwen35MoeBlock::forward on x bf16 [T, d] -> out f32 [T, d].

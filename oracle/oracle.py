@@ -119,9 +119,11 @@ def dispatch(ids, E):
     return counts, offsets, srt, inv
 
 
-def gather_qmm(x, wq, scales, biases, rhs, lhs=None, group_size=64, bits=4, nthreads=1):
+def gather_qmm(x, wq, scales, biases, rhs, lhs=None, group_size=64, bits=4, nthreads=1,
+               tiled=False):
     """x uint16 [x_batch, M, K]; wq uint32 [E, N, K*bits/32]; scales/biases
-    uint16 [E, N, K/g]; rhs [B] -> out uint16 [B, M, N]."""
+    uint16 [E, N, K/g]; rhs [B] -> out uint16 [B, M, N].  tiled: the
+    bf16-dequantised (tiled) numerics instead of the f32 (vector) ones."""
     x = np.ascontiguousarray(x, np.uint16)
     xb, M, Kd = x.shape
     E, N = wq.shape[0], wq.shape[1]
@@ -134,7 +136,7 @@ def gather_qmm(x, wq, scales, biases, rhs, lhs=None, group_size=64, bits=4, nthr
                               _p(np.ascontiguousarray(scales, np.uint16)),
                               _p(np.ascontiguousarray(biases, np.uint16)), c_int64(E),
                               c_int64(N), _p(lhs_a), _p(rhs), c_int64(B), c_int(group_size),
-                              c_int(bits), _p(out), c_int(nthreads))
+                              c_int(bits), c_int(1 if tiled else 0), _p(out), c_int(nthreads))
     if rc:
         raise ValueError("orc_gather_qmm rejected the arguments")
     return out
@@ -172,7 +174,7 @@ class _Block(Structure):
         ("group_size", c_int32), ("router_w", c_void_p), ("router_b", c_void_p),
         ("gate_proj", _QL), ("up_proj", _QL), ("down_proj", _QL),
         ("shared_gate", _QL), ("shared_up", _QL), ("shared_down", _QL),
-        ("shared_gate_w", c_void_p),
+        ("shared_gate_w", c_void_p), ("switch_tiled", c_int32), ("shared_tiled", c_int32),
     ]
 
 
@@ -182,10 +184,11 @@ def _ql(t):
     return _QL(t[0].ctypes.data, t[1].ctypes.data, t[2].ctypes.data)
 
 
-def block_forward(p: dict, x, nthreads=1):
+def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
     """p: numpy block parameters -- d, E, K, f, fs, bits, group_size,
     router_w, router_b (or None), gate/up/down = (wq, scales, biases),
     shared_gate/shared_up/shared_down, shared_gate_w (None when fs == 0).
+    tiled: gather_qmm numerics of (routed experts, shared expert).
     Returns (out f32 [T, d], idx [T, K], weights [T, K])."""
     keep = []
 
@@ -209,7 +212,8 @@ def block_forward(p: dict, x, nthreads=1):
                  rw.ctypes.data, None if rb is None else rb.ctypes.data,
                  _ql(q(p["gate"])), _ql(q(p["up"])), _ql(q(p["down"])),
                  _ql(q(p.get("shared_gate"))), _ql(q(p.get("shared_up"))),
-                 _ql(q(p.get("shared_down"))), None if sgw is None else sgw.ctypes.data)
+                 _ql(q(p.get("shared_down"))), None if sgw is None else sgw.ctypes.data,
+                 1 if tiled[0] else 0, 1 if tiled[1] else 0)
     out = np.zeros((T, p["d"]), np.float32)
     idx = np.zeros((T, p["K"]), np.int32)
     w = np.zeros((T, p["K"]), np.float32)

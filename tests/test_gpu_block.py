@@ -30,7 +30,11 @@ def check_block(pkg, orc, bw, x, nthreads=16):
     out = block(x)
     torch.cuda.synchronize()
     print(f"  block {bw.cfg.name} T={x.shape[0]}", flush=True)
-    ref, ridx, rw = orc.block_forward(orc.block_params(bw), orc.to_np(x), nthreads=nthreads)
+    T, cfg = x.shape[0], bw.cfg
+    # the gather_qmm numerics the library picks for each GEMM set
+    tiled = (pkg.ops.gather_qmm_tiled(T * cfg.K, cfg.E), pkg.ops.gather_qmm_tiled(T, 1))
+    ref, ridx, rw = orc.block_forward(orc.block_params(bw), orc.to_np(x), nthreads=nthreads,
+                                      tiled=tiled)
     idx = block.last_indices.cpu().numpy()
     assert np.array_equal(idx, ridx), "routing indices differ"
     assert np.allclose(block.last_weights.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
@@ -111,9 +115,11 @@ def test_switch_glu_forward_matches_composition(pkg, orc, dev):
     p = orc.block_params(bw)
     xs = orc.to_np(x)[:, None, :]
     ids = idx.cpu().numpy().reshape(-1)
-    ga = orc.gather_qmm(xs, *p["gate"], ids, nthreads=16)
-    ua = orc.gather_qmm(xs, *p["up"], ids, nthreads=16)
-    ya = orc.gather_qmm(orc.swiglu(ga, ua), *p["down"], ids, nthreads=16).reshape(T, cfg.K, -1)
+    tl = pkg.ops.gather_qmm_tiled(T * cfg.K, cfg.E)
+    ga = orc.gather_qmm(xs, *p["gate"], ids, nthreads=16, tiled=tl)
+    ua = orc.gather_qmm(xs, *p["up"], ids, nthreads=16, tiled=tl)
+    ya = orc.gather_qmm(orc.swiglu(ga, ua), *p["down"], ids, nthreads=16,
+                        tiled=tl).reshape(T, cfg.K, -1)
     yf = orc.bf16_to_f32(ya).astype(np.float64)
     rms = np.sqrt(np.mean(yf ** 2))
     assert np.abs(orc.bf16_to_f32(orc.to_np(y)) - yf).max() <= 2e-2 * rms

@@ -134,7 +134,7 @@ def test_gather_qmm_reference_cases(pkg, orc, dev, bits):
         got = pkg.ops.gather_qmm(x, wq, sc, bi, l_t, r_t, True, 64, bits)
         assert tuple(got.shape) == (2, 32, 64)
         want = orc.gather_qmm(_np(orc, x), _np(orc, wq), _np(orc, sc), _np(orc, bi), [2, 1],
-                              lhs, bits=bits)
+                              lhs, bits=bits, tiled=pkg.ops.gather_qmm_tiled(2 * 32, 3))
         _close(orc.bf16_to_f32(_np(orc, got)), orc.bf16_to_f32(want), (xb, bits))
         # gather_mm of the dequantised weights (fp64) as a second reference
         wd = orc.bf16_to_f32(_np(orc, pkg.ops.dequantize(wq, sc, bi, 64, bits))).astype(np.float64)
@@ -146,7 +146,9 @@ def test_gather_qmm_reference_cases(pkg, orc, dev, bits):
 @pytest.mark.parametrize("T,K,E,N,Kd,bits", [
     (1, 8, 128, 768, 2048, 4), (64, 8, 128, 768, 2048, 4), (64, 8, 128, 2048, 768, 4),
     (16, 2, 8, 256, 512, 4), (32, 8, 128, 1536, 4096, 8), (7, 10, 512, 512, 2048, 4),
-    (300, 8, 16, 128, 256, 4), (40, 1, 2, 64, 64, 8)])
+    (300, 8, 16, 128, 256, 4), (40, 1, 2, 64, 64, 8),
+    # many rows per expert: the M-tiled prefill kernel, ragged last tiles
+    (1024, 4, 8, 256, 512, 8), (600, 8, 32, 384, 1024, 4)])
 def test_gather_qmm_moe_unsorted_shapes(pkg, orc, dev, T, K, E, N, Kd, bits):
     """x [T, 1, 1, Kd] against indices [T, K] -> [T, K, 1, N]."""
     wq, sc, bi = _qbank(pkg, orc, E, N, Kd, bits, dev, T + E)
@@ -157,8 +159,9 @@ def test_gather_qmm_moe_unsorted_shapes(pkg, orc, dev, T, K, E, N, Kd, bits):
         idx[: T // 2, 0] = 3 % E  # one expert with many rows
     got = pkg.ops.gather_qmm(x, wq, sc, bi, None, torch.from_numpy(idx).to(dev), True, 64, bits)
     assert tuple(got.shape) == (T, K, 1, N)
+    tiled = pkg.ops.gather_qmm_tiled(T * K, E)
     want = orc.gather_qmm(_np(orc, x).reshape(T, 1, Kd), _np(orc, wq), _np(orc, sc),
-                          _np(orc, bi), idx.reshape(-1), bits=bits, nthreads=16)
+                          _np(orc, bi), idx.reshape(-1), bits=bits, nthreads=16, tiled=tiled)
     _close(orc.bf16_to_f32(_np(orc, got)).reshape(T * K, N),
            orc.bf16_to_f32(want).reshape(T * K, N), (T, K, E, N, Kd, bits))
 

@@ -193,6 +193,31 @@ def test_gather_qmm_equals_gather_mm_of_dequant(orc, bits):
         assert np.allclose(got, want, rtol=2 ** -7, atol=1e-3 * np.abs(want).max())
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_tiled_is_gather_mm_of_bf16_dequant(orc, bits):
+    """The tiled numerics are gather_mm(x, dequantize(w)^T) with the
+    dequantised weights in bf16 (the array dtype), as the reference test
+    states gather_qmm (quantization.rs:344-421): every product is exact in
+    f32, so only the f32 accumulation separates it from an fp64 matmul of
+    the bf16 dequantize output; the vector numerics keep f32 weights and do
+    differ from it."""
+    rng = np.random.default_rng(18)
+    E, N, K, T = 3, 64, 256, 40
+    wq, sc, bi = orc.quantize(orc.f32_to_bf16(0.02 * rng.standard_normal((E, N, K)).astype(np.float32)),
+                              64, bits)
+    wd16 = orc.bf16_to_f32(orc.dequantize(wq, sc, bi, 64, bits, out_bf16=True)).astype(np.float64)
+    x = orc.f32_to_bf16(rng.standard_normal((T, 1, K)).astype(np.float32))
+    rhs = rng.integers(0, E, T).astype(np.int32)
+    xf = orc.bf16_to_f32(x).astype(np.float64)[:, 0]
+    exact = np.stack([wd16[rhs[t]] @ xf[t] for t in range(T)])
+    bound = np.stack([np.abs(wd16[rhs[t]]) @ np.abs(xf[t]) for t in range(T)])
+    tiled = orc.bf16_to_f32(orc.gather_qmm(x, wq, sc, bi, rhs, bits=bits, tiled=True))[:, 0]
+    # f32 accumulation error (K terms) plus the final bf16 rounding
+    assert np.all(np.abs(tiled - exact) <= K * 2.0 ** -24 * bound + 2.0 ** -8 * np.abs(exact) + 1e-30)
+    vec = orc.gather_qmm(x, wq, sc, bi, rhs, bits=bits, tiled=False)[:, 0]
+    assert not np.array_equal(vec, orc.f32_to_bf16(tiled.astype(np.float32)))
+
+
 def test_gather_qmm_broadcast_x_over_topk(orc):
     """x [T, 1, K] against indices [T, k]: out row (t, j) uses x[t]."""
     rng = np.random.default_rng(9)
