@@ -60,19 +60,44 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_rank_kernel(
   if (ok) rank[gi] = tab[wave * E + id] + r;
 }
 
+// Index of the last entry of the ascending start[0..n) that is <= v.
+__device__ __forceinline__ int upper_slot(const int* start, int n, int v) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (start[mid] <= v)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+// One workgroup: per-expert prefix over the workgroups' histograms,
+// counts/offsets, the active list, and the work item and M-tile lists
+// (written by all threads, each list entry finding its expert by binary
+// search).  The scatter into sorted/inv is dispatch_scatter_kernel.
 __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
-    const int32_t* __restrict__ ids, int n, int E, int nb, int tile_rows,
-    DispatchBuffers b) {
-  __shared__ int s_off[kMaxExperts];
-  __shared__ int s_wpos[kMaxExperts];
+    int n, int E, int nb, int tile_rows, DispatchBuffers b) {
+  __shared__ int s_off[kMaxExperts], s_wpos[kMaxExperts], s_tpos[kMaxExperts];
   __shared__ int wsum[kWaves + 1];
   const int tid = threadIdx.x;
+  // exclusive prefix of each expert's column over the workgroups, 16 loads
+  // in flight at a time (a load after a store of the same array would wait
+  // for it)
   int cnt = 0;
   if (tid < E) {
-    for (int blk = 0; blk < nb; ++blk) {
-      const int c = b.block_hist[(int64_t)blk * E + tid];
-      b.block_hist[(int64_t)blk * E + tid] = cnt;
-      cnt += c;
+    constexpr int kChunk = 16;
+    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+      int c[kChunk];
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j)
+        c[j] = b0 + j < nb ? b.block_hist[(int64_t)(b0 + j) * E + tid] : 0;
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        if (b0 + j < nb) b.block_hist[(int64_t)(b0 + j) * E + tid] = cnt;
+        cnt += c[j];
+      }
     }
   }
   int total;
@@ -92,37 +117,50 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
   const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
   int n_work;
   const int wpos = block_exclusive_scan(nw, &n_work, wsum);
-  if (tid < E) s_wpos[tid] = wpos;
-  for (int j = 0; j < nw; ++j) {
-    int32_t* w = b.work + kWorkInts * (wpos + j);
-    w[0] = tid;
-    w[1] = off + j * kWorkRows;
-    w[2] = min(kWorkRows, cnt - j * kWorkRows);
-    w[3] = cnt;
+  if (tid < E) {
+    s_wpos[tid] = wpos;
+    b.work_first[tid] = wpos;
   }
   if (tid == 0) *b.num_work = n_work;
-
   const int nt = (tid < E) ? (cnt + tile_rows - 1) / tile_rows : 0;
   int n_tiles;
   const int tpos = block_exclusive_scan(nt, &n_tiles, wsum);
-  for (int j = 0; j < nt; ++j) {
-    b.tiles[2 * (tpos + j)] = tid;
-    b.tiles[2 * (tpos + j) + 1] = off + j * tile_rows;
-  }
+  if (tid < E) s_tpos[tid] = tpos;
   if (tid == 0) *b.num_tiles = n_tiles;
   __syncthreads();
-
-  for (int i = tid; i < n; i += kDispatchBlock) {
-    const int e = ids[i];
-    if (e < 0 || e >= E) continue;
-    const int pos = s_off[e] +
-                    b.block_hist[(int64_t)(i / kDispatchBlock) * E + e] +
-                    b.rank[i];
-    b.sorted[pos] = i;
-    b.inv[i] = pos;
-    const int r = pos - s_off[e];
-    b.work[kWorkInts * (s_wpos[e] + r / kWorkRows) + 4 + r % kWorkRows] = i;
+  // experts with no rows share their start with the next: the search finds
+  // the last expert starting at or before the entry, which has rows
+  for (int i = tid; i < n_work; i += kDispatchBlock) {
+    const int e = upper_slot(s_wpos, E, i), j = i - s_wpos[e];
+    const int cnt_e = (e + 1 < E ? s_off[e + 1] : total) - s_off[e];
+    int32_t* w = b.work + kWorkInts * i;
+    w[0] = e;
+    w[1] = s_off[e] + j * kWorkRows;
+    w[2] = min(kWorkRows, cnt_e - j * kWorkRows);
+    w[3] = cnt_e;
   }
+  for (int i = tid; i < n_tiles; i += kDispatchBlock) {
+    const int e = upper_slot(s_tpos, E, i), j = i - s_tpos[e];
+    b.tiles[2 * i] = e;
+    b.tiles[2 * i + 1] = s_off[e] + j * tile_rows;
+  }
+}
+
+// Every workgroup of the rank pass again: sorted/inv and the flat rows of
+// the work records, from the offsets and per-workgroup prefixes.
+__global__ __launch_bounds__(kDispatchBlock) void dispatch_scatter_kernel(
+    const int32_t* __restrict__ ids, int n, int E, DispatchBuffers b) {
+  const int64_t i = (int64_t)blockIdx.x * kDispatchBlock + threadIdx.x;
+  if (i >= n) return;
+  const int e = ids[i];
+  if (e < 0 || e >= E) return;
+  const int base = b.offsets[e];
+  const int r = b.block_hist[(int64_t)blockIdx.x * E + e] + b.rank[i];
+  const int pos = base + r;
+  b.sorted[pos] = (int32_t)i;
+  b.inv[i] = pos;
+  b.work[kWorkInts * (b.work_first[e] + r / kWorkRows) + 4 + r % kWorkRows] =
+      (int32_t)i;
 }
 
 // n <= 1024 ids: the whole sort in one workgroup.
@@ -247,8 +285,9 @@ hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
   dispatch_rank_kernel<<<nb, kDispatchBlock,
                          (size_t)kWaves * E * sizeof(uint16_t), s>>>(
       ids, (int)n, (int)E, b.block_hist, b.rank, b.status);
-  dispatch_scan_kernel<<<1, kDispatchBlock, 0, s>>>(ids, (int)n, (int)E, nb,
+  dispatch_scan_kernel<<<1, kDispatchBlock, 0, s>>>((int)n, (int)E, nb,
                                                     tile_rows, b);
+  dispatch_scatter_kernel<<<nb, kDispatchBlock, 0, s>>>(ids, (int)n, (int)E, b);
   return hipGetLastError();
 }
 

@@ -69,6 +69,7 @@ struct DispatchBuffers {
   int32_t* work;        // [max_work][kWorkInts] work item records: each
                         // expert's rows in chunks of at most kWorkRows
   int32_t* num_work;    // [1]
+  int32_t* work_first;  // [E] first work item of each expert
   int32_t* tiles;       // [max_tiles] packed (expert, first row) of M-tiles
   int32_t* num_tiles;   // [1]
   int32_t* block_hist;  // [ceil(n/1024), E] scratch
@@ -94,7 +95,8 @@ inline int64_t dispatch_max_work(int64_t n, int64_t E) {
 // so the call stays valid under stream capture).
 hipError_t launch_zero_status(int32_t* status, hipStream_t s);
 // Ids equal to -1 are left out silently (rows excluded by the caller);
-// other ids outside [0, E) are left out and set *status = 1.
+// other ids outside [0, E) are left out and set *status = 1.  n above 1024
+// takes three kernels (rank, scan, scatter).
 hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
                            int tile_rows, const DispatchBuffers& b,
                            bool reset_status, hipStream_t s);
@@ -148,7 +150,7 @@ struct QGemmArgs {
 constexpr int kMaxInputDims = 4096;
 // Rows per M-tile of the prefill kernel (64 per wave along M); the dispatch
 // builds its tile list.  Waves along N: 64 B columns each.
-constexpr int kPrefillTileRows = 128;
+constexpr int kPrefillTileRows = 256;
 constexpr int kPrefillWavesN = 2;
 // max_items bounds the number of work items (dispatch_max_work); prefill
 // selects the M-tiled kernel (prefill.hip) where it applies.
@@ -156,10 +158,11 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s);
 
 // ---------------------------------------------------------------- prefill.hip
-bool prefill_supported(const QGemmArgs& a);
-// max_tiles bounds the M-tile list (dispatch_max_tiles).
-hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t max_tiles,
-                                hipStream_t s);
+// x_rows bounds the rows of x the GEMM reads; max_tiles bounds the M-tile
+// list (dispatch_max_tiles).
+bool prefill_supported(const QGemmArgs& a, int64_t x_rows);
+hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
+                                int64_t max_tiles, hipStream_t s);
 
 // -------------------------------------------------------------- combine.hip
 hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,

@@ -55,6 +55,7 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
   b.num_active = c.take<int32_t>(1);
   b.work = c.take<int32_t>(kWorkInts * dispatch_max_work(n, E));
   b.num_work = c.take<int32_t>(1);
+  b.work_first = c.take<int32_t>(E);
   b.tiles = c.take<int32_t>(2 * dispatch_max_tiles(n, E, kPrefillTileRows));
   b.num_tiles = c.take<int32_t>(1);
   b.block_hist = c.take<int32_t>(nb * E);
@@ -66,8 +67,8 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
 namespace nn {
 
 bool use_prefill_path(int64_t rows, int64_t experts) {
-  // the M-tiled kernel pays once the experts average a quarter tile
-  return rows >= (int64_t)(kPrefillTileRows / 4) * experts;
+  // the M-tiled kernel pays once the experts average 32 rows
+  return rows >= 32 * experts;
 }
 
 namespace {

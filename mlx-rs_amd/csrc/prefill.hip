@@ -12,13 +12,17 @@
 // bf16(fmaf(code, scale, bias)) -- into LDS, where every wave of the
 // workgroup reuses them.
 //
-// Workgroup: WM x WN waves; tile BM = 64 WM rows x BN = 64 WN columns (the
-// gated kernel's columns are BN/2 gate channels then the same BN/2 up
-// channels, so each wave holds matching gate and up sums for the SwiGLU
-// epilogue).  K advances one quantisation group (64) per step through two
-// LDS stages: while the waves multiply stage s, the global loads of the next
-// group are in flight in registers, and after the multiplies they are
-// dequantised into stage s^1.  One barrier per step.
+// Workgroup: kWM x kWN waves (4 x 2); tile kBM = 256 rows x kBN = 128
+// columns (the gated kernel's columns are 64 gate channels then the same 64
+// up channels, so each wave holds matching gate and up sums for the SwiGLU
+// epilogue).  A tall tile spreads the dequantisation (the VALU cost, about
+// three instructions per weight) over many rows; waves whose rows lie past
+// the expert's last row skip their MFMAs.  Global loads are raw buffer loads
+// with the K step in the scalar offset: no per-step address arithmetic.
+// K advances one quantisation group (64) per step through two LDS stages:
+// while the waves multiply stage s, the global loads of the next group are
+// in flight in registers, and after the multiplies they are dequantised into
+// stage s^1.  One barrier per step.
 //
 // Each wave owns 64 x 64 outputs as 2 x 2 blocks of v_mfma_f32_32x32x16_bf16
 // (K = 16 per instruction, four per group).  LDS rows are 64 bf16 padded to
@@ -31,6 +35,20 @@ namespace mlxr_moe {
 namespace {
 
 constexpr int kRowPad = 72;  // LDS row stride (bf16)
+constexpr int kWM = kPrefillTileRows / 64, kWN = kPrefillWavesN;
+constexpr int kNT = 64 * kWM * kWN;     // threads
+constexpr int kBM = 64 * kWM;           // rows per tile
+constexpr int kBN = 64 * kWN;           // B columns per tile
+constexpr int kACH = kBM * 8 / kNT;     // 16-byte x chunks per thread
+constexpr int kPARTS = kNT / kBN;       // threads per B column per group
+constexpr int kCODES = 64 / kPARTS;     // codes per thread per group
+static_assert(kBM * 8 % kNT == 0 && kNT % kBN == 0 && kCODES == 16,
+              "tile split");
+// raw buffer resource word 3 (gfx9 family)
+constexpr int kBufFlags = 0x00020000;
+// XCDs of an MI355X (the workgroup numbering below assumes this many; any
+// other count only changes which workgroups share an L2)
+constexpr unsigned kXcds = 8;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -39,139 +57,224 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t,
                             __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
+// x & m, opaque to the optimiser so that the byte extracts below stay
+// v_cvt_f32_ubyte{0..3} (it would otherwise fold the masks into bit-field
+// extracts plus a conversion)
+__device__ __forceinline__ uint32_t and_opaque(uint32_t x, uint32_t m) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(x), "s"(m));
+  return r;
+}
+// 8 four-bit codes of one word (little end first) -> 4 words of bf16 pairs,
+// each bf16(fmaf(code, s, b)); the even codes sit in the low nibbles.
+__device__ __forceinline__ void dequant4(uint32_t w, float s, float b,
+                                         uint32_t* o) {
+  const uint32_t lo = and_opaque(w, 0x0F0F0F0Fu);
+  const uint32_t hi = and_opaque(w >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = pack_bf16(__builtin_fmaf((float)((lo >> (8 * j)) & 255u), s, b),
+                     __builtin_fmaf((float)((hi >> (8 * j)) & 255u), s, b));
+}
+// 4 eight-bit codes -> 2 words of pairs
+__device__ __forceinline__ void dequant8(uint32_t w, float s, float b,
+                                         uint32_t* o) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    o[j] = pack_bf16(__builtin_fmaf((float)((w >> (16 * j)) & 255u), s, b),
+                     __builtin_fmaf((float)((w >> (16 * j + 8)) & 255u), s, b));
+}
 
-// 8 codes of one 32-bit word (little end first) -> 4 words of bf16 pairs,
-// each bf16(fmaf(code, s, b)).
+// Everything the K-loop needs, in registers.
 template <int BITS>
-__device__ __forceinline__ void dequant_word(uint32_t w, float s, float b,
-                                             uint32_t* o);
-template <>
-__device__ __forceinline__ void dequant_word<4>(uint32_t w, float s, float b,
-                                                uint32_t* o) {
+struct PrefillCtx {
+  __amdgpu_buffer_rsrc_t xr, wr, sr, br;  // x, weights, scales, biases
+  uint32_t aoff[kACH];                     // x chunk offsets (bytes)
+  uint32_t woff, soff;                     // code chunk / scale offsets
+  uint16_t* As;
+  uint16_t* Bs;
+  int tid, arow, bc0, bc1, kh, col_off, groups;
+};
+
+// One group's global loads, held in registers until they are staged.
+template <int BITS>
+struct PrefillRegs {
+  typedef uint32_t u32w_t __attribute__((ext_vector_type(BITS / 2)));
+  u32x4_t a[kACH];
+  u32w_t b;
+  uint32_t s, c;
+};
+
+template <int BITS>
+__device__ __forceinline__ void prefill_load(const PrefillCtx<BITS>& c,
+                                             PrefillRegs<BITS>& R, int g_in) {
+  // the group index is uniform; said so, the step offsets stay scalar
+  const int g = __builtin_amdgcn_readfirstlane(g_in);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float c0 = (float)((w >> (8 * j)) & 15u);
-    const float c1 = (float)((w >> (8 * j + 4)) & 15u);
-    o[j] = pack_bf16(__builtin_fmaf(c0, s, b), __builtin_fmaf(c1, s, b));
-  }
+  for (int j = 0; j < kACH; ++j)
+    R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(c.xr, c.aoff[j], 128 * g, 0);
+  if constexpr (BITS == 4)
+    R.b = __builtin_amdgcn_raw_buffer_load_b64(c.wr, c.woff, 32 * g, 0);
+  else
+    R.b = __builtin_amdgcn_raw_buffer_load_b128(c.wr, c.woff, 64 * g, 0);
+  R.s = __builtin_amdgcn_raw_buffer_load_b16(c.sr, c.soff, 2 * g, 0);
+  R.c = __builtin_amdgcn_raw_buffer_load_b16(c.br, c.soff, 2 * g, 0);
 }
-// 8-bit: one word = 4 codes -> 2 words of pairs
-__device__ __forceinline__ void dequant_word8(uint32_t w, float s, float b,
-                                              uint32_t* o) {
+
+// x chunks to LDS as they are; codes dequantised to bf16 pairs.
+template <int BITS>
+__device__ __forceinline__ void prefill_store(const PrefillCtx<BITS>& c,
+                                              const PrefillRegs<BITS>& R, int st) {
+  uint16_t* A = c.As + st * kBM * kRowPad;
+  uint16_t* B = c.Bs + st * kBN * kRowPad;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const float c0 = (float)((w >> (16 * j)) & 255u);
-    const float c1 = (float)((w >> (16 * j + 8)) & 255u);
-    o[j] = pack_bf16(__builtin_fmaf(c0, s, b), __builtin_fmaf(c1, s, b));
+  for (int j = 0; j < kACH; ++j) {
+    const int id = c.tid + kNT * j;
+    *reinterpret_cast<u32x4_t*>(A + (id >> 3) * kRowPad + 8 * (id & 7)) = R.a[j];
+  }
+  const float s = __uint_as_float(R.s << 16), b = __uint_as_float(R.c << 16);
+  uint32_t o[8];
+  if constexpr (BITS == 4) {
+    dequant4(R.b[0], s, b, o);
+    dequant4(R.b[1], s, b, o + 4);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dequant8(R.b[i], s, b, o + 2 * i);
+  }
+  uint16_t* dst = B + c.col_off;
+  *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{o[0], o[1], o[2], o[3]};
+  *reinterpret_cast<u32x4_t*>(dst + 8) = u32x4_t{o[4], o[5], o[6], o[7]};
+}
+
+// The multiplies of one group from LDS stage st: every fragment is read
+// first, then the NMB x 2 x 4 MFMAs.
+template <int NMB>
+__device__ __forceinline__ void prefill_mma(const uint16_t* A, const uint16_t* B,
+                                            int arow, int bc0, int bc1, int kh,
+                                            f32x16_t (&acc)[2][2]) {
+  bf16x8_t af[4][2], bf[4][2];
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) {
+    bf[kc][0] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(B + bc0 * kRowPad + 16 * kc + kh));
+    bf[kc][1] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(B + bc1 * kRowPad + 16 * kc + kh));
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+      af[kc][mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(
+          A + (arow + 32 * mb) * kRowPad + 16 * kc + kh));
+  }
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        acc[mb][nb] = mfma32x32x16(af[kc][mb], bf[kc][nb], acc[mb][nb]);
+}
+
+// K-loop over the groups.  Two register buffers: the loads of group g + 2
+// are issued while group g is multiplied and group g + 1 (loaded a step
+// earlier) is staged into the other LDS stage, so each staging finds its
+// data resident.  One barrier per group.
+template <int BITS, int NMB>
+__device__ __forceinline__ void prefill_kloop(const PrefillCtx<BITS>& c,
+                                              f32x16_t (&acc)[2][2]) {
+  const int G = c.groups;
+  PrefillRegs<BITS> R0, R1;
+  prefill_load(c, R0, 0);
+  if (G > 1) prefill_load(c, R1, 1);
+  prefill_store(c, R0, 0);
+  __syncthreads();
+  for (int g = 0; g < G; g += 2) {
+    // even group g: stage 0 holds it, R1 holds g + 1
+    if (g + 2 < G) prefill_load(c, R0, g + 2);
+    prefill_mma<NMB>(c.As, c.Bs, c.arow, c.bc0, c.bc1, c.kh, acc);
+    if (g + 1 < G) prefill_store(c, R1, 1);
+    __syncthreads();
+    if (g + 1 >= G) break;
+    // odd group g + 1: stage 1 holds it, R0 holds g + 2
+    if (g + 3 < G) prefill_load(c, R1, g + 3);
+    prefill_mma<NMB>(c.As + kBM * kRowPad, c.Bs + kBN * kRowPad, c.arow, c.bc0,
+                     c.bc1, c.kh, acc);
+    if (g + 2 < G) prefill_store(c, R0, 0);
+    __syncthreads();
   }
 }
 
-template <int BITS, bool GATED, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN) void qgemm_prefill_kernel(
-    QGemmArgs a, int tiles_n) {
-  constexpr int NT = 64 * WM * WN;      // threads
-  constexpr int BM = 64 * WM;           // rows per tile
-  constexpr int BN = 64 * WN;           // B columns per tile
-  constexpr int ACH = BM * 8 / NT;      // 16-byte x chunks per thread
-  constexpr int CPC = 64 * BITS / 128;  // 16-byte code chunks per column
-  constexpr int BCH = BN * CPC / NT;    // code chunks per thread
-  constexpr int CODES = 128 / BITS;     // codes per chunk
-  static_assert(BM * 8 % NT == 0 && BN * CPC % NT == 0, "even split");
+template <int BITS, bool GATED>
+__global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
+                                                           int tiles_n,
+                                                           uint32_t x_bytes) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  uint16_t* As = reinterpret_cast<uint16_t*>(smem);  // [2][BM][kRowPad]
-  uint16_t* Bs = As + 2 * BM * kRowPad;              // [2][BN][kRowPad]
+  uint16_t* As = reinterpret_cast<uint16_t*>(smem);  // [2][kBM][kRowPad]
+  uint16_t* Bs = As + 2 * kBM * kRowPad;             // [2][kBN][kRowPad]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tile = blockIdx.x / tiles_n, nt = blockIdx.x - tile * tiles_n;
-  if (tile >= *a.num_tiles) return;
+  // Workgroups go to the XCDs round robin (blockIdx % kXcds).  Number them
+  // so that the N-tiles of one M-tile run on one XCD, one after another:
+  // they read the same x rows, which then come from that XCD's L2.
+  // (The live units, num_tiles x tiles_n, are dealt out evenly: the grid
+  // is sized for the most tiles the dispatch can make.)
+  const unsigned live = (unsigned)*a.num_tiles * tiles_n;
+  const unsigned per = (live + kXcds - 1) / kXcds, j = blockIdx.x / kXcds;
+  const unsigned L = (blockIdx.x % kXcds) * per + j;
+  if (j >= per || L >= live) return;
+  const int tile = (int)(L / tiles_n), nt = (int)(L - (unsigned)tile * tiles_n);
   const int e = a.tiles[2 * tile], slot0 = a.tiles[2 * tile + 1];
-  const int rows = min(BM, a.offsets[e + 1] - slot0);
+  const int rows = min(kBM, a.offsets[e + 1] - slot0);
   const int groups = a.K >> 6;
-  const int wm = wave / WN, wn = wave - wm * WN;
+  const int wm = wave / kWN, wn = wave - wm * kWN;
 
-  // x rows of this thread's A chunks (row = id / 8, 16-byte column id % 8)
-  const uint16_t* ap[ACH];
-  bool av[ACH];
+  // x: one buffer over all rows (rows past the tile read out of range, 0)
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), 0, (int)x_bytes, kBufFlags);
+  uint32_t aoff[kACH];
 #pragma unroll
-  for (int j = 0; j < ACH; ++j) {
-    const int id = tid + NT * j, r = id >> 3, c = id & 7;
-    av[j] = r < rows;
-    int64_t xr = 0;
-    if (av[j]) {
+  for (int j = 0; j < kACH; ++j) {
+    const int id = tid + kNT * j, r = id >> 3, c = id & 7;
+    uint32_t off = 0xFFFFFFF0u;
+    if (r < rows) {
       const int slot = slot0 + r;
+      int64_t row;
       if (a.x_by_slot) {
-        xr = slot;
+        row = slot;
       } else {
         const int flat = a.sorted[slot];
-        xr = a.row_map ? a.row_map[flat] : flat / a.row_div;
+        row = a.row_map ? a.row_map[flat] : flat / a.row_div;
       }
+      off = (uint32_t)(row * a.x_ld * 2 + 16 * c);
     }
-    ap[j] = a.x + xr * a.x_ld + 8 * c;
+    aoff[j] = off;
   }
-  // code chunks of this thread: column col, chunk q of the group
-  const uint32_t* bp[BCH];
-  const uint16_t* sp[BCH];
-  const uint16_t* bbp[BCH];
-  int bcol[BCH], bq[BCH];
-#pragma unroll
-  for (int j = 0; j < BCH; ++j) {
-    const int id = tid + NT * j, col = id / CPC, q = id - col * CPC;
-    bcol[j] = col;
-    bq[j] = q;
-    int m = 0, ch;
-    if constexpr (GATED) {
-      m = col >= BN / 2;
-      ch = nt * (BN / 2) + (col - m * (BN / 2));
-    } else {
-      ch = nt * BN + col;
-    }
-    const QWeights& W = m ? a.w1 : a.w0;
-    const int64_t row = (int64_t)e * a.N + ch;
-    bp[j] = W.w + row * groups * (2 * BITS) + q * 4;
-    sp[j] = W.scales + row * groups;
-    bbp[j] = W.biases + row * groups;
-  }
+  // weights: thread -> column col, codes [kCODES*part, +kCODES) of a group;
+  // the gated tile's first kBN/2 columns are gate channels, the rest up
+  // (whole waves on each side)
+  const int col = tid / kPARTS, part = tid - col * kPARTS;
+  // which projection, from the (uniform) wave index: a buffer resource
+  // must sit in scalar registers
+  const int m = GATED ? (__builtin_amdgcn_readfirstlane(wave) >= kWM * kWN / 2) : 0;
+  const int ch = GATED ? nt * (kBN / 2) + (col - m * (kBN / 2)) : nt * kBN + col;
+  const QWeights& W = m ? a.w1 : a.w0;
+  const int64_t row_bytes = (int64_t)a.K * BITS / 8;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(W.w) + (int64_t)e * a.N * (row_bytes / 4), 0,
+      (int)(a.N * row_bytes), kBufFlags);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(W.scales) + (int64_t)e * a.N * groups, 0,
+      a.N * groups * 2, kBufFlags);
+  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(W.biases) + (int64_t)e * a.N * groups, 0,
+      a.N * groups * 2, kBufFlags);
+  const uint32_t woff = (uint32_t)(ch * row_bytes + part * (kCODES * BITS / 8));
+  const uint32_t soff = (uint32_t)(ch * groups * 2);
 
-  u32x4_t areg[ACH], breg[BCH];
-  uint16_t sreg[BCH], creg[BCH];
-  auto load = [&](int g) {
+  // operand rows of this lane: A rows wm*64 + 32 mb + l%32, B columns
+  const int arow = wm * 64 + (lane & 31);
+  int bc[2];
 #pragma unroll
-    for (int j = 0; j < ACH; ++j)
-      areg[j] = av[j] ? *reinterpret_cast<const u32x4_t*>(ap[j] + 64 * g)
-                      : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int j = 0; j < BCH; ++j) {
-      breg[j] = *reinterpret_cast<const u32x4_t*>(bp[j] + g * (2 * BITS));
-      sreg[j] = sp[j][g];
-      creg[j] = bbp[j][g];
-    }
-  };
-  auto store = [&](int st) {
-    uint16_t* A = As + st * BM * kRowPad;
-    uint16_t* B = Bs + st * BN * kRowPad;
-#pragma unroll
-    for (int j = 0; j < ACH; ++j) {
-      const int id = tid + NT * j;
-      *reinterpret_cast<u32x4_t*>(A + (id >> 3) * kRowPad + 8 * (id & 7)) = areg[j];
-    }
-#pragma unroll
-    for (int j = 0; j < BCH; ++j) {
-      const float s = bf16_to_f32(sreg[j]), b = bf16_to_f32(creg[j]);
-      uint32_t o[CODES / 2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if constexpr (BITS == 4)
-          dequant_word<4>(breg[j][i], s, b, o + 4 * i);
-        else
-          dequant_word8(breg[j][i], s, b, o + 2 * i);
-      }
-      uint16_t* dst = B + bcol[j] * kRowPad + bq[j] * CODES;
-#pragma unroll
-      for (int i = 0; i < CODES / 8; ++i)
-        *reinterpret_cast<u32x4_t*>(dst + 8 * i) =
-            u32x4_t{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-    }
-  };
+  for (int nb = 0; nb < 2; ++nb)
+    bc[nb] = (GATED ? nb * (kBN / 2) + wn * 32 : wn * 64 + nb * 32) + (lane & 31);
+  const int kh = 8 * (lane >> 5);
+  const int col_off = col * kRowPad + part * kCODES;
 
   f32x16_t acc[2][2];
 #pragma unroll
@@ -180,42 +283,20 @@ __global__ __launch_bounds__(64 * WM * WN) void qgemm_prefill_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  // operand rows of this lane: A rows wm*64 + 32 mb + l%32, B columns
-  const int arow = wm * 64 + (lane & 31);
-  int bc[2];
+  // M-blocks of this wave that hold rows of the tile (the rest would
+  // multiply zeros): one K-loop per count, chosen once
+  const int wm_u = __builtin_amdgcn_readfirstlane(wm);
+  const int nmb = rows > wm_u * 64 + 32 ? 2 : (rows > wm_u * 64 ? 1 : 0);
+  PrefillCtx<BITS> c{xr, wr, sr, br, {}, woff, soff, As, Bs, tid,
+                     arow, bc[0], bc[1], kh, col_off, groups};
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
-    bc[nb] = (GATED ? nb * (BN / 2) + wn * 32 : wn * 64 + nb * 32) + (lane & 31);
-  const int kh = 8 * (lane >> 5);
-
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int g = 0; g < groups; ++g) {
-    const int st = g & 1;
-    if (g + 1 < groups) load(g + 1);
-    const uint16_t* A = As + st * BM * kRowPad;
-    const uint16_t* B = Bs + st * BN * kRowPad;
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      bf16x8_t af[2], bf[2];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-        af[mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(
-            A + (arow + 32 * mb) * kRowPad + 16 * kc + kh));
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-        bf[nb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(
-            B + bc[nb] * kRowPad + 16 * kc + kh));
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          acc[mb][nb] = mfma32x32x16(af[mb], bf[nb], acc[mb][nb]);
-    }
-    if (g + 1 < groups) store(st ^ 1);
-    __syncthreads();
-  }
+  for (int j = 0; j < kACH; ++j) c.aoff[j] = aoff[j];
+  if (nmb == 2)
+    prefill_kloop<BITS, 2>(c, acc);
+  else if (nmb == 1)
+    prefill_kloop<BITS, 1>(c, acc);
+  else
+    prefill_kloop<BITS, 0>(c, acc);
 
   // D[8(r/4) + 4(l/32) + r%4][l%32] of each 32 x 32 block
 #pragma unroll
@@ -226,15 +307,15 @@ __global__ __launch_bounds__(64 * WM * WN) void qgemm_prefill_kernel(
       if (row >= rows) continue;
       const int slot = slot0 + row;
       if constexpr (GATED) {
-        const int ch = nt * (BN / 2) + wn * 32 + (lane & 31);
-        a.out[(int64_t)slot * a.out_ld + ch] =
+        const int och = nt * (kBN / 2) + wn * 32 + (lane & 31);
+        a.out[(int64_t)slot * a.out_ld + och] =
             swiglu_bf16(bf16_round(acc[mb][0][r]), bf16_round(acc[mb][1][r]));
       } else {
         const int64_t orow = a.out_by_flat ? a.sorted[slot] : slot;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          const int ch = nt * BN + wn * 64 + 32 * nb + (lane & 31);
-          a.out[orow * a.out_ld + ch] = f32_to_bf16(acc[mb][nb][r]);
+          const int och = nt * kBN + wn * 64 + 32 * nb + (lane & 31);
+          a.out[orow * a.out_ld + och] = f32_to_bf16(acc[mb][nb][r]);
         }
       }
     }
@@ -243,24 +324,25 @@ __global__ __launch_bounds__(64 * WM * WN) void qgemm_prefill_kernel(
 
 }  // namespace
 
-bool prefill_supported(const QGemmArgs& a) {
-  constexpr int BN = 64 * kPrefillWavesN;
-  const int cols = a.gated ? BN / 2 : BN;
+bool prefill_supported(const QGemmArgs& a, int64_t x_rows) {
+  const int cols = a.gated ? kBN / 2 : kBN;
+  // buffer offsets are 32-bit: x, and one expert's weights, under 2 GB
   return (a.bits == 4 || a.bits == 8) && a.K % 64 == 0 && a.N % cols == 0 &&
-         a.sorted != nullptr;
+         a.sorted != nullptr &&
+         x_rows * a.x_ld * 2 < ((int64_t)1 << 31) &&
+         (int64_t)a.N * a.K * a.bits / 8 < ((int64_t)1 << 31);
 }
 
-hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t max_tiles,
-                                hipStream_t s) {
-  constexpr int WM = kPrefillTileRows / 64, WN = kPrefillWavesN;
-  constexpr int BM = 64 * WM, BN = 64 * WN;
+hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
+                                int64_t max_tiles, hipStream_t s) {
   if (max_tiles <= 0) return hipSuccess;
-  const int tiles_n = a.N / (a.gated ? BN / 2 : BN);
-  const size_t lds = (size_t)2 * (BM + BN) * kRowPad * 2;
-  const dim3 grid((unsigned)(max_tiles * tiles_n));
+  const int tiles_n = a.N / (a.gated ? kBN / 2 : kBN);
+  const size_t lds = (size_t)2 * (kBM + kBN) * kRowPad * 2;
+  const dim3 grid((unsigned)((max_tiles * tiles_n + kXcds - 1) / kXcds * kXcds));
+  const uint32_t x_bytes = (uint32_t)(x_rows * a.x_ld * 2);
   ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
 #define MLXR_PF(B, G) \
-  qgemm_prefill_kernel<B, G, WM, WN><<<grid, 64 * WM * WN, lds, s>>>(a, tiles_n)
+  qgemm_prefill_kernel<B, G><<<grid, kNT, lds, s>>>(a, tiles_n, x_bytes)
   if (a.bits == 4) {
     if (a.gated)
       MLXR_PF(4, true);

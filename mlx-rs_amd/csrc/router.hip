@@ -103,6 +103,132 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   }
 }
 
+// Many tokens: one workgroup computes 32 tokens x 16 logit columns.  Each
+// 256-wide step of d is staged in LDS (x as bf16, the weights as f32; the
+// next step's loads are in flight in registers meanwhile) and every wave
+// multiplies 8 tokens x 16 columns from it, so each value loaded from memory
+// feeds 8 or 16 dot products.  A lane accumulates exactly the elements
+// j = 4l + 256i + c in (i, c) order, like router_logits_kernel, and the 64
+// lane sums of a logit are added in the butterfly's pairwise tree (lanes
+// l and l^32 first, ... l and l^1 last) -- by one lane reading them from
+// LDS rather than by six shuffles on every lane.  Same bits.
+constexpr int kRtTok = 32, kRtCol = 16, kRtWaveTok = 8;
+__global__ __launch_bounds__(256) void router_logits_tiled_kernel(
+    const uint16_t* __restrict__ x, int T, int d, const float* __restrict__ w,
+    const float* __restrict__ bias, int E, const float* __restrict__ w_extra,
+    float* __restrict__ logits, int64_t ld) {
+  // 32 KB: the step's x [32][256] bf16 and w [16][256] f32; afterwards the
+  // lane sums [wave][32 logits][64 lanes] f32, 32 logits at a time
+  __shared__ __attribute__((aligned(16))) char lds[kRtTok * 256 * 2 + kRtCol * 256 * 4];
+  uint16_t (*xs)[256] = reinterpret_cast<uint16_t (*)[256]>(lds);
+  float (*ws)[256] = reinterpret_cast<float (*)[256]>(lds + kRtTok * 256 * 2);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int e_tot = E + (w_extra ? 1 : 0);
+  const int e0 = blockIdx.x * kRtCol, t0 = blockIdx.y * kRtTok;
+  float acc[kRtCol][kRtWaveTok];
+#pragma unroll
+  for (int q = 0; q < kRtCol; ++q)
+#pragma unroll
+    for (int tt = 0; tt < kRtWaveTok; ++tt) acc[q][tt] = 0.0f;
+  // this thread's staging chunks: x rows id/32 (8 bf16 at (id%32)*8), w rows
+  // id/64 (4 f32 at (id%64)*4), id = tid + 256k; zeros past d / T / e_tot
+  const uint16_t* xp[4];
+  const float* wp[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int id = tid + 256 * k;
+    const int t = t0 + (id >> 5), e = e0 + (id >> 6);
+    xp[k] = t < T ? x + (int64_t)t * d + (id & 31) * 8 : nullptr;
+    const float* row = e < E ? w + (int64_t)e * d : (e == E ? w_extra : nullptr);
+    wp[k] = row ? row + (id & 63) * 4 : nullptr;
+  }
+  u32x4_t xr[4];
+  float4 wr[4];
+  auto fetch = [&](int i) {
+    const int j0 = 256 * i;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int id = tid + 256 * k;
+      xr[k] = (xp[k] && j0 + (id & 31) * 8 < d)
+                  ? *reinterpret_cast<const u32x4_t*>(xp[k] + j0)
+                  : u32x4_t{0u, 0u, 0u, 0u};
+      wr[k] = (wp[k] && j0 + (id & 63) * 4 < d)
+                  ? *reinterpret_cast<const float4*>(wp[k] + j0)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  const int steps = (d + 255) / 256;
+  fetch(0);
+  for (int i = 0; i < steps; ++i) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int id = tid + 256 * k;
+      *reinterpret_cast<u32x4_t*>(&xs[id >> 5][(id & 31) * 8]) = xr[k];
+      *reinterpret_cast<float4*>(&ws[id >> 6][(id & 63) * 4]) = wr[k];
+    }
+    __syncthreads();
+    if (i + 1 < steps) fetch(i + 1);
+    float xv[kRtWaveTok][4];
+#pragma unroll
+    for (int tt = 0; tt < kRtWaveTok; ++tt) {
+      const uint2 u = *reinterpret_cast<const uint2*>(&xs[wave * kRtWaveTok + tt][4 * lane]);
+      xv[tt][0] = __uint_as_float(u.x << 16);
+      xv[tt][1] = __uint_as_float(u.x & 0xffff0000u);
+      xv[tt][2] = __uint_as_float(u.y << 16);
+      xv[tt][3] = __uint_as_float(u.y & 0xffff0000u);
+    }
+#pragma unroll
+    for (int q = 0; q < kRtCol; ++q) {
+      const float4 wv = *reinterpret_cast<const float4*>(&ws[q][4 * lane]);
+#pragma unroll
+      for (int tt = 0; tt < kRtWaveTok; ++tt) {
+        float a = acc[q][tt];
+        a = __builtin_fmaf(xv[tt][0], wv.x, a);
+        a = __builtin_fmaf(xv[tt][1], wv.y, a);
+        a = __builtin_fmaf(xv[tt][2], wv.z, a);
+        a = __builtin_fmaf(xv[tt][3], wv.w, a);
+        acc[q][tt] = a;
+      }
+    }
+    __syncthreads();
+  }
+  // lane sums -> logits, 32 logits (4 columns x 8 tokens) per round; each
+  // wave uses its own quarter of the LDS, logit i's row swizzled by i
+  float* red = reinterpret_cast<float*>(lds) + wave * 32 * 64;
+#pragma unroll
+  for (int q0 = 0; q0 < kRtCol; q0 += 4) {
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+      for (int tt = 0; tt < kRtWaveTok; ++tt)
+        red[(qq * kRtWaveTok + tt) * 64 + (lane ^ (qq * kRtWaveTok + tt))] =
+            acc[q0 + qq][tt];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 32) {
+      // lane j's sum of logit `lane` sits at [lane][j ^ lane] (the swizzle
+      // keeps the 32 readers on distinct banks)
+      const float* v = red + lane * 64;
+      float s[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) s[j] = v[j ^ lane] + v[(j + 32) ^ lane];
+#pragma unroll
+      for (int h = 16; h >= 1; h >>= 1)
+#pragma unroll
+        for (int j = 0; j < h; ++j) s[j] = s[j] + s[j + h];
+      const int qq = lane / kRtWaveTok, tt = lane % kRtWaveTok;
+      const int e = e0 + q0 + qq, t = t0 + wave * kRtWaveTok + tt;
+      float r = s[0];
+      if (bias && e < E) r += bias[e];
+      if (e < e_tot && t < T) logits[(int64_t)t * ld + e] = r;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // One wave per token: top-K, softmax and renormalised weights (wave_topk).
 // Workgroup 0 also clears the workspace status word when given.
 template <int SLOTS>
@@ -208,7 +334,10 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
   else if (T <= 256)
     MLXR_RL(2, 4, 4);
   else
-    MLXR_RL(4, 8, 2);
+    router_logits_tiled_kernel<<<dim3((unsigned)((e_tot + kRtCol - 1) / kRtCol),
+                                      (unsigned)((T + kRtTok - 1) / kRtTok)),
+                                 256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E,
+                                              w_extra, logits, ld);
 #undef MLXR_RL
   return hipGetLastError();
 }
