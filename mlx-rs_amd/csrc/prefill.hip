@@ -57,6 +57,28 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t,
                             __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
+// f rounded to bf16 (the hardware conversion: round to nearest even)
+__device__ __forceinline__ float bf16_hw(float f) { return (float)(__bf16)f; }
+// silu(g) * u with the reference's bf16 rounding points
+// (crates/mlxr-lm/src/activations.rs:187-200), the sigmoid from the
+// hardware exp2 and reciprocal (about 1 ulp each in f32; the bf16 rounding
+// that follows hides that except next to a rounding boundary)
+__device__ __forceinline__ uint16_t swiglu_fast(float g_acc, float u_acc) {
+  const float g = bf16_hw(g_acc), u = bf16_hw(u_acc);
+  const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+  const float sg = bf16_hw(__builtin_amdgcn_rcpf(1.0f + e));
+  const float h = bf16_hw(g * sg);
+  return __builtin_bit_cast(uint16_t, (__bf16)(h * u));
+}
+// q = n / d for 0 <= n < 2^31, 1 <= d <= 2^16: a float estimate and one
+// correction step either way
+__device__ __forceinline__ int div_small(int n, int d, float rd) {
+  int q = (int)((float)n * rd);
+  q -= (q * d > n) ? 1 : 0;
+  q += ((q + 1) * d <= n) ? 1 : 0;
+  return q;
+}
+
 // x & m, opaque to the optimiser so that the byte extracts below stay
 // v_cvt_f32_ubyte{0..3} (it would otherwise fold the masks into bit-field
 // extracts plus a conversion)
@@ -85,15 +107,30 @@ __device__ __forceinline__ void dequant8(uint32_t w, float s, float b,
                      __builtin_fmaf((float)((w >> (16 * j + 8)) & 255u), s, b));
 }
 
+// LDS: three stages, each an x tile [kBM rows][128 B] and a dequantised
+// weight tile [kBN rows][128 B].  Neither is padded: the eight 16-byte
+// chunks of row r sit at positions chunk ^ ((r >> 1) & 7), which keeps the
+// MFMA operand reads of 16 consecutive rows on distinct banks.
+constexpr int kStages = 3;
+constexpr int kAStage = kBM * 128;  // bytes
+constexpr int kBStage = kBN * 128;  // bytes
+constexpr int kStage = kAStage + kBStage;
+constexpr int kPrefillLds = kStages * kStage;
+
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
 // Everything the K-loop needs, in registers.
 template <int BITS>
 struct PrefillCtx {
   __amdgpu_buffer_rsrc_t xr, wr, sr, br;  // x, weights, scales, biases
   uint32_t aoff[kACH];                     // x chunk offsets (bytes)
+  int awr[kACH];                           // where they go in an x stage
   uint32_t woff, soff;                     // code chunk / scale offsets
-  uint16_t* As;
-  uint16_t* Bs;
-  int tid, arow, bc0, bc1, kh, col_off, groups;
+  int bwr0, bwr1;                          // where the dequantised runs go
+  char* lds;
+  int aread[2], aswz[2];                   // A rows (bytes) and swizzles
+  int bread[2], bswz[2];                   // B rows (bytes) and swizzles
+  int hi, groups;
 };
 
 // One group's global loads, held in registers until they are staged.
@@ -121,17 +158,15 @@ __device__ __forceinline__ void prefill_load(const PrefillCtx<BITS>& c,
   R.c = __builtin_amdgcn_raw_buffer_load_b16(c.br, c.soff, 2 * g, 0);
 }
 
-// x chunks to LDS as they are; codes dequantised to bf16 pairs.
-template <int BITS>
+// x chunks as they are, codes dequantised to bf16 pairs, into stage st.
+template <int BITS, int ST>
 __device__ __forceinline__ void prefill_store(const PrefillCtx<BITS>& c,
-                                              const PrefillRegs<BITS>& R, int st) {
-  uint16_t* A = c.As + st * kBM * kRowPad;
-  uint16_t* B = c.Bs + st * kBN * kRowPad;
+                                              const PrefillRegs<BITS>& R) {
+  char* A = c.lds + ST * kStage;
+  char* B = A + kAStage;
 #pragma unroll
-  for (int j = 0; j < kACH; ++j) {
-    const int id = c.tid + kNT * j;
-    *reinterpret_cast<u32x4_t*>(A + (id >> 3) * kRowPad + 8 * (id & 7)) = R.a[j];
-  }
+  for (int j = 0; j < kACH; ++j)
+    *reinterpret_cast<u32x4_t*>(A + c.awr[j]) = R.a[j];
   const float s = __uint_as_float(R.s << 16), b = __uint_as_float(R.c << 16);
   uint32_t o[8];
   if constexpr (BITS == 4) {
@@ -141,73 +176,83 @@ __device__ __forceinline__ void prefill_store(const PrefillCtx<BITS>& c,
 #pragma unroll
     for (int i = 0; i < 4; ++i) dequant8(R.b[i], s, b, o + 2 * i);
   }
-  uint16_t* dst = B + c.col_off;
-  *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{o[0], o[1], o[2], o[3]};
-  *reinterpret_cast<u32x4_t*>(dst + 8) = u32x4_t{o[4], o[5], o[6], o[7]};
+  *reinterpret_cast<u32x4_t*>(B + c.bwr0) = u32x4_t{o[0], o[1], o[2], o[3]};
+  *reinterpret_cast<u32x4_t*>(B + c.bwr1) = u32x4_t{o[4], o[5], o[6], o[7]};
 }
 
-// The multiplies of one group from LDS stage st: every fragment is read
-// first, then the NMB x 2 x 4 MFMAs.
-template <int NMB>
-__device__ __forceinline__ void prefill_mma(const uint16_t* A, const uint16_t* B,
-                                            int arow, int bc0, int bc1, int kh,
+// The multiplies of one group from stage st: per 16-wide K chunk the 2 B
+// fragments and NMB A fragments, then their NMB x 2 MFMAs.
+template <int BITS, int NMB, int ST>
+__device__ __forceinline__ void prefill_mma(const PrefillCtx<BITS>& c,
                                             f32x16_t (&acc)[2][2]) {
-  bf16x8_t af[4][2], bf[4][2];
+  const char* A = c.lds + ST * kStage;
+  const char* B = A + kAStage;
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc) {
-    bf[kc][0] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(B + bc0 * kRowPad + 16 * kc + kh));
-    bf[kc][1] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(B + bc1 * kRowPad + 16 * kc + kh));
+    const int ch = 2 * kc + c.hi;  // 16-byte chunk of the 64-wide group
+    bf16x8_t af[2], bf[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+      bf[nb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(
+          B + c.bread[nb] + 16 * (ch ^ c.bswz[nb])));
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb)
-      af[kc][mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(
-          A + (arow + 32 * mb) * kRowPad + 16 * kc + kh));
-  }
-#pragma unroll
-  for (int kc = 0; kc < 4; ++kc)
+      af[mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(
+          A + c.aread[mb] + 16 * (ch ^ c.aswz[mb])));
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
-        acc[mb][nb] = mfma32x32x16(af[kc][mb], bf[kc][nb], acc[mb][nb]);
+        acc[mb][nb] = mfma32x32x16(af[mb], bf[nb], acc[mb][nb]);
+  }
 }
 
-// K-loop over the groups.  Two register buffers: the loads of group g + 2
-// are issued while group g is multiplied and group g + 1 (loaded a step
-// earlier) is staged into the other LDS stage, so each staging finds its
-// data resident.  One barrier per group.
+// K-loop.  Group q lives in register buffer q % 3 and LDS stage q % 3.
+// Step g: issue group g + 3's loads (its buffer held group g, staged a step
+// ago), multiply group g, stage group g + 1 (loaded two steps ago), barrier.
+// The body unrolls three steps.
 template <int BITS, int NMB>
 __device__ __forceinline__ void prefill_kloop(const PrefillCtx<BITS>& c,
                                               f32x16_t (&acc)[2][2]) {
   const int G = c.groups;
-  PrefillRegs<BITS> R0, R1;
+  // Every step issues the same loads (past the last group it reloads it, a
+  // cache hit), so the compiler can count exactly which loads a staging
+  // must wait for.
+  PrefillRegs<BITS> R0, R1, R2;
   prefill_load(c, R0, 0);
-  if (G > 1) prefill_load(c, R1, 1);
-  prefill_store(c, R0, 0);
+  prefill_load(c, R1, min(1, G - 1));
+  prefill_load(c, R2, min(2, G - 1));
+  prefill_store<BITS, 0>(c, R0);
   __syncthreads();
-  for (int g = 0; g < G; g += 2) {
-    // even group g: stage 0 holds it, R1 holds g + 1
-    if (g + 2 < G) prefill_load(c, R0, g + 2);
-    prefill_mma<NMB>(c.As, c.Bs, c.arow, c.bc0, c.bc1, c.kh, acc);
-    if (g + 1 < G) prefill_store(c, R1, 1);
-    __syncthreads();
-    if (g + 1 >= G) break;
-    // odd group g + 1: stage 1 holds it, R0 holds g + 2
-    if (g + 3 < G) prefill_load(c, R1, g + 3);
-    prefill_mma<NMB>(c.As + kBM * kRowPad, c.Bs + kBN * kRowPad, c.arow, c.bc0,
-                     c.bc1, c.kh, acc);
-    if (g + 2 < G) prefill_store(c, R0, 0);
-    __syncthreads();
+#define MLXR_PF_STEP(K, RL, RS)                                               \
+  {                                                                           \
+    const int gg = g + K;                                                     \
+    prefill_load(c, RL, min(gg + 3, G - 1));                                  \
+    __builtin_amdgcn_sched_barrier(0); /* keep the loads first */             \
+    prefill_mma<BITS, NMB, K>(c, acc);                                        \
+    if (gg + 1 < G) prefill_store<BITS, (K + 1) % 3>(c, RS);                  \
+    __syncthreads();                                                          \
   }
+  // whole triples, then the G % 3 steps left (no early exit from the
+  // unrolled body: the accumulators then keep one set of registers)
+  int g = 0;
+#pragma nounroll
+  for (; g + 3 <= G; g += 3) {
+    MLXR_PF_STEP(0, R0, R1)
+    MLXR_PF_STEP(1, R1, R2)
+    MLXR_PF_STEP(2, R2, R0)
+  }
+  if (g < G) MLXR_PF_STEP(0, R0, R1)
+  if (g + 1 < G) MLXR_PF_STEP(1, R1, R2)
+#undef MLXR_PF_STEP
 }
 
 template <int BITS, bool GATED>
 __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
                                                            int tiles_n,
                                                            uint32_t x_bytes) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  uint16_t* As = reinterpret_cast<uint16_t*>(smem);  // [2][kBM][kRowPad]
-  uint16_t* Bs = As + 2 * kBM * kRowPad;             // [2][kBN][kRowPad]
 
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Workgroups go to the XCDs round robin (blockIdx % kXcds).  Number them
   // so that the N-tiles of one M-tile run on one XCD, one after another:
@@ -227,10 +272,15 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
   // x: one buffer over all rows (rows past the tile read out of range, 0)
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.x), 0, (int)x_bytes, kBufFlags);
+  // x chunk j of this thread: row id / 8, chunk id % 8 (id = tid + kNT j),
+  // stored at its swizzled position
   uint32_t aoff[kACH];
+  int awr[kACH];
+  const float rdiv = 1.0f / (float)a.row_div;
 #pragma unroll
   for (int j = 0; j < kACH; ++j) {
     const int id = tid + kNT * j, r = id >> 3, c = id & 7;
+    awr[j] = r * 128 + 16 * (c ^ swz(r));
     uint32_t off = 0xFFFFFFF0u;
     if (r < rows) {
       const int slot = slot0 + r;
@@ -239,7 +289,7 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
         row = slot;
       } else {
         const int flat = a.sorted[slot];
-        row = a.row_map ? a.row_map[flat] : flat / a.row_div;
+        row = a.row_map ? a.row_map[flat] : div_small(flat, a.row_div, rdiv);
       }
       off = (uint32_t)(row * a.x_ld * 2 + 16 * c);
     }
@@ -287,10 +337,19 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
   // multiply zeros): one K-loop per count, chosen once
   const int wm_u = __builtin_amdgcn_readfirstlane(wm);
   const int nmb = rows > wm_u * 64 + 32 ? 2 : (rows > wm_u * 64 ? 1 : 0);
-  PrefillCtx<BITS> c{xr, wr, sr, br, {}, woff, soff, As, Bs, tid,
-                     arow, bc[0], bc[1], kh, col_off, groups};
+  // this thread's 16 dequantised weights: column col, chunks 2 part and
+  // 2 part + 1 of the group
+  const int bwr0 = col * 128 + 16 * ((2 * part) ^ swz(col));
+  const int bwr1 = col * 128 + 16 * ((2 * part + 1) ^ swz(col));
+  PrefillCtx<BITS> c{xr, wr, sr, br, {}, {}, woff, soff, bwr0, bwr1, smem,
+                     {arow * 128, (arow + 32) * 128}, {swz(arow), swz(arow + 32)},
+                     {bc[0] * 128, bc[1] * 128}, {swz(bc[0]), swz(bc[1])},
+                     kh >> 3, groups};
 #pragma unroll
-  for (int j = 0; j < kACH; ++j) c.aoff[j] = aoff[j];
+  for (int j = 0; j < kACH; ++j) {
+    c.aoff[j] = aoff[j];
+    c.awr[j] = awr[j];
+  }
   if (nmb == 2)
     prefill_kloop<BITS, 2>(c, acc);
   else if (nmb == 1)
@@ -298,27 +357,45 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
   else
     prefill_kloop<BITS, 0>(c, acc);
 
-  // D[8(r/4) + 4(l/32) + r%4][l%32] of each 32 x 32 block
+  // Epilogue through LDS (the K-loop's last barrier freed the stages): the
+  // waves write the tile's bf16 outputs -- SwiGLU of the gate and up sums,
+  // or the down sums -- as [row][channel], rows 64 wm..64 wm + 63 in the
+  // stage region wm, then every thread stores whole 16-byte runs of a row.
+  // D[8(r/4) + 4(l/32) + r%4][l%32] of each 32 x 32 block.
+  constexpr int OC = GATED ? kBN / 2 : kBN;  // output channels of the tile
+  constexpr int OST = OC + 8;                // LDS row stride (bf16)
+  static_assert((size_t)kBM * OST * 2 + kBM * 4 <= (size_t)kPrefillLds,
+                "epilogue fits");
+  auto region = [&](int q) -> uint16_t* {
+    return reinterpret_cast<uint16_t*>(smem) + q * 64 * OST;
+  };
+  uint16_t* O = region(wm);
+  int32_t* orow_s = reinterpret_cast<int32_t*>(smem + kBM * OST * 2);
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = wm * 64 + 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      if (row >= rows) continue;
-      const int slot = slot0 + row;
+      const int row = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);  // in the region
       if constexpr (GATED) {
-        const int och = nt * (kBN / 2) + wn * 32 + (lane & 31);
-        a.out[(int64_t)slot * a.out_ld + och] =
-            swiglu_bf16(bf16_round(acc[mb][0][r]), bf16_round(acc[mb][1][r]));
+        O[row * OST + wn * 32 + (lane & 31)] = swiglu_fast(acc[mb][0][r], acc[mb][1][r]);
       } else {
-        const int64_t orow = a.out_by_flat ? a.sorted[slot] : slot;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const int och = nt * kBN + wn * 64 + 32 * nb + (lane & 31);
-          a.out[orow * a.out_ld + och] = f32_to_bf16(acc[mb][nb][r]);
-        }
+        for (int nb = 0; nb < 2; ++nb)
+          O[row * OST + wn * 64 + 32 * nb + (lane & 31)] =
+              __builtin_bit_cast(uint16_t, (__bf16)acc[mb][nb][r]);
       }
     }
+  }
+  if (!GATED && a.out_by_flat)
+    for (int i = tid; i < rows; i += kNT) orow_s[i] = a.sorted[slot0 + i];
+  __syncthreads();
+  constexpr int CPR = OC / 8;  // 16-byte runs per row
+  const int och0 = GATED ? nt * (kBN / 2) : nt * kBN;
+  for (int id = tid; id < rows * CPR; id += kNT) {
+    const int row = id / CPR, c = id - row * CPR;
+    const int64_t orow = (!GATED && a.out_by_flat) ? orow_s[row] : slot0 + row;
+    *reinterpret_cast<u32x4_t*>(a.out + orow * a.out_ld + och0 + 8 * c) =
+        *reinterpret_cast<const u32x4_t*>(region(row >> 6) + (row & 63) * OST + 8 * c);
   }
 }
 
@@ -327,8 +404,10 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
 bool prefill_supported(const QGemmArgs& a, int64_t x_rows) {
   const int cols = a.gated ? kBN / 2 : kBN;
   // buffer offsets are 32-bit: x, and one expert's weights, under 2 GB
+  // outputs leave as 16-byte runs of a row
+  const bool out16 = (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && a.out_ld % 8 == 0;
   return (a.bits == 4 || a.bits == 8) && a.K % 64 == 0 && a.N % cols == 0 &&
-         a.sorted != nullptr &&
+         a.sorted != nullptr && out16 && a.row_div >= 1 && a.row_div <= 65536 &&
          x_rows * a.x_ld * 2 < ((int64_t)1 << 31) &&
          (int64_t)a.N * a.K * a.bits / 8 < ((int64_t)1 << 31);
 }
@@ -337,7 +416,7 @@ hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 int64_t max_tiles, hipStream_t s) {
   if (max_tiles <= 0) return hipSuccess;
   const int tiles_n = a.N / (a.gated ? kBN / 2 : kBN);
-  const size_t lds = (size_t)2 * (kBM + kBN) * kRowPad * 2;
+  const size_t lds = kPrefillLds;
   const dim3 grid((unsigned)((max_tiles * tiles_n + kXcds - 1) / kXcds * kXcds));
   const uint32_t x_bytes = (uint32_t)(x_rows * a.x_ld * 2);
   ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
