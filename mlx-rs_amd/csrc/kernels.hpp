@@ -150,7 +150,10 @@ struct QGemmArgs {
 constexpr int kMaxInputDims = 4096;
 // Rows per M-tile of the prefill kernel (64 per wave along M); the dispatch
 // builds its tile list.  Waves along N: 64 B columns each.
-constexpr int kPrefillTileRows = 256;
+#ifndef MLXR_PREFILL_TILE_ROWS
+#define MLXR_PREFILL_TILE_ROWS 256
+#endif
+constexpr int kPrefillTileRows = MLXR_PREFILL_TILE_ROWS;
 constexpr int kPrefillWavesN = 2;
 // max_items bounds the number of work items (dispatch_max_work); prefill
 // selects the M-tiled kernel (prefill.hip) where it applies.

@@ -42,8 +42,9 @@ constexpr int kBN = 64 * kWN;           // B columns per tile
 constexpr int kACH = kBM * 8 / kNT;     // 16-byte x chunks per thread
 constexpr int kPARTS = kNT / kBN;       // threads per B column per group
 constexpr int kCODES = 64 / kPARTS;     // codes per thread per group
-static_assert(kBM * 8 % kNT == 0 && kNT % kBN == 0 && kCODES == 16,
-              "tile split");
+constexpr int kCPT = kCODES / 8;        // 16-byte bf16 runs per thread
+static_assert(kBM * 8 % kNT == 0 && kNT % kBN == 0 &&
+                  (kCODES == 16 || kCODES == 32), "tile split");
 // raw buffer resource word 3 (gfx9 family)
 constexpr int kBufFlags = 0x00020000;
 // XCDs of an MI355X (the workgroup numbering below assumes this many; any
@@ -111,7 +112,8 @@ __device__ __forceinline__ void dequant8(uint32_t w, float s, float b,
 // weight tile [kBN rows][128 B].  Neither is padded: the eight 16-byte
 // chunks of row r sit at positions chunk ^ ((r >> 1) & 7), which keeps the
 // MFMA operand reads of 16 consecutive rows on distinct banks.
-constexpr int kStages = 3;
+// three stages when one workgroup holds the CU, two when two share it
+constexpr int kStages = kBM == 256 ? 3 : 2;
 constexpr int kAStage = kBM * 128;  // bytes
 constexpr int kBStage = kBN * 128;  // bytes
 constexpr int kStage = kAStage + kBStage;
@@ -126,7 +128,7 @@ struct PrefillCtx {
   uint32_t aoff[kACH];                     // x chunk offsets (bytes)
   int awr[kACH];                           // where they go in an x stage
   uint32_t woff, soff;                     // code chunk / scale offsets
-  int bwr0, bwr1;                          // where the dequantised runs go
+  int bwr[kCPT];                           // where the dequantised runs go
   char* lds;
   int aread[2], aswz[2];                   // A rows (bytes) and swizzles
   int bread[2], bswz[2];                   // B rows (bytes) and swizzles
@@ -136,9 +138,10 @@ struct PrefillCtx {
 // One group's global loads, held in registers until they are staged.
 template <int BITS>
 struct PrefillRegs {
-  typedef uint32_t u32w_t __attribute__((ext_vector_type(BITS / 2)));
+  static constexpr int kWords = kCODES * BITS / 32;  // code words per thread
+  typedef uint32_t u32w_t __attribute__((ext_vector_type(kWords < 4 ? kWords : 4)));
   u32x4_t a[kACH];
-  u32w_t b;
+  u32w_t b[kWords < 4 ? 1 : kWords / 4];
   uint32_t s, c;
 };
 
@@ -150,10 +153,15 @@ __device__ __forceinline__ void prefill_load(const PrefillCtx<BITS>& c,
 #pragma unroll
   for (int j = 0; j < kACH; ++j)
     R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(c.xr, c.aoff[j], 128 * g, 0);
-  if constexpr (BITS == 4)
-    R.b = __builtin_amdgcn_raw_buffer_load_b64(c.wr, c.woff, 32 * g, 0);
-  else
-    R.b = __builtin_amdgcn_raw_buffer_load_b128(c.wr, c.woff, 64 * g, 0);
+  constexpr int kW = PrefillRegs<BITS>::kWords;
+  if constexpr (kW == 2) {
+    R.b[0] = __builtin_amdgcn_raw_buffer_load_b64(c.wr, c.woff, 32 * g, 0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kW / 4; ++i)
+      R.b[i] = __builtin_amdgcn_raw_buffer_load_b128(c.wr, c.woff + 16 * i,
+                                                     8 * BITS * g, 0);
+  }
   R.s = __builtin_amdgcn_raw_buffer_load_b16(c.sr, c.soff, 2 * g, 0);
   R.c = __builtin_amdgcn_raw_buffer_load_b16(c.br, c.soff, 2 * g, 0);
 }
@@ -168,25 +176,42 @@ __device__ __forceinline__ void prefill_store(const PrefillCtx<BITS>& c,
   for (int j = 0; j < kACH; ++j)
     *reinterpret_cast<u32x4_t*>(A + c.awr[j]) = R.a[j];
   const float s = __uint_as_float(R.s << 16), b = __uint_as_float(R.c << 16);
-  uint32_t o[8];
-  if constexpr (BITS == 4) {
-    dequant4(R.b[0], s, b, o);
-    dequant4(R.b[1], s, b, o + 4);
-  } else {
+  constexpr int kW = PrefillRegs<BITS>::kWords;
+  uint32_t w[kW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dequant8(R.b[i], s, b, o + 2 * i);
+  for (int i = 0; i < kW; ++i) w[i] = R.b[i / 4][i % 4];
+  uint32_t o[kCODES / 2];
+#pragma unroll
+  for (int i = 0; i < kW; ++i) {
+    if constexpr (BITS == 4)
+      dequant4(w[i], s, b, o + 4 * i);
+    else
+      dequant8(w[i], s, b, o + 2 * i);
   }
-  *reinterpret_cast<u32x4_t*>(B + c.bwr0) = u32x4_t{o[0], o[1], o[2], o[3]};
-  *reinterpret_cast<u32x4_t*>(B + c.bwr1) = u32x4_t{o[4], o[5], o[6], o[7]};
+#pragma unroll
+  for (int i = 0; i < kCPT; ++i)
+    *reinterpret_cast<u32x4_t*>(B + c.bwr[i]) =
+        u32x4_t{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
 }
 
-// The multiplies of one group from stage st: per 16-wide K chunk the 2 B
-// fragments and NMB A fragments, then their NMB x 2 MFMAs.
-template <int BITS, int NMB, int ST>
-__device__ __forceinline__ void prefill_mma(const PrefillCtx<BITS>& c,
-                                            f32x16_t (&acc)[2][2]) {
+// The multiplies of one group from stage ST, with the staging of the next
+// group (register buffer R, into stage SS) spread between them: a quarter
+// of the x copies and of the dequantisation after each 16-wide K chunk's
+// MFMAs, so the VALU work runs while the matrix core is busy.  Per chunk:
+// the 2 B fragments and NMB A fragments, then their NMB x 2 MFMAs.
+template <int BITS, int NMB, int ST, int SS>
+__device__ __forceinline__ void prefill_mma_store(const PrefillCtx<BITS>& c,
+                                                  const PrefillRegs<BITS>& R,
+                                                  f32x16_t (&acc)[2][2]) {
   const char* A = c.lds + ST * kStage;
   const char* B = A + kAStage;
+  char* As = c.lds + SS * kStage;
+  char* Bs = As + kAStage;
+  constexpr int kW = PrefillRegs<BITS>::kWords;
+  constexpr int kWPK = (kW + 3) / 4;   // code words dequantised per chunk
+  constexpr int kOPW = BITS == 4 ? 4 : 2;  // bf16 pair words per code word
+  const float s = __uint_as_float(R.s << 16), b = __uint_as_float(R.c << 16);
+  uint32_t o[kCODES / 2];
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc) {
     const int ch = 2 * kc + c.hi;  // 16-byte chunk of the 64-wide group
@@ -204,13 +229,34 @@ __device__ __forceinline__ void prefill_mma(const PrefillCtx<BITS>& c,
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
         acc[mb][nb] = mfma32x32x16(af[mb], bf[nb], acc[mb][nb]);
+    // staging, part kc
+#pragma unroll
+    for (int j = kc; j < kACH; j += 4)
+      *reinterpret_cast<u32x4_t*>(As + c.awr[j]) = R.a[j];
+#pragma unroll
+    for (int i = kc * kWPK; i < kW && i < (kc + 1) * kWPK; ++i) {
+      const uint32_t w = R.b[i / 4][i % 4];
+      if constexpr (BITS == 4)
+        dequant4(w, s, b, o + kOPW * i);
+      else
+        dequant8(w, s, b, o + kOPW * i);
+    }
+    // runs whose words are all done by the end of this part
+#pragma unroll
+    for (int r = 0; r < kCPT; ++r) {
+      const int last_word = (4 * r + 3) / kOPW;  // word holding the run's end
+      if (last_word / kWPK == kc)
+        *reinterpret_cast<u32x4_t*>(Bs + c.bwr[r]) =
+            u32x4_t{o[4 * r], o[4 * r + 1], o[4 * r + 2], o[4 * r + 3]};
+    }
   }
 }
 
-// K-loop.  Group q lives in register buffer q % 3 and LDS stage q % 3.
-// Step g: issue group g + 3's loads (its buffer held group g, staged a step
-// ago), multiply group g, stage group g + 1 (loaded two steps ago), barrier.
-// The body unrolls three steps.
+// K-loop.  Group q lives in register buffer q % 3 and LDS stage
+// q % kStages.  Step g: issue group g + 3's loads (its buffer held group g,
+// staged a step ago), multiply group g while staging group g + 1 (loaded
+// two steps ago; after the last group this stages a copy nobody reads),
+// barrier.  The body unrolls lcm(3, kStages) steps.
 template <int BITS, int NMB>
 __device__ __forceinline__ void prefill_kloop(const PrefillCtx<BITS>& c,
                                               f32x16_t (&acc)[2][2]) {
@@ -218,32 +264,41 @@ __device__ __forceinline__ void prefill_kloop(const PrefillCtx<BITS>& c,
   // Every step issues the same loads (past the last group it reloads it, a
   // cache hit), so the compiler can count exactly which loads a staging
   // must wait for.
-  PrefillRegs<BITS> R0, R1, R2;
-  prefill_load(c, R0, 0);
-  prefill_load(c, R1, min(1, G - 1));
-  prefill_load(c, R2, min(2, G - 1));
-  prefill_store<BITS, 0>(c, R0);
+  PrefillRegs<BITS> R[3];
+  prefill_load(c, R[0], 0);
+  prefill_load(c, R[1], min(1, G - 1));
+  prefill_load(c, R[2], min(2, G - 1));
+  prefill_store<BITS, 0>(c, R[0]);
   __syncthreads();
-#define MLXR_PF_STEP(K, RL, RS)                                               \
+#define MLXR_PF_STEP(K)                                                       \
   {                                                                           \
     const int gg = g + K;                                                     \
-    prefill_load(c, RL, min(gg + 3, G - 1));                                  \
+    prefill_load(c, R[K % 3], min(gg + 3, G - 1));                            \
     __builtin_amdgcn_sched_barrier(0); /* keep the loads first */             \
-    prefill_mma<BITS, NMB, K>(c, acc);                                        \
-    if (gg + 1 < G) prefill_store<BITS, (K + 1) % 3>(c, RS);                  \
+    prefill_mma_store<BITS, NMB, K % kStages, (K + 1) % kStages>(             \
+        c, R[(K + 1) % 3], acc);                                              \
     __syncthreads();                                                          \
   }
-  // whole triples, then the G % 3 steps left (no early exit from the
-  // unrolled body: the accumulators then keep one set of registers)
+  // whole bodies, then the steps left (no early exit from the unrolled
+  // body: the accumulators then keep one set of registers)
+  constexpr int U = kStages == 3 ? 3 : 6;
   int g = 0;
 #pragma nounroll
-  for (; g + 3 <= G; g += 3) {
-    MLXR_PF_STEP(0, R0, R1)
-    MLXR_PF_STEP(1, R1, R2)
-    MLXR_PF_STEP(2, R2, R0)
+  for (; g + U <= G; g += U) {
+    MLXR_PF_STEP(0)
+    MLXR_PF_STEP(1)
+    MLXR_PF_STEP(2)
+    if constexpr (U == 6) {
+      MLXR_PF_STEP(3)
+      MLXR_PF_STEP(4)
+      MLXR_PF_STEP(5)
+    }
   }
-  if (g < G) MLXR_PF_STEP(0, R0, R1)
-  if (g + 1 < G) MLXR_PF_STEP(1, R1, R2)
+  if (g < G) MLXR_PF_STEP(0)
+  if (g + 1 < G) MLXR_PF_STEP(1)
+  if (g + 2 < G) MLXR_PF_STEP(2)
+  if (U == 6 && g + 3 < G) MLXR_PF_STEP(3)
+  if (U == 6 && g + 4 < G) MLXR_PF_STEP(4)
 #undef MLXR_PF_STEP
 }
 
@@ -337,11 +392,9 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
   // multiply zeros): one K-loop per count, chosen once
   const int wm_u = __builtin_amdgcn_readfirstlane(wm);
   const int nmb = rows > wm_u * 64 + 32 ? 2 : (rows > wm_u * 64 ? 1 : 0);
-  // this thread's 16 dequantised weights: column col, chunks 2 part and
-  // 2 part + 1 of the group
-  const int bwr0 = col * 128 + 16 * ((2 * part) ^ swz(col));
-  const int bwr1 = col * 128 + 16 * ((2 * part + 1) ^ swz(col));
-  PrefillCtx<BITS> c{xr, wr, sr, br, {}, {}, woff, soff, bwr0, bwr1, smem,
+  // this thread's kCODES dequantised weights: column col, runs
+  // kCPT part .. kCPT part + kCPT - 1 of the group
+  PrefillCtx<BITS> c{xr, wr, sr, br, {}, {}, woff, soff, {}, smem,
                      {arow * 128, (arow + 32) * 128}, {swz(arow), swz(arow + 32)},
                      {bc[0] * 128, bc[1] * 128}, {swz(bc[0]), swz(bc[1])},
                      kh >> 3, groups};
@@ -350,6 +403,9 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
     c.aoff[j] = aoff[j];
     c.awr[j] = awr[j];
   }
+#pragma unroll
+  for (int i = 0; i < kCPT; ++i)
+    c.bwr[i] = col * 128 + 16 * ((kCPT * part + i) ^ swz(col));
   if (nmb == 2)
     prefill_kloop<BITS, 2>(c, acc);
   else if (nmb == 1)
