@@ -22,6 +22,9 @@ namespace mlxr_moe {
 namespace {
 
 constexpr int kWaves = kDispatchBlock / 64;
+#ifndef MLXR_ROUTE_SMALL_TOKENS
+#define MLXR_ROUTE_SMALL_TOKENS 16
+#endif
 
 __global__ __launch_bounds__(kDispatchBlock) void dispatch_rank_kernel(
     const int32_t* __restrict__ ids, int n, int E,
@@ -295,9 +298,10 @@ hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
                         int64_t K, int32_t* idx, float* wts, int tile_rows,
                         const DispatchBuffers& b, hipStream_t s) {
   if (T == 0) return launch_zero_status(b.status, s);
-  // one workgroup while each of its 16 waves has one token; beyond that the
-  // top-k spreads over the GPU (a wave per token) before the sort
-  if (T > kDispatchBlock / 64 || T * K > kDispatchBlock) {
+  // one workgroup while the T*K ids fit it and its 16 waves have at most
+  // MLXR_ROUTE_SMALL_TOKENS / 16 tokens each; beyond that the top-k spreads
+  // over the GPU (a wave per token) before the sort
+  if (T > MLXR_ROUTE_SMALL_TOKENS || T * K > kDispatchBlock) {
     hipError_t e = launch_router_topk(logits, ld, T, E, K, idx, wts, b.status, s);
     if (e != hipSuccess) return e;
     return launch_dispatch(idx, T * K, E, tile_rows, b, false, s);

@@ -67,8 +67,9 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
 namespace nn {
 
 bool use_prefill_path(int64_t rows, int64_t experts) {
-  // the M-tiled kernel pays once the experts average 32 rows
-  return rows >= 32 * experts;
+  // the M-tiled kernel pays once the experts average 32 rows and there are
+  // rows enough for its tiles to spread over the GPU
+  return rows >= 32 * experts && rows >= 512;
 }
 
 namespace {
