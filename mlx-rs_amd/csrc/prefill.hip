@@ -19,22 +19,23 @@
 // three instructions per weight) over many rows; waves whose rows lie past
 // the expert's last row skip their MFMAs.  Global loads are raw buffer loads
 // with the K step in the scalar offset: no per-step address arithmetic.
-// K advances one quantisation group (64) per step through two LDS stages:
-// while the waves multiply stage s, the global loads of the next group are
-// in flight in registers, and after the multiplies they are dequantised into
-// stage s^1.  One barrier per step.
+// K advances one quantisation group (64) per step.  Three register buffers
+// hold the loads of the next groups in flight, and three LDS stages hold
+// dequantised tiles: while the waves multiply stage s, the group loaded two
+// steps ago is dequantised into the next stage, interleaved with the MFMAs.
+// One barrier per step.
 //
 // Each wave owns 64 x 64 outputs as 2 x 2 blocks of v_mfma_f32_32x32x16_bf16
-// (K = 16 per instruction, four per group).  LDS rows are 64 bf16 padded to
-// 72 (144 bytes), which keeps the 16-byte operand reads of 16 lanes on
-// distinct banks.
+// (K = 16 per instruction, four per group).  LDS rows are 64 bf16 (128
+// bytes) with the eight 16-byte chunks of row r stored at chunk ^ ((r >> 1)
+// & 7), which keeps the 16-byte operand reads of a wave on distinct banks.
+// The epilogue goes through LDS so that every output store is 16 bytes.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace mlxr_moe {
 namespace {
 
-constexpr int kRowPad = 72;  // LDS row stride (bf16)
 constexpr int kWM = kPrefillTileRows / 64, kWN = kPrefillWavesN;
 constexpr int kNT = 64 * kWM * kWN;     // threads
 constexpr int kBM = 64 * kWM;           // rows per tile
@@ -379,7 +380,6 @@ __global__ __launch_bounds__(kNT) void qgemm_prefill_kernel(QGemmArgs a,
   for (int nb = 0; nb < 2; ++nb)
     bc[nb] = (GATED ? nb * (kBN / 2) + wn * 32 : wn * 64 + nb * 32) + (lane & 31);
   const int kh = 8 * (lane >> 5);
-  const int col_off = col * kRowPad + part * kCODES;
 
   f32x16_t acc[2][2];
 #pragma unroll
