@@ -196,7 +196,7 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
                                    N, ids, xrow, o, status, s),
                 "gather_qmm prep");
   if (st.ok)
-    st = from_hip(launch_dispatch(ids, R, E, kPrefillTileRows, db, false, s),
+    st = from_hip(launch_dispatch(ids, R, E, prefill_tile_rows(R, E), db, false, s),
                   "gather_qmm dispatch");
   if (!st.ok) return finish(st);
   QGemmArgs a{};
@@ -329,7 +329,7 @@ int mlxr_moe_dispatch(const int32_t* ids, int64_t n, int64_t E,
   db.offsets = offsets;
   db.sorted = sorted;
   db.inv = inv;
-  return finish(from_hip(launch_dispatch(ids, n, E, kPrefillTileRows, db, true,
+  return finish(from_hip(launch_dispatch(ids, n, E, prefill_tile_rows(n, E), db, true,
                                          as_stream(stream)),
                          "dispatch"));
 }

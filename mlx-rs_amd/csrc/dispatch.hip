@@ -83,7 +83,7 @@ __device__ __forceinline__ int upper_slot(const int* start, int n, int v) {
 __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
     int n, int E, int nb, int tile_rows, DispatchBuffers b) {
   __shared__ int s_off[kMaxExperts], s_wpos[kMaxExperts], s_tpos[kMaxExperts];
-  __shared__ int wsum[kWaves + 1];
+  __shared__ int wsum[kWaves + 1][4];
   const int tid = threadIdx.x;
   // exclusive prefix of each expert's column over the workgroups, 16 loads
   // in flight at a time (a load after a store of the same array would wait
@@ -103,33 +103,29 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
       }
     }
   }
-  int total;
-  const int off = block_exclusive_scan(cnt, &total, wsum);
+  // one scan: row offsets, active experts, work items, M-tiles
+  const int has = (tid < E && cnt > 0) ? 1 : 0;
+  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
+  const int nt = (tid < E) ? (cnt + tile_rows - 1) / tile_rows : 0;
+  int ex[4], tot[4];
+  block_exclusive_scan4({cnt, has, nw, nt}, ex, tot, wsum);
+  const int off = ex[0], wpos = ex[2], tpos = ex[3];
+  const int total = tot[0], n_work = tot[2], n_tiles = tot[3];
   if (tid < E) {
     b.counts[tid] = cnt;
     b.offsets[tid] = off;
     s_off[tid] = off;
-  }
-  if (tid == 0) b.offsets[E] = total;
-
-  const int has = (tid < E && cnt > 0) ? 1 : 0;
-  int n_active;
-  const int apos = block_exclusive_scan(has, &n_active, wsum);
-  if (has) b.active[apos] = tid;
-  if (tid == 0) *b.num_active = n_active;
-  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
-  int n_work;
-  const int wpos = block_exclusive_scan(nw, &n_work, wsum);
-  if (tid < E) {
     s_wpos[tid] = wpos;
     b.work_first[tid] = wpos;
+    s_tpos[tid] = tpos;
   }
-  if (tid == 0) *b.num_work = n_work;
-  const int nt = (tid < E) ? (cnt + tile_rows - 1) / tile_rows : 0;
-  int n_tiles;
-  const int tpos = block_exclusive_scan(nt, &n_tiles, wsum);
-  if (tid < E) s_tpos[tid] = tpos;
-  if (tid == 0) *b.num_tiles = n_tiles;
+  if (has) b.active[ex[1]] = tid;
+  if (tid == 0) {
+    b.offsets[E] = total;
+    *b.num_active = tot[1];
+    *b.num_work = n_work;
+    *b.num_tiles = n_tiles;
+  }
   __syncthreads();
   // experts with no rows share their start with the next: the search finds
   // the last expert starting at or before the entry, which has rows

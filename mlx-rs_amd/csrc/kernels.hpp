@@ -148,24 +148,28 @@ struct QGemmArgs {
 };
 // Largest input dim (K) of a projection: 8 waves x 8 groups of 64.
 constexpr int kMaxInputDims = 4096;
-// Rows per M-tile of the prefill kernel (64 per wave along M); the dispatch
-// builds its tile list.  Waves along N: 64 B columns each.
-#ifndef MLXR_PREFILL_TILE_ROWS
-#define MLXR_PREFILL_TILE_ROWS 256
+// Prefill kernel M-tiles: 256 rows when the experts average at least
+// MLXR_PREFILL_TALL_ROWS rows, else 128 (prefill_tile_rows).  The dispatch
+// cuts its M-tile list with the same choice; tile lists are sized for the
+// shorter tiles.
+#ifndef MLXR_PREFILL_TALL_ROWS
+#define MLXR_PREFILL_TALL_ROWS 192
 #endif
-constexpr int kPrefillTileRows = MLXR_PREFILL_TILE_ROWS;
-constexpr int kPrefillWavesN = 2;
+constexpr int kPrefillMinTileRows = 128;
+int prefill_tile_rows(int64_t rows, int64_t experts);
 // max_items bounds the number of work items (dispatch_max_work); prefill
 // selects the M-tiled kernel (prefill.hip) where it applies.
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s);
 
 // ---------------------------------------------------------------- prefill.hip
-// x_rows bounds the rows of x the GEMM reads; max_tiles bounds the M-tile
-// list (dispatch_max_tiles).
+// x_rows bounds the rows of x the GEMM reads; tile_rows is the M-tile height
+// the dispatch used (prefill_tile_rows); max_tiles bounds the M-tile list
+// (dispatch_max_tiles).
 bool prefill_supported(const QGemmArgs& a, int64_t x_rows);
 hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
-                                int64_t max_tiles, hipStream_t s);
+                                int tile_rows, int64_t max_tiles,
+                                hipStream_t s);
 
 // -------------------------------------------------------------- combine.hip
 hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,

@@ -56,7 +56,7 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
   b.work = c.take<int32_t>(kWorkInts * dispatch_max_work(n, E));
   b.num_work = c.take<int32_t>(1);
   b.work_first = c.take<int32_t>(E);
-  b.tiles = c.take<int32_t>(2 * dispatch_max_tiles(n, E, kPrefillTileRows));
+  b.tiles = c.take<int32_t>(2 * dispatch_max_tiles(n, E, kPrefillMinTileRows));
   b.num_tiles = c.take<int32_t>(1);
   b.block_hist = c.take<int32_t>(nb * E);
   b.rank = c.take<int32_t>(n);
@@ -105,7 +105,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   const int64_t d = gate_.input_dims, f = gate_.output_dims;
   const DispatchBuffers db = carve_dispatch(ws, T, 1, status);
   uint16_t* act = ws.take<uint16_t>(T * f);
-  Status st = from_hip(launch_dispatch_identity(T, kPrefillTileRows, db, s),
+  Status st = from_hip(launch_dispatch_identity(T, prefill_tile_rows(T, 1), db, s),
                        "shared_expert dispatch");
   if (!st.ok) return st;
   const bool prefill = use_prefill_path(T, 1);
@@ -182,7 +182,7 @@ Status SplitSwitchFfn::forward(const uint16_t* x, int64_t T,
   const int64_t n = T * K;
   const DispatchBuffers db = carve_dispatch(ws, n, E, status);
   Status st = from_hip(
-      launch_dispatch(indices, n, E, kPrefillTileRows, db, false, s),
+      launch_dispatch(indices, n, E, prefill_tile_rows(n, E), db, false, s),
       "switch_mlp dispatch");
   if (!st.ok) return st;
   return experts(x, T, K, db, y, ws, s);
@@ -325,7 +325,7 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
   if (!st.ok) return st;
   // softmax, argpartition top-k, renormalise (moe.rs:124-138) + gather_sort
   st = from_hip(
-      launch_route(logits, ld, T, E, K, idx, wts, kPrefillTileRows, db, s),
+      launch_route(logits, ld, T, E, K, idx, wts, prefill_tile_rows(T * K, E), db, s),
       "router top-k / dispatch");
   if (!st.ok) return st;
   if (shared) {

@@ -687,9 +687,11 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s) {
   if (max_items <= 0) return hipSuccess;
-  if (prefill && prefill_supported(a, total_rows))
-    return launch_qgemm_prefill(
-        a, total_rows, dispatch_max_tiles(total_rows, a.E, kPrefillTileRows), s);
+  if (prefill && prefill_supported(a, total_rows)) {
+    const int tile_rows = prefill_tile_rows(total_rows, a.E);
+    return launch_qgemm_prefill(a, total_rows, tile_rows,
+                                dispatch_max_tiles(total_rows, a.E, tile_rows), s);
+  }
   const int groups = a.K / 64;
   // Many (expert, block) items: the streaming kernel (one block per wave,
   // x in LDS, a ring of weight loads).  Few: the split-K kernel below, which

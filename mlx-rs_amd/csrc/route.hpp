@@ -22,6 +22,7 @@ __device__ __forceinline__ uint32_t float_key(float f) {
 struct TopkScratch {
   uint32_t key[64];
   int32_t id[64];
+  float val[64];
 };
 
 // Top-K of logits[e], e < E, for one token, selected on the logits (softmax
@@ -70,6 +71,7 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
       const int pos = base + __popcll(sm & below);
       sc->key[pos] = key[s];
       sc->id[pos] = lane + 64 * s;
+      sc->val[pos] = v[s];
     }
     base += __popcll(sm);
   }
@@ -79,9 +81,11 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
   // rank of each selected pair: larger key first, then lower id
   int my_id = 0, rank = 0;
   uint32_t my_key = 0u;
+  float my_val = 0.0f;
   if (lane < K) {
     my_key = sc->key[lane];
     my_id = sc->id[lane];
+    my_val = sc->val[lane];
     for (int j = 0; j < K; ++j) {
       const uint32_t kj = sc->key[j];
       const int ij = sc->id[j];
@@ -91,18 +95,22 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane < K) sc->id[rank] = my_id;
+  if (lane < K) {
+    sc->id[rank] = my_id;
+    sc->val[rank] = my_val;
+  }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // the selected logits come from LDS: no dependent re-read of memory
   const int id = lane < K ? sc->id[lane] : 0;
-  const float m = logits[sc->id[0]];
+  const float m = sc->val[0];
   float acc = 0.0f;
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s)
     if (lane + 64 * s < E) acc += expf(v[s] - m);
   const float S = wave_sum_butterfly(acc);
-  const float p = lane < K ? expf(logits[id] - m) / S : 0.0f;
+  const float p = lane < K ? expf(sc->val[lane] - m) / S : 0.0f;
   float psum = 0.0f;
   for (int k = 0; k < K; ++k) psum += __shfl(p, k, 64);
   *out_id = id;
@@ -112,38 +120,54 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
 // LDS of block_dispatch: per-wave match counts, scan scratch, offsets.
 struct DispatchScratch {
   uint16_t tab[kDispatchBlock / 64][kMaxExperts];
-  int wsum[kDispatchBlock / 64 + 1];
+  int wsum[kDispatchBlock / 64 + 1][4];
   int off[kMaxExperts];
   int wpos[kMaxExperts];
 };
 
-// Exclusive scan of one int per thread over a 1024-thread workgroup.
-__device__ __forceinline__ int block_exclusive_scan(int v, int* total,
-                                                    int* wsum) {
+// Exclusive scans of four ints per thread over a 1024-thread workgroup at
+// once: wave scans, then wave 0 scans the 16 wave totals.  Two barriers.
+__device__ __forceinline__ void block_exclusive_scan4(const int (&v)[4],
+                                                      int (&ex)[4],
+                                                      int (&total)[4],
+                                                      int (*wsum)[4]) {
   constexpr int kWaves = kDispatchBlock / 64;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int inc = v;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc[4];
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += u;
-  }
-  if (lane == 63) wsum[wave] = inc;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < kWaves; ++w) {
-      const int c = wsum[w];
-      wsum[w] = run;
-      run += c;
+  for (int k = 0; k < 4; ++k) {
+    inc[k] = v[k];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(inc[k], o, 64);
+      if (lane >= o) inc[k] += u;
     }
-    wsum[kWaves] = run;
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wsum[wave][k] = inc[k];
   }
   __syncthreads();
-  const int ex = wsum[wave] + inc - v;
-  *total = wsum[kWaves];
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int t = lane < kWaves ? wsum[lane][k] : 0;
+      int s = t;
+#pragma unroll
+      for (int o = 1; o < kWaves; o <<= 1) {
+        const int u = __shfl_up(s, o, 64);
+        if (lane >= o) s += u;
+      }
+      if (lane < kWaves) wsum[lane][k] = s - t;
+      if (lane == kWaves - 1) wsum[kWaves][k] = s;
+    }
+  }
   __syncthreads();
-  return ex;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    ex[k] = wsum[wave][k] + inc[k] - v[k];
+    total[k] = wsum[kWaves][k];
+  }
 }
 
 // Stable counting sort of ids[0..n) (n <= 1024, read by thread i) by expert
@@ -181,23 +205,20 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
       cnt += c;
     }
   }
-  int total;
-  const int off = block_exclusive_scan(cnt, &total, ls->wsum);
+  // one scan: row offsets, active experts, work items, M-tiles
+  const int has = (tid < E && cnt > 0) ? 1 : 0;
+  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
+  const int nt = tid < E ? (cnt + tile_rows - 1) / tile_rows : 0;
+  int ex[4], tot[4];
+  block_exclusive_scan4({cnt, has, nw, nt}, ex, tot, ls->wsum);
+  const int off = ex[0], apos = ex[1], wpos = ex[2], tpos = ex[3];
   if (tid < E) {
     b.counts[tid] = cnt;
     b.offsets[tid] = off;
     ls->off[tid] = off;
+    ls->wpos[tid] = wpos;
   }
-  if (tid == 0) b.offsets[E] = total;
-  const int has = (tid < E && cnt > 0) ? 1 : 0;
-  int n_active;
-  const int apos = block_exclusive_scan(has, &n_active, ls->wsum);
   if (has) b.active[apos] = tid;
-  if (tid == 0) *b.num_active = n_active;
-  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
-  int n_work;
-  const int wpos = block_exclusive_scan(nw, &n_work, ls->wsum);
-  if (tid < E) ls->wpos[tid] = wpos;
   for (int j = 0; j < nw; ++j) {
     int32_t* w = b.work + kWorkInts * (wpos + j);
     w[0] = tid;
@@ -205,15 +226,16 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
     w[2] = min(kWorkRows, cnt - j * kWorkRows);
     w[3] = cnt;
   }
-  if (tid == 0) *b.num_work = n_work;
-  const int nt = tid < E ? (cnt + tile_rows - 1) / tile_rows : 0;
-  int n_tiles;
-  const int tpos = block_exclusive_scan(nt, &n_tiles, ls->wsum);
   for (int j = 0; j < nt; ++j) {
     b.tiles[2 * (tpos + j)] = tid;
     b.tiles[2 * (tpos + j) + 1] = off + j * tile_rows;
   }
-  if (tid == 0) *b.num_tiles = n_tiles;
+  if (tid == 0) {
+    b.offsets[E] = tot[0];
+    *b.num_active = tot[1];
+    *b.num_work = tot[2];
+    *b.num_tiles = tot[3];
+  }
   __syncthreads();
   if (ok) {
     const int rank = ls->tab[wave][id] + r;
