@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=64, help="T of the headline line")
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
                     help="replay one captured HIP graph per step, or launch eagerly")
-    ap.add_argument("--sweep", default="c2:1,c2:8,c2:32,c3:4096",
+    ap.add_argument("--sweep", default="c2:1,c2:8,c2:32,c3:512,c3:2048,c3:4096,c4:64,c4:2048",
                     help="extra cfg:T points timed after the headline ('' for none)")
     ap.add_argument("--sweep-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -251,12 +251,13 @@ def main():
         r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch)
         s2 = r2.timed(args.sweep_steps, 5)
         U2 = W.distinct(r2.idx)
+        # both rates for every point: the decode sizes and the small prefills
+        # (c3 T=512, c4 T=2048, c5 T=512: arithmetic intensity below the
+        # ridge) are HBM-bound, the large prefills MFMA-bound
         ent = dict(config=c2.name, T=tt, tokens_per_s=round(tt / s2, 1),
-                   us_per_step=round(s2 * 1e6, 2), distinct_experts=U2)
-        if tt * c2.K < 2048:
-            ent["block_hbm_gbs"] = round(W.algorithmic_bytes(c2, tt, U2) / s2 / 1e9, 1)
-        else:
-            ent["block_tflops"] = round(W.algorithmic_flops(c2, tt) / s2 / 1e12, 2)
+                   us_per_step=round(s2 * 1e6, 2), distinct_experts=U2,
+                   block_hbm_gbs=round(W.algorithmic_bytes(c2, tt, U2) / s2 / 1e9, 1),
+                   block_tflops=round(W.algorithmic_flops(c2, tt) / s2 / 1e12, 2))
         sweep.append(ent)
         print(f"bench: sweep {ent}", file=sys.stderr, flush=True)
         del r2
@@ -266,6 +267,10 @@ def main():
         orc = entry.load_oracle()
         threads = args.cpu_threads or host_cores()
         cpu = cpu_baseline(pkg, orc, bw, T, args.cpu_seconds, threads)
+        # and on one core (a single-threaded run of the same restatement)
+        one = cpu_baseline(pkg, orc, bw, T, args.cpu_seconds / 2, 1)
+        cpu["value_1core"] = one["value"]
+        cpu["sample_1core"] = one["sample"]
         print(f"bench: cpu baseline {cpu}", file=sys.stderr, flush=True)
 
     line = {
