@@ -76,7 +76,7 @@ class Runner:
         self.T = T
         self.block = bw.block()
         self.x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
-        self.out = torch.empty((T, bw.cfg.d), dtype=torch.float32, device=dev)
+        self.out = torch.empty((T, bw.cfg.d), dtype=self.block.out_dtype, device=dev)
         self.ws = pkg.ops.workspace(self.block.workspace_size(T), dev)
         # one routed run: distinct experts for the byte count
         self.block(self.x, out=self.out, workspace=self.ws, keep_routing=True)

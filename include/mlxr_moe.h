@@ -173,6 +173,18 @@ typedef struct {
   int32_t bits;
 } mlxr_moe_qlinear;
 
+/* mlxr_moe_router_topk with the router as a QuantizedLinear
+ * (crates/mlxr/src/layers/quantized.rs:356-373; gate: num_experts 1,
+ * output_dims E, input_dims d, group 64, bits 4 or 8): bf16 logits and
+ * probabilities, top-K on the probabilities (descending, ties to the lower
+ * id), bf16 weights returned as f32 values.  Same workspace as
+ * mlxr_moe_router_topk. */
+int mlxr_moe_router_topk_quantized(const void* x, int64_t T,
+                                   const mlxr_moe_qlinear* gate, int64_t K,
+                                   int32_t* topk_idx, float* topk_w,
+                                   void* workspace, size_t workspace_size,
+                                   mlxr_moe_stream stream);
+
 /* SplitSwitchFfn<SwigluActivation> (crates/mlxr-lm/src/nn/switch.rs:
  * 366-491): gate_proj, up_proj [E, f, d], down_proj [E, d, f]. */
 typedef struct {
@@ -206,7 +218,19 @@ int mlxr_moe_switch_glu_experts(const mlxr_moe_switch_glu* ffn, const void* x,
  * expert
  * (SwigluMlp, crates/mlxr-lm/src/nn/swiglu_mlp.rs:24-75, num_experts = 1)
  * with f32 shared_expert_gate_weight [1, d].  shared_expert_gate_weight ==
- * NULL means a plain SwitchGLU block without the shared branch. */
+ * NULL means a plain SwitchGLU block without the shared branch.
+ *
+ * Quantised router (gate: MaybeQuantized<Linear> quantised, moe.rs:57,123
+ * -> QuantizedLinear::forward, crates/mlxr/src/layers/quantized.rs:
+ * 356-373; the shipped Qwen3.6 checkpoints quantise mlp.gate and
+ * mlp.shared_expert_gate at 8 bits, group 64, moe.rs:255-284): set
+ * gate_q.weight (num_experts 1, output_dims E, input_dims d, group 64, bits
+ * 4 or 8) and leave gate_weight, gate_bias and shared_expert_gate_weight
+ * NULL; the shared gate is then shared_expert_gate_q (output_dims 1, same
+ * bits; weight NULL = no shared branch).  As in the reference with a bf16
+ * router the block then computes in bf16: bf16 logits and probabilities
+ * (the top-K selects on the probabilities, ties to the lower id), bf16
+ * routing weights (returned in topk_w as f32 values) and a bf16 out. */
 typedef struct {
   int64_t hidden_size;
   int64_t num_experts;
@@ -220,14 +244,16 @@ typedef struct {
   mlxr_moe_qlinear shared_up_proj;
   mlxr_moe_qlinear shared_down_proj;
   const float* shared_expert_gate_weight;
+  mlxr_moe_qlinear gate_q;
+  mlxr_moe_qlinear shared_expert_gate_q;
 } mlxr_moe_block;
 
-/* Qwen35MoeBlock::forward (moe.rs:116-146): x bf16 [T, d] -> out f32
- * [T, d].  topk_idx [T, K] / topk_w [T, K] optionally receive the routing
- * (NULL to skip). */
+/* Qwen35MoeBlock::forward (moe.rs:116-146): x bf16 [T, d] -> out [T, d],
+ * f32 with the f32 router, bf16 with a quantised one.  topk_idx [T, K] /
+ * topk_w [T, K] optionally receive the routing (NULL to skip). */
 size_t mlxr_moe_block_workspace_size(const mlxr_moe_block* block, int64_t T);
 int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
-                           int64_t T, float* out, int32_t* topk_idx,
+                           int64_t T, void* out, int32_t* topk_idx,
                            float* topk_w, void* workspace,
                            size_t workspace_size, mlxr_moe_stream stream);
 

@@ -58,6 +58,8 @@ class Block(Structure):
         ("shared_up_proj", QLinear),
         ("shared_down_proj", QLinear),
         ("shared_expert_gate_weight", c_void_p),
+        ("gate_q", QLinear),
+        ("shared_expert_gate_q", QLinear),
     ]
 
 
@@ -80,6 +82,8 @@ SIGNATURES = {
     "mlxr_moe_softmax": (c_int, [P, c_int64, c_int64, c_int, c_int, P, P]),
     "mlxr_moe_router_workspace_size": (c_size_t, [c_int64, c_int64]),
     "mlxr_moe_router_topk": (c_int, [P, c_int64, c_int64, P, c_int64, c_int64, P, P, P, c_size_t, P]),
+    "mlxr_moe_router_topk_quantized": (
+        c_int, [P, c_int64, POINTER(QLinear), c_int64, P, P, P, c_size_t, P]),
     "mlxr_moe_dispatch_workspace_size": (c_size_t, [c_int64, c_int64]),
     "mlxr_moe_dispatch": (c_int, [P, c_int64, c_int64, P, P, P, P, P, c_size_t, P]),
     "mlxr_moe_combine": (c_int, [P, P, c_int64, c_int64, c_int64, P, P, P, P]),

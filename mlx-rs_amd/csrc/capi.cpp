@@ -88,7 +88,7 @@ extern "C" {
 
 const char* mlxr_moe_last_error(void) { return g_last_error.c_str(); }
 
-int mlxr_moe_version(void) { return 100; }
+int mlxr_moe_version(void) { return 200; }
 
 int mlxr_moe_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
                       mlxr_moe_optional_int group_size,
@@ -292,12 +292,62 @@ int mlxr_moe_router_topk(const void* x, int64_t T, int64_t d,
   float* logits = c.take<float>(T * E);
   hipStream_t s = as_stream(stream);
   st = from_hip(launch_router_logits(static_cast<const uint16_t*>(x), T, d,
-                                     gate_w, nullptr, E, nullptr, logits, E,
-                                     s),
+                                     router_weights_f32(gate_w, nullptr),
+                                     nullptr, E, logits, E, s),
                 "router logits");
   if (st.ok)
-    st = from_hip(launch_router_topk(logits, E, T, E, K, topk_idx, topk_w,
-                                     nullptr, s),
+    st = from_hip(launch_router_topk(logits, E, T, E, K, false, topk_idx,
+                                     topk_w, nullptr, s),
+                  "router top-k");
+  return finish(st);
+}
+
+int mlxr_moe_router_topk_quantized(const void* x, int64_t T,
+                                   const mlxr_moe_qlinear* gate, int64_t K,
+                                   int32_t* topk_idx, float* topk_w,
+                                   void* workspace, size_t workspace_size,
+                                   mlxr_moe_stream stream) {
+  if (!gate) return fail("router_topk_quantized: null gate");
+  const int64_t E = gate->output_dims, d = gate->input_dims;
+  if (T < 0 || d <= 0 || E <= 0 || gate->num_experts != 1)
+    return fail("router_topk_quantized: bad shape (gate must be one "
+                "[E, d] QuantizedLinear)");
+  if ((gate->bits != 4 && gate->bits != 8) || gate->group_size != 64)
+    return fail("router_topk_quantized: bits must be 4 or 8 and group size 64");
+  if (d % 64) return fail("router_topk_quantized: d must be a multiple of 64");
+  if (E > kMaxExperts)
+    return fail("router_topk_quantized: at most " +
+                std::to_string(kMaxExperts) + " experts");
+  if (K < 1 || K > E || K > 64)
+    return fail("router_topk_quantized: k must be in [1, min(E, 64)], got " +
+                std::to_string(K));
+  if (!gate->weight || !gate->scales || !gate->biases ||
+      (T && (!x || !topk_idx || !topk_w)))
+    return fail("router_topk_quantized: null array");
+  if (!aligned(x, 8) || !aligned(gate->weight, 4) ||
+      !aligned(gate->scales, 2) || !aligned(gate->biases, 2))
+    return fail("router_topk_quantized: x must be 8-byte and the weights "
+                "4-byte aligned");
+  Carve plan(nullptr);
+  plan.take<float>(T * E);
+  Status st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  Carve c(workspace);
+  float* logits = c.take<float>(T * E);
+  hipStream_t s = as_stream(stream);
+  const RouterWeights rw{gate->bits,
+                         gate->weight,
+                         static_cast<const uint16_t*>(gate->scales),
+                         static_cast<const uint16_t*>(gate->biases),
+                         nullptr,
+                         nullptr,
+                         nullptr};
+  st = from_hip(launch_router_logits(static_cast<const uint16_t*>(x), T, d, rw,
+                                     nullptr, E, logits, E, s),
+                "router logits");
+  if (st.ok)
+    st = from_hip(launch_router_topk(logits, E, T, E, K, true, topk_idx,
+                                     topk_w, nullptr, s),
                   "router top-k");
   return finish(st);
 }
@@ -349,7 +399,7 @@ int mlxr_moe_combine(const void* y, const float* w, int64_t T, int64_t K,
   return finish(from_hip(
       launch_combine(static_cast<const uint16_t*>(y), w, T, K, d,
                      static_cast<const uint16_t*>(shared_y), shared_logit, 1,
-                     out, as_stream(stream)),
+                     out, false, as_stream(stream)),
       "combine"));
 }
 
@@ -436,7 +486,7 @@ size_t mlxr_moe_block_workspace_size(const mlxr_moe_block* block, int64_t T) {
 }
 
 int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
-                           int64_t T, float* out, int32_t* topk_idx,
+                           int64_t T, void* out, int32_t* topk_idx,
                            float* topk_w, void* workspace,
                            size_t workspace_size, mlxr_moe_stream stream) {
   if (!block) return fail("block: null module");
@@ -450,6 +500,13 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
       (block->shared_expert_gate_weight &&
        !aligned(block->shared_expert_gate_weight, 16)))
     return fail("block: x, out and router weights must be 16-byte aligned");
+  if (!aligned(block->gate_q.weight, 4) ||
+      !aligned(block->shared_expert_gate_q.weight, 4) ||
+      !aligned(block->gate_q.scales, 2) || !aligned(block->gate_q.biases, 2) ||
+      !aligned(block->shared_expert_gate_q.scales, 2) ||
+      !aligned(block->shared_expert_gate_q.biases, 2))
+    return fail("block: quantised router words must be 4-byte and its "
+                "scales and biases 2-byte aligned");
   Carve plan(nullptr);
   plan.take<int32_t>(1);
   nn::Qwen35MoeBlock::plan(plan, *block, T);

@@ -6,6 +6,10 @@
 // over K; and, from Qwen35MoeBlock::forward (moe.rs:117-120, 145),
 // shared * sigmoid(shared_gate(x)) + routed.  Each product is rounded to f32
 // before the k-ordered sum, as in the reference's two-op sequence.
+// With a quantised (bf16) router the weights and the shared-gate logit are
+// bf16 and so is every op: w * y rounded to bf16, the sum over k in f32
+// rounded to bf16, shared = bf16(y_s * bf16(sigmoid(sg))), out =
+// bf16(shared + routed).
 // HBM-bound elementwise pass: 8 outputs per thread, 16 B loads of y.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -13,11 +17,12 @@
 namespace mlxr_moe {
 namespace {
 
+template <bool BF16>
 __global__ __launch_bounds__(256) void combine_kernel(
     const uint16_t* __restrict__ y, const float* __restrict__ w, int T, int K,
     int d, const uint16_t* __restrict__ shared_y,
     const float* __restrict__ shared_logit, int64_t shared_ld,
-    float* __restrict__ out) {
+    void* __restrict__ out) {
   const int t = blockIdx.y;
   const int n0 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (t >= T || n0 >= d) return;
@@ -31,29 +36,51 @@ __global__ __launch_bounds__(256) void combine_kernel(
     const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float lo = __fmul_rn(wk, __uint_as_float(pk[j] << 16));
-      const float hi = __fmul_rn(wk, __uint_as_float(pk[j] & 0xffff0000u));
+      float lo = __fmul_rn(wk, __uint_as_float(pk[j] << 16));
+      float hi = __fmul_rn(wk, __uint_as_float(pk[j] & 0xffff0000u));
+      if (BF16) {
+        lo = bf16_round(lo);
+        hi = bf16_round(hi);
+      }
       acc[2 * j] = __fadd_rn(acc[2 * j], lo);
       acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], hi);
     }
   }
+  if (BF16) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = bf16_round(acc[j]);
+  }
   if (shared_y) {
-    const float gate = 1.0f / (1.0f + expf(-shared_logit[t * shared_ld]));
+    float gate = 1.0f / (1.0f + expf(-shared_logit[t * shared_ld]));
+    if (BF16) gate = bf16_round(gate);
     const u32x4_t v =
         *reinterpret_cast<const u32x4_t*>(shared_y + (int64_t)t * d + n0);
     const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      acc[2 * j] = __fadd_rn(__fmul_rn(__uint_as_float(pk[j] << 16), gate),
-                             acc[2 * j]);
-      acc[2 * j + 1] = __fadd_rn(
-          __fmul_rn(__uint_as_float(pk[j] & 0xffff0000u), gate),
-          acc[2 * j + 1]);
+      float lo = __fmul_rn(__uint_as_float(pk[j] << 16), gate);
+      float hi = __fmul_rn(__uint_as_float(pk[j] & 0xffff0000u), gate);
+      if (BF16) {
+        lo = bf16_round(lo);
+        hi = bf16_round(hi);
+      }
+      acc[2 * j] = __fadd_rn(lo, acc[2 * j]);
+      acc[2 * j + 1] = __fadd_rn(hi, acc[2 * j + 1]);
     }
   }
-  float4* o = reinterpret_cast<float4*>(out + (int64_t)t * d + n0);
-  o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  if (BF16) {
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      pk[j] = (uint32_t)f32_to_bf16(acc[2 * j]) |
+              ((uint32_t)f32_to_bf16(acc[2 * j + 1]) << 16);
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(out) + (int64_t)t * d + n0) =
+        u32x4_t{pk[0], pk[1], pk[2], pk[3]};
+  } else {
+    float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)t * d + n0);
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
 }
 
 }  // namespace
@@ -61,12 +88,16 @@ __global__ __launch_bounds__(256) void combine_kernel(
 hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,
                           int64_t K, int64_t d, const uint16_t* shared_y,
                           const float* shared_logit, int64_t shared_ld,
-                          float* out, hipStream_t s) {
+                          void* out, bool bf16, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const dim3 grid((unsigned)((d / 8 + 255) / 256), (unsigned)T);
   ProfileScope prof("combine", s);
-  combine_kernel<<<grid, 256, 0, s>>>(y, w, (int)T, (int)K, (int)d, shared_y,
-                                      shared_logit, shared_ld, out);
+  if (bf16)
+    combine_kernel<true><<<grid, 256, 0, s>>>(y, w, (int)T, (int)K, (int)d, shared_y,
+                                              shared_logit, shared_ld, out);
+  else
+    combine_kernel<false><<<grid, 256, 0, s>>>(y, w, (int)T, (int)K, (int)d, shared_y,
+                                               shared_logit, shared_ld, out);
   return hipGetLastError();
 }
 

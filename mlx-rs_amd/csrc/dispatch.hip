@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_small_kernel(
 // Decode routing in one workgroup (T * K <= 1024): top-K of every token
 // (16 waves over the tokens), the renormalised weights, the status reset and
 // the counting sort of the T * K expert ids.
-template <int SLOTS>
+template <int SLOTS, bool BF16>
 __global__ __launch_bounds__(kDispatchBlock) void route_small_kernel(
     const float* __restrict__ logits, int64_t ld, int T, int E, int K,
     int32_t* __restrict__ idx, float* __restrict__ wts, int tile_rows,
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(kDispatchBlock) void route_small_kernel(
   for (int t = wave; t < T; t += kDispatchBlock / 64) {
     int id;
     float wt;
-    wave_topk<SLOTS>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
+    wave_topk<SLOTS, BF16>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
     if (lane < K) {
       idx[(int64_t)t * K + lane] = id;
       wts[(int64_t)t * K + lane] = wt;
@@ -290,22 +290,13 @@ hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
   return hipGetLastError();
 }
 
-hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
+template <bool BF16>
+void route_small_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
                         int64_t K, int32_t* idx, float* wts, int tile_rows,
                         const DispatchBuffers& b, hipStream_t s) {
-  if (T == 0) return launch_zero_status(b.status, s);
-  // one workgroup while the T*K ids fit it and its 16 waves have at most
-  // MLXR_ROUTE_SMALL_TOKENS / 16 tokens each; beyond that the top-k spreads
-  // over the GPU (a wave per token) before the sort
-  if (T > MLXR_ROUTE_SMALL_TOKENS || T * K > kDispatchBlock) {
-    hipError_t e = launch_router_topk(logits, ld, T, E, K, idx, wts, b.status, s);
-    if (e != hipSuccess) return e;
-    return launch_dispatch(idx, T * K, E, tile_rows, b, false, s);
-  }
-  ProfileScope prof("router_topk", s);
   const int slots = (int)((E + 63) / 64);
 #define MLXR_RS(S)                                                         \
-  route_small_kernel<S><<<1, kDispatchBlock, 0, s>>>(                      \
+  route_small_kernel<S, BF16><<<1, kDispatchBlock, 0, s>>>(                \
       logits, ld, (int)T, (int)E, (int)K, idx, wts, tile_rows, b)
   if (slots <= 1)
     MLXR_RS(1);
@@ -318,6 +309,27 @@ hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
   else
     MLXR_RS(16);
 #undef MLXR_RS
+}
+
+hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
+                        int64_t K, bool bf16, int32_t* idx, float* wts,
+                        int tile_rows, const DispatchBuffers& b,
+                        hipStream_t s) {
+  if (T == 0) return launch_zero_status(b.status, s);
+  // one workgroup while the T*K ids fit it and its 16 waves have at most
+  // MLXR_ROUTE_SMALL_TOKENS / 16 tokens each; beyond that the top-k spreads
+  // over the GPU (a wave per token) before the sort
+  if (T > MLXR_ROUTE_SMALL_TOKENS || T * K > kDispatchBlock) {
+    hipError_t e =
+        launch_router_topk(logits, ld, T, E, K, bf16, idx, wts, b.status, s);
+    if (e != hipSuccess) return e;
+    return launch_dispatch(idx, T * K, E, tile_rows, b, false, s);
+  }
+  ProfileScope prof("router_topk", s);
+  if (bf16)
+    route_small_launch<true>(logits, ld, T, E, K, idx, wts, tile_rows, b, s);
+  else
+    route_small_launch<false>(logits, ld, T, E, K, idx, wts, tile_rows, b, s);
   return hipGetLastError();
 }
 

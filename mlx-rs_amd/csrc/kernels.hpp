@@ -41,17 +41,35 @@ hipError_t launch_dequantize(const uint32_t* wq, const void* scales,
                              bool out_bf16, hipStream_t s);
 
 // --------------------------------------------------------------- router.hip
-// logits[t, e] for e < E from w [E, d] (+ bias[e] when given); column E
-// from w_extra [1, d] when given (the shared-expert gate).  ld = row stride
-// of logits.
+// Router weights: an f32 Linear [E, d] (bits == 0), or a QuantizedLinear
+// (bits 4 or 8, group 64): packed codes [E, d*bits/32], bf16 scales and
+// biases [E, d/64].  The extra row (the shared-expert gate, logit column
+// E) takes the same form when w_extra is set.
+struct RouterWeights {
+  int bits;
+  const void* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  const void* w_extra;
+  const uint16_t* scales_extra;
+  const uint16_t* biases_extra;
+};
+inline RouterWeights router_weights_f32(const float* w, const float* w_extra) {
+  return RouterWeights{0, w, nullptr, nullptr, w_extra, nullptr, nullptr};
+}
+// logits[t, e] for e < E (+ bias[e] when given, f32 weights only) and
+// column E from the extra row.  Quantised weights give bf16 logits (stored
+// as their f32 values).  ld = row stride of logits.
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
-                                const float* w, const float* bias, int64_t E,
-                                const float* w_extra, float* logits,
-                                int64_t ld, hipStream_t s);
-// One wave per token; clears *status first when status != nullptr.
+                                const RouterWeights& w, const float* bias,
+                                int64_t E, float* logits, int64_t ld,
+                                hipStream_t s);
+// One wave per token; clears *status first when status != nullptr.  bf16:
+// the logits are bf16 and the selection is on their bf16 probabilities,
+// with bf16 weights (stored as f32).
 hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
-                              int64_t E, int64_t K, int32_t* idx, float* wts,
-                              int32_t* status, hipStream_t s);
+                              int64_t E, int64_t K, bool bf16, int32_t* idx,
+                              float* wts, int32_t* status, hipStream_t s);
 hipError_t launch_argsort_rows(const float* a, int64_t rows, int64_t n,
                                uint32_t* out, hipStream_t s);
 hipError_t launch_softmax_rows(const float* a, int64_t rows, int64_t n,
@@ -104,8 +122,9 @@ hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
 // counting sort of the T*K ids, clearing *b.status first.  T <= 16 runs as
 // one workgroup; larger T as the top-k kernel plus launch_dispatch.
 hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
-                        int64_t K, int32_t* idx, float* wts, int tile_rows,
-                        const DispatchBuffers& b, hipStream_t s);
+                        int64_t K, bool bf16, int32_t* idx, float* wts,
+                        int tile_rows, const DispatchBuffers& b,
+                        hipStream_t s);
 // gather_qmm helper: per flat row r = b*M + m the expert id and x row.
 hipError_t launch_gather_prep(const uint32_t* lhs, const uint32_t* rhs,
                               int64_t B, int64_t M, int64_t x_batch, int64_t E,
@@ -172,9 +191,11 @@ hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 hipStream_t s);
 
 // -------------------------------------------------------------- combine.hip
+// out f32 [T, d], or bf16 when bf16 (the routing weights are then bf16
+// values and every op rounds to bf16).
 hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,
                           int64_t K, int64_t d, const uint16_t* shared_y,
                           const float* shared_logit, int64_t shared_ld,
-                          float* out, hipStream_t s);
+                          void* out, bool bf16, hipStream_t s);
 
 }  // namespace mlxr_moe

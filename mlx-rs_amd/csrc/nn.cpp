@@ -254,7 +254,7 @@ Status SplitSwitchFfn::forward_with_combine(
   Status st = forward(x, T, indices, K, y, ws, status, s);
   if (!st.ok) return st;
   return from_hip(launch_combine(y, weights, T, K, d, shared_y, shared_logit,
-                                 shared_ld, out, s),
+                                 shared_ld, out, false, s),
                   "combine");
 }
 
@@ -270,7 +270,32 @@ Status Qwen35MoeBlock::validate() const {
                          "min(num_experts, 64)], got " + std::to_string(K));
   if (d % 64)
     return Status::error("block: hidden_size must be a multiple of 64");
-  if (!b_.gate_weight) return Status::error("block: gate_weight is required");
+  if (quantised_router()) {
+    // QuantizedLinear router and shared gate (layers/quantized.rs:356-373)
+    const mlxr_moe_qlinear& g = b_.gate_q;
+    if (b_.gate_weight || b_.gate_bias || b_.shared_expert_gate_weight)
+      return Status::error("block: a quantised router (gate_q) replaces "
+                           "gate_weight, gate_bias and "
+                           "shared_expert_gate_weight; leave them NULL");
+    if ((g.bits != 4 && g.bits != 8) || g.group_size != 64)
+      return Status::error("block: gate_q must be 4- or 8-bit with group "
+                           "size 64");
+    if (g.num_experts != 1 || g.output_dims != E || g.input_dims != d ||
+        !g.scales || !g.biases)
+      return Status::error("block: gate_q must be one [num_experts, "
+                           "hidden_size] QuantizedLinear with scales and "
+                           "biases");
+    const mlxr_moe_qlinear& sg = b_.shared_expert_gate_q;
+    if (sg.weight &&
+        (sg.bits != g.bits || sg.group_size != 64 || sg.num_experts != 1 ||
+         sg.output_dims != 1 || sg.input_dims != d || !sg.scales ||
+         !sg.biases))
+      return Status::error("block: shared_expert_gate_q must be a [1, "
+                           "hidden_size] QuantizedLinear with gate_q's bits "
+                           "and group size 64");
+  } else if (!b_.gate_weight) {
+    return Status::error("block: gate_weight (or gate_q) is required");
+  }
   Status st = SplitSwitchFfn(b_.switch_mlp).validate(d, f, E);
   if (st.ok && has_shared()) {
     const int64_t fs = b_.shared_expert_intermediate_size;
@@ -284,7 +309,7 @@ Status Qwen35MoeBlock::validate() const {
 void Qwen35MoeBlock::plan(Carve& ws, const mlxr_moe_block& b, int64_t T) {
   const int64_t d = b.hidden_size, E = b.num_experts;
   const int64_t K = b.num_experts_per_tok, f = b.moe_intermediate_size;
-  const bool shared = b.shared_expert_gate_weight != nullptr;
+  const bool shared = Qwen35MoeBlock(b).has_shared();
   ws.take<float>(T * (E + (shared ? 1 : 0)));
   ws.take<int32_t>(T * K);
   ws.take<float>(T * K);
@@ -298,12 +323,13 @@ void Qwen35MoeBlock::plan(Carve& ws, const mlxr_moe_block& b, int64_t T) {
 // Qwen35MoeBlock::forward (moe.rs:116-146).  Kernels: router logits (with
 // the shared-expert gate as one more column), routing (top-k, weights and
 // the expert dispatch), [shared expert], gate/up, down, combine.
-Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
+Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
                                int32_t* topk_idx, float* topk_w, Carve& ws,
                                hipStream_t s) const {
   const int64_t d = b_.hidden_size, E = b_.num_experts;
   const int64_t K = b_.num_experts_per_tok;
   const bool shared = has_shared();
+  const bool bf16 = quantised_router();
   const int64_t ld = E + (shared ? 1 : 0);
   int32_t* status = reinterpret_cast<int32_t*>(ws.base);
   float* logits = ws.take<float>(T * ld);
@@ -317,16 +343,26 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
   uint16_t* y = ws.take<uint16_t>(T * K * d);
   const DispatchBuffers db = carve_dispatch(ws, T * K, E, status);
   // gate.forward + shared_expert_gate.forward (moe.rs:118,123) in one pass.
+  RouterWeights rw = router_weights_f32(
+      b_.gate_weight, shared ? b_.shared_expert_gate_weight : nullptr);
+  if (bf16) {
+    const mlxr_moe_qlinear &g = b_.gate_q, &sg = b_.shared_expert_gate_q;
+    rw = RouterWeights{g.bits,
+                       g.weight,
+                       static_cast<const uint16_t*>(g.scales),
+                       static_cast<const uint16_t*>(g.biases),
+                       shared ? sg.weight : nullptr,
+                       static_cast<const uint16_t*>(sg.scales),
+                       static_cast<const uint16_t*>(sg.biases)};
+  }
   Status st = from_hip(
-      launch_router_logits(x, T, d, b_.gate_weight, b_.gate_bias, E,
-                           shared ? b_.shared_expert_gate_weight : nullptr,
-                           logits, ld, s),
+      launch_router_logits(x, T, d, rw, b_.gate_bias, E, logits, ld, s),
       "router logits");
   if (!st.ok) return st;
   // softmax, argpartition top-k, renormalise (moe.rs:124-138) + gather_sort
-  st = from_hip(
-      launch_route(logits, ld, T, E, K, idx, wts, prefill_tile_rows(T * K, E), db, s),
-      "router top-k / dispatch");
+  st = from_hip(launch_route(logits, ld, T, E, K, bf16, idx, wts,
+                             prefill_tile_rows(T * K, E), db, s),
+                "router top-k / dispatch");
   if (!st.ok) return st;
   if (shared) {
     st = SwigluMlp(b_.shared_gate_proj, b_.shared_up_proj,
@@ -338,7 +374,8 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, float* out,
   st = mlp.experts(x, T, K, db, y, ws, s);
   if (!st.ok) return st;
   return from_hip(launch_combine(y, wts, T, K, d, sy,
-                                 shared ? logits + E : nullptr, ld, out, s),
+                                 shared ? logits + E : nullptr, ld, out, bf16,
+                                 s),
                   "combine");
 }
 

@@ -102,8 +102,14 @@ class Qwen35MoeBlock {
  public:
   explicit Qwen35MoeBlock(const mlxr_moe_block& b) : b_(b) {}
   Status validate() const;
-  bool has_shared() const { return b_.shared_expert_gate_weight != nullptr; }
-  Status forward(const uint16_t* x, int64_t T, float* out, int32_t* topk_idx,
+  // quantised (bf16) router: QuantizedLinear gate and shared gate
+  bool quantised_router() const { return b_.gate_q.weight != nullptr; }
+  bool has_shared() const {
+    return quantised_router() ? b_.shared_expert_gate_q.weight != nullptr
+                              : b_.shared_expert_gate_weight != nullptr;
+  }
+  // out f32 [T, d], bf16 with a quantised router
+  Status forward(const uint16_t* x, int64_t T, void* out, int32_t* topk_idx,
                  float* topk_w, Carve& ws, hipStream_t s) const;
   static void plan(Carve& ws, const mlxr_moe_block& b, int64_t T);
 

@@ -31,8 +31,14 @@ struct TopkScratch {
 // (crates/mlxr/src/ops/sort.rs:186-226, whose order is undefined).  Then
 // softmax over all E (max-subtracted, lane sums in expert order e = l + 64s,
 // butterfly across lanes) and w_k = p_k / sum_k p_k (k in order).
+// BF16 (bf16 logits of a quantised router): softmax_axis keeps the bf16
+// dtype (ops/arithmetic.rs:1298-1311), so the selection is on the bf16
+// probabilities, where distinct logits can tie.  p_e = bf16((float)(
+// exp((double)l_e - m) / S)) with S summed in double in the order above
+// (double makes p independent of exp's last bits on either side); then
+// denom = bf16(sum_k p_k in f32, k in order), w_k = bf16(p_k / denom).
 // Returns on lane k < K its expert id (*out_id) and weight (*out_w).
-template <int SLOTS>
+template <int SLOTS, bool BF16 = false>
 __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
                           TopkScratch* sc, int* out_id, float* out_w) {
   const int lane = threadIdx.x & 63;
@@ -43,8 +49,29 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
   for (int s = 0; s < SLOTS; ++s) {
     const int e = lane + 64 * s;
     v[s] = e < E ? logits[e] : 0.0f;
-    key[s] = e < E ? float_key(v[s]) : 0u;  // 0: below every real key
   }
+  if constexpr (BF16) {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s)
+      if (lane + 64 * s < E) m = fmaxf(m, v[s]);
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) m = fmaxf(m, __shfl_xor(m, msk, 64));
+    double ex[SLOTS];
+    double acc = 0.0;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      ex[s] = lane + 64 * s < E ? exp((double)v[s] - (double)m) : 0.0;
+      if (lane + 64 * s < E) acc += ex[s];
+    }
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) acc += __shfl_xor(acc, msk, 64);
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) v[s] = bf16_round((float)(ex[s] / acc));
+  }
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s)
+    key[s] = lane + 64 * s < E ? float_key(v[s]) : 0u;  // 0: below every real key
   // theta = largest key with at least K keys >= theta (the K-th largest)
   uint32_t theta = 0u;
   for (int b = 31; b >= 0; --b) {
@@ -102,8 +129,16 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // the selected logits come from LDS: no dependent re-read of memory
   const int id = lane < K ? sc->id[lane] : 0;
+  if constexpr (BF16) {
+    const float p = lane < K ? sc->val[lane] : 0.0f;
+    float psum = 0.0f;
+    for (int k = 0; k < K; ++k) psum += __shfl(p, k, 64);
+    *out_id = id;
+    *out_w = bf16_round(p / bf16_round(psum));
+    return;
+  }
+  // the selected logits come from LDS: no dependent re-read of memory
   const float m = sc->val[0];
   float acc = 0.0f;
 #pragma unroll

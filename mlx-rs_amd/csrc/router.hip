@@ -12,8 +12,17 @@
 // Logits are computed with a fixed summation order (per lane: fmaf over
 // elements j = 4l + 256i + c in (i, c) order; across lanes: butterfly
 // v += v[l^m], m = 32..1; then + bias[e] when the router has one) so the
-// selected expert sets reproduce bit for bit on the CPU.  Selection is on logits (softmax is monotone), descending,
-// ties to the lower expert id.
+// selected expert sets reproduce bit for bit on the CPU.  Selection is on
+// logits (softmax is monotone), descending, ties to the lower expert id.
+//
+// The router may also be a QuantizedLinear (QuantizedLinear::forward,
+// crates/mlxr/src/layers/quantized.rs:356-373; the shipped Qwen3.6
+// checkpoints quantise mlp.gate and mlp.shared_expert_gate at 8 bits, group
+// 64, qwen3_5/text/moe.rs:255-284).  Then element j's weight is the f32
+// fmaf(code_j, scale, bias) of its group, the same lane order applies, and
+// the logit is rounded to bf16 (the reference's result dtype with bf16 x
+// and scales); the selection is then on the bf16 probabilities
+// (wave_topk).
 #include "common.hpp"
 #include "kernels.hpp"
 #include "route.hpp"
@@ -21,28 +30,76 @@
 namespace mlxr_moe {
 namespace {
 
+// One router weight row: f32 values, or packed codes with their group
+// scales and biases.  w == nullptr: no row (zeros).
+struct WRow {
+  const void* w;
+  const uint16_t* s;
+  const uint16_t* b;
+};
+
+template <int BITS>
+__device__ __forceinline__ WRow router_row(const RouterWeights& rw, int e,
+                                           int E, int d) {
+  if (e < E) {
+    if (BITS == 0)
+      return {static_cast<const float*>(rw.w) + (int64_t)e * d, nullptr, nullptr};
+    return {static_cast<const uint8_t*>(rw.w) + (int64_t)e * d * BITS / 8,
+            rw.scales + (int64_t)e * (d / 64), rw.biases + (int64_t)e * (d / 64)};
+  }
+  if (e == E && rw.w_extra) return {rw.w_extra, rw.scales_extra, rw.biases_extra};
+  return {nullptr, nullptr, nullptr};
+}
+
+// Weights j..j+3 of a row (j % 4 == 0): four f32, or four codes (one word
+// at 8 bits, half a word at 4, little end first) dequantised in f32 as
+// fmaf(code, scale, bias) with the scale and bias of group j / 64.
+template <int BITS>
+__device__ __forceinline__ float4 router_w4(const WRow& r, int j) {
+  if constexpr (BITS == 0) {
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(r.w) + j);
+  } else {
+    const uint8_t* p = static_cast<const uint8_t*>(r.w);
+    const uint32_t c = BITS == 8
+                           ? *reinterpret_cast<const uint32_t*>(p + j)
+                           : (uint32_t)*reinterpret_cast<const uint16_t*>(p + j / 2);
+    const float sc = bf16_to_f32(r.s[j >> 6]), bi = bf16_to_f32(r.b[j >> 6]);
+    constexpr uint32_t m = (1u << BITS) - 1u;
+    return make_float4(__builtin_fmaf((float)(c & m), sc, bi),
+                       __builtin_fmaf((float)((c >> BITS) & m), sc, bi),
+                       __builtin_fmaf((float)((c >> (2 * BITS)) & m), sc, bi),
+                       __builtin_fmaf((float)((c >> (3 * BITS)) & m), sc, bi));
+  }
+}
+
+// The finished dot product of logit column e: + bias for an f32 Linear
+// that has one, one bf16 rounding for a quantised router.
+template <int BITS>
+__device__ __forceinline__ float router_finish(float v, const float* bias,
+                                               int e, int E) {
+  if (BITS) return bf16_round(v);
+  return (bias && e < E) ? v + bias[e] : v;
+}
+
 // One wave computes EB logit columns for up to TB tokens of a token block.
 // Router weights stream as float4 (16 B per lane), x as 4 bf16 (8 B); the
 // loads of U consecutive 256-wide steps are issued before their FMAs.
-template <int EB, int TB, int U>
+template <int EB, int TB, int U, int BITS>
 __global__ __launch_bounds__(256) void router_logits_kernel(
-    const uint16_t* __restrict__ x, int T, int d, const float* __restrict__ w,
-    const float* __restrict__ bias, int E, const float* __restrict__ w_extra,
-    float* __restrict__ logits, int64_t ld) {
+    const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
+    const float* __restrict__ bias, int E, float* __restrict__ logits,
+    int64_t ld) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int e_tot = E + (w_extra ? 1 : 0);
+  const int e_tot = E + (rw.w_extra ? 1 : 0);
   const int e0 = (blockIdx.x * 4 + wave) * EB;
   if (e0 >= e_tot) return;
   const int t0 = blockIdx.y * TB;
   const int nt = min(TB, T - t0);
 
-  const float* wrow[EB];
+  WRow wrow[EB];
 #pragma unroll
-  for (int q = 0; q < EB; ++q) {
-    const int e = e0 + q;
-    wrow[q] = e < E ? w + (int64_t)e * d : (e == E ? w_extra : nullptr);
-  }
+  for (int q = 0; q < EB; ++q) wrow[q] = router_row<BITS>(rw, e0 + q, E, d);
   const uint16_t* xrow[TB];
 #pragma unroll
   for (int tt = 0; tt < TB; ++tt)
@@ -63,8 +120,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
       const bool in = j < d;
 #pragma unroll
       for (int q = 0; q < EB; ++q)
-        wv[u][q] = (in && wrow[q]) ? *reinterpret_cast<const float4*>(wrow[q] + j)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[u][q] = (in && wrow[q].w) ? router_w4<BITS>(wrow[q], j)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int tt = 0; tt < TB; ++tt)
         xv[u][tt] = in ? *reinterpret_cast<const uint2*>(xrow[tt] + j)
@@ -95,8 +152,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   for (int q = 0; q < EB; ++q) {
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt) {
-      float v = wave_sum_butterfly(acc[q][tt]);
-      if (bias && e0 + q < E) v += bias[e0 + q];
+      const float v =
+          router_finish<BITS>(wave_sum_butterfly(acc[q][tt]), bias, e0 + q, E);
       if (lane == 0 && e0 + q < e_tot && tt < nt)
         logits[(int64_t)(t0 + tt) * ld + e0 + q] = v;
     }
@@ -113,17 +170,18 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 // l and l^32 first, ... l and l^1 last) -- by one lane reading them from
 // LDS rather than by six shuffles on every lane.  Same bits.
 constexpr int kRtTok = 32, kRtCol = 16, kRtWaveTok = 8;
+template <int BITS>
 __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
-    const uint16_t* __restrict__ x, int T, int d, const float* __restrict__ w,
-    const float* __restrict__ bias, int E, const float* __restrict__ w_extra,
-    float* __restrict__ logits, int64_t ld) {
+    const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
+    const float* __restrict__ bias, int E, float* __restrict__ logits,
+    int64_t ld) {
   // 32 KB: the step's x [32][256] bf16 and w [16][256] f32; afterwards the
   // lane sums [wave][32 logits][64 lanes] f32, 32 logits at a time
   __shared__ __attribute__((aligned(16))) char lds[kRtTok * 256 * 2 + kRtCol * 256 * 4];
   uint16_t (*xs)[256] = reinterpret_cast<uint16_t (*)[256]>(lds);
   float (*ws)[256] = reinterpret_cast<float (*)[256]>(lds + kRtTok * 256 * 2);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int e_tot = E + (w_extra ? 1 : 0);
+  const int e_tot = E + (rw.w_extra ? 1 : 0);
   const int e0 = blockIdx.x * kRtCol, t0 = blockIdx.y * kRtTok;
   float acc[kRtCol][kRtWaveTok];
 #pragma unroll
@@ -131,16 +189,16 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
 #pragma unroll
     for (int tt = 0; tt < kRtWaveTok; ++tt) acc[q][tt] = 0.0f;
   // this thread's staging chunks: x rows id/32 (8 bf16 at (id%32)*8), w rows
-  // id/64 (4 f32 at (id%64)*4), id = tid + 256k; zeros past d / T / e_tot
+  // id/64 (4 weights at (id%64)*4, dequantised to f32 on the way to LDS),
+  // id = tid + 256k; zeros past d / T / e_tot
   const uint16_t* xp[4];
-  const float* wp[4];
+  WRow wp[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int id = tid + 256 * k;
-    const int t = t0 + (id >> 5), e = e0 + (id >> 6);
+    const int t = t0 + (id >> 5);
     xp[k] = t < T ? x + (int64_t)t * d + (id & 31) * 8 : nullptr;
-    const float* row = e < E ? w + (int64_t)e * d : (e == E ? w_extra : nullptr);
-    wp[k] = row ? row + (id & 63) * 4 : nullptr;
+    wp[k] = router_row<BITS>(rw, e0 + (id >> 6), E, d);
   }
   u32x4_t xr[4];
   float4 wr[4];
@@ -152,8 +210,8 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
       xr[k] = (xp[k] && j0 + (id & 31) * 8 < d)
                   ? *reinterpret_cast<const u32x4_t*>(xp[k] + j0)
                   : u32x4_t{0u, 0u, 0u, 0u};
-      wr[k] = (wp[k] && j0 + (id & 63) * 4 < d)
-                  ? *reinterpret_cast<const float4*>(wp[k] + j0)
+      wr[k] = (wp[k].w && j0 + (id & 63) * 4 < d)
+                  ? router_w4<BITS>(wp[k], j0 + (id & 63) * 4)
                   : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
@@ -219,8 +277,7 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
         for (int j = 0; j < h; ++j) s[j] = s[j] + s[j + h];
       const int qq = lane / kRtWaveTok, tt = lane % kRtWaveTok;
       const int e = e0 + q0 + qq, t = t0 + wave * kRtWaveTok + tt;
-      float r = s[0];
-      if (bias && e < E) r += bias[e];
+      const float r = router_finish<BITS>(s[0], bias, e, E);
       if (e < e_tot && t < T) logits[(int64_t)t * ld + e] = r;
     }
     __builtin_amdgcn_wave_barrier();
@@ -231,7 +288,7 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
 
 // One wave per token: top-K, softmax and renormalised weights (wave_topk).
 // Workgroup 0 also clears the workspace status word when given.
-template <int SLOTS>
+template <int SLOTS, bool BF16>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, int64_t ld, int T, int E, int K,
     int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* status) {
@@ -242,7 +299,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   if (t >= T) return;
   int id;
   float wt;
-  wave_topk<SLOTS>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
+  wave_topk<SLOTS, BF16>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
   if (lane < K) {
     idx[(int64_t)t * K + lane] = id;
     wts[(int64_t)t * K + lane] = wt;
@@ -311,22 +368,18 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(
     out[row * n + i] = expf(r[i] - mx) / sum;
 }
 
-}  // namespace
-
-hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
-                                const float* w, const float* bias, int64_t E,
-                                const float* w_extra, float* logits,
-                                int64_t ld, hipStream_t s) {
-  if (T == 0) return hipSuccess;
-  const int64_t e_tot = E + (w_extra ? 1 : 0);
-  ProfileScope prof("router_logits", s);
+template <int BITS>
+void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
+                          const RouterWeights& w, const float* bias, int64_t E,
+                          float* logits, int64_t ld, hipStream_t s) {
+  const int64_t e_tot = E + (w.w_extra ? 1 : 0);
   // Enough waves to have every CU pulling router weights at small T, and
   // register reuse of both operands (EB experts x TB tokens) at large T.
 #define MLXR_RL(EB, TB, U)                                                   \
-  router_logits_kernel<EB, TB, U>                                            \
+  router_logits_kernel<EB, TB, U, BITS>                                      \
       <<<dim3((unsigned)((e_tot + 4 * EB - 1) / (4 * EB)),                   \
               (unsigned)((T + TB - 1) / TB)),                                \
-         256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, w_extra, logits, ld)
+         256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld)
   if (T <= 2)
     MLXR_RL(1, 1, 8);
   else if (T <= 16)
@@ -334,24 +387,22 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
   else if (T <= 256)
     MLXR_RL(2, 4, 4);
   else
-    router_logits_tiled_kernel<<<dim3((unsigned)((e_tot + kRtCol - 1) / kRtCol),
-                                      (unsigned)((T + kRtTok - 1) / kRtTok)),
-                                 256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E,
-                                              w_extra, logits, ld);
+    router_logits_tiled_kernel<BITS>
+        <<<dim3((unsigned)((e_tot + kRtCol - 1) / kRtCol),
+                (unsigned)((T + kRtTok - 1) / kRtTok)),
+           256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld);
 #undef MLXR_RL
-  return hipGetLastError();
 }
 
-hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
-                              int64_t E, int64_t K, int32_t* idx, float* wts,
-                              int32_t* status, hipStream_t s) {
-  if (T == 0) return hipSuccess;
-  ProfileScope prof("router_topk", s);
+template <bool BF16>
+void router_topk_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
+                        int64_t K, int32_t* idx, float* wts, int32_t* status,
+                        hipStream_t s) {
   const dim3 grid((unsigned)((T + 3) / 4));
   const int slots = (int)((E + 63) / 64);
-#define MLXR_TOPK(S)                                                     \
-  router_topk_kernel<S><<<grid, 256, 0, s>>>(logits, ld, (int)T, (int)E, \
-                                             (int)K, idx, wts, status)
+#define MLXR_TOPK(S)                                                           \
+  router_topk_kernel<S, BF16><<<grid, 256, 0, s>>>(logits, ld, (int)T, (int)E, \
+                                                   (int)K, idx, wts, status)
   if (slots <= 1)
     MLXR_TOPK(1);
   else if (slots <= 2)
@@ -363,6 +414,35 @@ hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
   else
     MLXR_TOPK(16);
 #undef MLXR_TOPK
+}
+
+}  // namespace
+
+hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
+                                const RouterWeights& w, const float* bias,
+                                int64_t E, float* logits, int64_t ld,
+                                hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  if (w.bits != 0 && w.bits != 4 && w.bits != 8) return hipErrorInvalidValue;
+  ProfileScope prof("router_logits", s);
+  if (w.bits == 8)
+    router_logits_launch<8>(x, T, d, w, bias, E, logits, ld, s);
+  else if (w.bits == 4)
+    router_logits_launch<4>(x, T, d, w, bias, E, logits, ld, s);
+  else
+    router_logits_launch<0>(x, T, d, w, bias, E, logits, ld, s);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
+                              int64_t E, int64_t K, bool bf16, int32_t* idx,
+                              float* wts, int32_t* status, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  ProfileScope prof("router_topk", s);
+  if (bf16)
+    router_topk_launch<true>(logits, ld, T, E, K, idx, wts, status, s);
+  else
+    router_topk_launch<false>(logits, ld, T, E, K, idx, wts, status, s);
   return hipGetLastError();
 }
 

@@ -170,34 +170,60 @@ class SwigluMlp:
 
 
 class Qwen35MoeBlock:
-    """Router (f32 Linear [E, d]) -> softmax -> top-k -> renormalise ->
-    SplitSwitchFfn, plus an optional sigmoid-gated shared SwigluMlp."""
+    """Router -> softmax -> top-k -> renormalise -> SplitSwitchFfn, plus an
+    optional sigmoid-gated shared SwigluMlp (moe.rs:43-159).
+
+    The router (`gate_weight`) and the shared gate
+    (`shared_expert_gate_weight`) are MaybeQuantized<Linear> as in the
+    reference (moe.rs:57-58): an f32 weight tensor [E, d] / [1, d], or both a
+    QuantizedLinear (the shipped Qwen3.6 checkpoints quantise them at 8 bits,
+    moe.rs:255-284).  With a quantised router the block is bf16 throughout
+    (logits, probabilities, routing weights and the output)."""
 
     def __init__(self, gate_weight, switch_mlp: SplitSwitchFfn, num_experts_per_tok: int,
                  shared_expert: SwigluMlp | None = None, shared_expert_gate_weight=None,
                  gate_bias=None):
         if (shared_expert is None) != (shared_expert_gate_weight is None):
             raise MlxrMoeError("shared_expert and shared_expert_gate_weight go together")
-        self.gate_weight = gate_weight.to(torch.float32).contiguous()
-        self.gate_bias = None if gate_bias is None else gate_bias.to(torch.float32).contiguous()
+        self.quantised_router = isinstance(gate_weight, QuantizedLinear)
+        if shared_expert_gate_weight is not None and (
+                isinstance(shared_expert_gate_weight, QuantizedLinear) != self.quantised_router):
+            raise MlxrMoeError("gate and shared_expert_gate must both be quantised or both f32")
+        if self.quantised_router and gate_bias is not None:
+            raise MlxrMoeError("a quantised router has no bias (moe.rs:90-92)")
+        z = C.QLinear()
+        if self.quantised_router:
+            self.gate_weight = gate_weight
+            self.gate_bias = None
+            self.shared_expert_gate_weight = shared_expert_gate_weight
+            E, d = gate_weight.output_dims, gate_weight.input_dims
+            gate_ptr = sgw_ptr = None
+            gate_q = gate_weight.descriptor()
+            sg_q = z if shared_expert_gate_weight is None else shared_expert_gate_weight.descriptor()
+        else:
+            self.gate_weight = gate_weight.to(torch.float32).contiguous()
+            self.gate_bias = (None if gate_bias is None
+                              else gate_bias.to(torch.float32).contiguous())
+            self.shared_expert_gate_weight = (
+                None if shared_expert_gate_weight is None
+                else shared_expert_gate_weight.to(torch.float32).contiguous())
+            E, d = self.gate_weight.shape
+            gate_ptr, sgw_ptr = self.gate_weight.data_ptr(), _ptr(self.shared_expert_gate_weight)
+            gate_q = sg_q = z
         self.switch_mlp = switch_mlp
         self.shared_expert = shared_expert
-        self.shared_expert_gate_weight = (
-            None if shared_expert_gate_weight is None
-            else shared_expert_gate_weight.to(torch.float32).contiguous())
         self.num_experts_per_tok = num_experts_per_tok
-        E, d = self.gate_weight.shape
+        self.out_dtype = torch.bfloat16 if self.quantised_router else torch.float32
         f = switch_mlp.gate_proj.output_dims
-        z = C.QLinear()
         se = shared_expert
         self._desc = C.Block(
             d, E, num_experts_per_tok, f,
             0 if se is None else se.gate_proj.output_dims,
-            self.gate_weight.data_ptr(), _ptr(self.gate_bias), switch_mlp.descriptor(),
+            gate_ptr, _ptr(self.gate_bias), switch_mlp.descriptor(),
             z if se is None else se.gate_proj.descriptor(),
             z if se is None else se.up_proj.descriptor(),
             z if se is None else se.down_proj.descriptor(),
-            _ptr(self.shared_expert_gate_weight))
+            sgw_ptr, gate_q, sg_q)
         self._ws = None
         self.last_indices = None
         self.last_weights = None
@@ -210,7 +236,7 @@ class Qwen35MoeBlock:
 
     def forward(self, x, out=None, workspace=None, keep_routing=True):
         """Qwen35MoeBlock::forward (moe.rs:116-146): x bf16 [..., d] ->
-        f32 [..., d]."""
+        [..., d], f32 (bf16 with a quantised router)."""
         d = x.shape[-1]
         x2 = x.reshape(-1, d)
         if not x2.is_contiguous():
@@ -218,7 +244,9 @@ class Qwen35MoeBlock:
         T = x2.shape[0]
         K = self.num_experts_per_tok
         if out is None:
-            out = torch.empty((T, d), dtype=torch.float32, device=x.device)
+            out = torch.empty((T, d), dtype=self.out_dtype, device=x.device)
+        elif out.dtype != self.out_dtype:
+            raise MlxrMoeError(f"out must be {self.out_dtype}")
         if workspace is None:
             need = self.workspace_size(T)
             if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:

@@ -205,6 +205,25 @@ def router_topk(x: torch.Tensor, gate_w: torch.Tensor, k: int):
     return idx.reshape(lead + (k,)), wts.reshape(lead + (k,))
 
 
+def router_topk_quantized(x: torch.Tensor, gate, k: int):
+    """router_topk with the router as a QuantizedLinear (nn.QuantizedLinear,
+    4 or 8 bits, group 64; layers/quantized.rs:356-373): bf16 logits and
+    probabilities, top-k on the probabilities.  Returns (indices int32
+    [T, k], weights [T, k] -- bf16 values held in f32)."""
+    _dev(x, gate.weight)
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    T = x2.shape[0]
+    idx = torch.empty((T, k), dtype=torch.int32, device=x.device)
+    wts = torch.empty((T, k), dtype=torch.float32, device=x.device)
+    lib = C.lib()
+    ws = workspace(lib.mlxr_moe_router_workspace_size(T, gate.output_dims), x.device)
+    desc = gate.descriptor()
+    C.check(lib.mlxr_moe_router_topk_quantized(_p(x2), T, ctypes.byref(desc), k, _p(idx),
+                                               _p(wts), _p(ws), ws.numel(), _stream(x)))
+    lead = tuple(x.shape[:-1])
+    return idx.reshape(lead + (k,)), wts.reshape(lead + (k,))
+
+
 def dispatch(ids: torch.Tensor, num_experts: int):
     """Stable expert sort of flat ids (gather_sort, switch.rs:499-512).
     Returns (counts [E], offsets [E+1], order [n], inv_order [n])."""

@@ -1,12 +1,17 @@
 """MoE block configurations and seeded synthetic weights/inputs.
 
-The five shapes the block is measured and tested on (c1 small CPU case,
-c2 Qwen3-30B-A3B-shaped decode, c3 the same shape at prefill with Zipf
-routing skew, c4 high-expert-count with shared expert, c5 wide 8-bit).
+The shapes the block is measured and tested on (c1 small CPU case, c2
+Qwen3-30B-A3B-shaped decode, c3 the same shape at prefill with Zipf routing
+skew, c4 high-expert-count with shared expert, c5 wide 8-bit), plus c6, the
+Qwen3.6-35B-A3B block as its shipped checkpoint quantises it
+(crates/mlxr-lm/tests/fixtures/qwen3_6_35b_a3b/config.json: d 2048, 256
+experts, top-8, f 512, shared expert 512, 4-bit experts, mlp.gate and
+mlp.shared_expert_gate at 8 bits, group 64).
 Weights are drawn N(0, 0.02) in f32, rounded to bf16 and affine-quantised
 on the device by this library's quantize kernel; x ~ N(0, 1) in bf16;
-router weights N(0, 0.02) in f32 (unquantised).  No checkpoint is read:
-everything is synthetic, from torch generators seeded per tensor.
+router weights N(0, 0.02) in f32 (unquantised), or for c6 N(0, 0.02) in
+bf16 quantised at router_bits.  No checkpoint is read: everything is
+synthetic, from torch generators seeded per tensor.
 """
 from __future__ import annotations
 
@@ -31,6 +36,7 @@ class MoEConfig:
     zipf_alpha: float | None = None   # routing skew via per-expert logit bias
     tokens: tuple = field(default_factory=tuple)
     seed: int = 0
+    router_bits: int = 0   # 0: f32 router; 4/8: QuantizedLinear router (bf16 block)
 
 
 CONFIGS = {
@@ -43,6 +49,8 @@ CONFIGS = {
                     tokens=(1, 64, 2048)),
     "c5": MoEConfig("c5_wide_8bit_zipf", d=4096, E=128, K=8, f=1536, bits=8,
                     zipf_alpha=1.1, tokens=(32, 512)),
+    "c6": MoEConfig("c6_qwen3_6_35b_a3b_q8router", d=2048, E=256, K=8, f=512, fs=512,
+                    router_bits=8, tokens=(1, 64, 2048)),
 }
 
 
@@ -88,11 +96,11 @@ def zipf_bias(cfg: MoEConfig, gate_w: torch.Tensor, device, iters: int = 20,
 @dataclass
 class BlockWeights:
     cfg: MoEConfig
-    gate_w: torch.Tensor
+    gate_w: torch.Tensor | nn.QuantizedLinear
     gate_b: torch.Tensor | None
     switch_mlp: nn.SplitSwitchFfn
     shared_expert: nn.SwigluMlp | None
-    shared_gate_w: torch.Tensor | None
+    shared_gate_w: torch.Tensor | nn.QuantizedLinear | None
 
     def block(self) -> nn.Qwen35MoeBlock:
         return nn.Qwen35MoeBlock(self.gate_w, self.switch_mlp, self.cfg.K, self.shared_expert,
@@ -104,6 +112,12 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
     s = cfg.seed
     gate_w = _normal((cfg.E, cfg.d), 0.02, device, s, 2)
     gate_b = zipf_bias(cfg, gate_w, device) if cfg.zipf_alpha else None
+
+    def qrouter(w):
+        return nn.QuantizedLinear.try_from_linear(w.to(torch.bfloat16), 64, cfg.router_bits)
+
+    if cfg.router_bits:
+        gate_w = qrouter(gate_w)
 
     def qbank(shape, stream):
         w = _normal(shape, 0.02, device, s, stream).to(torch.bfloat16)
@@ -119,18 +133,23 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
         shared = nn.SwigluMlp(qlin((cfg.fs, cfg.d), 8), qlin((cfg.fs, cfg.d), 9),
                               qlin((cfg.d, cfg.fs), 10))
         sgw = _normal((1, cfg.d), 0.02, device, s, 12)
+        if cfg.router_bits:
+            sgw = qrouter(sgw)
     return BlockWeights(cfg, gate_w, gate_b, mlp, shared, sgw)
 
 
 def algorithmic_bytes(cfg: MoEConfig, T: int, distinct_experts: int) -> int:
     """HBM bytes one block forward must move at decode: the packed weights,
     scales and biases of the distinct selected experts (3 projections), the
-    f32 router weights, x in, f32 out, and the routing (idx + weight)."""
+    router weights (f32, or packed at router_bits with bf16 scales/biases
+    per 64), x in, the output (f32, bf16 with a quantised router), and the
+    routing (idx + weight)."""
     per_w = cfg.bits / 8 + 4 / cfg.group_size
-    b = distinct_experts * 3 * cfg.f * cfg.d * per_w + cfg.E * cfg.d * 4
+    per_r = cfg.router_bits / 8 + 4 / 64 if cfg.router_bits else 4
+    b = distinct_experts * 3 * cfg.f * cfg.d * per_w + cfg.E * cfg.d * per_r
     if cfg.fs:
-        b += 3 * cfg.fs * cfg.d * per_w + cfg.d * 4
-    b += T * cfg.d * 2 + T * cfg.d * 4 + T * cfg.K * 8
+        b += 3 * cfg.fs * cfg.d * per_w + cfg.d * per_r
+    b += T * cfg.d * 2 + T * cfg.d * (2 if cfg.router_bits else 4) + T * cfg.K * 8
     return int(b)
 
 

@@ -36,6 +36,13 @@
  *                     the tiled form bit-for-bit equals that gather_mm on
  *                     bf16 weights up to f32 accumulation (fp64 bound).
  *   orc_swiglu        reference test activations.rs:341-351.
+ *   orc_router_logits_q  equals orc_router_logits on the dequantised
+ *                     weights, then one bf16 rounding (same lane order);
+ *                     fp64 bound.
+ *   orc_router_topk_bf16 full sort of the bf16 probabilities on small E,
+ *                     ties to the lower id; probabilities within one bf16
+ *                     rounding of the exact softmax.
+ *   orc_combine_bf16  per-op bf16 roundings restated elementwise in numpy.
  *   orc_block_forward sorted and unsorted dispatch give identical outputs
  *                     (switch.rs:446-474); K=1 reduces to one expert;
  *                     linearity in the routing weights.
@@ -245,6 +252,112 @@ void orc_router_topk(const float* logits, int64_t T, int64_t E, int64_t K,
   free(taken);
 }
 
+/* ------------------------------------------------------ quantised router */
+/* Router as QuantizedLinear (gate: MaybeQuantized<Linear>, moe.rs:57,123;
+ * QuantizedLinear::forward, layers/quantized.rs:356-373 ->
+ * quantized_matmul, ops/quantization.rs:81-112).  The shipped Qwen3.6
+ * checkpoints quantise mlp.gate and mlp.shared_expert_gate at 8 bits, group
+ * 64 (tests/fixtures/qwen3_6_35b_a3b/config.json, applied by
+ * qwen3_5/text/moe.rs:255-284).  With bf16 x and bf16 scales the result is
+ * bf16.  Same lane order as lane_dot; the weight of element j is the f32
+ * fmaf(code_j, scale, bias) of its group of 64; the f32 sum is rounded once
+ * to bf16 (returned as its f32 value). */
+static float lane_dot_q(const uint16_t* xrow, const uint32_t* wrow,
+                        const uint16_t* srow, const uint16_t* brow, int64_t d,
+                        int bits) {
+  const int per_word = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  float lane[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int64_t i = 0; 4 * l + 256 * i < d; ++i) {
+      for (int c = 0; c < 4; ++c) {
+        const int64_t j = 4 * l + 256 * i + c;
+        if (j >= d) continue;
+        const uint32_t code =
+            (wrow[j / per_word] >> ((j % per_word) * bits)) & mask;
+        const float w = fmaf((float)code, orc_bf16_to_f32(srow[j / 64]),
+                             orc_bf16_to_f32(brow[j / 64]));
+        acc = fmaf(orc_bf16_to_f32(xrow[j]), w, acc);
+      }
+    }
+    lane[l] = acc;
+  }
+  for (int m = 32; m >= 1; m >>= 1) {
+    float nxt[64];
+    for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ m];
+    memcpy(lane, nxt, sizeof(lane));
+  }
+  return orc_bf16_to_f32(orc_f32_to_bf16(lane[0]));
+}
+
+int orc_router_logits_q(const uint16_t* x, const uint32_t* wq,
+                        const uint16_t* scales, const uint16_t* biases,
+                        int bits, int64_t T, int64_t d, int64_t E,
+                        float* logits) {
+  if ((bits != 4 && bits != 8) || d % 64) return -1;
+  const int64_t wpr = d * bits / 32, gpr = d / 64;
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t e = 0; e < E; ++e)
+      logits[t * E + e] = lane_dot_q(x + t * d, wq + e * wpr, scales + e * gpr,
+                                     biases + e * gpr, d, bits);
+  return 0;
+}
+
+/* softmax_axis(precise) keeps the input dtype (arithmetic.rs:1298-1311), so
+ * bf16 logits give bf16 probabilities, and argpartition (sort.rs:211-226)
+ * selects on those: distinct logits can tie.  Here m = max logit;
+ * e_j = exp((double)l_j - m) in double; S = sum of e_j in double (lane l
+ * holds experts l, l+64, ..., then the butterfly); p_j =
+ * bf16((float)(e_j / S)).  Double keeps p independent of the exp and
+ * summation details of either side.  Selection on p, descending, ties to
+ * the lower id.  take_along_axis / sum / divide (moe.rs:136-138) in bf16:
+ * denom = bf16(f32 sum of p_k in k order), w_k = bf16(p_k / denom) with an
+ * f32 division. */
+void orc_router_topk_bf16(const float* logits, int64_t T, int64_t E,
+                          int64_t K, int32_t* idx, float* weights) {
+  char* taken = (char*)malloc((size_t)E);
+  float* p = (float*)malloc(sizeof(float) * (size_t)E);
+  for (int64_t t = 0; t < T; ++t) {
+    const float* l = logits + t * E;
+    float m = l[0];
+    for (int64_t e = 1; e < E; ++e) m = l[e] > m ? l[e] : m;
+    double lane[64];
+    for (int ln = 0; ln < 64; ++ln) {
+      double acc = 0.0;
+      for (int64_t e = ln; e < E; e += 64) acc += exp((double)l[e] - (double)m);
+      lane[ln] = acc;
+    }
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+      double nxt[64];
+      for (int ln = 0; ln < 64; ++ln) nxt[ln] = lane[ln] + lane[ln ^ msk];
+      memcpy(lane, nxt, sizeof(lane));
+    }
+    const double S = lane[0];
+    for (int64_t e = 0; e < E; ++e)
+      p[e] = orc_bf16_to_f32(
+          orc_f32_to_bf16((float)(exp((double)l[e] - (double)m) / S)));
+    memset(taken, 0, (size_t)E);
+    float psum = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      int64_t best = -1;
+      for (int64_t e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        if (best < 0 || p[e] > p[best]) best = e;
+      }
+      taken[best] = 1;
+      idx[t * K + k] = (int32_t)best;
+      psum += p[best];
+    }
+    const float denom = orc_bf16_to_f32(orc_f32_to_bf16(psum));
+    for (int64_t k = 0; k < K; ++k)
+      weights[t * K + k] =
+          orc_bf16_to_f32(orc_f32_to_bf16(p[idx[t * K + k]] / denom));
+  }
+  free(p);
+  free(taken);
+}
+
 /* ------------------------------------------------------------- dispatch */
 /* gather_sort (switch.rs:499-512): order = argsort(flat ids) (stable),
  * inv = argsort(order).  Counting sort gives the same permutation. */
@@ -386,6 +499,34 @@ void orc_combine(const uint16_t* y, const float* w, int64_t T, int64_t K,
   }
 }
 
+/* The same with bf16 routing weights (a bf16 router, see
+ * orc_router_topk_bf16): w * y is bf16, the sum over k is accumulated in
+ * f32 in k order and rounded to bf16; shared = bf16(y_s *
+ * bf16(sigmoid(sg))); out = bf16(shared + routed). */
+void orc_combine_bf16(const uint16_t* y, const float* w, int64_t T, int64_t K,
+                      int64_t d, const uint16_t* shared_y,
+                      const float* shared_logit, uint16_t* out) {
+  for (int64_t t = 0; t < T; ++t) {
+    float gate = 0.0f;
+    if (shared_y)
+      gate = orc_bf16_to_f32(
+          orc_f32_to_bf16(1.0f / (1.0f + expf(-shared_logit[t]))));
+    for (int64_t n = 0; n < d; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k)
+        acc += orc_bf16_to_f32(orc_f32_to_bf16(
+            w[t * K + k] * orc_bf16_to_f32(y[(t * K + k) * d + n])));
+      float r = orc_bf16_to_f32(orc_f32_to_bf16(acc));
+      if (shared_y) {
+        const float sh = orc_bf16_to_f32(
+            orc_f32_to_bf16(orc_bf16_to_f32(shared_y[t * d + n]) * gate));
+        r = sh + r;
+      }
+      out[t * d + n] = orc_f32_to_bf16(r);
+    }
+  }
+}
+
 /* --------------------------------------------------------------- block */
 /* One expert FFN on one token: y = down(swiglu(gate(x), up(x))). */
 static void expert_ffn(const float* xf, const orc_qlinear* g,
@@ -403,7 +544,7 @@ static void expert_ffn(const float* xf, const orc_qlinear* g,
 }
 
 int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
-                      float* out, int32_t* idx_out, float* w_out,
+                      void* out, int32_t* idx_out, float* w_out,
                       int nthreads) {
   const int64_t d = blk->hidden, E = blk->num_experts, K = blk->top_k;
   const int64_t f = blk->intermediate, fs = blk->shared_intermediate;
@@ -413,6 +554,10 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
     return -1;
   if (nthreads <= 0) nthreads = 1;
 
+  const int qr = blk->router_q.w != NULL;
+  if (qr && ((blk->router_bits != 4 && blk->router_bits != 8) ||
+             (fs && !blk->shared_gate_q.w)))
+    return -1;
   float* logits = (float*)malloc(sizeof(float) * (size_t)(T * E));
   int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * (size_t)(T * K));
   float* wts = (float*)malloc(sizeof(float) * (size_t)(T * K));
@@ -420,17 +565,32 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
   uint16_t* sy = fs ? (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * d)) : NULL;
   float* sg = fs ? (float*)malloc(sizeof(float) * (size_t)T) : NULL;
 
-  /* router */
+  /* router: f32 Linear (f32 logits) or QuantizedLinear (bf16 logits) */
+  const int rb = blk->router_bits;
 #pragma omp parallel for schedule(static) num_threads(nthreads)
   for (int64_t t = 0; t < T; ++t) {
     for (int64_t e = 0; e < E; ++e) {
-      float v = lane_dot(x + t * d, blk->router_w + e * d, d);
-      if (blk->router_b) v += blk->router_b[e];
+      float v;
+      if (qr) {
+        v = lane_dot_q(x + t * d, blk->router_q.w + e * (d * rb / 32),
+                       blk->router_q.scales + e * (d / 64),
+                       blk->router_q.biases + e * (d / 64), d, rb);
+      } else {
+        v = lane_dot(x + t * d, blk->router_w + e * d, d);
+        if (blk->router_b) v += blk->router_b[e];
+      }
       logits[t * E + e] = v;
     }
-    if (fs) sg[t] = lane_dot(x + t * d, blk->shared_gate_w, d);
+    if (fs)
+      sg[t] = qr ? lane_dot_q(x + t * d, blk->shared_gate_q.w,
+                              blk->shared_gate_q.scales,
+                              blk->shared_gate_q.biases, d, rb)
+                 : lane_dot(x + t * d, blk->shared_gate_w, d);
   }
-  orc_router_topk(logits, T, E, K, idx, wts);
+  if (qr)
+    orc_router_topk_bf16(logits, T, E, K, idx, wts);
+  else
+    orc_router_topk(logits, T, E, K, idx, wts);
 
   /* routed experts, one (token, k) pair at a time (gather_qmm's
    * unsorted path; the sorted path gives identical rows) */
@@ -468,7 +628,10 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
     free(ub);
   }
 
-  orc_combine(y, wts, T, K, d, sy, sg, out);
+  if (qr)
+    orc_combine_bf16(y, wts, T, K, d, sy, sg, (uint16_t*)out);
+  else
+    orc_combine(y, wts, T, K, d, sy, sg, (float*)out);
   if (idx_out) memcpy(idx_out, idx, sizeof(int32_t) * (size_t)(T * K));
   if (w_out) memcpy(w_out, wts, sizeof(float) * (size_t)(T * K));
   free(logits);

@@ -17,7 +17,9 @@
  *   - router logits use a fixed 64-lane summation order (see
  *     orc_router_logits), so expert selection is bit-reproducible.
  *   - top-k selects on logits (softmax is monotone), descending, ties to
- *     the lower expert id.
+ *     the lower expert id.  With a quantised (bf16) router it selects on the
+ *     bf16 probabilities, as the reference does, whose softmax is computed
+ *     in double on both sides so that they agree bit for bit.
  *
  * Parity status (what pins each function) is listed in the header of
  * moe_oracle.c and checked by tests/test_oracle.py.
@@ -61,6 +63,20 @@ void orc_router_logits(const uint16_t* x, const float* w, int64_t T,
 void orc_router_topk(const float* logits, int64_t T, int64_t E, int64_t K,
                      int32_t* idx, float* weights);
 
+/* Router as QuantizedLinear: logits [T, E] (bf16 values as f32) =
+ * bf16(x . dequant(wq[e])) with the f32 weights fmaf(code, scale, bias) in
+ * orc_router_logits' lane order.  wq [E, d*bits/32], scales/biases bf16
+ * [E, d/64]; bits 4 or 8, d % 64 == 0.  Returns 0 or -1. */
+int orc_router_logits_q(const uint16_t* x, const uint32_t* wq,
+                        const uint16_t* scales, const uint16_t* biases,
+                        int bits, int64_t T, int64_t d, int64_t E,
+                        float* logits);
+
+/* Top-K of bf16 logits [T, E] with bf16 probabilities: selection on the
+ * probabilities (descending, ties -> lower id), weights bf16 (as f32). */
+void orc_router_topk_bf16(const float* logits, int64_t T, int64_t E,
+                          int64_t K, int32_t* idx, float* weights);
+
 /* Stable counting sort of ids [n] by expert (== argsort(flat ids)).
  * counts [E], offsets [E+1], sorted [n] (flat index per sorted slot),
  * inv [n] (sorted slot per flat index).  Returns 0 or -1 (id out of range). */
@@ -91,6 +107,12 @@ void orc_combine(const uint16_t* y, const float* w, int64_t T, int64_t K,
                  int64_t d, const uint16_t* shared_y, const float* shared_logit,
                  float* out);
 
+/* out bf16 [T, d]: combine with bf16 routing weights (w holds bf16
+ * values), every op rounded to bf16. */
+void orc_combine_bf16(const uint16_t* y, const float* w, int64_t T, int64_t K,
+                      int64_t d, const uint16_t* shared_y,
+                      const float* shared_logit, uint16_t* out);
+
 /* One quantised linear bank: w [E, out, in*bits/32], scales/biases bf16. */
 typedef struct {
   const uint32_t* w;
@@ -113,12 +135,20 @@ typedef struct {
   const float* shared_gate_w; /* [1, d] f32 */
   int32_t switch_tiled;     /* gather_qmm form of the routed experts */
   int32_t shared_tiled;     /* and of the shared expert (see orc_gather_qmm) */
+  /* Quantised router (QuantizedLinear, group 64): router_q.w != NULL
+   * replaces router_w/router_b (and shared_gate_q replaces shared_gate_w),
+   * and the block computes in bf16: bf16 logits, probabilities, weights
+   * and out.  E = 1 views of [E, d*bits/32] and [1, d*bits/32]. */
+  orc_qlinear router_q;
+  orc_qlinear shared_gate_q;
+  int32_t router_bits;
 } orc_block;
 
-/* Qwen35MoeBlock::forward on x bf16 [T, d] -> out f32 [T, d].
- * idx_out/w_out (optional) receive the routing.  nthreads <= 0 means 1. */
+/* Qwen35MoeBlock::forward on x bf16 [T, d] -> out [T, d], f32 with an f32
+ * router, bf16 (uint16 bits) with a quantised one.  idx_out/w_out
+ * (optional) receive the routing.  nthreads <= 0 means 1. */
 int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
-                      float* out, int32_t* idx_out, float* w_out,
+                      void* out, int32_t* idx_out, float* w_out,
                       int nthreads);
 
 #ifdef __cplusplus

@@ -105,6 +105,31 @@ def router_topk(logits, K):
     return idx, w
 
 
+def router_logits_q(x_bf16, wq, scales, biases, bits):
+    """QuantizedLinear router: bf16 logits (as f32) [T, E]."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    wq = np.ascontiguousarray(wq, np.uint32)
+    T, d = x.shape
+    E = wq.shape[0]
+    out = np.zeros((T, E), np.float32)
+    rc = lib().orc_router_logits_q(_p(x), _p(wq), _p(np.ascontiguousarray(scales, np.uint16)),
+                                   _p(np.ascontiguousarray(biases, np.uint16)), c_int(bits),
+                                   c_int64(T), c_int64(d), c_int64(E), _p(out))
+    if rc:
+        raise ValueError("orc_router_logits_q rejected the arguments")
+    return out
+
+
+def router_topk_bf16(logits, K):
+    """Top-K on the bf16 probabilities of bf16 logits; bf16 weights."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    T, E = lg.shape
+    idx = np.zeros((T, K), np.int32)
+    w = np.zeros((T, K), np.float32)
+    lib().orc_router_topk_bf16(_p(lg), c_int64(T), c_int64(E), c_int64(K), _p(idx), _p(w))
+    return idx, w
+
+
 def dispatch(ids, E):
     ids = np.ascontiguousarray(ids, np.int32).reshape(-1)
     n = ids.size
@@ -163,6 +188,21 @@ def combine(y, w, shared_y=None, shared_logit=None):
     return out
 
 
+def combine_bf16(y, w, shared_y=None, shared_logit=None):
+    """Combine with bf16 routing weights; bf16 out (uint16 bits)."""
+    y = np.ascontiguousarray(y, np.uint16)
+    T, K, d = y.shape
+    out = np.zeros((T, d), np.uint16)
+    lib().orc_combine_bf16(_p(y), _p(np.ascontiguousarray(w, np.float32)), c_int64(T),
+                           c_int64(K), c_int64(d),
+                           _p(None if shared_y is None
+                              else np.ascontiguousarray(shared_y, np.uint16)),
+                           _p(None if shared_logit is None
+                              else np.ascontiguousarray(shared_logit, np.float32)),
+                           _p(out))
+    return out
+
+
 class _QL(Structure):
     _fields_ = [("w", c_void_p), ("scales", c_void_p), ("biases", c_void_p)]
 
@@ -175,6 +215,7 @@ class _Block(Structure):
         ("gate_proj", _QL), ("up_proj", _QL), ("down_proj", _QL),
         ("shared_gate", _QL), ("shared_up", _QL), ("shared_down", _QL),
         ("shared_gate_w", c_void_p), ("switch_tiled", c_int32), ("shared_tiled", c_int32),
+        ("router_q", _QL), ("shared_gate_q", _QL), ("router_bits", c_int32),
     ]
 
 
@@ -188,8 +229,11 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
     """p: numpy block parameters -- d, E, K, f, fs, bits, group_size,
     router_w, router_b (or None), gate/up/down = (wq, scales, biases),
     shared_gate/shared_up/shared_down, shared_gate_w (None when fs == 0).
+    A quantised router instead: router_q = (wq, scales, biases) [E, ...],
+    shared_gate_q likewise [1, ...], router_bits; then the block is bf16.
     tiled: gather_qmm numerics of (routed experts, shared expert).
-    Returns (out f32 [T, d], idx [T, K], weights [T, K])."""
+    Returns (out [T, d] -- f32, or bf16 as uint16 with a quantised router --,
+    idx [T, K], weights [T, K])."""
     keep = []
 
     def c(a, dt):
@@ -206,15 +250,17 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
 
     x = c(x, np.uint16)
     T = x.shape[0]
-    rw, rb = c(p["router_w"], np.float32), c(p.get("router_b"), np.float32)
+    rq = p.get("router_q")
+    rw, rb = c(p.get("router_w"), np.float32), c(p.get("router_b"), np.float32)
     sgw = c(p.get("shared_gate_w"), np.float32)
     blk = _Block(p["d"], p["E"], p["K"], p["f"], p.get("fs", 0), p["bits"], p["group_size"],
-                 rw.ctypes.data, None if rb is None else rb.ctypes.data,
+                 None if rw is None else rw.ctypes.data, None if rb is None else rb.ctypes.data,
                  _ql(q(p["gate"])), _ql(q(p["up"])), _ql(q(p["down"])),
                  _ql(q(p.get("shared_gate"))), _ql(q(p.get("shared_up"))),
                  _ql(q(p.get("shared_down"))), None if sgw is None else sgw.ctypes.data,
-                 1 if tiled[0] else 0, 1 if tiled[1] else 0)
-    out = np.zeros((T, p["d"]), np.float32)
+                 1 if tiled[0] else 0, 1 if tiled[1] else 0,
+                 _ql(q(rq)), _ql(q(p.get("shared_gate_q"))), p.get("router_bits", 0))
+    out = np.zeros((T, p["d"]), np.uint16 if rq is not None else np.float32)
     idx = np.zeros((T, p["K"]), np.int32)
     w = np.zeros((T, p["K"]), np.float32)
     rc = lib().orc_block_forward(ctypes.byref(blk), _p(x), c_int64(T), _p(out), _p(idx), _p(w),
@@ -225,7 +271,8 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
 
 
 __all__ = ["build", "lib", "f32_to_bf16", "bf16_to_f32", "quantize", "dequantize",
-           "router_logits", "router_topk", "dispatch", "gather_qmm", "swiglu", "combine",
+           "router_logits", "router_topk", "router_logits_q", "router_topk_bf16", "dispatch",
+           "gather_qmm", "swiglu", "combine", "combine_bf16",
            "block_forward", "POINTER", "c_float", "c_uint16", "c_uint32"]
 
 
@@ -253,11 +300,18 @@ def block_params(bw) -> dict:
 
     m = bw.switch_mlp
     p = dict(d=cfg.d, E=cfg.E, K=cfg.K, f=cfg.f, fs=cfg.fs, bits=cfg.bits,
-             group_size=cfg.group_size, router_w=to_np(bw.gate_w),
+             group_size=cfg.group_size,
              router_b=None if bw.gate_b is None else to_np(bw.gate_b),
              gate=q(m.gate_proj), up=q(m.up_proj), down=q(m.down_proj))
+    if cfg.router_bits:
+        p.update(router_q=q(bw.gate_w), router_bits=cfg.router_bits)
+    else:
+        p.update(router_w=to_np(bw.gate_w))
     if cfg.fs:
         s = bw.shared_expert
-        p.update(shared_gate=q(s.gate_proj), shared_up=q(s.up_proj), shared_down=q(s.down_proj),
-                 shared_gate_w=to_np(bw.shared_gate_w))
+        p.update(shared_gate=q(s.gate_proj), shared_up=q(s.up_proj), shared_down=q(s.down_proj))
+        if cfg.router_bits:
+            p.update(shared_gate_q=q(bw.shared_gate_w))
+        else:
+            p.update(shared_gate_w=to_np(bw.shared_gate_w))
     return p

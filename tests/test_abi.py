@@ -93,6 +93,37 @@ def test_block_validation(pkg):
     assert lib.mlxr_moe_block_forward(ctypes.byref(blk), None, 1, None, None, None, None, 0,
                                       None) == -1
     assert "gate_weight" in _err(pkg)
+    # a quantised router replaces the f32 one and must be 4/8-bit, group 64
+    blk.gate_q = C.QLinear(1, 1, 1, 1, 128, 2048, 64, 3)
+    assert lib.mlxr_moe_block_forward(ctypes.byref(blk), None, 1, None, None, None, None, 0,
+                                      None) == -1
+    assert "gate_q must be 4- or 8-bit" in _err(pkg)
+    blk.gate_q = C.QLinear(4, 4, 4, 1, 64, 2048, 64, 8)
+    assert lib.mlxr_moe_block_forward(ctypes.byref(blk), None, 1, None, None, None, None, 0,
+                                      None) == -1
+    assert "[num_experts, hidden_size]" in _err(pkg)
+    blk.gate_q = C.QLinear(4, 4, 4, 1, 128, 2048, 64, 8)
+    blk.gate_weight = 16
+    assert lib.mlxr_moe_block_forward(ctypes.byref(blk), None, 1, None, None, None, None, 0,
+                                      None) == -1
+    assert "replaces gate_weight" in _err(pkg)
+
+
+def test_router_topk_quantized_validation(pkg):
+    C = pkg._capi
+    lib = C.lib()
+    g = C.QLinear(4, 4, 4, 1, 128, 2048, 64, 2)
+    assert lib.mlxr_moe_router_topk_quantized(None, 1, ctypes.byref(g), 8, None, None, None,
+                                              0, None) == -1
+    assert "bits must be 4 or 8" in _err(pkg)
+    g.bits, g.input_dims = 8, 2000
+    assert lib.mlxr_moe_router_topk_quantized(None, 1, ctypes.byref(g), 8, None, None, None,
+                                              0, None) == -1
+    assert "multiple of 64" in _err(pkg)
+    g.input_dims = 2048
+    assert lib.mlxr_moe_router_topk_quantized(None, 1, ctypes.byref(g), 200, None, None, None,
+                                              0, None) == -1
+    assert "k must be" in _err(pkg)
 
 
 def test_last_error_is_thread_local(pkg):

@@ -1,8 +1,12 @@
 """GPU parity of the whole MoE block (Qwen35MoeBlock::forward) and of
 SplitSwitchFfn against the CPU oracle on the benchmark configurations.
 
-Bar: routing indices bit-exact; routing weights to 2e-6 relative;
-max |out - oracle| <= 2e-2 * RMS(oracle) with f32 accumulation."""
+Bar: routing indices bit-exact; routing weights to 2e-6 relative (bit-exact
+with a quantised router, whose weights are bf16); max |out - oracle| <=
+2e-2 * RMS(oracle) with f32 accumulation.  A quantised router makes the
+output bf16, and the GPU's and the oracle's f32 sums (in different orders)
+can round to neighbouring bf16 values, so there each element may also
+differ by one bf16 step of the oracle's value."""
 import sys
 from pathlib import Path
 
@@ -37,12 +41,25 @@ def check_block(pkg, orc, bw, x, nthreads=16):
                                       tiled=tiled)
     idx = block.last_indices.cpu().numpy()
     assert np.array_equal(idx, ridx), "routing indices differ"
-    assert np.allclose(block.last_weights.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
-    got = out.cpu().numpy().astype(np.float64)
+    if cfg.router_bits:
+        # bf16 block: bf16 routing weights, bit for bit; bf16 out
+        assert out.dtype == torch.bfloat16
+        assert np.array_equal(block.last_weights.cpu().numpy(), rw)
+        got = orc.bf16_to_f32(orc.to_np(out)).astype(np.float64)
+        ref = orc.bf16_to_f32(ref)
+    else:
+        assert np.allclose(block.last_weights.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+        got = out.cpu().numpy().astype(np.float64)
     rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-    err = np.abs(got - ref).max()
+    diff = np.abs(got - ref)
+    err = diff.max()
     print(f"  max|err| {err:.3e}  rms {rms:.3e}  ratio {err / rms:.2e}", flush=True)
-    assert err <= 2e-2 * rms
+    if cfg.router_bits:
+        a = np.abs(ref.astype(np.float64))
+        ulp = np.where(a > 0, 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - 7), 0.0)
+        assert np.all(diff <= 2e-2 * rms + ulp)
+    else:
+        assert err <= 2e-2 * rms
     assert pkg.ops.workspace_status(block.last_workspace) == 0
     return out, block
 
@@ -77,7 +94,8 @@ def test_c1_golden_fixture(pkg, orc, dev):
 
 
 @pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 8), ("c2", 64), ("c5", 32),
-                                   ("c4", 1), ("c4", 64), ("c3", 512)])
+                                   ("c4", 1), ("c4", 64), ("c3", 512), ("c6", 1), ("c6", 64),
+                                   ("c6", 512)])
 def test_block_parity(pkg, orc, dev, cfg, T):
     bw = weights(pkg, cfg, dev)
     x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)

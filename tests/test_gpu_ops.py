@@ -72,6 +72,28 @@ def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
     assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("T,d,E,K,bits", [(1, 2048, 256, 8, 8), (40, 2048, 256, 8, 8),
+                                          (1024, 2048, 256, 8, 8), (16, 512, 8, 2, 4),
+                                          (300, 4096, 128, 8, 4), (7, 2048, 512, 10, 8)])
+def test_router_topk_quantized_bit_exact(pkg, orc, dev, T, d, E, K, bits):
+    """QuantizedLinear router (layers/quantized.rs:356-373): bf16 logits,
+    top-K on the bf16 probabilities and bf16 weights, all bit for bit
+    against the oracle, through each logits kernel (T <= 2, <= 256,
+    tiled)."""
+    rng = np.random.default_rng(T * 11 + E + bits)
+    print(f"  router_topk_quantized T={T} d={d} E={E} K={K} bits={bits}", flush=True)
+    x = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev)
+    w = _bf16(orc, (rng.standard_normal((E, d)) * 0.05).astype(np.float32), dev)
+    gate = pkg.nn.QuantizedLinear.try_from_linear(w, 64, bits)
+    idx, wts = pkg.ops.router_topk_quantized(x, gate, K)
+    wq, sc, bi = (_np(orc, t) for t in (gate.weight, gate.scales, gate.biases))
+    lg = orc.router_logits_q(_np(orc, x), wq.reshape(E, -1), sc.reshape(E, -1),
+                             bi.reshape(E, -1), bits)
+    ridx, rw = orc.router_topk_bf16(lg, K)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(wts.cpu().numpy(), rw)
+
+
 def test_router_ties_pick_lower_ids(pkg, dev):
     x = torch.zeros((4, 512), dtype=torch.bfloat16, device=dev)
     w = torch.randn((64, 512), device=dev)

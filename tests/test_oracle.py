@@ -154,6 +154,91 @@ def test_router_topk_matches_full_sort(orc):
     assert list(idx[1]) == [2, 5]
 
 
+# ---------------------------------------------- quantised (bf16) router
+@pytest.mark.parametrize("bits", [4, 8])
+def test_router_logits_q_is_dequant_then_bf16(orc, bits):
+    """QuantizedLinear router (layers/quantized.rs:356-373): the f32 router
+    on the f32-dequantised weights (same lane order), rounded once to bf16;
+    within half a bf16 ulp (plus the f32 accumulation bound) of the fp64
+    product."""
+    rng = np.random.default_rng(40 + bits)
+    T, d, E = 6, 2048, 16
+    x = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    w = orc.f32_to_bf16((rng.standard_normal((E, d)) * 0.02).astype(np.float32))
+    wq, sc, bi = orc.quantize(w, 64, bits)
+    got = orc.router_logits_q(x, wq, sc, bi, bits)
+    wd = orc.dequantize(wq, sc, bi, 64, bits, out_bf16=False)
+    want = orc.bf16_to_f32(orc.f32_to_bf16(orc.router_logits(x, wd)))
+    assert np.array_equal(got, want)
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    exact = xf @ wd.astype(np.float64).T
+    bound = (d * 2.0 ** -23 * (np.abs(xf) @ np.abs(wd.astype(np.float64)).T)
+             + 2.0 ** -8 * np.abs(exact))
+    assert np.all(np.abs(got - exact) <= bound)
+    # a one-hot row picks the dequantised weight column, rounded to bf16
+    x1 = np.zeros((1, d), np.float32)
+    x1[0, 777] = 1.0
+    col = orc.router_logits_q(orc.f32_to_bf16(x1), wq, sc, bi, bits)[0]
+    assert np.array_equal(col, orc.bf16_to_f32(orc.f32_to_bf16(wd[:, 777])))
+
+
+def test_router_topk_bf16_selects_on_bf16_probs(orc):
+    """softmax of bf16 logits is bf16 (arithmetic.rs:1298-1311) and
+    argpartition selects on it: a full sort of the bf16 probabilities of
+    the exact softmax, ties to the lower id -- also where the logits
+    differ."""
+    rng = np.random.default_rng(41)
+    T, E, K = 64, 8, 3
+    lg = orc.bf16_to_f32(orc.f32_to_bf16(rng.standard_normal((T, E)).astype(np.float32)))
+    lg[0, :] = 0.5                       # all tied
+    lg[1, :] = -6.0                      # distinct logits, equal bf16 probabilities:
+    lg[1, 6] = 0.0                       # exp(2^-10) - 1 = 0.1% is well below one
+    lg[1, 4] = 2.0 ** -10                # bf16 step of p ~ 0.5
+    lg = lg.astype(np.float32)
+    idx, w = orc.router_topk_bf16(lg, K)
+    p = np.exp(lg.astype(np.float64) - lg.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    pb = orc.bf16_to_f32(orc.f32_to_bf16(p.astype(np.float32)))
+    assert np.all(np.abs(pb - p) <= 2.0 ** -8 * p)
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-float(pb[t, e]), e))
+        assert list(idx[t]) == order[:K]
+    assert list(idx[0]) == [0, 1, 2]
+    assert pb[1, 4] == pb[1, 6] and lg[1, 6] < lg[1, 4]
+    assert list(idx[1][:2]) == [4, 6] and pb[1, 4] == pb[1, 6]
+    # bf16 weights within two bf16 roundings of the renormalised top-K
+    pk = np.take_along_axis(pb, idx, 1).astype(np.float64)
+    exact = pk / pk.sum(1, keepdims=True)
+    assert np.all(np.abs(w - exact) <= 2.0 ** -7 * exact)
+    assert np.array_equal(w, orc.bf16_to_f32(orc.f32_to_bf16(w)))
+
+
+def test_combine_bf16_per_op_rounding(orc):
+    """w * y, the sum over k and the shared branch each rounded to bf16
+    (MLX evaluates bf16 ops in the arrays' dtype), restated elementwise."""
+    rng = np.random.default_rng(42)
+    T, K, d = 5, 4, 128
+    bf = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(np.asarray(a, np.float32)))
+    y = orc.f32_to_bf16(rng.standard_normal((T, K, d)).astype(np.float32))
+    w = bf(rng.random((T, K)))
+    sy = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    sl = bf(rng.standard_normal(T))
+    got = orc.bf16_to_f32(orc.combine_bf16(y, w, sy, sl))
+    want = np.zeros((T, d), np.float32)
+    for t in range(T):
+        acc = np.zeros(d, np.float32)
+        for k in range(K):
+            acc = (acc + bf(w[t, k] * orc.bf16_to_f32(y[t, k]))).astype(np.float32)
+        gate = bf(np.float32(1.0) / (np.float32(1.0) + np.exp(np.float32(-sl[t]))))
+        want[t] = bf(bf(orc.bf16_to_f32(sy[t]) * gate) + bf(acc))
+    assert np.array_equal(got, want)
+    # against the f32 combine: K + 1 bf16 roundings of terms bounded by
+    # sum_k |w_k y_k|
+    routed = orc.bf16_to_f32(orc.combine_bf16(y, w)).astype(np.float64)
+    mag = np.einsum("tk,tkd->td", np.abs(w), np.abs(orc.bf16_to_f32(y))).astype(np.float64)
+    assert np.all(np.abs(routed - orc.combine(y, w)) <= (K + 1) * 2.0 ** -8 * mag)
+
+
 # ------------------------------------------------------------ dispatch
 def test_dispatch_is_stable_argsort(orc):
     rng = np.random.default_rng(7)
@@ -241,7 +326,7 @@ def test_swiglu_reference_values(orc):
 
 
 # --------------------------------------------------------------- block
-def _c1_params(orc, seed=0, K=2, E=8, fs=0, bits=4, bias=False):
+def _c1_params(orc, seed=0, K=2, E=8, fs=0, bits=4, bias=False, router_bits=0):
     rng = np.random.default_rng(seed)
     d, f = 512, 256
 
@@ -256,6 +341,14 @@ def _c1_params(orc, seed=0, K=2, E=8, fs=0, bits=4, bias=False):
     if fs:
         p.update(shared_gate=q((1, fs, d)), shared_up=q((1, fs, d)), shared_down=q((1, d, fs)),
                  shared_gate_w=(rng.standard_normal((1, d)) * 0.02).astype(np.float32))
+    if router_bits:
+        # QuantizedLinear router and shared gate, quantised from bf16
+        rq = lambda a: orc.quantize(orc.f32_to_bf16(a), 64, router_bits)
+        p.update(router_w=None, router_b=None, router_bits=router_bits,
+                 router_q=rq((rng.standard_normal((E, d)) * 0.05).astype(np.float32)))
+        if fs:
+            p.update(shared_gate_w=None,
+                     shared_gate_q=rq((rng.standard_normal((1, d)) * 0.05).astype(np.float32)))
     x = orc.f32_to_bf16(rng.standard_normal((16, d)).astype(np.float32))
     return p, x
 
@@ -290,6 +383,34 @@ def test_block_equals_sorted_composition(orc, fs, bias):
         sy = orc.gather_qmm(sa, *p["shared_down"], zeros).reshape(T, d)
         sl = orc.router_logits(x, p["shared_gate_w"])[:, 0]
     assert np.array_equal(out, orc.combine(y, w, sy, sl))
+
+
+@pytest.mark.parametrize("fs", [0, 256])
+def test_block_quantised_router_equals_composition(orc, fs):
+    """With an 8-bit QuantizedLinear router and shared gate the block is
+    bf16 throughout: router_logits_q -> router_topk_bf16 -> the sorted
+    expert path -> combine_bf16, bit for bit."""
+    p, x = _c1_params(orc, fs=fs, router_bits=8)
+    out, idx, w = orc.block_forward(p, x)
+    assert out.dtype == np.uint16
+    T, K, d = x.shape[0], p["K"], p["d"]
+    lg = orc.router_logits_q(x, *p["router_q"], 8)
+    idx2, w2 = orc.router_topk_bf16(lg, K)
+    assert np.array_equal(idx, idx2) and np.array_equal(w, w2)
+    _, _, order, inv = orc.dispatch(idx, p["E"])
+    xs = x[order // K][:, None, :]
+    ids = idx.reshape(-1)[order]
+    a = orc.swiglu(orc.gather_qmm(xs, *p["gate"], ids), orc.gather_qmm(xs, *p["up"], ids))
+    y = orc.gather_qmm(a, *p["down"], ids)[inv].reshape(T, K, d)
+    sy = sl = None
+    if fs:
+        x1 = x[:, None, :]
+        zeros = np.zeros(T, np.int32)
+        sa = orc.swiglu(orc.gather_qmm(x1, *p["shared_gate"], zeros),
+                        orc.gather_qmm(x1, *p["shared_up"], zeros))
+        sy = orc.gather_qmm(sa, *p["shared_down"], zeros).reshape(T, d)
+        sl = orc.router_logits_q(x, *p["shared_gate_q"], 8)[:, 0]
+    assert np.array_equal(out, orc.combine_bf16(y, w, sy, sl))
 
 
 def test_block_top1_is_single_expert(orc):
