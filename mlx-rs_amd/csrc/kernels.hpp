@@ -174,6 +174,11 @@ constexpr int kMaxInputDims = 4096;
 #ifndef MLXR_PREFILL_TALL_ROWS
 #define MLXR_PREFILL_TALL_ROWS 192
 #endif
+// 1: the prefill GEMM keeps each tile's scales and biases in LDS (where they
+// fit) instead of loading them every K step
+#ifndef MLXR_PREFILL_SCALES_LDS
+#define MLXR_PREFILL_SCALES_LDS 1
+#endif
 constexpr int kPrefillMinTileRows = 128;
 int prefill_tile_rows(int64_t rows, int64_t experts);
 // max_items bounds the number of work items (dispatch_max_work); prefill

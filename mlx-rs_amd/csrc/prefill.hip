@@ -27,7 +27,9 @@
 // the loads of the next groups in flight, and LDS stages hold dequantised
 // tiles: while the waves multiply stage s, the group loaded a step earlier
 // is dequantised into the next stage, interleaved with the MFMAs.  One
-// barrier per step.
+// barrier per step.  When K has 16 or more groups, each tile's scales and
+// biases are copied to LDS once (coalesced) instead of loaded every step:
+// a step's per-column scale loads put a different cache line on every lane.
 //
 // LDS rows are 64 bf16 (128 bytes) with the eight 16-byte chunks of row r
 // stored at chunk ^ ((r >> 1) & 7), which keeps the 16-byte operand reads of
@@ -125,7 +127,10 @@ namespace tile128 {
 #define MLXR_PF_MBLOCKS 2
 #define MLXR_PF_WAVES_N 4
 #define MLXR_PF_REGBUF 2
+// two stages (96 KB) leave room for the scales and biases of K up to 4096
+#define MLXR_PF_STAGES 2
 #include "prefill_tile.inc"
+#undef MLXR_PF_STAGES
 #undef MLXR_PF_TILE_ROWS
 #undef MLXR_PF_MBLOCKS
 #undef MLXR_PF_WAVES_N
