@@ -211,6 +211,69 @@ int mlxr_moe_switch_glu_experts(const mlxr_moe_switch_glu* ffn, const void* x,
                                 void* y, void* workspace,
                                 size_t workspace_size, mlxr_moe_stream stream);
 
+/* gemma4's Router (crates/mlxr-lm/src/gemma4/text/text.rs:568-665):
+ * normed = fast::rms_norm(x, norm_weight, eps), where norm_weight = scale *
+ * root_size (root_size = hidden_size^-1/2, folded into the scale once,
+ * text.rs:626-637); scores = proj(normed), a bf16 Linear [E, D]
+ * (proj_weight) or a QuantizedLinear (proj_q.weight set, 4 or 8 bits,
+ * group 64); top-K of the scores (argpartition, text.rs:643-648:
+ * descending, ties to the lower id); weights = softmax(top-K scores) *
+ * per_expert_scale[top-K] (router_post, activations.rs:309-331).  bf16
+ * throughout: x bf16 [T, D], norm_weight and per_expert_scale bf16,
+ * topk_idx int32 [T, K], topk_w bf16 [T, K]. */
+typedef struct {
+  int64_t hidden_size;
+  int64_t num_experts;
+  int64_t top_k;
+  float eps;
+  const void* norm_weight;
+  const void* proj_weight;
+  mlxr_moe_qlinear proj_q;
+  const void* per_expert_scale;
+} mlxr_moe_gemma_router;
+size_t mlxr_moe_gemma_router_workspace_size(const mlxr_moe_gemma_router* r,
+                                            int64_t T);
+int mlxr_moe_gemma_router_forward(const mlxr_moe_gemma_router* r,
+                                  const void* x, int64_t T, int32_t* topk_idx,
+                                  void* topk_w, void* workspace,
+                                  size_t workspace_size,
+                                  mlxr_moe_stream stream);
+
+/* PackedSwitchFfn (crates/mlxr-lm/src/nn/switch.rs:236-335), the gemma4
+ * expert layout: gate_up_proj [E, 2H, D] (split_sections at H: gate
+ * channels first, switch.rs:305-307) and down_proj [E, D, H], with GeGLU
+ * (gemma4's GemmaSwitchGlu = PackedSwitchFfn<GegluActivation>,
+ * crates/mlxr-lm/src/gemma4/text/mod.rs:27; activations.rs:223-259) or
+ * SwiGLU between them. */
+enum { MLXR_MOE_ACT_SWIGLU = 0, MLXR_MOE_ACT_GEGLU = 1 };
+typedef struct {
+  mlxr_moe_qlinear gate_up_proj;
+  mlxr_moe_qlinear down_proj;
+  int32_t activation;
+} mlxr_moe_packed_switch_glu;
+
+/* PackedSwitchFfn::forward_with_combine (switch.rs:290-335): x bf16
+ * [T, D], indices int32 [T, K], weights [T, K] f32 or bf16
+ * (weights_dtype) -> out [T, D], f32 for f32 weights (bf16 x f32
+ * promotes) and bf16 for bf16 weights (gemma4's router returns bf16). */
+size_t mlxr_moe_packed_switch_glu_workspace_size(
+    const mlxr_moe_packed_switch_glu* ffn, int64_t T, int64_t K);
+int mlxr_moe_packed_switch_glu_forward(const mlxr_moe_packed_switch_glu* ffn,
+                                       const void* x, int64_t T,
+                                       const int32_t* indices,
+                                       const void* weights, int weights_dtype,
+                                       int64_t K, void* out, void* workspace,
+                                       size_t workspace_size,
+                                       mlxr_moe_stream stream);
+/* PackedSwitchFfn::forward (switch.rs:290-315): per-expert outputs y bf16
+ * [T, K, D].  Same workspace size. */
+int mlxr_moe_packed_switch_glu_experts(const mlxr_moe_packed_switch_glu* ffn,
+                                       const void* x, int64_t T,
+                                       const int32_t* indices, int64_t K,
+                                       void* y, void* workspace,
+                                       size_t workspace_size,
+                                       mlxr_moe_stream stream);
+
 /* Qwen35MoeBlock (crates/mlxr-lm/src/qwen3_5/text/moe.rs:43-159):
  * f32 router gate_weight [E, d] with optional f32 gate_bias [E] (Linear
  * with bias = addmm, crates/mlxr/src/layers/linear.rs:91-95; the Qwen

@@ -6,7 +6,8 @@ fallback behind these functions.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32, c_int64,
+                    c_size_t, c_void_p)
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlxr_moe.so"
@@ -42,6 +43,26 @@ class QLinear(Structure):
 
 class SwitchGlu(Structure):
     _fields_ = [("gate_proj", QLinear), ("up_proj", QLinear), ("down_proj", QLinear)]
+
+
+class PackedSwitchGlu(Structure):
+    _fields_ = [("gate_up_proj", QLinear), ("down_proj", QLinear), ("activation", c_int32)]
+
+
+class GemmaRouter(Structure):
+    _fields_ = [
+        ("hidden_size", c_int64),
+        ("num_experts", c_int64),
+        ("top_k", c_int64),
+        ("eps", c_float),
+        ("norm_weight", c_void_p),
+        ("proj_weight", c_void_p),
+        ("proj_q", QLinear),
+        ("per_expert_scale", c_void_p),
+    ]
+
+
+ACT_SWIGLU, ACT_GEGLU = 0, 1
 
 
 class Block(Structure):
@@ -92,6 +113,15 @@ SIGNATURES = {
         c_int, [POINTER(SwitchGlu), P, c_int64, P, P, c_int64, P, P, c_size_t, P]),
     "mlxr_moe_switch_glu_experts": (
         c_int, [POINTER(SwitchGlu), P, c_int64, P, c_int64, P, P, c_size_t, P]),
+    "mlxr_moe_packed_switch_glu_workspace_size": (
+        c_size_t, [POINTER(PackedSwitchGlu), c_int64, c_int64]),
+    "mlxr_moe_packed_switch_glu_forward": (
+        c_int, [POINTER(PackedSwitchGlu), P, c_int64, P, P, c_int, c_int64, P, P, c_size_t, P]),
+    "mlxr_moe_packed_switch_glu_experts": (
+        c_int, [POINTER(PackedSwitchGlu), P, c_int64, P, c_int64, P, P, c_size_t, P]),
+    "mlxr_moe_gemma_router_workspace_size": (c_size_t, [POINTER(GemmaRouter), c_int64]),
+    "mlxr_moe_gemma_router_forward": (
+        c_int, [POINTER(GemmaRouter), P, c_int64, P, P, P, c_size_t, P]),
     "mlxr_moe_block_workspace_size": (c_size_t, [POINTER(Block), c_int64]),
     "mlxr_moe_block_forward": (c_int, [POINTER(Block), P, c_int64, P, P, P, P, c_size_t, P]),
     "mlxr_moe_workspace_status": (c_int, [P, c_size_t, P]),

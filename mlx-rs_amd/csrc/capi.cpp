@@ -217,6 +217,8 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
                   static_cast<const uint16_t*>(biases)};
   a.E = (int32_t)E;
   a.N = (int32_t)N;
+  a.e_rows = (int32_t)N;
+  a.act = kActSwiglu;
   a.K = (int32_t)K;
   a.bits = b;
   a.out = o;
@@ -397,7 +399,7 @@ int mlxr_moe_combine(const void* y, const float* w, int64_t T, int64_t K,
       (shared_y && !aligned(shared_y, 16)))
     return fail("combine: y, shared_y and out must be 16-byte aligned");
   return finish(from_hip(
-      launch_combine(static_cast<const uint16_t*>(y), w, T, K, d,
+      launch_combine(static_cast<const uint16_t*>(y), w, false, T, K, d,
                      static_cast<const uint16_t*>(shared_y), shared_logit, 1,
                      out, false, as_stream(stream)),
       "combine"));
@@ -442,8 +444,8 @@ int mlxr_moe_switch_glu_forward(const mlxr_moe_switch_glu* ffn, const void* x,
   st = from_hip(launch_zero_status(status, s), "switch_glu status");
   if (st.ok)
     st = m.forward_with_combine(static_cast<const uint16_t*>(x), T, indices,
-                                weights, K, out, nullptr, nullptr, 0, c,
-                                status, s);
+                                weights, false, K, out, nullptr, nullptr, 0,
+                                c, status, s);
   return finish(st);
 }
 
@@ -471,6 +473,181 @@ int mlxr_moe_switch_glu_experts(const mlxr_moe_switch_glu* ffn, const void* x,
   int32_t* status = c.take<int32_t>(1);
   c.take<uint16_t>(T * K * d);  // the combine's y slot, unused here
   st = from_hip(launch_zero_status(status, s), "switch_glu status");
+  if (st.ok)
+    st = m.forward(static_cast<const uint16_t*>(x), T, indices, K,
+                   static_cast<uint16_t*>(y), c, status, s);
+  return finish(st);
+}
+
+namespace {
+
+void gemma_router_plan(Carve& c, const mlxr_moe_gemma_router& r, int64_t T) {
+  c.take<uint16_t>(T * r.hidden_size);  // normed x
+  c.take<float>(T * r.num_experts);     // scores
+}
+
+}  // namespace
+
+size_t mlxr_moe_gemma_router_workspace_size(const mlxr_moe_gemma_router* r,
+                                            int64_t T) {
+  if (!r) return 0;
+  Carve c(nullptr);
+  gemma_router_plan(c, *r, T);
+  return c.off;
+}
+
+int mlxr_moe_gemma_router_forward(const mlxr_moe_gemma_router* r,
+                                  const void* x, int64_t T, int32_t* topk_idx,
+                                  void* topk_w, void* workspace,
+                                  size_t workspace_size,
+                                  mlxr_moe_stream stream) {
+  if (!r) return fail("gemma_router: null module");
+  const int64_t d = r->hidden_size, E = r->num_experts, K = r->top_k;
+  const bool q = r->proj_q.weight != nullptr;
+  if (T < 0 || d <= 0 || E <= 0) return fail("gemma_router: bad shape");
+  if (d % (q ? 64 : 4))
+    return fail(std::string("gemma_router: hidden_size must be a multiple of ") +
+                (q ? "64" : "4"));
+  if (E > kMaxExperts)
+    return fail("gemma_router: at most " + std::to_string(kMaxExperts) +
+                " experts");
+  if (K < 1 || K > E || K > 64)
+    return fail("gemma_router: top_k must be in [1, min(num_experts, 64)], got " +
+                std::to_string(K));
+  if (!(r->eps >= 0.0f)) return fail("gemma_router: eps must be >= 0");
+  if (q == (r->proj_weight != nullptr))
+    return fail("gemma_router: give exactly one of proj_weight and proj_q");
+  if (q) {
+    const mlxr_moe_qlinear& p = r->proj_q;
+    if ((p.bits != 4 && p.bits != 8) || p.group_size != 64)
+      return fail("gemma_router: proj_q must be 4- or 8-bit with group size 64");
+    if (p.num_experts != 1 || p.output_dims != E || p.input_dims != d ||
+        !p.scales || !p.biases)
+      return fail("gemma_router: proj_q must be one [num_experts, "
+                  "hidden_size] QuantizedLinear with scales and biases");
+    if (!aligned(p.weight, 4) || !aligned(p.scales, 2) || !aligned(p.biases, 2))
+      return fail("gemma_router: proj_q arrays misaligned");
+  } else if (!aligned(r->proj_weight, 8)) {
+    return fail("gemma_router: proj_weight must be 8-byte aligned");
+  }
+  if (!r->norm_weight || !r->per_expert_scale ||
+      (T && (!x || !topk_idx || !topk_w)))
+    return fail("gemma_router: null array");
+  if (!aligned(x, 8) || !aligned(r->norm_weight, 2) ||
+      !aligned(r->per_expert_scale, 2) || !aligned(topk_w, 2))
+    return fail("gemma_router: x must be 8-byte aligned");
+  Carve plan(nullptr);
+  gemma_router_plan(plan, *r, T);
+  Status st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  if (T == 0) return 0;
+  Carve c(workspace);
+  uint16_t* normed = c.take<uint16_t>(T * d);
+  float* scores = c.take<float>(T * E);
+  hipStream_t s = as_stream(stream);
+  const RouterWeights rw =
+      q ? RouterWeights{r->proj_q.bits,
+                        r->proj_q.weight,
+                        static_cast<const uint16_t*>(r->proj_q.scales),
+                        static_cast<const uint16_t*>(r->proj_q.biases),
+                        nullptr,
+                        nullptr,
+                        nullptr}
+        : RouterWeights{16, r->proj_weight, nullptr, nullptr, nullptr, nullptr, nullptr};
+  st = from_hip(launch_rms_norm(static_cast<const uint16_t*>(x), T, d,
+                                static_cast<const uint16_t*>(r->norm_weight),
+                                r->eps, normed, s),
+                "gemma_router rms_norm");
+  if (st.ok)
+    st = from_hip(launch_router_logits(normed, T, d, rw, nullptr, E, scores, E, s),
+                  "gemma_router scores");
+  if (st.ok)
+    st = from_hip(launch_gemma_topk(scores, E, T, E, K,
+                                    static_cast<const uint16_t*>(r->per_expert_scale),
+                                    topk_idx, static_cast<uint16_t*>(topk_w), s),
+                  "gemma_router top-k");
+  return finish(st);
+}
+
+size_t mlxr_moe_packed_switch_glu_workspace_size(
+    const mlxr_moe_packed_switch_glu* ffn, int64_t T, int64_t K) {
+  if (!ffn) return 0;
+  Carve c(nullptr);
+  c.take<int32_t>(1);
+  const mlxr_moe_qlinear& gu = ffn->gate_up_proj;
+  nn::SwitchFfn::plan(c, T, K, gu.input_dims, gu.output_dims / 2,
+                      gu.num_experts);
+  return c.off;
+}
+
+namespace {
+
+// Shared checks and set-up of the two PackedSwitchFfn entry points.
+Status packed_prologue(const mlxr_moe_packed_switch_glu* ffn, const void* x,
+                       int64_t T, const int32_t* indices, int64_t K,
+                       const void* out, void* workspace, size_t workspace_size,
+                       nn::PackedSwitchFfn& m) {
+  Status st = m.validate();
+  if (!st.ok) return st;
+  const nn::SwitchWeights& w = m.weights();
+  if (T < 0 || K < 1 || K > w.E)
+    return Status::error("packed_switch_glu: bad T or K");
+  if (T && (!x || !indices || !out))
+    return Status::error("packed_switch_glu: null array");
+  if (!aligned(x, 16) || !aligned(out, 16))
+    return Status::error("packed_switch_glu: x and out must be 16-byte aligned");
+  Carve plan(nullptr);
+  plan.take<int32_t>(1);
+  nn::SwitchFfn::plan(plan, T, K, w.d, w.f, w.E);
+  return check_workspace(plan, workspace, workspace_size);
+}
+
+}  // namespace
+
+int mlxr_moe_packed_switch_glu_forward(const mlxr_moe_packed_switch_glu* ffn,
+                                       const void* x, int64_t T,
+                                       const int32_t* indices,
+                                       const void* weights, int weights_dtype,
+                                       int64_t K, void* out, void* workspace,
+                                       size_t workspace_size,
+                                       mlxr_moe_stream stream) {
+  if (!ffn) return fail("packed_switch_glu: null module");
+  if (weights_dtype != MLXR_MOE_FLOAT32 && weights_dtype != MLXR_MOE_BFLOAT16)
+    return fail("packed_switch_glu: weights must be f32 or bf16");
+  nn::PackedSwitchFfn m(*ffn);
+  Status st = packed_prologue(ffn, x, T, indices, K, out, workspace,
+                              workspace_size, m);
+  if (!st.ok) return finish(st);
+  if (T && !weights) return fail("packed_switch_glu: null array");
+  if (T == 0) return 0;
+  hipStream_t s = as_stream(stream);
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  st = from_hip(launch_zero_status(status, s), "packed_switch_glu status");
+  if (st.ok)
+    st = m.forward_with_combine(static_cast<const uint16_t*>(x), T, indices,
+                                weights, weights_dtype == MLXR_MOE_BFLOAT16, K,
+                                out, nullptr, nullptr, 0, c, status, s);
+  return finish(st);
+}
+
+int mlxr_moe_packed_switch_glu_experts(const mlxr_moe_packed_switch_glu* ffn,
+                                       const void* x, int64_t T,
+                                       const int32_t* indices, int64_t K,
+                                       void* y, void* workspace,
+                                       size_t workspace_size,
+                                       mlxr_moe_stream stream) {
+  if (!ffn) return fail("packed_switch_glu: null module");
+  nn::PackedSwitchFfn m(*ffn);
+  Status st = packed_prologue(ffn, x, T, indices, K, y, workspace,
+                              workspace_size, m);
+  if (!st.ok) return finish(st);
+  if (T == 0) return 0;
+  hipStream_t s = as_stream(stream);
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  c.take<uint16_t>(T * K * m.weights().d);  // the combine's y slot, unused
+  st = from_hip(launch_zero_status(status, s), "packed_switch_glu status");
   if (st.ok)
     st = m.forward(static_cast<const uint16_t*>(x), T, indices, K,
                    static_cast<uint16_t*>(y), c, status, s);

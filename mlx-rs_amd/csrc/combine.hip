@@ -17,9 +17,9 @@
 namespace mlxr_moe {
 namespace {
 
-template <bool BF16>
+template <bool BF16, typename WT>
 __global__ __launch_bounds__(256) void combine_kernel(
-    const uint16_t* __restrict__ y, const float* __restrict__ w, int T, int K,
+    const uint16_t* __restrict__ y, const WT* __restrict__ w, int T, int K,
     int d, const uint16_t* __restrict__ shared_y,
     const float* __restrict__ shared_logit, int64_t shared_ld,
     void* __restrict__ out) {
@@ -30,7 +30,11 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
   for (int k = 0; k < K; ++k) {
-    const float wk = w[(int64_t)t * K + k];
+    float wk;
+    if constexpr (sizeof(WT) == 2)
+      wk = bf16_to_f32(w[(int64_t)t * K + k]);
+    else
+      wk = w[(int64_t)t * K + k];
     const u32x4_t v =
         *reinterpret_cast<const u32x4_t*>(y + ((int64_t)t * K + k) * d + n0);
     const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
@@ -85,19 +89,26 @@ __global__ __launch_bounds__(256) void combine_kernel(
 
 }  // namespace
 
-hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,
-                          int64_t K, int64_t d, const uint16_t* shared_y,
-                          const float* shared_logit, int64_t shared_ld,
-                          void* out, bool bf16, hipStream_t s) {
+hipError_t launch_combine(const uint16_t* y, const void* w, bool w_bf16,
+                          int64_t T, int64_t K, int64_t d,
+                          const uint16_t* shared_y, const float* shared_logit,
+                          int64_t shared_ld, void* out, bool bf16,
+                          hipStream_t s) {
   if (T == 0) return hipSuccess;
+  if (w_bf16 && !bf16) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((d / 8 + 255) / 256), (unsigned)T);
   ProfileScope prof("combine", s);
-  if (bf16)
-    combine_kernel<true><<<grid, 256, 0, s>>>(y, w, (int)T, (int)K, (int)d, shared_y,
-                                              shared_logit, shared_ld, out);
+  const float* wf = static_cast<const float*>(w);
+  const uint16_t* wh = static_cast<const uint16_t*>(w);
+  if (w_bf16)
+    combine_kernel<true, uint16_t><<<grid, 256, 0, s>>>(
+        y, wh, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, out);
+  else if (bf16)
+    combine_kernel<true, float><<<grid, 256, 0, s>>>(
+        y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, out);
   else
-    combine_kernel<false><<<grid, 256, 0, s>>>(y, w, (int)T, (int)K, (int)d, shared_y,
-                                               shared_logit, shared_ld, out);
+    combine_kernel<false, float><<<grid, 256, 0, s>>>(
+        y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, out);
   return hipGetLastError();
 }
 

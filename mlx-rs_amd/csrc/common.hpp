@@ -54,6 +54,26 @@ __device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
   return f32_to_bf16(h * u);
 }
 
+// gelu_approx(g) * u with the reference's bf16 rounding points
+// (gelu_approximate_in_dtype, crates/mlxr-lm/src/activations.rs:246-259:
+// every op in the input dtype, the constants cast to bf16 first):
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).  g and u are bf16 values
+// held in f32.
+__device__ __forceinline__ uint16_t geglu_bf16(float g, float u) {
+  const float k = 0.044677734375f;  // bf16(0.044715)
+  const float c = 0.796875f;        // bf16(sqrt(2 / pi))
+  const float x3 = bf16_round(bf16_round(g * g) * g);
+  const float inner = bf16_round(g + bf16_round(k * x3));
+  const float t = bf16_round(tanhf(bf16_round(c * inner)));
+  const float gl = bf16_round(bf16_round(0.5f * g) * bf16_round(1.0f + t));
+  return f32_to_bf16(gl * u);
+}
+
+// The gated GEMMs' activation: act(g, u) for g and u bf16 values in f32.
+__device__ __forceinline__ uint16_t gated_act_bf16(int act, float g, float u) {
+  return act == 1 ? geglu_bf16(g, u) : swiglu_bf16(g, u);
+}
+
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
   // v += v[l ^ m] for m = 32, 16, 8, 4, 2, 1: every lane ends with the
   // same bits, and the CPU restatement reproduces the association.

@@ -41,9 +41,9 @@ hipError_t launch_dequantize(const uint32_t* wq, const void* scales,
                              bool out_bf16, hipStream_t s);
 
 // --------------------------------------------------------------- router.hip
-// Router weights: an f32 Linear [E, d] (bits == 0), or a QuantizedLinear
-// (bits 4 or 8, group 64): packed codes [E, d*bits/32], bf16 scales and
-// biases [E, d/64].  The extra row (the shared-expert gate, logit column
+// Router weights: an f32 Linear [E, d] (bits == 0), a bf16 Linear (bits ==
+// 16), or a QuantizedLinear (bits 4 or 8, group 64): packed codes
+// [E, d*bits/32], bf16 scales and biases [E, d/64].  The extra row (the shared-expert gate, logit column
 // E) takes the same form when w_extra is set.
 struct RouterWeights {
   int bits;
@@ -70,6 +70,15 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
 hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
                               int64_t E, int64_t K, bool bf16, int32_t* idx,
                               float* wts, int32_t* status, hipStream_t s);
+// out bf16 [T, d] = fast::rms_norm(x, w, eps) (gemma4's router prologue)
+hipError_t launch_rms_norm(const uint16_t* x, int64_t T, int64_t d,
+                           const uint16_t* w, float eps, uint16_t* out,
+                           hipStream_t s);
+// gemma4's router top-k on bf16 scores [T, ld]: idx [T, K], bf16 weights
+// softmax(top-K scores) * per_expert_scale (pes, bf16 [E]).
+hipError_t launch_gemma_topk(const float* scores, int64_t ld, int64_t T,
+                             int64_t E, int64_t K, const uint16_t* pes,
+                             int32_t* idx, uint16_t* wts, hipStream_t s);
 hipError_t launch_argsort_rows(const float* a, int64_t rows, int64_t n,
                                uint32_t* out, hipStream_t s);
 hipError_t launch_softmax_rows(const float* a, int64_t rows, int64_t n,
@@ -160,11 +169,17 @@ struct QGemmArgs {
   QWeights w0;             // gate (or the only projection)
   QWeights w1;             // up (gated mode only)
   int32_t E, N, K, bits;
+  // weight rows per expert: N, or 2N for the packed gate/up tensor of
+  // PackedSwitchFfn ([E, 2H, D]; w1 then points H rows past w0)
+  int32_t e_rows;
+  int32_t act;             // gated mode: kActSwiglu or kActGeglu
   uint16_t* out;           // bf16
   int64_t out_ld;
   bool out_by_flat;        // out row of slot p = its flat row (else p)
-  bool gated;              // out = swiglu(x.w0, x.w1)
+  bool gated;              // out = act(x.w0, x.w1)
 };
+constexpr int32_t kActSwiglu = 0;  // silu(g) * u  (Qwen3.5/3.6 experts)
+constexpr int32_t kActGeglu = 1;   // gelu_approx(g) * u  (gemma4 experts)
 // Largest input dim (K) of a projection: 8 waves x 8 groups of 64.
 constexpr int kMaxInputDims = 4096;
 // Prefill kernel M-tiles: 256 rows when the experts average at least
@@ -197,10 +212,12 @@ hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
 
 // -------------------------------------------------------------- combine.hip
 // out f32 [T, d], or bf16 when bf16 (the routing weights are then bf16
-// values and every op rounds to bf16).
-hipError_t launch_combine(const uint16_t* y, const float* w, int64_t T,
-                          int64_t K, int64_t d, const uint16_t* shared_y,
-                          const float* shared_logit, int64_t shared_ld,
-                          void* out, bool bf16, hipStream_t s);
+// values and every op rounds to bf16).  w is f32 [T, K], or bf16 when
+// w_bf16 (only with a bf16 out).
+hipError_t launch_combine(const uint16_t* y, const void* w, bool w_bf16,
+                          int64_t T, int64_t K, int64_t d,
+                          const uint16_t* shared_y, const float* shared_logit,
+                          int64_t shared_ld, void* out, bool bf16,
+                          hipStream_t s);
 
 }  // namespace mlxr_moe

@@ -128,6 +128,8 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.w1 = qw(up_);
   g.E = 1;
   g.N = (int32_t)f;
+  g.e_rows = (int32_t)f;
+  g.act = kActSwiglu;
   g.K = (int32_t)d;
   g.bits = gate_.bits;
   g.out = act;
@@ -143,6 +145,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   h.w0 = qw(down_);
   h.w1 = QWeights{};
   h.N = (int32_t)d;
+  h.e_rows = (int32_t)d;
   h.K = (int32_t)f;
   h.out = y;
   h.out_ld = d;
@@ -150,7 +153,19 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   return from_hip(launch_qgemm(h, T, items, prefill, s), "shared_expert down");
 }
 
-// -------------------------------------------------------- SplitSwitchFfn
+// ----------------------------------------------------------- switch FFNs
+SplitSwitchFfn::SplitSwitchFfn(const mlxr_moe_switch_glu& w) : w_(w) {
+  sw_.gate = qw(w.gate_proj);
+  sw_.up = qw(w.up_proj);
+  sw_.down = qw(w.down_proj);
+  sw_.E = w.gate_proj.num_experts;
+  sw_.d = w.gate_proj.input_dims;
+  sw_.f = w.gate_proj.output_dims;
+  sw_.bits = w.gate_proj.bits;
+  sw_.gate_rows = (int32_t)sw_.f;
+  sw_.act = kActSwiglu;
+}
+
 Status SplitSwitchFfn::validate(int64_t d, int64_t f, int64_t E) const {
   Status st = check_qlinear(w_.gate_proj, E, f, d, "switch_mlp.gate_proj");
   if (st.ok) st = check_qlinear(w_.up_proj, E, f, d, "switch_mlp.up_proj");
@@ -165,20 +180,61 @@ Status SplitSwitchFfn::validate(int64_t d, int64_t f, int64_t E) const {
   return st;
 }
 
-void SplitSwitchFfn::plan(Carve& ws, int64_t T, int64_t K, int64_t d,
-                          int64_t f, int64_t E) {
+// The packed tensor's up half starts H rows into each expert: the same
+// tensor seen twice, H rows apart, with 2H rows per expert.
+PackedSwitchFfn::PackedSwitchFfn(const mlxr_moe_packed_switch_glu& w) : w_(w) {
+  const mlxr_moe_qlinear& gu = w.gate_up_proj;
+  sw_.E = gu.num_experts;
+  sw_.d = gu.input_dims;
+  sw_.f = gu.output_dims / 2;
+  sw_.bits = gu.bits;
+  sw_.gate = qw(gu);
+  sw_.up = sw_.gate;
+  if (gu.weight && gu.bits > 0) {
+    const int64_t words = sw_.f * sw_.d * gu.bits / 32;
+    const int64_t g = sw_.d / (gu.group_size > 0 ? gu.group_size : 64);
+    sw_.up.w = gu.weight + words;
+    sw_.up.scales = sw_.gate.scales + sw_.f * g;
+    sw_.up.biases = sw_.gate.biases + sw_.f * g;
+  }
+  sw_.down = qw(w.down_proj);
+  sw_.gate_rows = (int32_t)gu.output_dims;
+  sw_.act = w.activation == MLXR_MOE_ACT_GEGLU ? kActGeglu : kActSwiglu;
+}
+
+Status PackedSwitchFfn::validate() const {
+  const mlxr_moe_qlinear &gu = w_.gate_up_proj, &dn = w_.down_proj;
+  const int64_t E = gu.num_experts, d = gu.input_dims, h2 = gu.output_dims;
+  if (h2 <= 0 || h2 % 2)
+    return Status::error("packed_switch_glu: gate_up_proj output_dims must "
+                         "be 2 * hidden_dims");
+  if (w_.activation != MLXR_MOE_ACT_SWIGLU && w_.activation != MLXR_MOE_ACT_GEGLU)
+    return Status::error("packed_switch_glu: activation must be "
+                         "MLXR_MOE_ACT_SWIGLU or MLXR_MOE_ACT_GEGLU");
+  Status st = check_qlinear(gu, E, h2, d, "packed_switch_glu.gate_up_proj");
+  if (st.ok) st = check_qlinear(dn, E, d, h2 / 2, "packed_switch_glu.down_proj");
+  if (st.ok && gu.bits != dn.bits)
+    st = Status::error("packed_switch_glu: projections must share bits");
+  if (st.ok && E > kMaxExperts)
+    st = Status::error("packed_switch_glu: at most " +
+                       std::to_string(kMaxExperts) + " experts");
+  return st;
+}
+
+void SwitchFfn::plan(Carve& ws, int64_t T, int64_t K, int64_t d, int64_t f,
+                     int64_t E) {
   ws.take<uint16_t>(T * K * d);  // y (forward_with_combine)
   carve_dispatch(ws, T * K, E, nullptr);
   ws.take<uint16_t>(T * K * f);
 }
 
-// SplitSwitchFfn::forward (switch.rs:417-442) on the sorted path: dispatch
-// (gather_sort), then the expert products.
-Status SplitSwitchFfn::forward(const uint16_t* x, int64_t T,
-                               const int32_t* indices, int64_t K, uint16_t* y,
-                               Carve& ws, int32_t* status,
-                               hipStream_t s) const {
-  const int64_t E = w_.gate_proj.num_experts;
+// SplitSwitchFfn::forward / PackedSwitchFfn::forward (switch.rs:417-442,
+// 290-315) on the sorted path: dispatch (gather_sort), then the expert
+// products.
+Status SwitchFfn::forward(const uint16_t* x, int64_t T, const int32_t* indices,
+                          int64_t K, uint16_t* y, Carve& ws, int32_t* status,
+                          hipStream_t s) const {
+  const int64_t E = sw_.E;
   const int64_t n = T * K;
   const DispatchBuffers db = carve_dispatch(ws, n, E, status);
   Status st = from_hip(
@@ -188,14 +244,15 @@ Status SplitSwitchFfn::forward(const uint16_t* x, int64_t T,
   return experts(x, T, K, db, y, ws, s);
 }
 
-// The expert products of SplitSwitchFfn::forward given the dispatch: gate and
-// up gather_qmm fused with swiglu (switch.rs:432-434), down gather_qmm whose
-// rows land at their flat (t, k) position (scatter_unsort, switch.rs:437-439).
-Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
-                               const DispatchBuffers& db, uint16_t* y,
-                               Carve& ws, hipStream_t s) const {
-  const int64_t d = w_.gate_proj.input_dims, f = w_.gate_proj.output_dims;
-  const int64_t E = w_.gate_proj.num_experts;
+// The expert products given the dispatch: gate and up gather_qmm fused with
+// the activation (switch.rs:432-434; the packed layout's split_sections,
+// switch.rs:305-307, is the H-row offset of the up half), down gather_qmm
+// whose rows land at their flat (t, k) position (scatter_unsort,
+// switch.rs:437-439).
+Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
+                          const DispatchBuffers& db, uint16_t* y, Carve& ws,
+                          hipStream_t s) const {
+  const int64_t d = sw_.d, f = sw_.f, E = sw_.E;
   const int64_t n = T * K;
   uint16_t* act = ws.take<uint16_t>(n * f);
   const int64_t max_items = dispatch_max_work(n, E);
@@ -215,12 +272,14 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   g.tiles = db.tiles;
   g.num_tiles = db.num_tiles;
   g.sorted = db.sorted;
-  g.w0 = qw(w_.gate_proj);
-  g.w1 = qw(w_.up_proj);
+  g.w0 = sw_.gate;
+  g.w1 = sw_.up;
   g.E = (int32_t)E;
   g.N = (int32_t)f;
+  g.e_rows = sw_.gate_rows;
+  g.act = sw_.act;
   g.K = (int32_t)d;
-  g.bits = w_.gate_proj.bits;
+  g.bits = sw_.bits;
   g.out = act;
   g.out_ld = f;
   g.gated = true;
@@ -231,9 +290,10 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   h.x = act;
   h.x_ld = f;
   h.x_by_slot = true;
-  h.w0 = qw(w_.down_proj);
+  h.w0 = sw_.down;
   h.w1 = QWeights{};
   h.N = (int32_t)d;
+  h.e_rows = (int32_t)d;
   h.K = (int32_t)f;
   h.out = y;
   h.out_ld = d;
@@ -243,18 +303,18 @@ Status SplitSwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
                   "switch_mlp down");
 }
 
-// forward_with_combine (switch.rs:446-474) + combine_with_weights
+// forward_with_combine (switch.rs:446-474, 322-335) + combine_with_weights
 // (switch.rs:223-234); the block's shared branch is added in the same pass.
-Status SplitSwitchFfn::forward_with_combine(
-    const uint16_t* x, int64_t T, const int32_t* indices, const float* weights,
-    int64_t K, float* out, const uint16_t* shared_y, const float* shared_logit,
-    int64_t shared_ld, Carve& ws, int32_t* status, hipStream_t s) const {
-  const int64_t d = w_.gate_proj.input_dims;
-  uint16_t* y = ws.take<uint16_t>(T * K * d);
+Status SwitchFfn::forward_with_combine(
+    const uint16_t* x, int64_t T, const int32_t* indices, const void* weights,
+    bool w_bf16, int64_t K, void* out, const uint16_t* shared_y,
+    const float* shared_logit, int64_t shared_ld, Carve& ws, int32_t* status,
+    hipStream_t s) const {
+  uint16_t* y = ws.take<uint16_t>(T * K * sw_.d);
   Status st = forward(x, T, indices, K, y, ws, status, s);
   if (!st.ok) return st;
-  return from_hip(launch_combine(y, weights, T, K, d, shared_y, shared_logit,
-                                 shared_ld, out, false, s),
+  return from_hip(launch_combine(y, weights, w_bf16, T, K, sw_.d, shared_y,
+                                 shared_logit, shared_ld, out, w_bf16, s),
                   "combine");
 }
 
@@ -373,7 +433,7 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
   const SplitSwitchFfn mlp(b_.switch_mlp);
   st = mlp.experts(x, T, K, db, y, ws, s);
   if (!st.ok) return st;
-  return from_hip(launch_combine(y, wts, T, K, d, sy,
+  return from_hip(launch_combine(y, wts, false, T, K, d, sy,
                                  shared ? logits + E : nullptr, ld, out, bf16,
                                  s),
                   "combine");

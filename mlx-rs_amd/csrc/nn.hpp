@@ -72,11 +72,21 @@ class SwigluMlp {
   mlxr_moe_qlinear gate_, up_, down_;
 };
 
-class SplitSwitchFfn {
+// The projections of a switch FFN as the kernels see them: gate and up
+// (separate tensors, or halves of one packed tensor), down, and the
+// activation between them.
+struct SwitchWeights {
+  QWeights gate, up, down;
+  int64_t E, d, f;
+  int32_t bits;
+  int32_t gate_rows;  // weight rows per expert of the gate/up tensor(s)
+  int32_t act;        // kActSwiglu / kActGeglu
+};
+
+// The forward shared by both expert layouts (switch.rs:417-474).
+class SwitchFfn {
  public:
-  explicit SplitSwitchFfn(const mlxr_moe_switch_glu& w) : w_(w) {}
-  Status validate(int64_t d, int64_t f, int64_t E) const;
-  // SplitSwitchFfn::forward: y bf16 [T, K, d] per-expert outputs.
+  // forward: y bf16 [T, K, d] per-expert outputs.
   Status forward(const uint16_t* x, int64_t T, const int32_t* indices,
                  int64_t K, uint16_t* y, Carve& ws, int32_t* status,
                  hipStream_t s) const;
@@ -84,18 +94,44 @@ class SplitSwitchFfn {
   Status experts(const uint16_t* x, int64_t T, int64_t K,
                  const DispatchBuffers& db, uint16_t* y, Carve& ws,
                  hipStream_t s) const;
-  // forward_with_combine: out f32 [T, d] = sum_k w * y (+ shared branch).
+  // forward_with_combine: out [T, d] = sum_k w * y (+ shared branch); f32
+  // weights give an f32 out, bf16 weights (w_bf16) a bf16 out.
   Status forward_with_combine(const uint16_t* x, int64_t T,
-                              const int32_t* indices, const float* weights,
-                              int64_t K, float* out, const uint16_t* shared_y,
+                              const int32_t* indices, const void* weights,
+                              bool w_bf16, int64_t K, void* out,
+                              const uint16_t* shared_y,
                               const float* shared_logit, int64_t shared_ld,
                               Carve& ws, int32_t* status,
                               hipStream_t s) const;
   static void plan(Carve& ws, int64_t T, int64_t K, int64_t d, int64_t f,
                    int64_t E);
+  const SwitchWeights& weights() const { return sw_; }
+
+ protected:
+  SwitchWeights sw_{};
+};
+
+// SplitSwitchFfn<SwigluActivation> (switch.rs:366-491): gate_proj and
+// up_proj [E, f, d], down_proj [E, d, f].
+class SplitSwitchFfn : public SwitchFfn {
+ public:
+  explicit SplitSwitchFfn(const mlxr_moe_switch_glu& w);
+  Status validate(int64_t d, int64_t f, int64_t E) const;
 
  private:
   mlxr_moe_switch_glu w_;
+};
+
+// PackedSwitchFfn (switch.rs:236-335): gate_up_proj [E, 2H, d] split at H
+// (gate channels first), down_proj [E, d, H]; GeGLU for gemma4's
+// GemmaSwitchGlu (gemma4/text/mod.rs:27) or SwiGLU.
+class PackedSwitchFfn : public SwitchFfn {
+ public:
+  explicit PackedSwitchFfn(const mlxr_moe_packed_switch_glu& w);
+  Status validate() const;
+
+ private:
+  mlxr_moe_packed_switch_glu w_;
 };
 
 class Qwen35MoeBlock {

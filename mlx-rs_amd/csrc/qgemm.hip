@@ -226,7 +226,7 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
   const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   const u32x4_t zq = {0u, 0u, 0u, 0u};
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  const int64_t wrow0 = (int64_t)e * a.N + (int64_t)tile * CB * 16 + c;
+  const int64_t wrow0 = (int64_t)e * a.e_rows + (int64_t)tile * CB * 16 + c;
 
   for (int tt = 0; tt < rows; tt += 16) {
     const int tok = tt + c;
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
           const int slot = row0 + t;
           if constexpr (GATED) {
             a.out[(int64_t)slot * a.out_ld + ch] =
-                swiglu_bf16(bf16_round(s0[r]), bf16_round(s1[r]));
+                gated_act_bf16(a.act, bf16_round(s0[r]), bf16_round(s1[r]));
           } else {
             const int64_t orow = a.out_by_flat ? rec[4 + t] : slot;
             a.out[orow * a.out_ld + ch] = f32_to_bf16(s0[r]);
@@ -434,7 +434,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   const u32x4_t zq = {0u, 0u, 0u, 0u};
   // this wave's blocks: nb consecutive 16-channel blocks from ch0
   const int ch0 = ((tile * waves + wave) * nb) * 16 + n;
-  const int64_t wrow0 = (int64_t)e * a.N + ch0;
+  const int64_t wrow0 = (int64_t)e * a.e_rows + ch0;
   // A operand row of this lane: (group m / TT, token m % TT), m = l % 16
   const int arow_g = n / TT, arow_t = n % TT;
 
@@ -649,7 +649,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
           const int slot = row0 + t;
           if constexpr (GATED) {
             a.out[(int64_t)slot * a.out_ld + ch] =
-                swiglu_bf16(bf16_round(tot[0][r]), bf16_round(tot[1][r]));
+                gated_act_bf16(a.act, bf16_round(tot[0][r]), bf16_round(tot[1][r]));
           } else {
             const int64_t orow = a.out_by_flat ? rec[4 + t] : slot;
             a.out[orow * a.out_ld + ch] = f32_to_bf16(tot[0][r]);

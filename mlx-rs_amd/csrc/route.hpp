@@ -37,10 +37,17 @@ struct TopkScratch {
 // exp((double)l_e - m) / S)) with S summed in double in the order above
 // (double makes p independent of exp's last bits on either side); then
 // denom = bf16(sum_k p_k in f32, k in order), w_k = bf16(p_k / denom).
+// GEMMA (gemma4 Router::forward, crates/mlxr-lm/src/gemma4/text/text.rs:
+// 621-665, router_post activations.rs:309-331): the selection is on the
+// bf16 scores as given; then softmax over the K selected scores in bf16
+// (non-precise: d_k = bf16(s_k - m), e_k = bf16(exp(d_k)) with exp in
+// double, S = bf16(sum_k e_k in f32, k in order), p_k = bf16(e_k / S)) and
+// w_k = bf16(p_k * per_expert_scale[id_k]).
 // Returns on lane k < K its expert id (*out_id) and weight (*out_w).
-template <int SLOTS, bool BF16 = false>
+template <int SLOTS, bool BF16 = false, bool GEMMA = false>
 __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
-                          TopkScratch* sc, int* out_id, float* out_w) {
+                          TopkScratch* sc, int* out_id, float* out_w,
+                          const uint16_t* __restrict__ pes = nullptr) {
   const int lane = threadIdx.x & 63;
   const uint64_t below = (1ull << lane) - 1ull;
   float v[SLOTS];
@@ -130,6 +137,17 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int id = lane < K ? sc->id[lane] : 0;
+  if constexpr (GEMMA) {
+    const float m = sc->val[0];
+    const float dk = lane < K ? bf16_round(sc->val[lane] - m) : 0.0f;
+    const float ek = lane < K ? bf16_round((float)exp((double)dk)) : 0.0f;
+    float S = 0.0f;
+    for (int k = 0; k < K; ++k) S += __shfl(ek, k, 64);
+    const float pk = bf16_round(ek / bf16_round(S));
+    *out_id = id;
+    *out_w = lane < K ? bf16_round(pk * bf16_to_f32(pes[id])) : 0.0f;
+    return;
+  }
   if constexpr (BF16) {
     const float p = lane < K ? sc->val[lane] : 0.0f;
     float psum = 0.0f;

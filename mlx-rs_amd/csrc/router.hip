@@ -44,6 +44,8 @@ __device__ __forceinline__ WRow router_row(const RouterWeights& rw, int e,
   if (e < E) {
     if (BITS == 0)
       return {static_cast<const float*>(rw.w) + (int64_t)e * d, nullptr, nullptr};
+    if (BITS == 16)
+      return {static_cast<const uint16_t*>(rw.w) + (int64_t)e * d, nullptr, nullptr};
     return {static_cast<const uint8_t*>(rw.w) + (int64_t)e * d * BITS / 8,
             rw.scales + (int64_t)e * (d / 64), rw.biases + (int64_t)e * (d / 64)};
   }
@@ -51,13 +53,18 @@ __device__ __forceinline__ WRow router_row(const RouterWeights& rw, int e,
   return {nullptr, nullptr, nullptr};
 }
 
-// Weights j..j+3 of a row (j % 4 == 0): four f32, or four codes (one word
-// at 8 bits, half a word at 4, little end first) dequantised in f32 as
-// fmaf(code, scale, bias) with the scale and bias of group j / 64.
+// Weights j..j+3 of a row (j % 4 == 0): four f32, four bf16 (BITS 16: a
+// dense bf16 Linear), or four codes (one word at 8 bits, half a word at 4,
+// little end first) dequantised in f32 as fmaf(code, scale, bias) with the
+// scale and bias of group j / 64.
 template <int BITS>
 __device__ __forceinline__ float4 router_w4(const WRow& r, int j) {
   if constexpr (BITS == 0) {
     return *reinterpret_cast<const float4*>(static_cast<const float*>(r.w) + j);
+  } else if constexpr (BITS == 16) {
+    const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(r.w) + j);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                       __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
   } else {
     const uint8_t* p = static_cast<const uint8_t*>(r.w);
     const uint32_t c = BITS == 8
@@ -73,7 +80,7 @@ __device__ __forceinline__ float4 router_w4(const WRow& r, int j) {
 }
 
 // The finished dot product of logit column e: + bias for an f32 Linear
-// that has one, one bf16 rounding for a quantised router.
+// that has one, one bf16 rounding for a bf16 or quantised router.
 template <int BITS>
 __device__ __forceinline__ float router_finish(float v, const float* bias,
                                                int e, int E) {
@@ -368,6 +375,54 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(
     out[row * n + i] = expf(r[i] - mx) / sum;
 }
 
+// fast::rms_norm as gemma4's router applies it (Router::forward,
+// crates/mlxr-lm/src/gemma4/text/text.rs:640): out_j = bf16(w_j *
+// bf16(x_j * r)), r = 1 / sqrt(sum_j x_j^2 / d + eps) -- MLX's rounding
+// points (the normalised value in the input dtype, then the weight
+// product) -- with the sum of squares in the router's lane order (fmaf over
+// j = 4l + 256i + c, then the butterfly).  One wave per row.
+__global__ __launch_bounds__(256) void rms_norm_kernel(
+    const uint16_t* __restrict__ x, int T, int d,
+    const uint16_t* __restrict__ w, float eps, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const uint16_t* xr = x + (int64_t)t * d;
+  float acc = 0.0f;
+  for (int j0 = 4 * lane; j0 < d; j0 += 256) {
+    const uint2 u = *reinterpret_cast<const uint2*>(xr + j0);
+    const float v[4] = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                        __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(v[c], v[c], acc);
+  }
+  const float ss = wave_sum_butterfly(acc);
+  const float r = 1.0f / sqrtf(ss / (float)d + eps);
+  uint16_t* orow = out + (int64_t)t * d;
+  for (int j = lane; j < d; j += 64)
+    orow[j] = f32_to_bf16(bf16_to_f32(w[j]) * bf16_round(bf16_to_f32(xr[j]) * r));
+}
+
+// gemma4's router top-k (wave_topk GEMMA): one wave per token; bf16 weights.
+template <int SLOTS>
+__global__ __launch_bounds__(256) void gemma_topk_kernel(
+    const float* __restrict__ scores, int64_t ld, int T, int E, int K,
+    const uint16_t* __restrict__ pes, int32_t* __restrict__ idx,
+    uint16_t* __restrict__ wts) {
+  __shared__ TopkScratch sc[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  int id;
+  float wt;
+  wave_topk<SLOTS, false, true>(scores + (int64_t)t * ld, E, K, &sc[wave], &id,
+                                &wt, pes);
+  if (lane < K) {
+    idx[(int64_t)t * K + lane] = id;
+    wts[(int64_t)t * K + lane] = f32_to_bf16(wt);
+  }
+}
+
 template <int BITS>
 void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
                           const RouterWeights& w, const float* bias, int64_t E,
@@ -423,9 +478,12 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 int64_t E, float* logits, int64_t ld,
                                 hipStream_t s) {
   if (T == 0) return hipSuccess;
-  if (w.bits != 0 && w.bits != 4 && w.bits != 8) return hipErrorInvalidValue;
+  if (w.bits != 0 && w.bits != 4 && w.bits != 8 && w.bits != 16)
+    return hipErrorInvalidValue;
   ProfileScope prof("router_logits", s);
-  if (w.bits == 8)
+  if (w.bits == 16)
+    router_logits_launch<16>(x, T, d, w, bias, E, logits, ld, s);
+  else if (w.bits == 8)
     router_logits_launch<8>(x, T, d, w, bias, E, logits, ld, s);
   else if (w.bits == 4)
     router_logits_launch<4>(x, T, d, w, bias, E, logits, ld, s);
@@ -443,6 +501,39 @@ hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
     router_topk_launch<true>(logits, ld, T, E, K, idx, wts, status, s);
   else
     router_topk_launch<false>(logits, ld, T, E, K, idx, wts, status, s);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const uint16_t* x, int64_t T, int64_t d,
+                           const uint16_t* w, float eps, uint16_t* out,
+                           hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  rms_norm_kernel<<<(unsigned)((T + 3) / 4), 256, 0, s>>>(x, (int)T, (int)d, w,
+                                                          eps, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemma_topk(const float* scores, int64_t ld, int64_t T,
+                             int64_t E, int64_t K, const uint16_t* pes,
+                             int32_t* idx, uint16_t* wts, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  ProfileScope prof("router_topk", s);
+  const dim3 grid((unsigned)((T + 3) / 4));
+  const int slots = (int)((E + 63) / 64);
+#define MLXR_GT(S)                                                        \
+  gemma_topk_kernel<S><<<grid, 256, 0, s>>>(scores, ld, (int)T, (int)E,   \
+                                            (int)K, pes, idx, wts)
+  if (slots <= 1)
+    MLXR_GT(1);
+  else if (slots <= 2)
+    MLXR_GT(2);
+  else if (slots <= 4)
+    MLXR_GT(4);
+  else if (slots <= 8)
+    MLXR_GT(8);
+  else
+    MLXR_GT(16);
+#undef MLXR_GT
   return hipGetLastError();
 }
 

@@ -152,6 +152,177 @@ class SplitSwitchFfn:
         return out.reshape(tuple(x.shape[:-1]) + (d,))
 
 
+class PackedSwitchFfn:
+    """PackedSwitchFfn (switch.rs:236-335), gemma4's expert layout:
+    gate_up_proj [E, 2H, d] (gate channels first, split_sections at H) and
+    down_proj [E, d, H], with GeGLU (GemmaSwitchGlu, gemma4/text/mod.rs:27)
+    or SwiGLU between them."""
+
+    def __init__(self, gate_up_proj: QuantizedSwitchLinear, down_proj: QuantizedSwitchLinear,
+                 activation: str = "geglu"):
+        if activation not in ("geglu", "swiglu"):
+            raise MlxrMoeError("PackedSwitchFfn: activation is 'geglu' or 'swiglu'")
+        if gate_up_proj.output_dims % 2:
+            raise MlxrMoeError("PackedSwitchFfn: gate_up_proj must have 2 * hidden_dims rows")
+        self.gate_up_proj, self.down_proj = gate_up_proj, down_proj
+        self.activation = activation
+        self.hidden_dims = gate_up_proj.output_dims // 2
+        self._desc = C.PackedSwitchGlu(gate_up_proj.descriptor(), down_proj.descriptor(),
+                                       C.ACT_GEGLU if activation == "geglu" else C.ACT_SWIGLU)
+
+    @classmethod
+    def from_dense(cls, gate_up_w, down_w, group_size=64, bits=4, activation="geglu"):
+        """Quantise dense expert weights (try_into_quantized, switch.rs:323-335)."""
+        q = QuantizedSwitchLinear.try_from_switch_linear
+        return cls(q(gate_up_w, group_size, bits), q(down_w, group_size, bits), activation)
+
+    def descriptor(self) -> C.PackedSwitchGlu:
+        return self._desc
+
+    def _prep(self, x, indices):
+        d = self.gate_up_proj.input_dims
+        x2 = x.reshape(-1, d).contiguous()
+        K = indices.shape[-1]
+        idx = indices.reshape(-1, K).to(torch.int32).contiguous()
+        if idx.shape[0] != x2.shape[0]:
+            raise MlxrMoeError("PackedSwitchFfn: indices must be [..., T, K] over x [..., T, d]")
+        return x2, idx, K
+
+    def workspace_size(self, T: int, K: int) -> int:
+        return C.lib().mlxr_moe_packed_switch_glu_workspace_size(ctypes.byref(self._desc), T, K)
+
+    def forward(self, x, indices):
+        """Per-expert outputs [..., K, d] bf16 (switch.rs:290-315)."""
+        x2, idx, K = self._prep(x, indices)
+        T, d = x2.shape
+        y = torch.empty((T, K, d), dtype=torch.bfloat16, device=x.device)
+        ws = ops.workspace(self.workspace_size(T, K), x.device)
+        C.check(C.lib().mlxr_moe_packed_switch_glu_experts(
+            ctypes.byref(self._desc), _ptr(x2), T, _ptr(idx), K, _ptr(y), _ptr(ws), ws.numel(),
+            ops._stream(x)))
+        self.last_workspace = ws
+        return y.reshape(tuple(indices.shape) + (d,))
+
+    def forward_with_combine(self, x, indices, weights, out=None, workspace=None):
+        """sum_k weights * expert_k(x) (switch.rs:316-335): f32 weights give
+        an f32 [..., d], bf16 weights (gemma4's router) a bf16 one."""
+        x2, idx, K = self._prep(x, indices)
+        T, d = x2.shape
+        bf16 = weights.dtype == torch.bfloat16
+        w = weights.reshape(-1, K).contiguous()
+        if not bf16:
+            w = w.to(torch.float32)
+        odt = torch.bfloat16 if bf16 else torch.float32
+        if out is None:
+            out = torch.empty((T, d), dtype=odt, device=x.device)
+        if workspace is None:
+            workspace = ops.workspace(self.workspace_size(T, K), x.device)
+        C.check(C.lib().mlxr_moe_packed_switch_glu_forward(
+            ctypes.byref(self._desc), _ptr(x2), T, _ptr(idx), _ptr(w),
+            C.BFLOAT16 if bf16 else C.FLOAT32, K, _ptr(out), _ptr(workspace), workspace.numel(),
+            ops._stream(x)))
+        self.last_workspace = workspace
+        return out.reshape(tuple(x.shape[:-1]) + (d,))
+
+    __call__ = forward_with_combine
+
+
+class GemmaRouter:
+    """gemma4's Router (gemma4/text/text.rs:568-665): rms_norm(x, scale *
+    root_size) -> proj (a bf16 Linear [E, d], or a QuantizedLinear) -> top-K
+    of the bf16 scores -> softmax of the K scores * per_expert_scale; bf16
+    throughout."""
+
+    def __init__(self, proj, scale, per_expert_scale, top_k: int, eps: float = 1e-6):
+        self.quantised = isinstance(proj, QuantizedLinear)
+        if self.quantised:
+            self.proj = proj
+            E, d = proj.output_dims, proj.input_dims
+        else:
+            self.proj = proj.to(torch.bfloat16).contiguous()
+            E, d = self.proj.shape
+        self.top_k, self.eps, self.num_experts, self.hidden_size = top_k, eps, E, d
+        # scale * root_size in scale's dtype, once (text.rs:626-637)
+        scale = scale.to(torch.bfloat16)
+        root = torch.tensor(d ** -0.5, dtype=torch.float32).to(torch.bfloat16)
+        self.norm_weight = (scale * root.to(scale.device)).contiguous()
+        self.per_expert_scale = per_expert_scale.to(torch.bfloat16).contiguous()
+        z = C.QLinear()
+        self._desc = C.GemmaRouter(
+            d, E, top_k, eps, self.norm_weight.data_ptr(),
+            None if self.quantised else self.proj.data_ptr(),
+            self.proj.descriptor() if self.quantised else z, self.per_expert_scale.data_ptr())
+
+    def descriptor(self) -> C.GemmaRouter:
+        return self._desc
+
+    def workspace_size(self, T: int) -> int:
+        return C.lib().mlxr_moe_gemma_router_workspace_size(ctypes.byref(self._desc), T)
+
+    def forward(self, x, idx=None, weights=None, workspace=None):
+        """x bf16 [..., d] -> (indices int32 [..., K], weights bf16 [..., K])."""
+        d = x.shape[-1]
+        x2 = x.reshape(-1, d).contiguous()
+        T, K = x2.shape[0], self.top_k
+        if idx is None:
+            idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
+        if weights is None:
+            weights = torch.empty((T, K), dtype=torch.bfloat16, device=x.device)
+        if workspace is None:
+            workspace = ops.workspace(self.workspace_size(T), x.device)
+        C.check(C.lib().mlxr_moe_gemma_router_forward(
+            ctypes.byref(self._desc), _ptr(x2), T, _ptr(idx), _ptr(weights), _ptr(workspace),
+            workspace.numel(), ops._stream(x)))
+        lead = tuple(x.shape[:-1])
+        return idx.reshape(lead + (K,)), weights.reshape(lead + (K,))
+
+    __call__ = forward
+
+
+class GemmaMoe:
+    """The routed half of a gemma4 MoE layer (text.rs:901-917): router(h)
+    and Experts(h2, indices, weights) = PackedSwitchFfn<Geglu>::
+    forward_with_combine.  bf16 in and out.  (The layer's norms and the
+    dense MLP branch around it are outside this path; here the experts see
+    the router's input.)"""
+
+    out_dtype = torch.bfloat16
+
+    def __init__(self, router: GemmaRouter, experts: PackedSwitchFfn):
+        self.router, self.experts = router, experts
+        self.last_indices = self.last_weights = self.last_workspace = None
+        self._ws = None
+
+    def workspace_size(self, T: int) -> int:
+        a = self.router.workspace_size(T)
+        return ((a + 255) // 256) * 256 + self.experts.workspace_size(T, self.router.top_k)
+
+    def forward(self, x, out=None, workspace=None, keep_routing=True):
+        d = x.shape[-1]
+        x2 = x.reshape(-1, d).contiguous()
+        T, K = x2.shape[0], self.router.top_k
+        if workspace is None:
+            need = self.workspace_size(T)
+            if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
+                self._ws = ops.workspace(need, x.device)
+            workspace = self._ws
+        ra = ((self.router.workspace_size(T) + 255) // 256) * 256
+        key = (T, x.device)
+        if getattr(self, "_route_key", None) != key:
+            self._route = (torch.empty((T, K), dtype=torch.int32, device=x.device),
+                           torch.empty((T, K), dtype=torch.bfloat16, device=x.device))
+            self._route_key = key
+        idx, w = self._route
+        self.router.forward(x2, idx, w, workspace[:ra])
+        o = self.experts.forward_with_combine(x2, idx, w, out=out, workspace=workspace[ra:])
+        self.last_indices = idx if keep_routing else None
+        self.last_weights = w if keep_routing else None
+        self.last_workspace = workspace[ra:]
+        return o.reshape(tuple(x.shape[:-1]) + (d,))
+
+    __call__ = forward
+
+
 class SwigluMlp:
     """down(silu(gate(x)) * up(x)) with QuantizedLinear projections."""
 

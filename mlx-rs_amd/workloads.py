@@ -36,7 +36,10 @@ class MoEConfig:
     zipf_alpha: float | None = None   # routing skew via per-expert logit bias
     tokens: tuple = field(default_factory=tuple)
     seed: int = 0
-    router_bits: int = 0   # 0: f32 router; 4/8: QuantizedLinear router (bf16 block)
+    router_bits: int = 0   # 0: f32 router; 4/8: QuantizedLinear router (bf16 block);
+                           # 16: bf16 Linear router (gemma4)
+    layout: str = "split"  # "split": Qwen35MoeBlock; "gemma": gemma4 router +
+                           # PackedSwitchFfn<Geglu> (GemmaMoe)
 
 
 CONFIGS = {
@@ -51,6 +54,10 @@ CONFIGS = {
                     zipf_alpha=1.1, tokens=(32, 512)),
     "c6": MoEConfig("c6_qwen3_6_35b_a3b_q8router", d=2048, E=256, K=8, f=512, fs=512,
                     router_bits=8, tokens=(1, 64, 2048)),
+    # gemma4's layout at the c2 shape: RMSNorm router (bf16 Linear, per-expert
+    # scales) and packed gate_up [E, 2f, d] experts with GeGLU
+    "c7": MoEConfig("c7_gemma4_packed_geglu", d=2048, E=128, K=8, f=768, router_bits=16,
+                    layout="gemma", tokens=(1, 64, 2048)),
 }
 
 
@@ -102,7 +109,13 @@ class BlockWeights:
     shared_expert: nn.SwigluMlp | None
     shared_gate_w: torch.Tensor | nn.QuantizedLinear | None
 
-    def block(self) -> nn.Qwen35MoeBlock:
+    gemma: object = None   # (scale, per_expert_scale) of the gemma4 router
+
+    def block(self):
+        if self.cfg.layout == "gemma":
+            scale, pes = self.gemma
+            router = nn.GemmaRouter(self.gate_w, scale, pes, self.cfg.K)
+            return nn.GemmaMoe(router, self.switch_mlp)
         return nn.Qwen35MoeBlock(self.gate_w, self.switch_mlp, self.cfg.K, self.shared_expert,
                                  self.shared_gate_w, self.gate_b)
 
@@ -116,12 +129,22 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
     def qrouter(w):
         return nn.QuantizedLinear.try_from_linear(w.to(torch.bfloat16), 64, cfg.router_bits)
 
-    if cfg.router_bits:
+    if cfg.router_bits in (4, 8):
         gate_w = qrouter(gate_w)
 
     def qbank(shape, stream):
         w = _normal(shape, 0.02, device, s, stream).to(torch.bfloat16)
         return nn.QuantizedSwitchLinear.try_from_switch_linear(w, cfg.group_size, cfg.bits)
+
+    if cfg.layout == "gemma":
+        # scores ~ N(0, 1): the normed input has rms d^-1/2 (scale 1 * root_size)
+        proj = _normal((cfg.E, cfg.d), 1.0, device, s, 2).to(torch.bfloat16)
+        scale = torch.ones(cfg.d, device=device, dtype=torch.bfloat16)
+        pes = (0.5 + torch.rand(cfg.E, generator=_gen(device, s, 13), device=device)).to(
+            torch.bfloat16)
+        mlp = nn.PackedSwitchFfn(qbank((cfg.E, 2 * cfg.f, cfg.d), 3),
+                                 qbank((cfg.E, cfg.d, cfg.f), 5), "geglu")
+        return BlockWeights(cfg, proj, None, mlp, None, None, (scale, pes))
 
     mlp = nn.SplitSwitchFfn(qbank((cfg.E, cfg.f, cfg.d), 3), qbank((cfg.E, cfg.f, cfg.d), 4),
                             qbank((cfg.E, cfg.d, cfg.f), 5))
@@ -133,7 +156,7 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
         shared = nn.SwigluMlp(qlin((cfg.fs, cfg.d), 8), qlin((cfg.fs, cfg.d), 9),
                               qlin((cfg.d, cfg.fs), 10))
         sgw = _normal((1, cfg.d), 0.02, device, s, 12)
-        if cfg.router_bits:
+        if cfg.router_bits in (4, 8):
             sgw = qrouter(sgw)
     return BlockWeights(cfg, gate_w, gate_b, mlp, shared, sgw)
 
@@ -145,7 +168,8 @@ def algorithmic_bytes(cfg: MoEConfig, T: int, distinct_experts: int) -> int:
     per 64), x in, the output (f32, bf16 with a quantised router), and the
     routing (idx + weight)."""
     per_w = cfg.bits / 8 + 4 / cfg.group_size
-    per_r = cfg.router_bits / 8 + 4 / 64 if cfg.router_bits else 4
+    per_r = (2 if cfg.router_bits == 16 else
+             cfg.router_bits / 8 + 4 / 64 if cfg.router_bits else 4)
     b = distinct_experts * 3 * cfg.f * cfg.d * per_w + cfg.E * cfg.d * per_r
     if cfg.fs:
         b += 3 * cfg.fs * cfg.d * per_w + cfg.d * per_r

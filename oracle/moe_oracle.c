@@ -474,6 +474,26 @@ void orc_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
         swiglu1(orc_bf16_to_f32(g[i]), orc_bf16_to_f32(u[i])));
 }
 
+/* geglu (activations.rs:223-259): gelu_approximate_in_dtype(g) * u, every
+ * op in bf16 with the constants cast to bf16 first:
+ * 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))). */
+static inline float bfr(float v) { return orc_bf16_to_f32(orc_f32_to_bf16(v)); }
+static inline float geglu1(float g, float u) {
+  const float k = bfr(0.044715f), c = bfr(0.7978845608028654f);
+  const float x3 = bfr(bfr(g * g) * g);
+  const float inner = bfr(g + bfr(k * x3));
+  const float t = bfr(tanhf(bfr(c * inner)));
+  const float gl = bfr(bfr(0.5f * g) * bfr(1.0f + t));
+  return gl * u;
+}
+
+void orc_geglu(const uint16_t* g, const uint16_t* u, int64_t n,
+               uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = orc_f32_to_bf16(
+        geglu1(orc_bf16_to_f32(g[i]), orc_bf16_to_f32(u[i])));
+}
+
 /* ------------------------------------------------------------- combine */
 /* combine_with_weights (switch.rs:223-234): (w * y) rounded to f32, then
  * summed over k in order.  Shared branch (moe.rs:117-120,145):
@@ -525,6 +545,155 @@ void orc_combine_bf16(const uint16_t* y, const float* w, int64_t T, int64_t K,
       out[t * d + n] = orc_f32_to_bf16(r);
     }
   }
+}
+
+/* ----------------------------------------------------- PackedSwitchFfn */
+/* PackedSwitchFfn::forward_with_combine (switch.rs:290-335): per (t, k),
+ * gate_up = gather_qmm over all 2H rows of expert idx, split_sections at H
+ * (gate first), the activation (GeGLU for gemma4's GemmaSwitchGlu, or
+ * SwiGLU), the down gather_qmm, then combine_with_weights: f32 weights give
+ * an f32 out (orc_combine), bf16 weights a bf16 out (orc_combine_bf16). */
+int orc_packed_switch_glu(const uint16_t* x, int64_t T, int64_t d, int64_t H,
+                          int64_t E, const uint32_t* gu_w,
+                          const uint16_t* gu_s, const uint16_t* gu_b,
+                          const uint32_t* dn_w, const uint16_t* dn_s,
+                          const uint16_t* dn_b, int bits, int act,
+                          const int32_t* idx, const float* w, int w_bf16,
+                          int64_t K, int tiled, void* out, uint16_t* y_out,
+                          int nthreads) {
+  if (!valid_quant(64, bits) || d % 64 || H % 64 || (act != 0 && act != 1))
+    return -1;
+  for (int64_t i = 0; i < T * K; ++i)
+    if (idx[i] < 0 || idx[i] >= E) return -1;
+  if (nthreads <= 0) nthreads = 1;
+  orc_qlinear gu = {gu_w, gu_s, gu_b}, dn = {dn_w, dn_s, dn_b};
+  uint16_t* y = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * K * d));
+#pragma omp parallel num_threads(nthreads)
+  {
+    float* xf = (float*)malloc(sizeof(float) * (size_t)d);
+    float* af = (float*)malloc(sizeof(float) * (size_t)H);
+    uint16_t* gub = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(2 * H));
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t tk = 0; tk < T * K; ++tk) {
+      const int64_t t = tk / K;
+      for (int64_t j = 0; j < d; ++j) xf[j] = orc_bf16_to_f32(x[t * d + j]);
+      qmv(xf, &gu, idx[tk], 2 * H, d, 64, bits, tiled, gub);
+      for (int64_t n = 0; n < H; ++n) {
+        const float g = orc_bf16_to_f32(gub[n]), u = orc_bf16_to_f32(gub[H + n]);
+        af[n] = orc_bf16_to_f32(orc_f32_to_bf16(act ? geglu1(g, u) : swiglu1(g, u)));
+      }
+      qmv(af, &dn, idx[tk], d, H, 64, bits, tiled, y + tk * d);
+    }
+    free(xf);
+    free(af);
+    free(gub);
+  }
+  if (out) {
+    if (w_bf16)
+      orc_combine_bf16(y, w, T, K, d, NULL, NULL, (uint16_t*)out);
+    else
+      orc_combine(y, w, T, K, d, NULL, NULL, (float*)out);
+  }
+  if (y_out) memcpy(y_out, y, sizeof(uint16_t) * (size_t)(T * K * d));
+  free(y);
+  return 0;
+}
+
+/* ------------------------------------------------------- gemma4 router */
+/* fast::rms_norm (gemma4 Router::forward, text.rs:640): out_j = bf16(w_j *
+ * bf16(x_j * r)), r = 1 / sqrt(sum_j x_j^2 / d + eps), the sum of squares
+ * in the router's lane order (lane l: fmaf over j = 4l + 256i + c; then
+ * the butterfly). */
+void orc_rms_norm(const uint16_t* x, int64_t T, int64_t d, const uint16_t* w,
+                  float eps, uint16_t* out) {
+  for (int64_t t = 0; t < T; ++t) {
+    const uint16_t* xr = x + t * d;
+    float lane[64];
+    for (int l = 0; l < 64; ++l) {
+      float acc = 0.0f;
+      for (int64_t i = 0; 4 * l + 256 * i < d; ++i)
+        for (int c = 0; c < 4; ++c) {
+          const int64_t j = 4 * l + 256 * i + c;
+          if (j < d) {
+            const float v = orc_bf16_to_f32(xr[j]);
+            acc = fmaf(v, v, acc);
+          }
+        }
+      lane[l] = acc;
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+      float nxt[64];
+      for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ m];
+      memcpy(lane, nxt, sizeof(lane));
+    }
+    const float r = 1.0f / sqrtf(lane[0] / (float)d + eps);
+    for (int64_t j = 0; j < d; ++j)
+      out[t * d + j] = orc_f32_to_bf16(
+          orc_bf16_to_f32(w[j]) * bfr(orc_bf16_to_f32(xr[j]) * r));
+  }
+}
+
+/* gemma4 Router::forward (text.rs:621-665): normed = rms_norm(x); scores =
+ * bf16(normed . W_e) (a bf16 Linear, proj_bf16 [E, d], or a QuantizedLinear
+ * (proj_q, bits, group 64) -- orc_router_logits' lane order); top-K on the
+ * scores (descending, ties to the lower id); router_post
+ * (activations.rs:309-331): softmax of the K selected scores in bf16
+ * (d_k = bf16(s_k - m), e_k = bf16(exp(d_k)) with exp in double,
+ * S = bf16(sum_k e_k in f32, k in order), p_k = bf16(e_k / S)) times
+ * per_expert_scale[id_k], rounded to bf16.  weights_out [T, K] bf16. */
+int orc_gemma_router(const uint16_t* x, int64_t T, int64_t d, int64_t E,
+                     int64_t K, const uint16_t* norm_w, float eps,
+                     const uint16_t* proj_bf16, const orc_qlinear* proj_q,
+                     int bits, const uint16_t* pes, int32_t* idx,
+                     uint16_t* weights_out) {
+  if (K < 1 || K > E || (!proj_bf16 && !proj_q)) return -1;
+  if (proj_q && ((bits != 4 && bits != 8) || d % 64)) return -1;
+  uint16_t* normed = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * d));
+  float* wrow = (float*)malloc(sizeof(float) * (size_t)d);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)E);
+  char* taken = (char*)malloc((size_t)E);
+  orc_rms_norm(x, T, d, norm_w, eps, normed);
+  for (int64_t t = 0; t < T; ++t) {
+    for (int64_t e = 0; e < E; ++e) {
+      if (proj_q) {
+        sc[e] = lane_dot_q(normed + t * d, proj_q->w + e * (d * bits / 32),
+                           proj_q->scales + e * (d / 64),
+                           proj_q->biases + e * (d / 64), d, bits);
+      } else {
+        for (int64_t j = 0; j < d; ++j) wrow[j] = orc_bf16_to_f32(proj_bf16[e * d + j]);
+        sc[e] = bfr(lane_dot(normed + t * d, wrow, d));
+      }
+    }
+    memset(taken, 0, (size_t)E);
+    float sel[64];
+    for (int64_t k = 0; k < K; ++k) {
+      int64_t best = -1;
+      for (int64_t e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        if (best < 0 || sc[e] > sc[best]) best = e;
+      }
+      taken[best] = 1;
+      idx[t * K + k] = (int32_t)best;
+      sel[k] = sc[best];
+    }
+    const float m = sel[0];
+    float ek[64], S = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      ek[k] = bfr((float)exp((double)bfr(sel[k] - m)));
+      S += ek[k];
+    }
+    S = bfr(S);
+    for (int64_t k = 0; k < K; ++k) {
+      const float p = bfr(ek[k] / S);
+      weights_out[t * K + k] =
+          orc_f32_to_bf16(p * orc_bf16_to_f32(pes[idx[t * K + k]]));
+    }
+  }
+  free(normed);
+  free(wrow);
+  free(sc);
+  free(taken);
+  return 0;
 }
 
 /* --------------------------------------------------------------- block */

@@ -107,6 +107,14 @@ void orc_combine(const uint16_t* y, const float* w, int64_t T, int64_t K,
                  int64_t d, const uint16_t* shared_y, const float* shared_logit,
                  float* out);
 
+/* act = gelu_approx(g) * u with MLX's per-op bf16 rounding (gemma4). */
+void orc_geglu(const uint16_t* g, const uint16_t* u, int64_t n,
+               uint16_t* out);
+
+/* fast::rms_norm: out bf16 [T, d] = bf16(w * bf16(x * r)). */
+void orc_rms_norm(const uint16_t* x, int64_t T, int64_t d, const uint16_t* w,
+                  float eps, uint16_t* out);
+
 /* out bf16 [T, d]: combine with bf16 routing weights (w holds bf16
  * values), every op rounded to bf16. */
 void orc_combine_bf16(const uint16_t* y, const float* w, int64_t T, int64_t K,
@@ -143,6 +151,28 @@ typedef struct {
   orc_qlinear shared_gate_q;
   int32_t router_bits;
 } orc_block;
+
+/* PackedSwitchFfn::forward_with_combine: gate_up [E, 2H, d] (gate rows
+ * first), down [E, d, H], act 0 = SwiGLU, 1 = GeGLU; w f32 [T, K] holding
+ * f32 (w_bf16 = 0, out f32) or bf16 values (w_bf16 = 1, out bf16 as
+ * uint16).  y_out (optional) receives the per-expert rows bf16 [T*K, d].
+ * Returns 0 or -1. */
+int orc_packed_switch_glu(const uint16_t* x, int64_t T, int64_t d, int64_t H,
+                          int64_t E, const uint32_t* gu_w,
+                          const uint16_t* gu_s, const uint16_t* gu_b,
+                          const uint32_t* dn_w, const uint16_t* dn_s,
+                          const uint16_t* dn_b, int bits, int act,
+                          const int32_t* idx, const float* w, int w_bf16,
+                          int64_t K, int tiled, void* out, uint16_t* y_out,
+                          int nthreads);
+
+/* gemma4 Router::forward: idx [T, K], weights_out bf16 [T, K].  proj_bf16
+ * [E, d] bf16, or proj_q (4/8-bit, group 64) with bits.  Returns 0 or -1. */
+int orc_gemma_router(const uint16_t* x, int64_t T, int64_t d, int64_t E,
+                     int64_t K, const uint16_t* norm_w, float eps,
+                     const uint16_t* proj_bf16, const orc_qlinear* proj_q,
+                     int bits, const uint16_t* pes, int32_t* idx,
+                     uint16_t* weights_out);
 
 /* Qwen35MoeBlock::forward on x bf16 [T, d] -> out [T, d], f32 with an f32
  * router, bf16 (uint16 bits) with a quantised one.  idx_out/w_out

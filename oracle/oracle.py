@@ -203,6 +203,80 @@ def combine_bf16(y, w, shared_y=None, shared_logit=None):
     return out
 
 
+def geglu(g, u):
+    g = np.ascontiguousarray(g, np.uint16)
+    u = np.ascontiguousarray(u, np.uint16)
+    out = np.zeros_like(g)
+    lib().orc_geglu(_p(g), _p(u), c_int64(g.size), _p(out))
+    return out
+
+
+def rms_norm(x, w, eps):
+    x = np.ascontiguousarray(x, np.uint16)
+    T, d = x.shape
+    out = np.zeros_like(x)
+    lib().orc_rms_norm(_p(x), c_int64(T), c_int64(d), _p(np.ascontiguousarray(w, np.uint16)),
+                       c_float(eps), _p(out))
+    return out
+
+
+def gemma_router(x, norm_w, eps, proj, pes, K, bits=0):
+    """gemma4 Router::forward.  proj: bf16 [E, d] (uint16) when bits == 0,
+    else (wq, scales, biases) of a QuantizedLinear.  Returns (idx [T, K],
+    weights bf16 [T, K] as uint16)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    T, d = x.shape
+    keep = []
+    if bits:
+        wq, sc, bi = (np.ascontiguousarray(a, dt) for a, dt in
+                      zip(proj, (np.uint32, np.uint16, np.uint16)))
+        keep += [wq, sc, bi]
+        E = wq.shape[0]
+        ql = _QL(wq.ctypes.data, sc.ctypes.data, bi.ctypes.data)
+        pb, pq = None, ctypes.byref(ql)
+    else:
+        pw = np.ascontiguousarray(proj, np.uint16)
+        keep.append(pw)
+        E = pw.shape[0]
+        pb, pq = _p(pw), None
+    idx = np.zeros((T, K), np.int32)
+    w = np.zeros((T, K), np.uint16)
+    rc = lib().orc_gemma_router(_p(x), c_int64(T), c_int64(d), c_int64(E), c_int64(K),
+                                _p(np.ascontiguousarray(norm_w, np.uint16)), c_float(eps),
+                                pb, pq, c_int(bits), _p(np.ascontiguousarray(pes, np.uint16)),
+                                _p(idx), _p(w))
+    if rc:
+        raise ValueError("orc_gemma_router rejected the arguments")
+    return idx, w
+
+
+def packed_switch_glu(x, gate_up, down, idx, w, act=1, w_bf16=True, tiled=False, nthreads=1,
+                      with_y=False):
+    """PackedSwitchFfn::forward_with_combine.  gate_up = (wq [E, 2H, d*b/32],
+    scales, biases); down likewise [E, d, H]; idx [T, K]; w [T, K] (f32, or
+    bf16 values when w_bf16).  Returns out ([T, d] bf16 as uint16 when
+    w_bf16, else f32) and, with_y, the per-expert rows [T, K, d]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    T, d = x.shape
+    gw, gs, gb = (np.ascontiguousarray(a, dt) for a, dt in zip(gate_up, (np.uint32, np.uint16, np.uint16)))
+    dw, ds, db = (np.ascontiguousarray(a, dt) for a, dt in zip(down, (np.uint32, np.uint16, np.uint16)))
+    E, H2 = gw.shape[0], gw.shape[1]
+    bits = gw.shape[2] * 32 // d
+    idx = np.ascontiguousarray(idx, np.int32)
+    K = idx.shape[1]
+    wf = np.ascontiguousarray(w, np.float32)
+    out = np.zeros((T, d), np.uint16 if w_bf16 else np.float32)
+    y = np.zeros((T, K, d), np.uint16)
+    rc = lib().orc_packed_switch_glu(_p(x), c_int64(T), c_int64(d), c_int64(H2 // 2),
+                                     c_int64(E), _p(gw), _p(gs), _p(gb), _p(dw), _p(ds), _p(db),
+                                     c_int(bits), c_int(act), _p(idx), _p(wf),
+                                     c_int(1 if w_bf16 else 0), c_int64(K),
+                                     c_int(1 if tiled else 0), _p(out), _p(y), c_int(nthreads))
+    if rc:
+        raise ValueError("orc_packed_switch_glu rejected the arguments")
+    return (out, y) if with_y else out
+
+
 class _QL(Structure):
     _fields_ = [("w", c_void_p), ("scales", c_void_p), ("biases", c_void_p)]
 
@@ -272,7 +346,8 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
 
 __all__ = ["build", "lib", "f32_to_bf16", "bf16_to_f32", "quantize", "dequantize",
            "router_logits", "router_topk", "router_logits_q", "router_topk_bf16", "dispatch",
-           "gather_qmm", "swiglu", "combine", "combine_bf16",
+           "gather_qmm", "swiglu", "combine", "combine_bf16", "geglu", "rms_norm", "gemma_router",
+           "packed_switch_glu",
            "block_forward", "POINTER", "c_float", "c_uint16", "c_uint32"]
 
 
@@ -303,14 +378,14 @@ def block_params(bw) -> dict:
              group_size=cfg.group_size,
              router_b=None if bw.gate_b is None else to_np(bw.gate_b),
              gate=q(m.gate_proj), up=q(m.up_proj), down=q(m.down_proj))
-    if cfg.router_bits:
+    if cfg.router_bits in (4, 8):
         p.update(router_q=q(bw.gate_w), router_bits=cfg.router_bits)
     else:
         p.update(router_w=to_np(bw.gate_w))
     if cfg.fs:
         s = bw.shared_expert
         p.update(shared_gate=q(s.gate_proj), shared_up=q(s.up_proj), shared_down=q(s.down_proj))
-        if cfg.router_bits:
+        if cfg.router_bits in (4, 8):
             p.update(shared_gate_q=q(bw.shared_gate_w))
         else:
             p.update(shared_gate_w=to_np(bw.shared_gate_w))

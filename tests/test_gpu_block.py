@@ -29,7 +29,43 @@ def weights(pkg, cfg_name, dev):
     return _WEIGHTS[cfg_name]
 
 
+def check_gemma(pkg, orc, bw, x, nthreads=16):
+    """gemma4 routed MoE (router + PackedSwitchFfn<Geglu>) against the
+    oracle: routing bit-exact (indices and bf16 weights), bf16 out within
+    2e-2 * RMS plus one bf16 step."""
+    block = bw.block()
+    out = block(x)
+    torch.cuda.synchronize()
+    T, cfg = x.shape[0], bw.cfg
+    print(f"  gemma block {cfg.name} T={T}", flush=True)
+    r = block.router
+    ridx, rw = orc.gemma_router(orc.to_np(x), orc.to_np(r.norm_weight), r.eps, orc.to_np(r.proj),
+                                orc.to_np(r.per_expert_scale), cfg.K)
+    assert np.array_equal(block.last_indices.cpu().numpy(), ridx), "routing indices differ"
+    assert np.array_equal(orc.to_np(block.last_weights), rw)
+    m = bw.switch_mlp
+
+    def q(lin):
+        return (orc.to_np(lin.weight).reshape(lin.weight.shape[0], lin.weight.shape[1], -1),
+                orc.to_np(lin.scales), orc.to_np(lin.biases))
+    tiled = pkg.ops.gather_qmm_tiled(T * cfg.K, cfg.E)
+    ref = orc.packed_switch_glu(orc.to_np(x), q(m.gate_up_proj), q(m.down_proj), ridx,
+                                orc.bf16_to_f32(rw), act=1, w_bf16=True, tiled=tiled,
+                                nthreads=nthreads)
+    got = orc.bf16_to_f32(orc.to_np(out)).astype(np.float64)
+    ref = orc.bf16_to_f32(ref).astype(np.float64)
+    rms = np.sqrt(np.mean(ref ** 2))
+    diff = np.abs(got - ref)
+    print(f"  max|err| {diff.max():.3e}  rms {rms:.3e}", flush=True)
+    a = np.abs(ref)
+    ulp = np.where(a > 0, 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - 7), 0.0)
+    assert np.all(diff <= 2e-2 * rms + ulp)
+    assert pkg.ops.workspace_status(block.last_workspace) == 0
+
+
 def check_block(pkg, orc, bw, x, nthreads=16):
+    if bw.cfg.layout == "gemma":
+        return check_gemma(pkg, orc, bw, x, nthreads)
     block = bw.block()
     out = block(x)
     torch.cuda.synchronize()
@@ -95,7 +131,7 @@ def test_c1_golden_fixture(pkg, orc, dev):
 
 @pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 8), ("c2", 64), ("c5", 32),
                                    ("c4", 1), ("c4", 64), ("c3", 512), ("c6", 1), ("c6", 64),
-                                   ("c6", 512)])
+                                   ("c6", 512), ("c7", 1), ("c7", 64), ("c7", 512)])
 def test_block_parity(pkg, orc, dev, cfg, T):
     bw = weights(pkg, cfg, dev)
     x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)

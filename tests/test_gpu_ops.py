@@ -94,6 +94,54 @@ def test_router_topk_quantized_bit_exact(pkg, orc, dev, T, d, E, K, bits):
     assert np.array_equal(wts.cpu().numpy(), rw)
 
 
+@pytest.mark.parametrize("T,d,E,K,bits", [(1, 2048, 128, 8, 16), (40, 2048, 128, 8, 16),
+                                          (300, 2048, 128, 8, 16), (33, 2048, 256, 8, 8),
+                                          (7, 512, 8, 2, 16)])
+def test_gemma_router_bit_exact(pkg, orc, dev, T, d, E, K, bits):
+    """gemma4 Router::forward (text.rs:621-665): RMSNorm, bf16 (or 8-bit)
+    projection, top-K of the bf16 scores, softmax of the K scores times
+    per_expert_scale -- indices and bf16 weights bit for bit."""
+    rng = np.random.default_rng(T + E + bits)
+    print(f"  gemma_router T={T} d={d} E={E} K={K} bits={bits}", flush=True)
+    x = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev)
+    projf = _bf16(orc, rng.standard_normal((E, d)).astype(np.float32), dev)
+    proj = pkg.nn.QuantizedLinear.try_from_linear(projf, 64, 8) if bits == 8 else projf
+    scale = _bf16(orc, (rng.random(d) + 0.5).astype(np.float32), dev)
+    pes = _bf16(orc, (rng.random(E) + 0.5).astype(np.float32), dev)
+    r = pkg.nn.GemmaRouter(proj, scale, pes, K)
+    idx, w = r(x)
+    oproj = ((_np(orc, proj.weight).reshape(E, -1), _np(orc, proj.scales).reshape(E, -1),
+              _np(orc, proj.biases).reshape(E, -1)) if bits == 8 else _np(orc, projf))
+    ridx, rw = orc.gemma_router(_np(orc, x), _np(orc, r.norm_weight), r.eps, oproj,
+                                _np(orc, pes), K, bits=8 if bits == 8 else 0)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(_np(orc, w), rw)
+
+
+@pytest.mark.parametrize("T", [24, 512])
+def test_packed_swiglu_equals_split(pkg, dev, T):
+    """PackedSwitchFfn with gate_up = [gate; up] along the output rows and
+    SwiGLU runs the same kernels as SplitSwitchFfn with the separate
+    tensors: identical bits, per-expert rows and combine, on the decode
+    (T=24) and prefill (T=512) paths."""
+    W = pkg.workloads
+    cfg = W.CONFIGS["c2"]
+    bw = W.make_weights(cfg, dev)
+    m = bw.switch_mlp
+    cat = lambda a, b: torch.cat([a, b], dim=1).contiguous()  # noqa: E731
+    gu = pkg.nn.QuantizedSwitchLinear(cat(m.gate_proj.weight, m.up_proj.weight),
+                                      cat(m.gate_proj.scales, m.up_proj.scales),
+                                      cat(m.gate_proj.biases, m.up_proj.biases), 64, cfg.bits)
+    packed = pkg.nn.PackedSwitchFfn(gu, m.down_proj, "swiglu")
+    g = torch.Generator().manual_seed(T)
+    x = W.make_x(cfg, T, dev, seed=T)
+    idx = torch.stack([torch.randperm(cfg.E, generator=g)[:cfg.K] for _ in range(T)]).int().to(dev)
+    w = torch.rand((T, cfg.K), generator=g).to(dev)
+    print(f"  packed vs split T={T}", flush=True)
+    assert torch.equal(packed.forward(x, idx), m.forward(x, idx))
+    assert torch.equal(packed.forward_with_combine(x, idx, w), m.forward_with_combine(x, idx, w))
+
+
 def test_router_ties_pick_lower_ids(pkg, dev):
     x = torch.zeros((4, 512), dtype=torch.bfloat16, device=dev)
     w = torch.randn((64, 512), device=dev)

@@ -440,3 +440,105 @@ def test_combine_linear_in_weights(orc):
     lhs = orc.combine(y, w1 + w2)
     rhs = orc.combine(y, w1) + orc.combine(y, w2)
     assert np.allclose(lhs, rhs, rtol=1e-5, atol=1e-6)
+
+
+# ----------------------------------------------- gemma4: GeGLU, router
+def test_geglu_closed_forms_and_fp64_bound(orc):
+    """gelu_approx(g) * u (activations.rs:223-259): large positive g pass
+    through (tanh -> 1), large negative g give 0 (tanh -> -1), g = 0 gives
+    0; elsewhere within a few bf16 roundings of the fp64 tanh-GELU."""
+    bf = lambda a: orc.f32_to_bf16(np.asarray(a, np.float32))  # noqa: E731
+    f = lambda h: orc.bf16_to_f32(h).astype(np.float64)  # noqa: E731
+    big = np.array([4.0, 5.5, 8.0, 17.0, 96.0], np.float32)
+    assert np.array_equal(orc.geglu(bf(big), bf(np.ones_like(big))), bf(big))
+    neg = np.array([-6.0, -9.0, -40.0], np.float32)
+    assert np.all(f(orc.geglu(bf(neg), bf(np.ones_like(neg)))) == 0.0)
+    assert f(orc.geglu(bf([0.0]), bf([3.0])))[0] == 0.0
+    rng = np.random.default_rng(50)
+    g = bf(rng.standard_normal(4096) * 2)
+    u = bf(rng.standard_normal(4096))
+    gd, ud = f(g), f(u)
+    exact = 0.5 * gd * (1 + np.tanh(np.sqrt(2 / np.pi) * (gd + 0.044715 * gd ** 3))) * ud
+    got = f(orc.geglu(g, u))
+    assert np.all(np.abs(got - exact) <= 2.0 ** -5 * (np.abs(gd) + 0.05) * np.abs(ud))
+
+
+def test_rms_norm_exact_and_fp64_bound(orc):
+    """fast::rms_norm: a constant row 2 with eps 0 normalises to 1, so the
+    output is the weight exactly; elsewhere within two bf16 roundings of
+    w * x / sqrt(mean(x^2) + eps)."""
+    rng = np.random.default_rng(51)
+    d = 512
+    w = orc.f32_to_bf16((rng.random(d) + 0.5).astype(np.float32))
+    x = orc.f32_to_bf16(np.full((1, d), 2.0, np.float32))
+    assert np.array_equal(orc.rms_norm(x, w, 0.0)[0], w)
+    x = orc.f32_to_bf16(rng.standard_normal((7, d)).astype(np.float32))
+    got = orc.bf16_to_f32(orc.rms_norm(x, w, 1e-6)).astype(np.float64)
+    xd = orc.bf16_to_f32(x).astype(np.float64)
+    exact = orc.bf16_to_f32(w).astype(np.float64) * xd / np.sqrt(
+        (xd ** 2).mean(1, keepdims=True) + 1e-6)
+    assert np.all(np.abs(got - exact) <= 2.0 ** -7 * np.abs(exact) + 1e-30)
+
+
+@pytest.mark.parametrize("bits", [0, 8])
+def test_gemma_router(orc, bits):
+    """gemma4 Router::forward (text.rs:621-665): top-K = full sort of the
+    bf16 scores (ties to the lower id); weights = bf16 softmax of the K
+    selected scores times per_expert_scale: within bf16 roundings of the
+    fp64 softmax, and exactly linear in per_expert_scale (x2 is exact)."""
+    rng = np.random.default_rng(52 + bits)
+    T, d, E, K = 24, 512, 16, 4
+    x = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    nw = orc.f32_to_bf16(np.full(d, d ** -0.5, np.float32))
+    projf = orc.f32_to_bf16(rng.standard_normal((E, d)).astype(np.float32))
+    proj = orc.quantize(projf, 64, 8) if bits else projf
+    pes = orc.f32_to_bf16((rng.random(E) + 0.5).astype(np.float32))
+    idx, w = orc.gemma_router(x, nw, 1e-6, proj, pes, K, bits=bits)
+    normed = orc.rms_norm(x, nw, 1e-6)
+    if bits:
+        sc = orc.router_logits_q(normed, *proj, 8)
+    else:
+        sc = orc.bf16_to_f32(orc.f32_to_bf16(orc.router_logits(normed, orc.bf16_to_f32(projf))))
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-float(sc[t, e]), e))
+        assert list(idx[t]) == order[:K]
+    s = np.take_along_axis(sc, idx, 1).astype(np.float64)
+    p = np.exp(s - s.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    exact = p * orc.bf16_to_f32(pes)[idx]
+    got = orc.bf16_to_f32(w).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= 2.0 ** -6 * exact + 1e-6)
+    _, w2 = orc.gemma_router(x, nw, 1e-6, proj, orc.f32_to_bf16(2 * orc.bf16_to_f32(pes)), K,
+                             bits=bits)
+    assert np.array_equal(orc.bf16_to_f32(w2), 2 * orc.bf16_to_f32(w))
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_packed_switch_glu_equals_split_composition(orc, act):
+    """PackedSwitchFfn (switch.rs:290-335): gate_up [E, 2H, d] is gate and up
+    stacked along the output rows; the forward equals gather_qmm of each
+    half, the activation (SwiGLU / GeGLU), the down gather_qmm and the
+    combine, bit for bit, with f32 or bf16 routing weights."""
+    rng = np.random.default_rng(53 + act)
+    T, d, H, E, K = 12, 512, 256, 8, 2
+
+    def q(shape):
+        return orc.quantize(orc.f32_to_bf16((rng.standard_normal(shape) * 0.02).astype(np.float32)),
+                            64, 4)
+    gate, up, down = q((E, H, d)), q((E, H, d)), q((E, d, H))
+    gu = tuple(np.concatenate([a, b], axis=1) for a, b in zip(gate, up))
+    x = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wf = rng.random((T, K)).astype(np.float32)
+    wb = orc.bf16_to_f32(orc.f32_to_bf16(wf))
+    flat = idx.reshape(-1)
+    xs = x[np.repeat(np.arange(T), K)][:, None, :]
+    g = orc.gather_qmm(xs, *gate, flat)
+    u = orc.gather_qmm(xs, *up, flat)
+    a = orc.geglu(g, u) if act else orc.swiglu(g, u)
+    y = orc.gather_qmm(a, *down, flat).reshape(T, K, d)
+    out_f, y_got = orc.packed_switch_glu(x, gu, down, idx, wf, act=act, w_bf16=False, with_y=True)
+    assert np.array_equal(y_got, y)
+    assert np.array_equal(out_f, orc.combine(y, wf))
+    out_b = orc.packed_switch_glu(x, gu, down, idx, wb, act=act, w_bf16=True)
+    assert np.array_equal(out_b, orc.combine_bf16(y, wb))
