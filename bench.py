@@ -37,7 +37,7 @@ def parse():
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
                     help="replay one captured HIP graph per step, or launch eagerly")
     ap.add_argument("--sweep", default="c2:1,c2:8,c2:32,c3:512,c3:2048,c3:4096,c4:64,c4:2048,"
-                    "c5:32,c5:512,c6:64,c6:2048",
+                    "c5:32,c5:512,c6:64,c6:2048,c7:64,c7:2048",
                     help="extra cfg:T points timed after the headline ('' for none)")
     ap.add_argument("--sweep-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
