@@ -6,10 +6,12 @@ include/mlxr_moe.h.  This package is the Python view of that ABI:
     ops       gather_qmm / quantize / dequantize / argpartition_axis /
               softmax_axis / router_topk / dispatch / combine
     nn        QuantizedSwitchLinear / QuantizedLinear / SwigluMlp /
-              SplitSwitchFfn / Qwen35MoeBlock
+              SplitSwitchFfn / PackedSwitchFfn / Qwen35MoeBlock /
+              GemmaRouter / GemmaMoe
+    loader    one MoE layer of an mlxr checkpoint (safetensors) into nn
     workloads the benchmark configurations and seeded synthetic weights
 """
-from . import _capi, nn, ops, workloads
+from . import _capi, loader, nn, ops, workloads
 from ._capi import LIB_PATH, MlxrMoeError
 
-__all__ = ["_capi", "nn", "ops", "workloads", "LIB_PATH", "MlxrMoeError"]
+__all__ = ["_capi", "loader", "nn", "ops", "workloads", "LIB_PATH", "MlxrMoeError"]

@@ -180,3 +180,47 @@ def test_switch_glu_forward_matches_composition(pkg, orc, dev):
     ref = orc.combine(ya, w.cpu().numpy())
     rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
     assert np.abs(out.cpu().numpy() - ref).max() <= 2e-2 * rms
+
+
+def test_checkpoint_round_trip_forward(pkg, orc, dev, tmp_path):
+    """A layer written as an mlxr checkpoint (the reference's key names,
+    per-path 8-bit overrides for mlp.gate / mlp.shared_expert_gate) and read
+    back by the loader runs bit-identically to the block it came from, and
+    within tolerance of the oracle."""
+    import json
+    from safetensors.torch import save_file
+    W = pkg.workloads
+    cfg = W.MoEConfig("ckpt", d=512, E=8, K=2, f=256, fs=256, router_bits=8, tokens=(16,))
+    bw = W.make_weights(cfg, dev)
+    p = "model.language_model.layers.5.mlp."
+    t = {}
+
+    def put(name, lin, squeeze=False):
+        w, s, b = lin.weight, lin.scales, lin.biases
+        if squeeze:
+            w, s, b = w[0], s[0], b[0]
+        t[p + name + ".weight"] = w.contiguous().cpu().view(torch.uint32)
+        t[p + name + ".scales"] = s.contiguous().cpu()
+        t[p + name + ".biases"] = b.contiguous().cpu()
+    m, se = bw.switch_mlp, bw.shared_expert
+    put("switch_mlp.gate_proj", m.gate_proj)
+    put("switch_mlp.up_proj", m.up_proj)
+    put("switch_mlp.down_proj", m.down_proj)
+    put("shared_expert.gate_proj", se.gate_proj, True)
+    put("shared_expert.up_proj", se.up_proj, True)
+    put("shared_expert.down_proj", se.down_proj, True)
+    put("gate", bw.gate_w, True)
+    put("shared_expert_gate", bw.shared_gate_w, True)
+    d = tmp_path / "ck"
+    d.mkdir()
+    save_file(t, str(d / "model.safetensors"), metadata={"format": "mlx"})
+    q = {"group_size": 64, "bits": 4, "mode": "affine",
+         "language_model.model.layers.5.mlp.gate": {"group_size": 64, "bits": 8},
+         "language_model.model.layers.5.mlp.shared_expert_gate": {"group_size": 64, "bits": 8}}
+    (d / "config.json").write_text(json.dumps({"quantization": q,
+                                               "text_config": {"num_experts_per_tok": 2}}))
+    loaded = pkg.loader.qwen35_moe_block(d, 5, dev)
+    x = W.make_x(cfg, 40, dev, seed=3)
+    print("  checkpoint round trip T=40", flush=True)
+    assert torch.equal(loaded(x), bw.block()(x))
+    check_block(pkg, orc, bw, x)
