@@ -103,6 +103,29 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
                         void* workspace, size_t workspace_size,
                         mlxr_moe_stream stream);
 
+/* gather_mm as SwitchLinear::apply calls it (crates/mlxr-lm/src/nn/
+ * switch.rs:84-93: gather_mm(x, swap_axes(weight, -1, -2), None, indices,
+ * sorted)): a bf16 [a_batch, M, K]; b bf16 stored [E, N, K] (the
+ * SwitchLinear weight as it is; b_transposed must be 1); rhs_indices uint32
+ * [B]; out bf16 [B, M, N]:
+ *   out[b] = a[ab(b)] @ b[rhs_indices[b]]^T
+ * with ab(b) as xb(b) of gather_qmm, f32 accumulation.  Replaces mlx_gather_mm
+ * as called by gather_mm_device (crates/mlxr/src/ops/arithmetic.rs:
+ * 1577-1613).  SwitchLinear's optional bias is not taken: every SwitchLinear
+ * of the MoE blocks is built without one (crates/mlxr-lm/src/qwen3_5/text/
+ * moe.rs:92-97, crates/mlxr-lm/src/gemma4/text/text.rs:679).  Requires
+ * N % 64 == 0, K % 64 == 0, K <= 4096.  Same workspace as gather_qmm. */
+size_t mlxr_moe_gather_mm_workspace_size(int64_t B, int64_t M,
+                                         int64_t num_experts);
+int mlxr_moe_gather_mm(const void* a, int a_dtype, int64_t a_batch, int64_t M,
+                       int64_t K, const void* b, int b_dtype,
+                       int64_t num_experts, int64_t N, int b_transposed,
+                       const uint32_t* lhs_indices,
+                       const uint32_t* rhs_indices, int64_t B,
+                       int sorted_indices, void* out, int out_dtype,
+                       void* workspace, size_t workspace_size,
+                       mlxr_moe_stream stream);
+
 /* Which numerics a gather_qmm (or a SplitSwitchFfn / shared-expert GEMM) of
  * `rows` flat rows over `num_experts` experts uses (no counterpart in the
  * reference, whose MLX backend makes the same kind of choice inside
@@ -161,7 +184,12 @@ int mlxr_moe_combine(const void* y, const float* w, int64_t T, int64_t K,
 /* One QuantizedSwitchLinear (crates/mlxr-lm/src/nn/switch.rs:115-168) or
  * QuantizedLinear (num_experts = 1; crates/mlxr/src/layers/quantized.rs:
  * 214-379): weight u32 [E, output_dims, input_dims*bits/32], scales and
- * biases bf16 [E, output_dims, input_dims/group_size]. */
+ * biases bf16 [E, output_dims, input_dims/group_size].
+ * bits = 16 describes the unquantised form of the same MaybeQuantized slot
+ * (crates/mlxr/src/quantization.rs:6-147): a dense SwitchLinear
+ * (switch.rs:49-94, applied with gather_mm) or Linear, weight bf16
+ * [E, output_dims, input_dims], scales and biases NULL, group_size
+ * ignored.  The projections of one module share their bits. */
 typedef struct {
   const uint32_t* weight;
   const void* scales;
@@ -175,7 +203,8 @@ typedef struct {
 
 /* mlxr_moe_router_topk with the router as a QuantizedLinear
  * (crates/mlxr/src/layers/quantized.rs:356-373; gate: num_experts 1,
- * output_dims E, input_dims d, group 64, bits 4 or 8): bf16 logits and
+ * output_dims E, input_dims d, group 64, bits 4 or 8) or a bf16 Linear
+ * (bits 16, crates/mlxr/src/layers/linear.rs:91-95): bf16 logits and
  * probabilities, top-K on the probabilities (descending, ties to the lower
  * id), bf16 weights returned as f32 values.  Same workspace as
  * mlxr_moe_router_topk. */
@@ -293,7 +322,11 @@ int mlxr_moe_packed_switch_glu_experts(const mlxr_moe_packed_switch_glu* ffn,
  * bits; weight NULL = no shared branch).  As in the reference with a bf16
  * router the block then computes in bf16: bf16 logits and probabilities
  * (the top-K selects on the probabilities, ties to the lower id), bf16
- * routing weights (returned in topk_w as f32 values) and a bf16 out. */
+ * routing weights (returned in topk_w as f32 values) and a bf16 out.
+ * An unquantised bf16 checkpoint's router is the same slot with bits 16
+ * (bf16 Linears, scales and biases NULL), computed the same way.  Dense
+ * bf16 experts (switch_mlp and shared projections with bits 16) run
+ * gather_mm (SwitchLinear::apply, switch.rs:84-93) with f32 accumulation. */
 typedef struct {
   int64_t hidden_size;
   int64_t num_experts;

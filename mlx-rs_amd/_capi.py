@@ -99,6 +99,12 @@ SIGNATURES = {
         [P, c_int, c_int64, c_int64, c_int64, P, P, P, c_int, c_int64, c_int64, P, P, c_int64,
          c_int, OI, OI, c_char_p, c_int, P, c_int, P, c_size_t, P],
     ),
+    "mlxr_moe_gather_mm_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "mlxr_moe_gather_mm": (
+        c_int,
+        [P, c_int, c_int64, c_int64, c_int64, P, c_int, c_int64, c_int64, c_int, P, P, c_int64,
+         c_int, P, c_int, P, c_size_t, P],
+    ),
     "mlxr_moe_argpartition": (c_int, [P, c_int64, c_int64, c_int, c_int, P, P]),
     "mlxr_moe_softmax": (c_int, [P, c_int64, c_int64, c_int, c_int, P, P]),
     "mlxr_moe_router_workspace_size": (c_size_t, [c_int64, c_int64]),

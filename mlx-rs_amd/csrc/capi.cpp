@@ -82,6 +82,90 @@ void plan_gather(Carve& c, int64_t B, int64_t M, int64_t E) {
   carve_dispatch(c, R, E, nullptr);
 }
 
+// gather_qmm and gather_mm after their own checks: the grouped GEMM over
+// the dispatch of the B*M rows (bits 16: dense bf16 weights).
+int run_gather(const char* op, const void* x, int64_t x_batch, int64_t M,
+               int64_t K, const uint32_t* w, const void* scales,
+               const void* biases, int bits, int64_t E, int64_t N,
+               const uint32_t* lhs_indices, const uint32_t* rhs_indices,
+               int64_t B, void* out, void* workspace, size_t workspace_size,
+               hipStream_t s) {
+  const std::string o(op);
+  if (!rhs_indices) return fail(o + ": rhs_indices are required");
+  if (E <= 0 || E > kMaxExperts)
+    return fail(o + ": num_experts must be in [1, " +
+                std::to_string(kMaxExperts) + "]");
+  if (M <= 0 || K <= 0 || N <= 0 || B < 0 || x_batch <= 0)
+    return fail(o + ": bad shape");
+  if (K % 64 || N % 64)
+    return fail(o + ": K and N must be multiples of 64");
+  if (K > kMaxInputDims)
+    return fail(o + ": K above " + std::to_string(kMaxInputDims) +
+                " is not supported");
+  if (!lhs_indices && B % x_batch)
+    return fail(o + ": x batch " + std::to_string(x_batch) +
+                " does not broadcast against " + std::to_string(B) +
+                " indices");
+  if (B * M > INT32_MAX / 2) return fail(o + ": too many rows");
+  if (bits == 16 && x_batch * M * K * 2 >= ((int64_t)1 << 31))
+    return fail(o + ": x must be under 2 GB");  // the M-tiled kernel's buffer
+  if (N * K * bits / 8 >= ((int64_t)1 << 31))
+    return fail(o + ": one expert's weights must be under 2 GB");
+  if (!x || !w || !out) return fail(o + ": null array");
+  if (!aligned(x, 16) || !aligned(w, 16))
+    return fail(o + ": x and w must be 16-byte aligned");
+  Carve plan(nullptr);
+  plan_gather(plan, B, M, E);
+  Status st = check_workspace(plan, workspace, workspace_size);
+  if (!st.ok) return finish(st);
+  if (B == 0) return 0;
+
+  const int64_t R = B * M;
+  Carve c(workspace);
+  int32_t* status = c.take<int32_t>(1);
+  int32_t* ids = c.take<int32_t>(R);
+  int32_t* xrow = c.take<int32_t>(R);
+  const DispatchBuffers db = carve_dispatch(c, R, E, status);
+  uint16_t* ob = static_cast<uint16_t*>(out);
+  st = from_hip(launch_gather_prep(lhs_indices, rhs_indices, B, M, x_batch, E,
+                                   N, ids, xrow, ob, status, s),
+                (o + " prep").c_str());
+  if (st.ok)
+    st = from_hip(launch_dispatch(ids, R, E, prefill_tile_rows(R, E), db, false, s),
+                  (o + " dispatch").c_str());
+  if (!st.ok) return finish(st);
+  QGemmArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_ld = K;
+  a.x_rows = x_batch * M;
+  a.row_map = xrow;
+  a.row_div = 1;
+  a.x_by_slot = false;
+  a.offsets = db.offsets;
+  a.active = db.active;
+  a.num_active = db.num_active;
+  a.work = db.work;
+  a.num_work = db.num_work;
+  a.tiles = db.tiles;
+  a.num_tiles = db.num_tiles;
+  a.sorted = db.sorted;
+  a.w0 = QWeights{w, static_cast<const uint16_t*>(scales),
+                  static_cast<const uint16_t*>(biases)};
+  a.E = (int32_t)E;
+  a.N = (int32_t)N;
+  a.e_rows = (int32_t)N;
+  a.act = kActSwiglu;
+  a.K = (int32_t)K;
+  a.bits = bits;
+  a.out = ob;
+  a.out_ld = N;
+  a.out_by_flat = true;
+  a.gated = false;
+  return finish(from_hip(launch_qgemm(a, R, dispatch_max_work(R, E),
+                                      nn::use_prefill_path(R, E), s),
+                         op));
+}
+
 }  // namespace
 
 extern "C" {
@@ -159,75 +243,36 @@ int mlxr_moe_gather_qmm(const void* x, int x_dtype, int64_t x_batch,
       out_dtype != MLXR_MOE_BFLOAT16)
     return fail("gather_qmm: x, scales/biases and out must be bf16");
   if (!biases) return fail("gather_qmm: biases are required for affine mode");
-  if (!rhs_indices) return fail("gather_qmm: rhs_indices are required");
-  if (E <= 0 || E > kMaxExperts)
-    return fail("gather_qmm: num_experts must be in [1, " +
-                std::to_string(kMaxExperts) + "]");
-  if (M <= 0 || K <= 0 || N <= 0 || B < 0 || x_batch <= 0)
-    return fail("gather_qmm: bad shape");
-  if (K % 64 || N % 64)
-    return fail("gather_qmm: K and N must be multiples of 64");
-  if (K > kMaxInputDims)
-    return fail("gather_qmm: K above " + std::to_string(kMaxInputDims) +
-                " is not supported");
-  if (!lhs_indices && B % x_batch)
-    return fail("gather_qmm: x batch " + std::to_string(x_batch) +
-                " does not broadcast against " + std::to_string(B) +
-                " indices");
-  if (B * M > INT32_MAX / 2) return fail("gather_qmm: too many rows");
-  if (!x || !w || !scales || !out) return fail("gather_qmm: null array");
-  if (!aligned(x, 16) || !aligned(w, 16))
-    return fail("gather_qmm: x and w must be 16-byte aligned");
-  Carve plan(nullptr);
-  plan_gather(plan, B, M, E);
-  st = check_workspace(plan, workspace, workspace_size);
-  if (!st.ok) return finish(st);
-  if (B == 0) return 0;
+  if (!scales) return fail("gather_qmm: null array");
+  return run_gather("gather_qmm", x, x_batch, M, K, w, scales, biases, b, E, N,
+                    lhs_indices, rhs_indices, B, out, workspace,
+                    workspace_size, as_stream(stream));
+}
 
-  hipStream_t s = as_stream(stream);
-  const int64_t R = B * M;
-  Carve c(workspace);
-  int32_t* status = c.take<int32_t>(1);
-  int32_t* ids = c.take<int32_t>(R);
-  int32_t* xrow = c.take<int32_t>(R);
-  const DispatchBuffers db = carve_dispatch(c, R, E, status);
-  uint16_t* o = static_cast<uint16_t*>(out);
-  st = from_hip(launch_gather_prep(lhs_indices, rhs_indices, B, M, x_batch, E,
-                                   N, ids, xrow, o, status, s),
-                "gather_qmm prep");
-  if (st.ok)
-    st = from_hip(launch_dispatch(ids, R, E, prefill_tile_rows(R, E), db, false, s),
-                  "gather_qmm dispatch");
-  if (!st.ok) return finish(st);
-  QGemmArgs a{};
-  a.x = static_cast<const uint16_t*>(x);
-  a.x_ld = K;
-  a.row_map = xrow;
-  a.row_div = 1;
-  a.x_by_slot = false;
-  a.offsets = db.offsets;
-  a.active = db.active;
-  a.num_active = db.num_active;
-  a.work = db.work;
-  a.num_work = db.num_work;
-  a.tiles = db.tiles;
-  a.num_tiles = db.num_tiles;
-  a.sorted = db.sorted;
-  a.w0 = QWeights{w, static_cast<const uint16_t*>(scales),
-                  static_cast<const uint16_t*>(biases)};
-  a.E = (int32_t)E;
-  a.N = (int32_t)N;
-  a.e_rows = (int32_t)N;
-  a.act = kActSwiglu;
-  a.K = (int32_t)K;
-  a.bits = b;
-  a.out = o;
-  a.out_ld = N;
-  a.out_by_flat = true;
-  a.gated = false;
-  return finish(from_hip(launch_qgemm(a, R, dispatch_max_work(R, E),
-                                      nn::use_prefill_path(R, E), s),
-                         "gather_qmm"));
+size_t mlxr_moe_gather_mm_workspace_size(int64_t B, int64_t M,
+                                         int64_t num_experts) {
+  return mlxr_moe_gather_qmm_workspace_size(B, M, num_experts);
+}
+
+int mlxr_moe_gather_mm(const void* a, int a_dtype, int64_t a_batch, int64_t M,
+                       int64_t K, const void* b, int b_dtype, int64_t E,
+                       int64_t N, int b_transposed,
+                       const uint32_t* lhs_indices,
+                       const uint32_t* rhs_indices, int64_t B,
+                       int sorted_indices, void* out, int out_dtype,
+                       void* workspace, size_t workspace_size,
+                       mlxr_moe_stream stream) {
+  (void)sorted_indices;
+  if (!b_transposed)
+    return fail("gather_mm: only b_transposed=1 (b stored [E, N, K], the "
+                "swap_axes view of SwitchLinear's weight) is supported");
+  if (a_dtype != MLXR_MOE_BFLOAT16 || b_dtype != MLXR_MOE_BFLOAT16 ||
+      out_dtype != MLXR_MOE_BFLOAT16)
+    return fail("gather_mm: a, b and out must be bf16");
+  return run_gather("gather_mm", a, a_batch, M, K,
+                    static_cast<const uint32_t*>(b), nullptr, nullptr, 16, E,
+                    N, lhs_indices, rhs_indices, B, out, workspace,
+                    workspace_size, as_stream(stream));
 }
 
 int mlxr_moe_gather_qmm_tiled(int64_t rows, int64_t num_experts) {
@@ -314,8 +359,10 @@ int mlxr_moe_router_topk_quantized(const void* x, int64_t T,
   if (T < 0 || d <= 0 || E <= 0 || gate->num_experts != 1)
     return fail("router_topk_quantized: bad shape (gate must be one "
                 "[E, d] QuantizedLinear)");
-  if ((gate->bits != 4 && gate->bits != 8) || gate->group_size != 64)
-    return fail("router_topk_quantized: bits must be 4 or 8 and group size 64");
+  const bool dense = gate->bits == 16;  // a bf16 Linear
+  if (!dense && ((gate->bits != 4 && gate->bits != 8) || gate->group_size != 64))
+    return fail("router_topk_quantized: bits must be 4 or 8 with group size "
+                "64, or 16 (a bf16 Linear)");
   if (d % 64) return fail("router_topk_quantized: d must be a multiple of 64");
   if (E > kMaxExperts)
     return fail("router_topk_quantized: at most " +
@@ -323,13 +370,16 @@ int mlxr_moe_router_topk_quantized(const void* x, int64_t T,
   if (K < 1 || K > E || K > 64)
     return fail("router_topk_quantized: k must be in [1, min(E, 64)], got " +
                 std::to_string(K));
-  if (!gate->weight || !gate->scales || !gate->biases ||
+  if (dense && (gate->scales || gate->biases))
+    return fail("router_topk_quantized: a bf16 Linear gate takes no scales "
+                "or biases");
+  if (!gate->weight || (!dense && (!gate->scales || !gate->biases)) ||
       (T && (!x || !topk_idx || !topk_w)))
     return fail("router_topk_quantized: null array");
-  if (!aligned(x, 8) || !aligned(gate->weight, 4) ||
+  if (!aligned(x, 8) || !aligned(gate->weight, dense ? 8 : 4) ||
       !aligned(gate->scales, 2) || !aligned(gate->biases, 2))
     return fail("router_topk_quantized: x must be 8-byte and the weights "
-                "4-byte aligned");
+                "4-byte (bf16: 8-byte) aligned");
   Carve plan(nullptr);
   plan.take<float>(T * E);
   Status st = check_workspace(plan, workspace, workspace_size);
@@ -677,13 +727,14 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
       (block->shared_expert_gate_weight &&
        !aligned(block->shared_expert_gate_weight, 16)))
     return fail("block: x, out and router weights must be 16-byte aligned");
-  if (!aligned(block->gate_q.weight, 4) ||
-      !aligned(block->shared_expert_gate_q.weight, 4) ||
+  const size_t rq_align = block->gate_q.bits == 16 ? 8 : 4;  // bf16 Linear: 8
+  if (!aligned(block->gate_q.weight, rq_align) ||
+      !aligned(block->shared_expert_gate_q.weight, rq_align) ||
       !aligned(block->gate_q.scales, 2) || !aligned(block->gate_q.biases, 2) ||
       !aligned(block->shared_expert_gate_q.scales, 2) ||
       !aligned(block->shared_expert_gate_q.biases, 2))
-    return fail("block: quantised router words must be 4-byte and its "
-                "scales and biases 2-byte aligned");
+    return fail("block: quantised router words must be 4-byte (bf16 "
+                "weights 8-byte) and its scales and biases 2-byte aligned");
   Carve plan(nullptr);
   plan.take<int32_t>(1);
   nn::Qwen35MoeBlock::plan(plan, *block, T);

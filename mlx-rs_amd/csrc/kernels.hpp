@@ -144,6 +144,8 @@ hipError_t launch_dispatch_identity(int64_t n, int tile_rows,
                                     const DispatchBuffers& b, hipStream_t s);
 
 // ---------------------------------------------------------------- qgemm.hip
+// bits 4/8: packed codes plus scales and biases; bits 16: dense bf16
+// weights [E, N, K] (gather_mm), no scales or biases.
 struct QWeights {
   const uint32_t* w;       // [E, N, K*bits/32]
   const uint16_t* scales;  // [E, N, K/64] bf16
@@ -152,6 +154,8 @@ struct QWeights {
 struct QGemmArgs {
   const uint16_t* x;       // activations (bf16)
   int64_t x_ld;            // row stride of x in elements
+  int64_t x_rows;          // rows of x (the M-tiled kernel's x bounds);
+                           // 0: the GEMM's total rows
   // x row of sorted slot p: p when x_by_slot; else, with f the flat row of
   // p (from the work record), row_map[f] when row_map is given, f / row_div
   // otherwise
@@ -197,7 +201,8 @@ constexpr int kMaxInputDims = 4096;
 constexpr int kPrefillMinTileRows = 128;
 int prefill_tile_rows(int64_t rows, int64_t experts);
 // max_items bounds the number of work items (dispatch_max_work); prefill
-// selects the M-tiled kernel (prefill.hip) where it applies.
+// selects the M-tiled kernel (prefill.hip) where it applies.  Dense bf16
+// weights (bits 16) always take the M-tiled kernel.
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s);
 

@@ -15,13 +15,19 @@ Status from_hip(hipError_t e, const char* where) {
 Status check_qlinear(const mlxr_moe_qlinear& q, int64_t experts, int64_t out,
                      int64_t in, const char* name) {
   const std::string n(name);
-  if (!q.weight || !q.scales || !q.biases)
+  // bits 16: a dense bf16 SwitchLinear / Linear (weight [E, out, in] bf16,
+  // no scales or biases; group_size unused)
+  const bool dense = q.bits == 16;
+  if (dense && (!q.weight || q.scales || q.biases))
+    return Status::error(n + ": a dense (bits 16) weight takes no scales or "
+                             "biases");
+  if (!dense && (!q.weight || !q.scales || !q.biases))
     return Status::error(n + ": weight, scales and biases are required "
                              "(affine mode)");
-  if (q.bits != 4 && q.bits != 8)
-    return Status::error(n + ": bits must be 4 or 8, got " +
-                         std::to_string(q.bits));
-  if (q.group_size != 64)
+  if (q.bits != 4 && q.bits != 8 && !dense)
+    return Status::error(n + ": bits must be 4 or 8 (16 for dense bf16 "
+                             "weights), got " + std::to_string(q.bits));
+  if (!dense && q.group_size != 64)
     return Status::error(n + ": group_size must be 64, got " +
                          std::to_string(q.group_size));
   if (q.num_experts != experts || q.output_dims != out || q.input_dims != in)
@@ -40,6 +46,8 @@ Status check_qlinear(const mlxr_moe_qlinear& q, int64_t experts, int64_t out,
       (reinterpret_cast<uintptr_t>(q.scales) & 1) ||
       (reinterpret_cast<uintptr_t>(q.biases) & 1))
     return Status::error(n + ": weight must be 16-byte aligned");
+  if (dense && (int64_t)out * in * 2 >= ((int64_t)1 << 31))
+    return Status::error(n + ": one expert's dense weights must be under 2 GB");
   return Status{};
 }
 
@@ -112,6 +120,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   QGemmArgs g{};
   g.x = x;
   g.x_ld = d;
+  g.x_rows = T;
   g.row_map = nullptr;
   g.row_div = 1;
   g.x_by_slot = false;
@@ -141,6 +150,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   QGemmArgs h = g;
   h.x = act;
   h.x_ld = f;
+  h.x_rows = T;
   h.x_by_slot = true;
   h.w0 = qw(down_);
   h.w1 = QWeights{};
@@ -192,10 +202,12 @@ PackedSwitchFfn::PackedSwitchFfn(const mlxr_moe_packed_switch_glu& w) : w_(w) {
   sw_.up = sw_.gate;
   if (gu.weight && gu.bits > 0) {
     const int64_t words = sw_.f * sw_.d * gu.bits / 32;
-    const int64_t g = sw_.d / (gu.group_size > 0 ? gu.group_size : 64);
     sw_.up.w = gu.weight + words;
-    sw_.up.scales = sw_.gate.scales + sw_.f * g;
-    sw_.up.biases = sw_.gate.biases + sw_.f * g;
+    if (gu.bits != 16 && gu.scales && gu.biases) {
+      const int64_t g = sw_.d / (gu.group_size > 0 ? gu.group_size : 64);
+      sw_.up.scales = sw_.gate.scales + sw_.f * g;
+      sw_.up.biases = sw_.gate.biases + sw_.f * g;
+    }
   }
   sw_.down = qw(w.down_proj);
   sw_.gate_rows = (int32_t)gu.output_dims;
@@ -260,6 +272,7 @@ Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   QGemmArgs g{};
   g.x = x;
   g.x_ld = d;
+  g.x_rows = T;
   g.row_map = nullptr;
   g.row_div = (int32_t)K;
   g.x_by_slot = false;
@@ -289,6 +302,7 @@ Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   QGemmArgs h = g;
   h.x = act;
   h.x_ld = f;
+  h.x_rows = n;
   h.x_by_slot = true;
   h.w0 = sw_.down;
   h.w1 = QWeights{};
@@ -331,28 +345,30 @@ Status Qwen35MoeBlock::validate() const {
   if (d % 64)
     return Status::error("block: hidden_size must be a multiple of 64");
   if (quantised_router()) {
-    // QuantizedLinear router and shared gate (layers/quantized.rs:356-373)
+    // QuantizedLinear router and shared gate (layers/quantized.rs:356-373),
+    // or bf16 Linears (bits 16, layers/linear.rs:91-95): bf16 logits
     const mlxr_moe_qlinear& g = b_.gate_q;
     if (b_.gate_weight || b_.gate_bias || b_.shared_expert_gate_weight)
-      return Status::error("block: a quantised router (gate_q) replaces "
-                           "gate_weight, gate_bias and "
+      return Status::error("block: a quantised or bf16 router (gate_q) "
+                           "replaces gate_weight, gate_bias and "
                            "shared_expert_gate_weight; leave them NULL");
-    if ((g.bits != 4 && g.bits != 8) || g.group_size != 64)
+    const bool dense = g.bits == 16;
+    if (!dense && ((g.bits != 4 && g.bits != 8) || g.group_size != 64))
       return Status::error("block: gate_q must be 4- or 8-bit with group "
-                           "size 64");
+                           "size 64, or a bf16 Linear (bits 16)");
     if (g.num_experts != 1 || g.output_dims != E || g.input_dims != d ||
-        !g.scales || !g.biases)
+        (dense ? (g.scales || g.biases) : (!g.scales || !g.biases)))
       return Status::error("block: gate_q must be one [num_experts, "
                            "hidden_size] QuantizedLinear with scales and "
-                           "biases");
+                           "biases, or a bf16 Linear without them");
     const mlxr_moe_qlinear& sg = b_.shared_expert_gate_q;
     if (sg.weight &&
-        (sg.bits != g.bits || sg.group_size != 64 || sg.num_experts != 1 ||
-         sg.output_dims != 1 || sg.input_dims != d || !sg.scales ||
-         !sg.biases))
+        (sg.bits != g.bits || (!dense && sg.group_size != 64) ||
+         sg.num_experts != 1 || sg.output_dims != 1 || sg.input_dims != d ||
+         (dense ? (sg.scales || sg.biases) : (!sg.scales || !sg.biases))))
       return Status::error("block: shared_expert_gate_q must be a [1, "
-                           "hidden_size] QuantizedLinear with gate_q's bits "
-                           "and group size 64");
+                           "hidden_size] linear of gate_q's form (same bits; "
+                           "group size 64 when quantised)");
   } else if (!b_.gate_weight) {
     return Status::error("block: gate_weight (or gate_q) is required");
   }

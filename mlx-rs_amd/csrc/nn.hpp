@@ -138,7 +138,7 @@ class Qwen35MoeBlock {
  public:
   explicit Qwen35MoeBlock(const mlxr_moe_block& b) : b_(b) {}
   Status validate() const;
-  // quantised (bf16) router: QuantizedLinear gate and shared gate
+  // bf16 router: QuantizedLinear (or bf16 Linear) gate and shared gate
   bool quantised_router() const { return b_.gate_q.weight != nullptr; }
   bool has_shared() const {
     return quantised_router() ? b_.shared_expert_gate_q.weight != nullptr

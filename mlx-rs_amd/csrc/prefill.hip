@@ -1,6 +1,7 @@
 // Grouped quantised expert GEMM for many rows per expert (prefill): an
 // LDS-tiled bf16 MFMA GEMM that dequantises each weight tile once per
-// workgroup.
+// workgroup.  The same kernel runs dense bf16 expert weights (gather_mm,
+// bits = 16: the weight tile is staged as it is) at every row count.
 //
 // Same operation as the decode kernels (gather_qmm with transpose = true,
 // crates/mlxr/src/ops/quantization.rs:171-221, as called by
@@ -149,7 +150,7 @@ bool prefill_supported(const QGemmArgs& a, int64_t x_rows) {
   // buffer offsets are 32-bit: x, and one expert's weights, under 2 GB
   // outputs leave as 16-byte runs of a row
   const bool out16 = (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && a.out_ld % 8 == 0;
-  return (a.bits == 4 || a.bits == 8) && a.K % 64 == 0 && a.N % 64 == 0 &&
+  return (a.bits == 4 || a.bits == 8 || a.bits == 16) && a.K % 64 == 0 && a.N % 64 == 0 &&
          a.sorted != nullptr && out16 && a.row_div >= 1 && a.row_div <= 65536 &&
          x_rows * a.x_ld * 2 < ((int64_t)1 << 31) &&
          (int64_t)a.N * a.K * a.bits / 8 < ((int64_t)1 << 31);

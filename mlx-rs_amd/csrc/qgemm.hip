@@ -687,9 +687,14 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s) {
   if (max_items <= 0) return hipSuccess;
-  if (prefill && prefill_supported(a, total_rows)) {
+  // the M-tiled kernel reads x through a buffer of x's own rows (gathered
+  // rows may lie anywhere in it: gather_mm / gather_qmm with lhs indices)
+  const int64_t x_rows = a.x_rows > 0 ? a.x_rows : total_rows;
+  // dense bf16 weights run on the tiled kernel at every row count
+  if (a.bits == 16 && !prefill_supported(a, x_rows)) return hipErrorInvalidValue;
+  if ((prefill || a.bits == 16) && prefill_supported(a, x_rows)) {
     const int tile_rows = prefill_tile_rows(total_rows, a.E);
-    return launch_qgemm_prefill(a, total_rows, tile_rows,
+    return launch_qgemm_prefill(a, x_rows, tile_rows,
                                 dispatch_max_tiles(total_rows, a.E, tile_rows), s);
   }
   const int groups = a.K / 64;

@@ -1,5 +1,7 @@
 """mlxr-lm MoE modules over the gfx950 C ABI.
 
+    SwitchLinear           crates/mlxr-lm/src/nn/switch.rs:49-94 (dense)
+    Linear                 crates/mlxr/src/layers/linear.rs (dense, bf16)
     QuantizedSwitchLinear  crates/mlxr-lm/src/nn/switch.rs:115-168
     QuantizedLinear        crates/mlxr/src/layers/quantized.rs:214-379
     SwigluMlp              crates/mlxr-lm/src/nn/swiglu_mlp.rs:24-75
@@ -19,6 +21,64 @@ import torch
 from . import _capi as C
 from . import ops
 from ._capi import MlxrMoeError
+
+
+class SwitchLinear:
+    """Expert-stacked dense linear (the unquantised MaybeQuantized slot):
+    weight bf16 [E, out, in], applied with gather_mm (switch.rs:84-93).  No
+    bias: the MoE blocks build theirs without (moe.rs:92-97,
+    gemma4/text/text.rs:679)."""
+
+    bits = 16
+    group_size = 0
+
+    def __init__(self, weight):
+        if weight.ndim != 3:
+            raise MlxrMoeError("SwitchLinear weight must be [E, out, in]")
+        self.weight = weight.to(torch.bfloat16).contiguous()
+
+    @property
+    def num_experts(self):
+        return self.weight.shape[0]
+
+    @property
+    def output_dims(self):
+        return self.weight.shape[1]
+
+    @property
+    def input_dims(self):
+        return self.weight.shape[2]
+
+    def apply(self, x, indices, sorted=False):
+        """SwitchLinear::apply (switch.rs:84-93)."""
+        return ops.gather_mm(x, self.weight, None, indices, sorted)
+
+    def try_into_quantized(self, group_size=64, bits=4):
+        """Quantizable::try_into_quantized (switch.rs:96-113)."""
+        return QuantizedSwitchLinear.try_from_switch_linear(self.weight, group_size, bits)
+
+    def descriptor(self) -> C.QLinear:
+        return C.QLinear(self.weight.data_ptr(), None, None, self.num_experts,
+                         self.output_dims, self.input_dims, 0, 16)
+
+
+class Linear(SwitchLinear):
+    """A dense bf16 Linear without bias (weight [out, in]) seen as one expert:
+    the router and shared-expert projections of an unquantised checkpoint."""
+
+    def __init__(self, weight):
+        super().__init__(weight.reshape((1,) + tuple(weight.shape)))
+
+    def try_into_quantized(self, group_size=64, bits=4):
+        return QuantizedLinear.try_from_linear(self.weight[0], group_size, bits)
+
+    def forward(self, x):
+        """x @ weight^T in bf16 (layers/linear.rs:91-95)."""
+        lead = tuple(x.shape[:-1])
+        x2 = x.reshape(-1, 1, x.shape[-1])
+        idx = torch.zeros(x2.shape[0], dtype=torch.int32, device=x.device)
+        y = ops.gather_mm(x2, self.weight, None, idx)
+        return y.reshape(lead + (self.output_dims,))
 
 
 class QuantizedSwitchLinear:
@@ -94,10 +154,12 @@ def _ptr(t):
 
 class SplitSwitchFfn:
     """SplitSwitchFfn<SwigluActivation>: gate_proj, up_proj [E, f, d],
-    down_proj [E, d, f]."""
+    down_proj [E, d, f]; all three QuantizedSwitchLinear or all three dense
+    SwitchLinear."""
 
-    def __init__(self, gate_proj: QuantizedSwitchLinear, up_proj: QuantizedSwitchLinear,
-                 down_proj: QuantizedSwitchLinear):
+    def __init__(self, gate_proj: QuantizedSwitchLinear | SwitchLinear,
+                 up_proj: QuantizedSwitchLinear | SwitchLinear,
+                 down_proj: QuantizedSwitchLinear | SwitchLinear):
         self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
         self._desc = C.SwitchGlu(gate_proj.descriptor(), up_proj.descriptor(),
                                  down_proj.descriptor())
@@ -158,8 +220,8 @@ class PackedSwitchFfn:
     down_proj [E, d, H], with GeGLU (GemmaSwitchGlu, gemma4/text/mod.rs:27)
     or SwiGLU between them."""
 
-    def __init__(self, gate_up_proj: QuantizedSwitchLinear, down_proj: QuantizedSwitchLinear,
-                 activation: str = "geglu"):
+    def __init__(self, gate_up_proj: QuantizedSwitchLinear | SwitchLinear,
+                 down_proj: QuantizedSwitchLinear | SwitchLinear, activation: str = "geglu"):
         if activation not in ("geglu", "swiglu"):
             raise MlxrMoeError("PackedSwitchFfn: activation is 'geglu' or 'swiglu'")
         if gate_up_proj.output_dims % 2:
@@ -324,7 +386,8 @@ class GemmaMoe:
 
 
 class SwigluMlp:
-    """down(silu(gate(x)) * up(x)) with QuantizedLinear projections."""
+    """down(silu(gate(x)) * up(x)) with QuantizedLinear (or dense bf16 Linear)
+    projections."""
 
     def __init__(self, gate_proj: QuantizedLinear, up_proj: QuantizedLinear,
                  down_proj: QuantizedLinear):
@@ -348,20 +411,28 @@ class Qwen35MoeBlock:
     (`shared_expert_gate_weight`) are MaybeQuantized<Linear> as in the
     reference (moe.rs:57-58): an f32 weight tensor [E, d] / [1, d], or both a
     QuantizedLinear (the shipped Qwen3.6 checkpoints quantise them at 8 bits,
-    moe.rs:255-284).  With a quantised router the block is bf16 throughout
-    (logits, probabilities, routing weights and the output)."""
+    moe.rs:255-284), or both a bf16 Linear (an unquantised checkpoint).  With
+    a QuantizedLinear or bf16 Linear router the block is bf16 throughout
+    (logits, probabilities, routing weights and the output).  The experts
+    and the shared expert may be dense (SwitchLinear / Linear projections)."""
 
     def __init__(self, gate_weight, switch_mlp: SplitSwitchFfn, num_experts_per_tok: int,
                  shared_expert: SwigluMlp | None = None, shared_expert_gate_weight=None,
                  gate_bias=None):
         if (shared_expert is None) != (shared_expert_gate_weight is None):
             raise MlxrMoeError("shared_expert and shared_expert_gate_weight go together")
-        self.quantised_router = isinstance(gate_weight, QuantizedLinear)
+        def form(w):
+            return ("q" if isinstance(w, QuantizedLinear) else
+                    "bf16" if isinstance(w, Linear) else "f32")
+
+        # the bf16 router: a QuantizedLinear or a bf16 Linear
+        self.quantised_router = form(gate_weight) != "f32"
         if shared_expert_gate_weight is not None and (
-                isinstance(shared_expert_gate_weight, QuantizedLinear) != self.quantised_router):
-            raise MlxrMoeError("gate and shared_expert_gate must both be quantised or both f32")
+                form(shared_expert_gate_weight) != form(gate_weight)):
+            raise MlxrMoeError("gate and shared_expert_gate must take the same form "
+                               "(both QuantizedLinear, both Linear or both f32 tensors)")
         if self.quantised_router and gate_bias is not None:
-            raise MlxrMoeError("a quantised router has no bias (moe.rs:90-92)")
+            raise MlxrMoeError("the router has no bias (moe.rs:89-91)")
         z = C.QLinear()
         if self.quantised_router:
             self.gate_weight = gate_weight

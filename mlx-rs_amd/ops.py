@@ -143,6 +143,43 @@ def gather_qmm(x, w, scales, biases=None, lhs_indices=None, rhs_indices=None,
     return out
 
 
+def gather_mm(a, b, lhs_indices=None, rhs_indices=None, sorted_indices=False,
+              b_transposed=True):
+    """gather_mm (ops/arithmetic.rs:1577-1613) as SwitchLinear::apply calls
+    it (nn/switch.rs:84-93): out[i] = a[ab(i)] @ b[rhs_indices[i]]^T with b
+    the SwitchLinear weight as stored, bf16 [E, N, K] (the reference passes
+    swap_axes(weight, -1, -2), the same memory).  a [..., M, K] bf16; output
+    rhs_indices.shape + [M, N] bf16, f32 accumulation.  Without lhs_indices,
+    a's batch broadcasts over the trailing index axis."""
+    _dev(a, b, lhs_indices, rhs_indices)
+    if rhs_indices is None:
+        raise MlxrMoeError("gather_mm: rhs_indices are required")
+    if not b_transposed:
+        raise MlxrMoeError("gather_mm: only b stored [E, N, K] (b_transposed) is supported")
+    if b.ndim != 3:
+        raise MlxrMoeError("gather_mm: b must be [E, N, K]")
+    a = a.contiguous()
+    M, K = a.shape[-2], a.shape[-1]
+    a_batch = math.prod(a.shape[:-2])
+    E, N = b.shape[0], b.shape[1]
+    if b.shape[2] != K:
+        raise MlxrMoeError(f"gather_mm: b last dim {b.shape[2]} does not match K={K}")
+    rhs = _as_u32(rhs_indices)
+    lhs = None if lhs_indices is None else _as_u32(lhs_indices)
+    B = rhs.numel()
+    if lhs is not None and lhs.numel() != B:
+        raise MlxrMoeError("gather_mm: lhs and rhs indices must have the same size")
+    out = torch.empty(tuple(rhs.shape) + (M, N), dtype=torch.bfloat16, device=a.device)
+    lib = C.lib()
+    ws = workspace(lib.mlxr_moe_gather_mm_workspace_size(B, M, E), a.device)
+    bc = b.contiguous()
+    C.check(lib.mlxr_moe_gather_mm(
+        _p(a), _code(a), a_batch, M, K, _p(bc), _code(bc), E, N, 1, _p(lhs), _p(rhs), B,
+        int(bool(sorted_indices)), _p(out), C.BFLOAT16, _p(ws), ws.numel(), _stream(a)))
+    out._mlxr_workspace = ws  # keep the status word alive with the result
+    return out
+
+
 def _check_axis(a: torch.Tensor, axis: int, what: str) -> int:
     if not -a.ndim <= axis < a.ndim:
         raise MlxrMoeError(
@@ -207,9 +244,10 @@ def router_topk(x: torch.Tensor, gate_w: torch.Tensor, k: int):
 
 def router_topk_quantized(x: torch.Tensor, gate, k: int):
     """router_topk with the router as a QuantizedLinear (nn.QuantizedLinear,
-    4 or 8 bits, group 64; layers/quantized.rs:356-373): bf16 logits and
-    probabilities, top-k on the probabilities.  Returns (indices int32
-    [T, k], weights [T, k] -- bf16 values held in f32)."""
+    4 or 8 bits, group 64; layers/quantized.rs:356-373) or a bf16 Linear
+    (nn.Linear): bf16 logits and probabilities, top-k on the probabilities.
+    Returns (indices int32 [T, k], weights [T, k] -- bf16 values held in
+    f32)."""
     _dev(x, gate.weight)
     x2 = x.reshape(-1, x.shape[-1]).contiguous()
     T = x2.shape[0]

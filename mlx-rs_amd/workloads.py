@@ -6,7 +6,9 @@ skew, c4 high-expert-count with shared expert, c5 wide 8-bit), plus c6, the
 Qwen3.6-35B-A3B block as its shipped checkpoint quantises it
 (crates/mlxr-lm/tests/fixtures/qwen3_6_35b_a3b/config.json: d 2048, 256
 experts, top-8, f 512, shared expert 512, 4-bit experts, mlp.gate and
-mlp.shared_expert_gate at 8 bits, group 64).
+mlp.shared_expert_gate at 8 bits, group 64), c7 gemma4's expert layout,
+and c8, the same Qwen3.6 block unquantised (bf16 experts through gather_mm,
+bf16 Linear router and shared gate).
 Weights are drawn N(0, 0.02) in f32, rounded to bf16 and affine-quantised
 on the device by this library's quantize kernel; x ~ N(0, 1) in bf16;
 router weights N(0, 0.02) in f32 (unquantised), or for c6 N(0, 0.02) in
@@ -31,13 +33,13 @@ class MoEConfig:
     K: int                 # experts per token
     f: int                 # expert intermediate size
     fs: int = 0            # shared-expert intermediate size (0: none)
-    bits: int = 4
+    bits: int = 4          # 4/8: quantised experts; 16: dense bf16 experts (gather_mm)
     group_size: int = 64
     zipf_alpha: float | None = None   # routing skew via per-expert logit bias
     tokens: tuple = field(default_factory=tuple)
     seed: int = 0
     router_bits: int = 0   # 0: f32 router; 4/8: QuantizedLinear router (bf16 block);
-                           # 16: bf16 Linear router (gemma4)
+                           # 16: bf16 Linear router (gemma4, or an unquantised block)
     layout: str = "split"  # "split": Qwen35MoeBlock; "gemma": gemma4 router +
                            # PackedSwitchFfn<Geglu> (GemmaMoe)
 
@@ -58,6 +60,10 @@ CONFIGS = {
     # scales) and packed gate_up [E, 2f, d] experts with GeGLU
     "c7": MoEConfig("c7_gemma4_packed_geglu", d=2048, E=128, K=8, f=768, router_bits=16,
                     layout="gemma", tokens=(1, 64, 2048)),
+    # the c6 block from an unquantised checkpoint: bf16 experts (gather_mm) and
+    # bf16 Linear router / shared gate
+    "c8": MoEConfig("c8_qwen3_6_35b_a3b_bf16", d=2048, E=256, K=8, f=512, fs=512, bits=16,
+                    router_bits=16, tokens=(1, 64, 2048)),
 }
 
 
@@ -103,11 +109,11 @@ def zipf_bias(cfg: MoEConfig, gate_w: torch.Tensor, device, iters: int = 20,
 @dataclass
 class BlockWeights:
     cfg: MoEConfig
-    gate_w: torch.Tensor | nn.QuantizedLinear
+    gate_w: torch.Tensor | nn.QuantizedLinear | nn.Linear
     gate_b: torch.Tensor | None
     switch_mlp: nn.SplitSwitchFfn
     shared_expert: nn.SwigluMlp | None
-    shared_gate_w: torch.Tensor | nn.QuantizedLinear | None
+    shared_gate_w: torch.Tensor | nn.QuantizedLinear | nn.Linear | None
 
     gemma: object = None   # (scale, per_expert_scale) of the gemma4 router
 
@@ -127,13 +133,17 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
     gate_b = zipf_bias(cfg, gate_w, device) if cfg.zipf_alpha else None
 
     def qrouter(w):
+        if cfg.router_bits == 16:
+            return nn.Linear(w.to(torch.bfloat16))
         return nn.QuantizedLinear.try_from_linear(w.to(torch.bfloat16), 64, cfg.router_bits)
 
-    if cfg.router_bits in (4, 8):
+    if cfg.router_bits in (4, 8) or (cfg.router_bits == 16 and cfg.layout == "split"):
         gate_w = qrouter(gate_w)
 
     def qbank(shape, stream):
         w = _normal(shape, 0.02, device, s, stream).to(torch.bfloat16)
+        if cfg.bits == 16:
+            return nn.SwitchLinear(w)
         return nn.QuantizedSwitchLinear.try_from_switch_linear(w, cfg.group_size, cfg.bits)
 
     if cfg.layout == "gemma":
@@ -152,11 +162,13 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
     if cfg.fs:
         def qlin(shape, stream):
             w = _normal(shape, 0.02, device, s, stream).to(torch.bfloat16)
+            if cfg.bits == 16:
+                return nn.Linear(w)
             return nn.QuantizedLinear.try_from_linear(w, cfg.group_size, cfg.bits)
         shared = nn.SwigluMlp(qlin((cfg.fs, cfg.d), 8), qlin((cfg.fs, cfg.d), 9),
                               qlin((cfg.d, cfg.fs), 10))
         sgw = _normal((1, cfg.d), 0.02, device, s, 12)
-        if cfg.router_bits in (4, 8):
+        if cfg.router_bits:
             sgw = qrouter(sgw)
     return BlockWeights(cfg, gate_w, gate_b, mlp, shared, sgw)
 
@@ -167,7 +179,7 @@ def algorithmic_bytes(cfg: MoEConfig, T: int, distinct_experts: int) -> int:
     router weights (f32, or packed at router_bits with bf16 scales/biases
     per 64), x in, the output (f32, bf16 with a quantised router), and the
     routing (idx + weight)."""
-    per_w = cfg.bits / 8 + 4 / cfg.group_size
+    per_w = weight_bytes_per_element(cfg)
     per_r = (2 if cfg.router_bits == 16 else
              cfg.router_bits / 8 + 4 / 64 if cfg.router_bits else 4)
     b = distinct_experts * 3 * cfg.f * cfg.d * per_w + cfg.E * cfg.d * per_r
@@ -189,9 +201,15 @@ def distinct(indices: torch.Tensor) -> int:
     return int(torch.unique(indices.reshape(-1)).numel())
 
 
+def weight_bytes_per_element(cfg: MoEConfig) -> float:
+    """Expert weight bytes per element: the code plus the group's bf16 scale
+    and bias, or 2 for dense bf16 weights."""
+    return 2.0 if cfg.bits == 16 else cfg.bits / 8 + 4 / cfg.group_size
+
+
 def expert_bytes_per_row(cfg: MoEConfig, K_dim: int) -> float:
-    return K_dim * (cfg.bits / 8 + 4 / cfg.group_size)
+    return K_dim * weight_bytes_per_element(cfg)
 
 
 __all__ = ["MoEConfig", "CONFIGS", "make_x", "make_weights", "BlockWeights", "zipf_bias",
-           "algorithmic_bytes", "algorithmic_flops", "distinct", "math", "ops"]
+           "algorithmic_bytes", "weight_bytes_per_element", "algorithmic_flops", "distinct", "math", "ops"]

@@ -45,7 +45,16 @@
  *   orc_combine_bf16  per-op bf16 roundings restated elementwise in numpy.
  *   orc_block_forward sorted and unsorted dispatch give identical outputs
  *                     (switch.rs:446-474); K=1 reduces to one expert;
- *                     linearity in the routing weights.
+ *                     linearity in the routing weights.  With dense bf16
+ *                     experts: bit-equal to the 4-bit block (tiled
+ *                     numerics) whose weights dequantise to them.
+ *   orc_gather_mm     the reference's doc example (arithmetic.rs:1565-1575,
+ *                     ones -> 32); fp64 bound; bit-equal to the tiled
+ *                     orc_gather_qmm at 4 bits on the bf16-dequantised
+ *                     weights (quantization.rs:344-421 states that
+ *                     identity).
+ *   dense router      (lane_dot_q, bits 16) bit-equal to the 8-bit router
+ *                     whose codes dequantise exactly to the bf16 weights.
  */
 #include "moe_oracle.h"
 
@@ -93,6 +102,11 @@ static inline float round_to(int dtype, float v) {
 static int valid_quant(int group_size, int bits) {
   return (bits == 2 || bits == 4 || bits == 8) &&
          (group_size == 32 || group_size == 64 || group_size == 128);
+}
+
+/* the expert GEMMs also take dense bf16 weights (bits 16, gather_mm) */
+static int valid_gemm(int group_size, int bits) {
+  return valid_quant(group_size, bits) || bits == 16;
 }
 
 /* -------------------------------------------------------------- quantize */
@@ -265,6 +279,17 @@ void orc_router_topk(const float* logits, int64_t T, int64_t E, int64_t K,
 static float lane_dot_q(const uint16_t* xrow, const uint32_t* wrow,
                         const uint16_t* srow, const uint16_t* brow, int64_t d,
                         int bits) {
+  if (bits == 16) {
+    /* a dense bf16 Linear ([E, d] bf16; Linear::forward, layers/linear.rs:
+     * 91-95, in bf16): the same lane order over the bf16 weights, one
+     * rounding of the sum */
+    const uint16_t* w16 = (const uint16_t*)wrow;
+    float* wf = (float*)malloc(sizeof(float) * (size_t)d);
+    for (int64_t j = 0; j < d; ++j) wf[j] = orc_bf16_to_f32(w16[j]);
+    const float v = lane_dot(xrow, wf, d);
+    free(wf);
+    return orc_bf16_to_f32(orc_f32_to_bf16(v));
+  }
   const int per_word = 32 / bits;
   const uint32_t mask = (1u << bits) - 1u;
   float lane[64];
@@ -295,12 +320,13 @@ int orc_router_logits_q(const uint16_t* x, const uint32_t* wq,
                         const uint16_t* scales, const uint16_t* biases,
                         int bits, int64_t T, int64_t d, int64_t E,
                         float* logits) {
-  if ((bits != 4 && bits != 8) || d % 64) return -1;
-  const int64_t wpr = d * bits / 32, gpr = d / 64;
+  if ((bits != 4 && bits != 8 && bits != 16) || d % 64) return -1;
+  const int64_t wpr = d * bits / 32, gpr = bits == 16 ? 0 : d / 64;
   for (int64_t t = 0; t < T; ++t)
     for (int64_t e = 0; e < E; ++e)
-      logits[t * E + e] = lane_dot_q(x + t * d, wq + e * wpr, scales + e * gpr,
-                                     biases + e * gpr, d, bits);
+      logits[t * E + e] = lane_dot_q(x + t * d, wq + e * wpr,
+                                     scales ? scales + e * gpr : NULL,
+                                     biases ? biases + e * gpr : NULL, d, bits);
   return 0;
 }
 
@@ -397,6 +423,16 @@ int orc_dispatch(const int32_t* ids, int64_t n, int64_t E, int32_t* counts,
 static float qdot(const float* xf, const uint32_t* wrow, const uint16_t* srow,
                   const uint16_t* brow, int64_t Kd, int gs, int bits,
                   int tiled) {
+  if (bits == 16) {
+    /* dense bf16 row (gather_mm): the same partial sums over the weights as
+     * they are */
+    const uint16_t* w16 = (const uint16_t*)wrow;
+    float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t k = 0; k < Kd; ++k)
+      part[k & 7] = fmaf(xf[k], orc_bf16_to_f32(w16[k]), part[k & 7]);
+    return ((part[0] + part[1]) + (part[2] + part[3])) +
+           ((part[4] + part[5]) + (part[6] + part[7]));
+  }
   const int per_word = 32 / bits;
   const uint32_t mask = (1u << bits) - 1u;
   float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -418,14 +454,17 @@ static float qdot(const float* xf, const uint32_t* wrow, const uint16_t* srow,
          ((part[4] + part[5]) + (part[6] + part[7]));
 }
 
-/* y[n] = bf16(x . dequant(W[e, n])) for n in [0, N) */
+/* y[n] = bf16(x . dequant(W[e, n])) for n in [0, N); bits 16: W is a
+ * dense bf16 [E, N, Kd] tensor (no scales or biases) */
 static void qmv(const float* xf, const orc_qlinear* q, int64_t e, int64_t N,
                 int64_t Kd, int gs, int bits, int tiled, uint16_t* y) {
-  const int64_t wpr = Kd * bits / 32, gpr = Kd / gs;
+  const int64_t wpr = Kd * bits / 32, gpr = bits == 16 ? 0 : Kd / gs;
   for (int64_t n = 0; n < N; ++n) {
     const int64_t row = e * N + n;
-    y[n] = orc_f32_to_bf16(qdot(xf, q->w + row * wpr, q->scales + row * gpr,
-                                q->biases + row * gpr, Kd, gs, bits, tiled));
+    y[n] = orc_f32_to_bf16(qdot(xf, q->w + row * wpr,
+                                q->scales ? q->scales + row * gpr : NULL,
+                                q->biases ? q->biases + row * gpr : NULL, Kd,
+                                gs, bits, tiled));
   }
 }
 
@@ -435,7 +474,7 @@ int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
                    const int32_t* lhs, const int32_t* rhs, int64_t B,
                    int group_size, int bits, int tiled, uint16_t* out,
                    int nthreads) {
-  if (!valid_quant(group_size, bits) || Kd % group_size) return -1;
+  if (!valid_gemm(group_size, bits) || Kd % group_size) return -1;
   if (!lhs && (x_batch <= 0 || B % x_batch)) return -1;
   for (int64_t b = 0; b < B; ++b) {
     if (rhs[b] < 0 || rhs[b] >= E) return -1;
@@ -455,6 +494,21 @@ int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
     free(xf);
   }
   return 0;
+}
+
+/* gather_mm with the SwitchLinear layout (SwitchLinear::apply,
+ * nn/switch.rs:84-93: gather_mm(x, swap_axes(weight, -1, -2), None,
+ * indices), ops/arithmetic.rs:1577-1613): w bf16 [E, N, Kd] as stored,
+ * out[b, m] = bf16(x[xb, m] . w[rhs[b], n]) with f32 accumulation -- the
+ * tiled gather_qmm's sum over weights that need no dequantisation.  No bias:
+ * every SwitchLinear on this path is built with bias = false (qwen3_5/text/
+ * moe.rs:92-97, gemma4/text/text.rs:679). */
+int orc_gather_mm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
+                  const uint16_t* w, int64_t E, int64_t N, const int32_t* lhs,
+                  const int32_t* rhs, int64_t B, uint16_t* out, int nthreads) {
+  /* (no groups: any Kd) */
+  return orc_gather_qmm(x, x_batch, M, Kd, (const uint32_t*)w, NULL, NULL, E,
+                        N, lhs, rhs, B, 1, 16, 1, out, nthreads);
 }
 
 /* ------------------------------------------------------------- swiglu */
@@ -561,7 +615,7 @@ int orc_packed_switch_glu(const uint16_t* x, int64_t T, int64_t d, int64_t H,
                           const int32_t* idx, const float* w, int w_bf16,
                           int64_t K, int tiled, void* out, uint16_t* y_out,
                           int nthreads) {
-  if (!valid_quant(64, bits) || d % 64 || H % 64 || (act != 0 && act != 1))
+  if (!valid_gemm(64, bits) || d % 64 || H % 64 || (act != 0 && act != 1))
     return -1;
   for (int64_t i = 0; i < T * K; ++i)
     if (idx[i] < 0 || idx[i] >= E) return -1;
@@ -718,13 +772,14 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
   const int64_t d = blk->hidden, E = blk->num_experts, K = blk->top_k;
   const int64_t f = blk->intermediate, fs = blk->shared_intermediate;
   const int gs = blk->group_size, bits = blk->bits;
-  if (!valid_quant(gs, bits) || d % gs || f % gs || (fs && fs % gs) ||
+  if (!valid_gemm(gs, bits) || d % gs || f % gs || (fs && fs % gs) ||
       K < 1 || K > E || K > 64)
     return -1;
   if (nthreads <= 0) nthreads = 1;
 
   const int qr = blk->router_q.w != NULL;
-  if (qr && ((blk->router_bits != 4 && blk->router_bits != 8) ||
+  if (qr && ((blk->router_bits != 4 && blk->router_bits != 8 &&
+              blk->router_bits != 16) ||
              (fs && !blk->shared_gate_q.w)))
     return -1;
   float* logits = (float*)malloc(sizeof(float) * (size_t)(T * E));
@@ -734,16 +789,18 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
   uint16_t* sy = fs ? (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * d)) : NULL;
   float* sg = fs ? (float*)malloc(sizeof(float) * (size_t)T) : NULL;
 
-  /* router: f32 Linear (f32 logits) or QuantizedLinear (bf16 logits) */
+  /* router: f32 Linear (f32 logits), or a QuantizedLinear or bf16 Linear
+   * (router_bits 16; bf16 logits) */
   const int rb = blk->router_bits;
 #pragma omp parallel for schedule(static) num_threads(nthreads)
   for (int64_t t = 0; t < T; ++t) {
     for (int64_t e = 0; e < E; ++e) {
       float v;
       if (qr) {
+        const int64_t gr = rb == 16 ? 0 : d / 64;  /* bf16 Linear: none */
         v = lane_dot_q(x + t * d, blk->router_q.w + e * (d * rb / 32),
-                       blk->router_q.scales + e * (d / 64),
-                       blk->router_q.biases + e * (d / 64), d, rb);
+                       rb == 16 ? NULL : blk->router_q.scales + e * gr,
+                       rb == 16 ? NULL : blk->router_q.biases + e * gr, d, rb);
       } else {
         v = lane_dot(x + t * d, blk->router_w + e * d, d);
         if (blk->router_b) v += blk->router_b[e];

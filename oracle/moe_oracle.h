@@ -99,6 +99,16 @@ int orc_gather_qmm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
                    int nthreads);
 
 /* act = silu(g) * u with MLX's per-op bf16 rounding. */
+/* gather_mm with the SwitchLinear layout: w bf16 [E, N, Kd] as stored
+ * (SwitchLinear::apply passes swap_axes(weight)); otherwise as
+ * orc_gather_qmm (same x broadcast, f32 accumulation, bf16 out).  The
+ * expert GEMMs of orc_block_forward / orc_packed_switch_glu take dense
+ * weights the same way: bits = 16, w the bf16 tensor, scales and biases
+ * NULL.  Returns 0 or -1. */
+int orc_gather_mm(const uint16_t* x, int64_t x_batch, int64_t M, int64_t Kd,
+                  const uint16_t* w, int64_t E, int64_t N, const int32_t* lhs,
+                  const int32_t* rhs, int64_t B, uint16_t* out, int nthreads);
+
 void orc_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
                 uint16_t* out);
 

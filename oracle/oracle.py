@@ -106,14 +106,16 @@ def router_topk(logits, K):
 
 
 def router_logits_q(x_bf16, wq, scales, biases, bits):
-    """QuantizedLinear router: bf16 logits (as f32) [T, E]."""
+    """QuantizedLinear router (or, bits 16, a bf16 Linear: wq the bf16 bits
+    [E, d], scales and biases None): bf16 logits (as f32) [T, E]."""
     x = np.ascontiguousarray(x_bf16, np.uint16)
-    wq = np.ascontiguousarray(wq, np.uint32)
+    wq = np.ascontiguousarray(wq, np.uint16 if bits == 16 else np.uint32)
     T, d = x.shape
     E = wq.shape[0]
     out = np.zeros((T, E), np.float32)
-    rc = lib().orc_router_logits_q(_p(x), _p(wq), _p(np.ascontiguousarray(scales, np.uint16)),
-                                   _p(np.ascontiguousarray(biases, np.uint16)), c_int(bits),
+    sc = None if scales is None else np.ascontiguousarray(scales, np.uint16)
+    bi = None if biases is None else np.ascontiguousarray(biases, np.uint16)
+    rc = lib().orc_router_logits_q(_p(x), _p(wq), _p(sc), _p(bi), c_int(bits),
                                    c_int64(T), c_int64(d), c_int64(E), _p(out))
     if rc:
         raise ValueError("orc_router_logits_q rejected the arguments")
@@ -164,6 +166,25 @@ def gather_qmm(x, wq, scales, biases, rhs, lhs=None, group_size=64, bits=4, nthr
                               c_int(bits), c_int(1 if tiled else 0), _p(out), c_int(nthreads))
     if rc:
         raise ValueError("orc_gather_qmm rejected the arguments")
+    return out
+
+
+def gather_mm(x, w, rhs, lhs=None, nthreads=1):
+    """x uint16 [x_batch, M, K]; w uint16 (bf16 bits) [E, N, K] -- the
+    SwitchLinear weight as stored; rhs [B] -> out uint16 [B, M, N]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    xb, M, Kd = x.shape
+    w = np.ascontiguousarray(w, np.uint16)
+    E, N = w.shape[0], w.shape[1]
+    rhs = np.ascontiguousarray(rhs, np.int32).reshape(-1)
+    lhs_a = None if lhs is None else np.ascontiguousarray(lhs, np.int32).reshape(-1)
+    B = rhs.size
+    out = np.zeros((B, M, N), np.uint16)
+    rc = lib().orc_gather_mm(_p(x), c_int64(xb), c_int64(M), c_int64(Kd), _p(w), c_int64(E),
+                             c_int64(N), _p(lhs_a), _p(rhs), c_int64(B), _p(out),
+                             c_int(nthreads))
+    if rc:
+        raise ValueError("orc_gather_mm rejected the arguments")
     return out
 
 
@@ -258,10 +279,18 @@ def packed_switch_glu(x, gate_up, down, idx, w, act=1, w_bf16=True, tiled=False,
     w_bf16, else f32) and, with_y, the per-expert rows [T, K, d]."""
     x = np.ascontiguousarray(x, np.uint16)
     T, d = x.shape
-    gw, gs, gb = (np.ascontiguousarray(a, dt) for a, dt in zip(gate_up, (np.uint32, np.uint16, np.uint16)))
-    dw, ds, db = (np.ascontiguousarray(a, dt) for a, dt in zip(down, (np.uint32, np.uint16, np.uint16)))
+
+    def arrs(t):
+        # (weight, scales, biases); dense bf16: (weight uint16 [E, N, K], None, None)
+        if t[1] is None:
+            return np.ascontiguousarray(t[0], np.uint16), None, None
+        return tuple(np.ascontiguousarray(a, dt)
+                     for a, dt in zip(t, (np.uint32, np.uint16, np.uint16)))
+
+    gw, gs, gb = arrs(gate_up)
+    dw, ds, db = arrs(down)
     E, H2 = gw.shape[0], gw.shape[1]
-    bits = gw.shape[2] * 32 // d
+    bits = 16 if gs is None else gw.shape[2] * 32 // d
     idx = np.ascontiguousarray(idx, np.int32)
     K = idx.shape[1]
     wf = np.ascontiguousarray(w, np.float32)
@@ -296,7 +325,7 @@ class _Block(Structure):
 def _ql(t):
     if t is None:
         return _QL()
-    return _QL(t[0].ctypes.data, t[1].ctypes.data, t[2].ctypes.data)
+    return _QL(*(None if a is None else a.ctypes.data for a in t))
 
 
 def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
@@ -320,6 +349,8 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
     def q(t):
         if t is None:
             return None
+        if t[1] is None:  # dense bf16 weights
+            return (c(t[0], np.uint16), None, None)
         return (c(t[0], np.uint32), c(t[1], np.uint16), c(t[2], np.uint16))
 
     x = c(x, np.uint16)
@@ -346,7 +377,7 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
 
 __all__ = ["build", "lib", "f32_to_bf16", "bf16_to_f32", "quantize", "dequantize",
            "router_logits", "router_topk", "router_logits_q", "router_topk_bf16", "dispatch",
-           "gather_qmm", "swiglu", "combine", "combine_bf16", "geglu", "rms_norm", "gemma_router",
+           "gather_qmm", "gather_mm", "swiglu", "combine", "combine_bf16", "geglu", "rms_norm", "gemma_router",
            "packed_switch_glu",
            "block_forward", "POINTER", "c_float", "c_uint16", "c_uint32"]
 
@@ -365,27 +396,34 @@ def to_np(t):
     return t.contiguous().cpu().numpy()
 
 
+def qlinear_np(lin):
+    """(weight, scales, biases) numpy arrays of an nn module's projection:
+    packed words uint32 [E, N, K*bits/32] with bf16 scales/biases, or for a
+    dense SwitchLinear / Linear (bits 16) the bf16 bits [E, N, K] and None."""
+    if lin.bits == 16:
+        return (to_np(lin.weight), None, None)
+    return (to_np(lin.weight).reshape(lin.weight.shape[0], lin.weight.shape[1], -1),
+            to_np(lin.scales), to_np(lin.biases))
+
+
 def block_params(bw) -> dict:
     """Numpy parameters for block_forward from a workloads.BlockWeights."""
     cfg = bw.cfg
-
-    def q(lin):
-        return (to_np(lin.weight).reshape(lin.weight.shape[0], lin.weight.shape[1], -1),
-                to_np(lin.scales), to_np(lin.biases))
+    q = qlinear_np
 
     m = bw.switch_mlp
     p = dict(d=cfg.d, E=cfg.E, K=cfg.K, f=cfg.f, fs=cfg.fs, bits=cfg.bits,
              group_size=cfg.group_size,
              router_b=None if bw.gate_b is None else to_np(bw.gate_b),
              gate=q(m.gate_proj), up=q(m.up_proj), down=q(m.down_proj))
-    if cfg.router_bits in (4, 8):
+    if cfg.router_bits:  # QuantizedLinear or bf16 Linear router
         p.update(router_q=q(bw.gate_w), router_bits=cfg.router_bits)
     else:
         p.update(router_w=to_np(bw.gate_w))
     if cfg.fs:
         s = bw.shared_expert
         p.update(shared_gate=q(s.gate_proj), shared_up=q(s.up_proj), shared_down=q(s.down_proj))
-        if cfg.router_bits in (4, 8):
+        if cfg.router_bits:
             p.update(shared_gate_q=q(bw.shared_gate_w))
         else:
             p.update(shared_gate_w=to_np(bw.shared_gate_w))

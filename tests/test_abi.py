@@ -146,3 +146,43 @@ def test_python_mirror_axis_errors_without_gpu(pkg):
     a = torch.zeros(5)
     with pytest.raises(pkg.MlxrMoeError):
         pkg.ops.argpartition_axis(a, 2, 1)
+
+
+def test_gather_mm_rejects_unsupported(pkg):
+    """gather_mm: only the [E, N, K] storage of SwitchLinear's weight, bf16
+    operands, K and N multiples of 64; errors before any device work."""
+    lib, C = pkg._capi.lib(), pkg._capi
+
+    def call(a_dt=C.BFLOAT16, b_dt=C.BFLOAT16, K=128, N=64, bt=1, rhs=None):
+        return lib.mlxr_moe_gather_mm(None, a_dt, 1, 1, K, None, b_dt, 4, N, bt, None, rhs, 1,
+                                      0, None, C.BFLOAT16, None, 0, None)
+
+    assert call(bt=0) == -1 and "b_transposed" in _err(pkg)
+    assert call(b_dt=C.FLOAT32) == -1 and "bf16" in _err(pkg)
+    assert call() == -1 and "rhs_indices" in _err(pkg)
+    assert call(K=96, rhs=8) == -1 and "multiples of 64" in _err(pkg)
+    assert call(K=8192, rhs=8) == -1 and "K above" in _err(pkg)
+    assert lib.mlxr_moe_gather_mm_workspace_size(8, 1, 4) == \
+        lib.mlxr_moe_gather_qmm_workspace_size(8, 1, 4)
+
+
+def test_dense_linear_descriptors_validation(pkg):
+    """bits 16 marks a dense bf16 SwitchLinear / Linear: it takes no scales
+    or biases, in the router entry and in the expert modules alike."""
+    C = pkg._capi
+    lib = C.lib()
+    g = C.QLinear(16, 16, None, 1, 128, 2048, 0, 16)
+    assert lib.mlxr_moe_router_topk_quantized(None, 1, ctypes.byref(g), 8, None, None, None,
+                                              0, None) == -1
+    assert "no scales" in _err(pkg)
+    dense = C.QLinear(16, None, None, 8, 256, 512, 0, 16)
+    with_scales = C.QLinear(16, 16, 16, 8, 256, 512, 0, 16)
+    down = C.QLinear(16, None, None, 8, 512, 256, 0, 16)
+    ffn = C.SwitchGlu(dense, with_scales, down)
+    assert lib.mlxr_moe_switch_glu_forward(ctypes.byref(ffn), None, 1, None, None, 2, None,
+                                           None, 0, None) == -1
+    assert "dense (bits 16) weight takes no scales" in _err(pkg)
+    mixed = C.SwitchGlu(dense, dense, C.QLinear(16, 16, 16, 8, 512, 256, 64, 4))
+    assert lib.mlxr_moe_switch_glu_forward(ctypes.byref(mixed), None, 1, None, None, 2, None,
+                                           None, 0, None) == -1
+    assert "share bits" in _err(pkg)

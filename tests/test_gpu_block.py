@@ -44,10 +44,7 @@ def check_gemma(pkg, orc, bw, x, nthreads=16):
     assert np.array_equal(block.last_indices.cpu().numpy(), ridx), "routing indices differ"
     assert np.array_equal(orc.to_np(block.last_weights), rw)
     m = bw.switch_mlp
-
-    def q(lin):
-        return (orc.to_np(lin.weight).reshape(lin.weight.shape[0], lin.weight.shape[1], -1),
-                orc.to_np(lin.scales), orc.to_np(lin.biases))
+    q = orc.qlinear_np
     tiled = pkg.ops.gather_qmm_tiled(T * cfg.K, cfg.E)
     ref = orc.packed_switch_glu(orc.to_np(x), q(m.gate_up_proj), q(m.down_proj), ridx,
                                 orc.bf16_to_f32(rw), act=1, w_bf16=True, tiled=tiled,
@@ -131,11 +128,55 @@ def test_c1_golden_fixture(pkg, orc, dev):
 
 @pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 8), ("c2", 64), ("c5", 32),
                                    ("c4", 1), ("c4", 64), ("c3", 512), ("c6", 1), ("c6", 64),
-                                   ("c6", 512), ("c7", 1), ("c7", 64), ("c7", 512)])
+                                   ("c6", 512), ("c7", 1), ("c7", 64), ("c7", 512),
+                                   ("c8", 1), ("c8", 64), ("c8", 512)])
 def test_block_parity(pkg, orc, dev, cfg, T):
     bw = weights(pkg, cfg, dev)
     x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
     check_block(pkg, orc, bw, x)
+
+
+@pytest.mark.parametrize("T", [1, 64, 600])
+def test_gemma_dense_experts(pkg, orc, dev, T):
+    """gemma4's layout with unquantised experts: PackedSwitchFfn over dense
+    bf16 gate_up [E, 2H, d] and down (gather_mm), GeGLU, gemma router."""
+    W = pkg.workloads
+    cfg = W.MoEConfig("gemma_dense", d=1024, E=32, K=4, f=512, bits=16, router_bits=16,
+                      layout="gemma", tokens=(T,))
+    bw = W.make_weights(cfg, dev)
+    x = W.make_x(cfg, T, dev, seed=T)
+    check_block(pkg, orc, bw, x)
+
+
+def test_dense_block_equals_dequantised_4bit_block(pkg, dev):
+    """The c1 block with its 4-bit experts replaced by their bf16
+    dequantisation (dense SwitchLinear / Linear, gather_mm) gives the 4-bit
+    block's output bit for bit where the 4-bit GEMMs run the M-tiled kernel
+    (weights dequantised to bf16 tiles): T = 4096 over 8 experts."""
+    W = pkg.workloads
+    cfg = W.MoEConfig("c1_shared", d=512, E=8, K=2, f=256, fs=256, tokens=(4096,))
+    bw = W.make_weights(cfg, dev)
+    T = 4096
+    assert pkg.ops.gather_qmm_tiled(T * cfg.K, cfg.E) and pkg.ops.gather_qmm_tiled(T, 1)
+    x = W.make_x(cfg, T, dev, seed=7)
+    q = bw.block()
+    nn = pkg.nn
+
+    def dq(lin):
+        E, N = lin.weight.shape[0], lin.weight.shape[1]
+        w = pkg.ops.dequantize(lin.weight, lin.scales, lin.biases, 64, lin.bits)
+        return nn.SwitchLinear(w.reshape(E, N, -1))
+
+    m = bw.switch_mlp
+    mlp = nn.SplitSwitchFfn(dq(m.gate_proj), dq(m.up_proj), dq(m.down_proj))
+    s = bw.shared_expert
+    shared = nn.SwigluMlp(*(nn.Linear(dq(lin).weight[0])
+                            for lin in (s.gate_proj, s.up_proj, s.down_proj)))
+    dense = nn.Qwen35MoeBlock(bw.gate_w, mlp, cfg.K, shared, bw.shared_gate_w, bw.gate_b)
+    a = q(x)
+    b = dense(x)
+    assert torch.equal(q.last_indices, dense.last_indices)
+    assert torch.equal(a, b)
 
 
 def test_block_token_permutation_equivariance(pkg, dev):

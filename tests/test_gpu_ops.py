@@ -236,6 +236,32 @@ def test_gather_qmm_moe_unsorted_shapes(pkg, orc, dev, T, K, E, N, Kd, bits):
            orc.bf16_to_f32(want).reshape(T * K, N), (T, K, E, N, Kd, bits))
 
 
+@pytest.mark.parametrize("bits", [4, 16])
+def test_gather_lhs_rows_beyond_gathered_count(pkg, orc, dev, bits):
+    """lhs indices may pick x rows past B * M (x batch 20 x M 64 rows, B = 8
+    gathers): the M-tiled kernel must bound x by x's own rows.  Regression
+    test: it once bounded x by B * M rows and read zeros past them."""
+    E, N, Kd, xb, M, B = 2, 128, 256, 20, 64, 8
+    assert pkg.ops.gather_qmm_tiled(B * M, E)
+    rng = np.random.default_rng(50 + bits)
+    x = _bf16(orc, rng.standard_normal((xb, M, Kd)).astype(np.float32), dev)
+    lhs = [19, 18, 0, 12, 19, 5, 17, 3]
+    rhs = [1, 0, 0, 1, 1, 0, 1, 0]
+    lt = torch.tensor(lhs, dtype=torch.int32, device=dev)
+    rt = torch.tensor(rhs, dtype=torch.int32, device=dev)
+    if bits == 16:
+        w = _bf16(orc, (0.05 * rng.standard_normal((E, N, Kd))).astype(np.float32), dev)
+        got = pkg.ops.gather_mm(x, w, lt, rt)
+        want = orc.gather_mm(_np(orc, x), _np(orc, w), rhs, lhs)
+    else:
+        wq, sc, bi = _qbank(pkg, orc, E, N, Kd, bits, dev, 51)
+        got = pkg.ops.gather_qmm(x, wq, sc, bi, lt, rt, True, 64, bits)
+        want = orc.gather_qmm(_np(orc, x), _np(orc, wq), _np(orc, sc), _np(orc, bi), rhs, lhs,
+                              bits=bits, tiled=True)
+    assert tuple(got.shape) == (B, M, N)
+    _close(orc.bf16_to_f32(_np(orc, got)), orc.bf16_to_f32(want), bits)
+
+
 def test_gather_qmm_out_of_range_index(pkg, orc, dev):
     wq, sc, bi = _qbank(pkg, orc, 4, 64, 64, 4, dev, 3)
     x = torch.ones((3, 1, 64), dtype=torch.bfloat16, device=dev)
@@ -245,6 +271,78 @@ def test_gather_qmm_out_of_range_index(pkg, orc, dev):
     assert torch.all(got[1] == 0)
     ok = pkg.ops.gather_qmm(x[[0, 2]], wq, sc, bi, None, idx[[0, 2]])
     assert torch.equal(got[[0, 2]], ok)
+
+
+# ----------------------------------------------- gather_mm (dense bf16)
+def test_gather_mm_reference_example(pkg, dev):
+    """arithmetic.rs:1565-1575 at the kernels' 64-multiple sizes: a = ones
+    [5, 64, 64], b = ones [3, 64, 64], lhs (0, 2), rhs (2, 1) -> all 64."""
+    a = torch.ones((5, 64, 64), dtype=torch.bfloat16, device=dev)
+    b = torch.ones((3, 64, 64), dtype=torch.bfloat16, device=dev)
+    lhs = torch.tensor([0, 2], dtype=torch.int32, device=dev)
+    rhs = torch.tensor([2, 1], dtype=torch.int32, device=dev)
+    out = pkg.ops.gather_mm(a, b, lhs, rhs)
+    assert tuple(out.shape) == (2, 64, 64)
+    assert torch.all(out.float() == 64.0)
+
+
+@pytest.mark.parametrize("T,K,E,N,Kd", [
+    (1, 8, 128, 768, 2048), (64, 8, 128, 2048, 768), (7, 10, 512, 512, 2048),
+    (300, 8, 16, 128, 256), (40, 1, 2, 64, 64), (1024, 4, 8, 256, 512),
+    (600, 8, 32, 384, 1024), (5, 8, 256, 1024, 4096)])
+def test_gather_mm_moe_shapes(pkg, orc, dev, T, K, E, N, Kd):
+    """SwitchLinear::apply (switch.rs:84-93): x [T, 1, 1, Kd] against
+    indices [T, K] -> [T, K, 1, N], against the oracle's gather_mm (f32
+    accumulation in another order: the bf16 outputs agree within the
+    block tolerance)."""
+    print(f"  gather_mm T={T} K={K} E={E} N={N} Kd={Kd}", flush=True)
+    rng = np.random.default_rng(T * 7 + E)
+    w = _bf16(orc, (0.05 * rng.standard_normal((E, N, Kd))).astype(np.float32), dev)
+    x = _bf16(orc, rng.standard_normal((T, 1, 1, Kd)).astype(np.float32), dev)
+    idx = rng.integers(0, E, (T, K)).astype(np.int32)
+    if T > 4:
+        idx[: T // 2, 0] = 3 % E  # one expert with many rows
+    lin = pkg.nn.SwitchLinear(w)
+    got = lin.apply(x, torch.from_numpy(idx).to(dev))
+    assert tuple(got.shape) == (T, K, 1, N)
+    want = orc.gather_mm(_np(orc, x).reshape(T, 1, Kd), _np(orc, w), idx.reshape(-1),
+                         nthreads=16)
+    _close(orc.bf16_to_f32(_np(orc, got)).reshape(T * K, N),
+           orc.bf16_to_f32(want).reshape(T * K, N), (T, K, E, N, Kd))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_mm_is_tiled_gather_qmm_of_dequant(pkg, orc, dev, bits):
+    """quantization.rs:344-421: gather_qmm(x, w) == gather_mm(x,
+    dequantize(w)).  Where gather_qmm runs the M-tiled kernel (weights
+    dequantised to bf16 tiles) the two calls multiply the same bf16 values
+    in the same order: bit for bit."""
+    E, N, Kd, T, K = 8, 256, 512, 1024, 4
+    assert pkg.ops.gather_qmm_tiled(T * K, E)
+    wq, sc, bi = _qbank(pkg, orc, E, N, Kd, bits, dev, 40 + bits)
+    wd = pkg.ops.dequantize(wq, sc, bi, 64, bits)
+    rng = np.random.default_rng(41)
+    x = _bf16(orc, rng.standard_normal((T, 1, 1, Kd)).astype(np.float32), dev)
+    idx = torch.from_numpy(rng.integers(0, E, (T, K)).astype(np.int32)).to(dev)
+    q = pkg.ops.gather_qmm(x, wq, sc, bi, None, idx, True, 64, bits)
+    m = pkg.ops.gather_mm(x, wd.reshape(E, N, Kd), None, idx)
+    assert torch.equal(q, m)
+
+
+@pytest.mark.parametrize("T,E", [(1, 256), (40, 256), (1024, 128)])
+def test_router_topk_bf16_linear_bit_exact(pkg, orc, dev, T, E):
+    """A bf16 Linear router (an unquantised checkpoint's mlp.gate): bf16
+    logits in the lane order, top-K on the bf16 probabilities, bit for bit,
+    through each logits kernel."""
+    rng = np.random.default_rng(T + E)
+    d, K = 2048, 8
+    x = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev)
+    w = _bf16(orc, (rng.standard_normal((E, d)) * 0.05).astype(np.float32), dev)
+    idx, wts = pkg.ops.router_topk_quantized(x, pkg.nn.Linear(w), K)
+    lg = orc.router_logits_q(_np(orc, x), _np(orc, w), None, None, 16)
+    ridx, rw = orc.router_topk_bf16(lg, K)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(wts.cpu().numpy(), rw)
 
 
 # -------------------------------------------------------- combine

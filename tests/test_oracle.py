@@ -542,3 +542,138 @@ def test_packed_switch_glu_equals_split_composition(orc, act):
     assert np.array_equal(out_f, orc.combine(y, wf))
     out_b = orc.packed_switch_glu(x, gu, down, idx, wb, act=act, w_bf16=True)
     assert np.array_equal(out_b, orc.combine_bf16(y, wb))
+
+
+# ------------------------------------------------- dense gather_mm (bf16)
+def test_gather_mm_reference_example(orc):
+    """arithmetic.rs:1565-1575: a = ones [5, 32, 32], b = ones [3, 32, 32],
+    lhs (0, 2), rhs (2, 1) -> [2, 32, 32], every entry 32."""
+    one = orc.f32_to_bf16(np.ones(1, np.float32))[0]
+    a = np.full((5, 32, 32), one, np.uint16)
+    b = np.full((3, 32, 32), one, np.uint16)
+    out = orc.gather_mm(a, b, [2, 1], [0, 2])
+    assert out.shape == (2, 32, 32)
+    assert np.all(orc.bf16_to_f32(out) == 32.0)
+
+
+def test_gather_mm_fp64_bound_and_indices(orc):
+    """f32 accumulation of exact bf16 products: within K * 2^-24 * |x||w| of
+    the fp64 matmul, then one bf16 rounding; lhs indices and the x broadcast
+    over the trailing index axis pick the same rows."""
+    rng = np.random.default_rng(31)
+    E, N, K, T, k = 5, 96, 320, 7, 3
+    w = orc.f32_to_bf16(rng.standard_normal((E, N, K)).astype(np.float32))
+    x = orc.f32_to_bf16(rng.standard_normal((T, 1, K)).astype(np.float32))
+    idx = rng.integers(0, E, (T, k)).astype(np.int32).reshape(-1)
+    got = orc.bf16_to_f32(orc.gather_mm(x, w, idx))[:, 0].astype(np.float64)
+    wf = orc.bf16_to_f32(w).astype(np.float64)
+    xf = orc.bf16_to_f32(x).astype(np.float64)[:, 0]
+    rows = np.repeat(np.arange(T), k)
+    exact = np.stack([wf[idx[i]] @ xf[rows[i]] for i in range(T * k)])
+    bound = np.stack([np.abs(wf[idx[i]]) @ np.abs(xf[rows[i]]) for i in range(T * k)])
+    assert np.all(np.abs(got - exact) <= K * 2.0 ** -24 * bound + 2.0 ** -8 * np.abs(exact))
+    assert np.array_equal(orc.gather_mm(x, w, idx), orc.gather_mm(x, w, idx, rows))
+
+
+def test_gather_mm_is_tiled_gather_qmm_of_dequant(orc):
+    """quantization.rs:344-421 states gather_qmm(x, w) == gather_mm(x,
+    dequantize(w)^T): at 4 bits the oracle's tiled gather_qmm and its
+    gather_mm over the bf16 dequantised weights sum the same products in the
+    same order, so they agree bit for bit."""
+    rng = np.random.default_rng(32)
+    E, N, K, T = 4, 64, 256, 24
+    wq, sc, bi = orc.quantize(orc.f32_to_bf16(0.02 * rng.standard_normal((E, N, K)).astype(np.float32)),
+                              64, 4)
+    wd = orc.dequantize(wq, sc, bi, 64, 4, out_bf16=True).reshape(E, N, K)
+    x = orc.f32_to_bf16(rng.standard_normal((T, 1, K)).astype(np.float32))
+    rhs = rng.integers(0, E, T).astype(np.int32)
+    assert np.array_equal(orc.gather_qmm(x, wq, sc, bi, rhs, bits=4, tiled=True),
+                          orc.gather_mm(x, wd, rhs))
+
+
+def _dequant_params(orc, p):
+    """The block parameters with every 4-bit expert bank replaced by its bf16
+    dequantisation (dense SwitchLinear / Linear weights)."""
+    d = dict(p, bits=16)
+    for k in ("gate", "up", "down", "shared_gate", "shared_up", "shared_down"):
+        if p.get(k) is not None:
+            wq, sc, bi = p[k]
+            E, N = wq.shape[0], wq.shape[1]
+            K = wq.shape[2] * 32 // p["bits"]
+            d[k] = (orc.dequantize(wq, sc, bi, 64, p["bits"], out_bf16=True).reshape(E, N, K),
+                    None, None)
+    return d
+
+
+@pytest.mark.parametrize("fs", [0, 256])
+def test_block_dense_experts_equal_tiled_4bit_block(orc, fs):
+    """A block with dense bf16 experts (gather_mm) equals, bit for bit, the
+    4-bit block whose weights dequantise to them, on the tiled numerics
+    (gather_qmm == gather_mm(dequantize(w)), quantization.rs:344-421)."""
+    p, x = _c1_params(orc, fs=fs)
+    ref, ridx, rw = orc.block_forward(p, x, tiled=(True, True))
+    got, gidx, gw = orc.block_forward(_dequant_params(orc, p), x)
+    assert np.array_equal(gidx, ridx) and np.array_equal(gw, rw)
+    assert np.array_equal(got, ref)
+
+
+def _exact_q8(orc, rng, shape):
+    """8-bit codes with scale 2^-7 and bias -1: every dequantised weight
+    code/128 - 1 is exact in f32 and in bf16.  Returns the QuantizedLinear
+    (wq, scales, biases) and the same weights as bf16 bits."""
+    rows, d = shape
+    codes = rng.integers(0, 256, (rows, d)).astype(np.uint32)
+    c4 = codes.reshape(rows, d // 4, 4)
+    wq = c4[..., 0] | (c4[..., 1] << 8) | (c4[..., 2] << 16) | (c4[..., 3] << 24)
+    sc = np.full((rows, d // 64), orc.f32_to_bf16(np.float32(2.0 ** -7)), np.uint16)
+    bi = np.full((rows, d // 64), orc.f32_to_bf16(np.float32(-1.0)), np.uint16)
+    wd = orc.f32_to_bf16((codes.astype(np.float32) / 128.0 - 1.0).astype(np.float32))
+    return (wq.astype(np.uint32), sc, bi), wd
+
+
+def test_bf16_linear_router_equals_exact_8bit_router(orc):
+    """A bf16 Linear router (bits 16) computes what the 8-bit
+    QuantizedLinear router computes when its codes dequantise exactly to the
+    bf16 weights: the same logits, routing and block output, bit for bit."""
+    rng = np.random.default_rng(33)
+    p, x = _c1_params(orc, fs=256, router_bits=8)
+    rq, rd = _exact_q8(orc, rng, (p["E"], p["d"]))
+    sq, sd = _exact_q8(orc, rng, (1, p["d"]))
+    # scale the router input so the logits stay O(1)
+    x = orc.f32_to_bf16((orc.bf16_to_f32(x) * 0.02).astype(np.float32))
+    lq = orc.router_logits_q(x, *rq, 8)
+    ld = orc.router_logits_q(x, rd, None, None, 16)
+    assert np.array_equal(lq, ld)
+    p8 = dict(p, router_q=rq, shared_gate_q=sq, router_bits=8)
+    p16 = dict(p, router_q=(rd, None, None), shared_gate_q=(sd, None, None), router_bits=16)
+    o8, i8, w8 = orc.block_forward(p8, x)
+    o16, i16, w16 = orc.block_forward(p16, x)
+    assert np.array_equal(i8, i16) and np.array_equal(w8, w16) and np.array_equal(o8, o16)
+    # fp64 bound on the dense logits themselves
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    wf = orc.bf16_to_f32(rd).astype(np.float64)
+    exact = xf @ wf.T
+    bound = np.abs(xf) @ np.abs(wf).T
+    assert np.all(np.abs(ld - exact) <= p["d"] * 2.0 ** -24 * bound + 2.0 ** -8 * np.abs(exact))
+
+
+def test_packed_switch_glu_dense_equals_split_composition(orc):
+    """PackedSwitchFfn over a dense [E, 2H, d] gate_up (SwitchLinear) is the
+    two gather_mm halves, the activation, the down gather_mm and the
+    combine."""
+    rng = np.random.default_rng(34)
+    E, d, H, T, K = 6, 256, 128, 9, 2
+    gu = orc.f32_to_bf16((0.05 * rng.standard_normal((E, 2 * H, d))).astype(np.float32))
+    dn = orc.f32_to_bf16((0.05 * rng.standard_normal((E, d, H))).astype(np.float32))
+    x = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, K)).astype(np.float32)
+    for act, fn in ((1, orc.geglu), (0, orc.swiglu)):
+        out = orc.packed_switch_glu(x, (gu, None, None), (dn, None, None), idx, w, act=act,
+                                    w_bf16=False)
+        ids = idx.reshape(-1)
+        xs = np.repeat(x, K, axis=0)[:, None, :]
+        g = orc.gather_mm(xs, np.ascontiguousarray(gu[:, :H]), ids)
+        u = orc.gather_mm(xs, np.ascontiguousarray(gu[:, H:]), ids)
+        y = orc.gather_mm(fn(g, u), dn, ids).reshape(T, K, d)
+        assert np.array_equal(out, orc.combine(y, w))
