@@ -32,12 +32,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="c2", help="c1..c5 (default c2, the decode block)")
+    ap.add_argument("--config", default="c2", help="c1..c8 (default c2, the decode block)")
     ap.add_argument("--tokens", type=int, default=64, help="T of the headline line")
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
                     help="replay one captured HIP graph per step, or launch eagerly")
     ap.add_argument("--sweep", default="c2:1,c2:8,c2:32,c3:512,c3:2048,c3:4096,c4:64,c4:2048,"
-                    "c5:32,c5:512,c6:64,c6:2048,c7:64,c7:2048",
+                    "c5:32,c5:512,c6:64,c6:2048,c7:64,c7:2048,c8:64,c8:2048",
                     help="extra cfg:T points timed after the headline ('' for none)")
     ap.add_argument("--sweep-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -147,10 +147,10 @@ class Runner:
 
 def gated_bytes(cfg, T, U):
     """Algorithmic HBM bytes of one gate/up launch: the packed words plus
-    bf16 scales and biases of the U distinct selected experts' gate and up
-    rows (2*f*d weights each), x read once (T*d bf16) and the activations
-    written (T*K*f bf16)."""
-    per_w = cfg.bits / 8 + 4 / cfg.group_size
+    bf16 scales and biases (or the dense bf16 weights) of the U distinct
+    selected experts' gate and up rows (2*f*d weights each), x read once
+    (T*d bf16) and the activations written (T*K*f bf16)."""
+    per_w = 2.0 if cfg.bits == 16 else cfg.bits / 8 + 4 / cfg.group_size
     return int(U * 2 * cfg.f * cfg.d * per_w + T * cfg.d * 2 + T * cfg.K * cfg.f * 2)
 
 

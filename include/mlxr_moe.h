@@ -363,7 +363,8 @@ int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,
  * models with criterion, crates/mlxr-lm/benches/lm_decode.rs): while
  * `kernel` is armed, each launch of that kernel is bracketed by HIP events
  * on the stream it is launched on.  Names: "router_logits", "router_topk",
- * "dispatch", "qgemm_gated", "qgemm_down", "combine".  NULL disarms.  Not
+ * "dispatch", "qgemm_gated", "qgemm_down", "combine", and the shared
+ * expert's GEMMs "shared_gated", "shared_down".  NULL disarms.  Not
  * for use while the stream is being captured into a graph. */
 int mlxr_moe_profile_start(const char* kernel);
 /* Waits for the armed kernel's last launch, returns the number of launches

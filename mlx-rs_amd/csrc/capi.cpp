@@ -162,7 +162,7 @@ int run_gather(const char* op, const void* x, int64_t x_batch, int64_t M,
   a.out_by_flat = true;
   a.gated = false;
   return finish(from_hip(launch_qgemm(a, R, dispatch_max_work(R, E),
-                                      nn::use_prefill_path(R, E), s),
+                                      nn::use_prefill_path(R, E, bits), s),
                          op));
 }
 
@@ -751,7 +751,8 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
 int mlxr_moe_profile_start(const char* kernel) {
   static const char* const kNames[] = {"router_logits", "router_topk",
                                        "dispatch",      "qgemm_gated",
-                                       "qgemm_down",    "combine"};
+                                       "qgemm_down",    "combine",
+                                       "shared_gated",  "shared_down"};
   if (kernel && *kernel) {
     bool known = false;
     for (const char* n : kNames) known = known || std::strcmp(n, kernel) == 0;

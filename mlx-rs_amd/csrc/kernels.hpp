@@ -202,9 +202,13 @@ constexpr int kPrefillMinTileRows = 128;
 int prefill_tile_rows(int64_t rows, int64_t experts);
 // max_items bounds the number of work items (dispatch_max_work); prefill
 // selects the M-tiled kernel (prefill.hip) where it applies.  Dense bf16
-// weights (bits 16) always take the M-tiled kernel.
+// weights (bits 16) take the split-K decode kernel or the M-tiled one.
+// `profile` names the launch for ProfileScope (default "qgemm_gated" or
+// "qgemm_down"; the shared expert's GEMMs are "shared_gated" /
+// "shared_down").
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
-                        int64_t max_items, bool prefill, hipStream_t s);
+                        int64_t max_items, bool prefill, hipStream_t s,
+                        const char* profile = nullptr);
 
 // ---------------------------------------------------------------- prefill.hip
 // x_rows bounds the rows of x the GEMM reads; tile_rows is the M-tile height
@@ -213,7 +217,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
 bool prefill_supported(const QGemmArgs& a, int64_t x_rows);
 hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 int tile_rows, int64_t max_tiles,
-                                hipStream_t s);
+                                hipStream_t s, const char* profile);
 
 // -------------------------------------------------------------- combine.hip
 // out f32 [T, d], or bf16 when bf16 (the routing weights are then bf16

@@ -74,7 +74,15 @@ DispatchBuffers carve_dispatch(Carve& c, int64_t n, int64_t E,
 
 namespace nn {
 
-bool use_prefill_path(int64_t rows, int64_t experts) {
+bool use_prefill_path(int64_t rows, int64_t experts, int bits) {
+  // Dense bf16 weights: the split-K kernel reads an expert's weights once
+  // per work item (kWorkRows rows), the M-tiled one once per M-tile, with
+  // no dequantisation to pay for; it takes over from
+  // MLXR_DENSE_TILED_ROWS rows per expert (measured on the c8 block: 2),
+  // given rows enough for its tiles to fill the GPU (one expert with 16
+  // rows makes four gate/up tiles).
+  if (bits == 16)
+    return rows >= (int64_t)MLXR_DENSE_TILED_ROWS * experts && rows >= 512;
   // the M-tiled kernel pays once the experts average 32 rows and there are
   // rows enough for its tiles to spread over the GPU
   return rows >= 32 * experts && rows >= 512;
@@ -116,7 +124,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   Status st = from_hip(launch_dispatch_identity(T, prefill_tile_rows(T, 1), db, s),
                        "shared_expert dispatch");
   if (!st.ok) return st;
-  const bool prefill = use_prefill_path(T, 1);
+  const bool prefill = use_prefill_path(T, 1, gate_.bits);
   QGemmArgs g{};
   g.x = x;
   g.x_ld = d;
@@ -145,7 +153,8 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   g.out_ld = f;
   g.gated = true;
   const int64_t items = dispatch_max_work(T, 1);
-  st = from_hip(launch_qgemm(g, T, items, prefill, s), "shared_expert gate/up");
+  st = from_hip(launch_qgemm(g, T, items, prefill, s, "shared_gated"),
+                "shared_expert gate/up");
   if (!st.ok) return st;
   QGemmArgs h = g;
   h.x = act;
@@ -160,7 +169,8 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   h.out = y;
   h.out_ld = d;
   h.gated = false;
-  return from_hip(launch_qgemm(h, T, items, prefill, s), "shared_expert down");
+  return from_hip(launch_qgemm(h, T, items, prefill, s, "shared_down"),
+                  "shared_expert down");
 }
 
 // ----------------------------------------------------------- switch FFNs
@@ -268,7 +278,7 @@ Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   const int64_t n = T * K;
   uint16_t* act = ws.take<uint16_t>(n * f);
   const int64_t max_items = dispatch_max_work(n, E);
-  const bool prefill = use_prefill_path(n, E);
+  const bool prefill = use_prefill_path(n, E, sw_.bits);
   QGemmArgs g{};
   g.x = x;
   g.x_ld = d;

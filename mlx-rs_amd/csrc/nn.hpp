@@ -55,7 +55,12 @@ namespace nn {
 // weights runs instead of the register-dequant kernel (the reference
 // switches to its sorted path at T*K >= SORT_THRESHOLD = 2048, switch.rs:40;
 // here the choice is about GEMM shape, not sorting, which always happens).
-bool use_prefill_path(int64_t rows, int64_t experts);
+// Dense bf16 GEMMs (bits 16) switch at MLXR_DENSE_TILED_ROWS rows per
+// expert.
+#ifndef MLXR_DENSE_TILED_ROWS
+#define MLXR_DENSE_TILED_ROWS 2
+#endif
+bool use_prefill_path(int64_t rows, int64_t experts, int bits = 4);
 
 class SwigluMlp {
  public:

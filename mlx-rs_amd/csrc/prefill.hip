@@ -1,7 +1,7 @@
 // Grouped quantised expert GEMM for many rows per expert (prefill): an
 // LDS-tiled bf16 MFMA GEMM that dequantises each weight tile once per
 // workgroup.  The same kernel runs dense bf16 expert weights (gather_mm,
-// bits = 16: the weight tile is staged as it is) at every row count.
+// bits = 16: the weight tile is staged as it is).
 //
 // Same operation as the decode kernels (gather_qmm with transpose = true,
 // crates/mlxr/src/ops/quantization.rs:171-221, as called by
@@ -158,9 +158,9 @@ bool prefill_supported(const QGemmArgs& a, int64_t x_rows) {
 
 hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 int tile_rows, int64_t max_tiles,
-                                hipStream_t s) {
-  if (tile_rows == tile256::kBM) return tile256::launch(a, x_rows, max_tiles, s);
-  if (tile_rows == tile128::kBM) return tile128::launch(a, x_rows, max_tiles, s);
+                                hipStream_t s, const char* profile) {
+  if (tile_rows == tile256::kBM) return tile256::launch(a, x_rows, max_tiles, s, profile);
+  if (tile_rows == tile128::kBM) return tile128::launch(a, x_rows, max_tiles, s, profile);
   return hipErrorInvalidValue;
 }
 

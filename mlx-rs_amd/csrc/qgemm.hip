@@ -25,6 +25,9 @@
 // The input dim is split over the waves of a workgroup (two groups per wave
 // per pass) so each wave keeps its x slice in registers and re-reads only
 // weights; the partial sums meet in LDS.
+// Dense bf16 weights (gather_mm, bits 16) run the same split-K kernel with
+// the weights as the MFMA operand and no group terms (P alone), or the
+// M-tiled kernel for many rows per expert.
 #include <algorithm>
 
 #include "common.hpp"
@@ -123,12 +126,17 @@ __device__ __forceinline__ u32x4_t unpack8(uint32_t w0, uint32_t w1) {
 // group (its own scale and bias), so at 4-bit the x operand exists twice per
 // step, zero on the lanes of the other group: xa feeds the first group's
 // sums, xb the second's, and the weight operand is shared.
-template <int NM, int SPW>
+// Dense bf16 weights (BITS 16) take two 16-byte loads per lane per step:
+// one group of 64 weights per row, lane q holding weights 16q..16q+15 (the
+// 8-bit lane layout), and no scales or biases.
+template <int NM, int SPW, int WV = 1>
 struct StepBuf {
-  u32x4_t w[NM][SPW];
+  u32x4_t w[NM][SPW][WV];
   uint32_t s[NM][SPW];  // bf16 scales: 4-bit (first | second << 16), 8-bit g
   uint32_t b[NM][SPW];  // bf16 biases, same packing
 };
+template <int BITS>
+constexpr int kStepWords = BITS == 16 ? 2 : 1;  // 16-byte loads per step
 
 // Scale or bias bits of one step: both groups at 4-bit (one u32 when
 // 4-byte aligned), the one group at 8-bit.
@@ -141,7 +149,7 @@ __device__ __forceinline__ uint32_t load_sb(const uint16_t* p, bool pair,
 // Loads of one 16-channel block: row `wrow` (this lane's channel), groups
 // [G0, G0 + mg) of this wave.  Nothing past the row's last group is read.
 template <int BITS, int NM, int SPW>
-__device__ __forceinline__ void load_steps(StepBuf<NM, SPW>& bb,
+__device__ __forceinline__ void load_steps(StepBuf<NM, SPW, kStepWords<BITS>>& bb,
                                            const QGemmArgs& a, int64_t wrow,
                                            int groups, int G0, int mg, int q,
                                            bool sb_pairs) {
@@ -150,25 +158,33 @@ __device__ __forceinline__ void load_steps(StepBuf<NM, SPW>& bb,
   for (int m = 0; m < NM; ++m) {
     const QWeights& W = m == 0 ? a.w0 : a.w1;
     const uint32_t* wr = W.w + wrow * groups * (2 * BITS);
-    const uint16_t* sr = W.scales + wrow * groups;
-    const uint16_t* br = W.biases + wrow * groups;
 #pragma unroll
     for (int st = 0; st < SPW; ++st) {
       const int g0 = G0 + GPS * st;  // first group of the step
-      bb.w[m][st] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int v = 0; v < kStepWords<BITS>; ++v) bb.w[m][st][v] = u32x4_t{0u, 0u, 0u, 0u};
       bb.s[m][st] = 0u;
       bb.b[m][st] = 0u;
       if (GPS * st < mg) {
-        if constexpr (BITS == 4) {
+        if constexpr (BITS == 16) {
+          // weights 16q..16q+7 and 16q+8..16q+15 of the group (32 words)
+          const uint32_t* p = wr + g0 * 32 + 8 * q;
+          bb.w[m][st][0] = *reinterpret_cast<const u32x4_t*>(p);
+          bb.w[m][st][1] = *reinterpret_cast<const u32x4_t*>(p + 4);
+        } else if constexpr (BITS == 4) {
+          const uint16_t* sr = W.scales + wrow * groups;
+          const uint16_t* br = W.biases + wrow * groups;
           const int gl = g0 + (q >> 1);  // this lane's group
           if (gl < G0 + mg)
-            bb.w[m][st] = *reinterpret_cast<const u32x4_t*>(
+            bb.w[m][st][0] = *reinterpret_cast<const u32x4_t*>(
                 wr + gl * 8 + 4 * (q & 1));
           const bool two = g0 + 1 < G0 + mg;
           bb.s[m][st] = load_sb(sr + g0, sb_pairs && two, two);
           bb.b[m][st] = load_sb(br + g0, sb_pairs && two, two);
         } else {
-          bb.w[m][st] =
+          const uint16_t* sr = W.scales + wrow * groups;
+          const uint16_t* br = W.biases + wrow * groups;
+          bb.w[m][st][0] =
               *reinterpret_cast<const u32x4_t*>(wr + g0 * 16 + 4 * q);
           bb.s[m][st] = sr[g0];
           bb.b[m][st] = br[g0];
@@ -246,7 +262,7 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
     for (int pass = 0; pass < passes; ++pass) {
       const int G0 = pass * per_pass + wave * GW;
       const int mg = max(0, min(GW, groups - G0));
-      StepBuf<NM, SPW> buf[CB > 1 ? 2 : 1];
+      StepBuf<NM, SPW, kStepWords<BITS>> buf[CB > 1 ? 2 : 1];
       load_steps<BITS, NM, SPW>(buf[0], a, wrow0, groups, G0, mg, q,
                                 sb_pairs);
       // x slice (A operand) and the per-group sums X
@@ -282,6 +298,7 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
       for (int st = 0; st < SPW; ++st) {
         XA[st] = zero;
         XB[st] = zero;
+        if constexpr (BITS == 16) continue;  // no bias term
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
           XA[st] = mfma16x16x32(xa[st][i], as_bf16x8(ones), XA[st]);
@@ -295,15 +312,21 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
           load_steps<BITS, NM, SPW>(buf[(bi + 1) & 1], a,
                                     wrow0 + (bi + 1) * 16, groups, G0, mg, q,
                                     sb_pairs);
-        const StepBuf<NM, SPW>& cur = buf[bi & 1];
+        const StepBuf<NM, SPW, kStepWords<BITS>>& cur = buf[bi & 1];
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
           f32x4_t ac = acc[bi][m];
 #pragma unroll
           for (int st = 0; st < SPW; ++st) {
             if (GPS * st < mg) {
-              const u32x4_t wv = cur.w[m][st];
-              if constexpr (BITS == 4) {
+              const u32x4_t wv = cur.w[m][st][0];
+              if constexpr (BITS == 16) {
+                // the weights are the B operand as they are
+                f32x4_t P = mfma16x16x32(xa[st][0], as_bf16x8(wv), zero);
+                P = mfma16x16x32(xa[st][1], as_bf16x8(cur.w[m][st][kStepWords<BITS> - 1]), P);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ac[r] += P[r];
+              } else if constexpr (BITS == 4) {
                 f32x4_t PA = zero, PB = zero;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -685,17 +708,17 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
 }  // namespace
 
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
-                        int64_t max_items, bool prefill, hipStream_t s) {
+                        int64_t max_items, bool prefill, hipStream_t s,
+                        const char* profile) {
   if (max_items <= 0) return hipSuccess;
+  if (!profile) profile = a.gated ? "qgemm_gated" : "qgemm_down";
   // the M-tiled kernel reads x through a buffer of x's own rows (gathered
   // rows may lie anywhere in it: gather_mm / gather_qmm with lhs indices)
   const int64_t x_rows = a.x_rows > 0 ? a.x_rows : total_rows;
-  // dense bf16 weights run on the tiled kernel at every row count
-  if (a.bits == 16 && !prefill_supported(a, x_rows)) return hipErrorInvalidValue;
-  if ((prefill || a.bits == 16) && prefill_supported(a, x_rows)) {
+  if (prefill && prefill_supported(a, x_rows)) {
     const int tile_rows = prefill_tile_rows(total_rows, a.E);
     return launch_qgemm_prefill(a, x_rows, tile_rows,
-                                dispatch_max_tiles(total_rows, a.E, tile_rows), s);
+                                dispatch_max_tiles(total_rows, a.E, tile_rows), s, profile);
   }
   const int groups = a.K / 64;
   // Many (expert, block) items: the streaming kernel (one block per wave,
@@ -706,7 +729,8 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   };
   const bool sb16 = a16(a.w0.scales) && a16(a.w0.biases) &&
                     (!a.gated || (a16(a.w1.scales) && a16(a.w1.biases)));
-  if (max_items * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0 &&
+  // (dense bf16 weights, bits 16, take the split-K kernel below)
+  if (a.bits != 16 && max_items * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0 &&
       groups % 4 == 0 && sb16) {
     constexpr int kWaves = MLXR_STREAM_WAVES, kMaxTT = 8;
     // blocks per wave: about one workgroup per slot (two per CU), so x is
@@ -724,7 +748,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
          ~size_t(15)) +
         (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
     const dim3 grid((unsigned)(max_items * tiles_n));
-    ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
+    ProfileScope prof(profile, s);
 #define MLXR_QS(B, G, D, NB) \
   qgemm_stream_kernel<B, G, D, NB><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n)
     if (a.bits == 4) {
@@ -766,7 +790,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   const size_t lds = (size_t)kw * cb * nm * 64 * sizeof(f32x4_t);
   const dim3 grid((unsigned)(max_items * tiles_n));
   const dim3 block((unsigned)(64 * kw));
-  ProfileScope prof(a.gated ? "qgemm_gated" : "qgemm_down", s);
+  ProfileScope prof(profile, s);
 #define MLXR_QG(B, G, SPW)                                                  \
   do {                                                                      \
     if (cb == 4)                                                            \
@@ -779,7 +803,12 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
       qgemm_decode_kernel<B, G, SPW, 1>                                     \
           <<<grid, block, lds, s>>>(a, tiles_n);                            \
   } while (0)
-  if (a.bits == 4) {
+  if (a.bits == 16) {
+    if (a.gated)
+      qgemm_decode_kernel<16, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n);
+    else
+      MLXR_QG(16, false, 2);
+  } else if (a.bits == 4) {
     if (a.gated)
       qgemm_decode_kernel<4, true, 1, 1><<<grid, block, lds, s>>>(a, tiles_n);
     else

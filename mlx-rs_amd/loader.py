@@ -137,11 +137,12 @@ def qwen35_moe_block(model_dir, layer: int, device, quantize_dense=None):
 
     Quantised modules keep the checkpoint's codes, scales and biases bit for
     bit, with (group_size, bits) from the config's per-path overrides
-    (quantization.rs:51-56).  Dense bf16 experts are quantised on load when
-    quantize_dense = (group_size, bits) is given (try_into_quantized,
-    switch.rs:478-491); the dense gather_mm path itself is not built here.
-    A dense router is kept in f32 (this library's f32 router; the
-    reference computes a bf16 router in bf16)."""
+    (quantization.rs:51-56).  Dense modules stay dense -- bf16
+    SwitchLinear experts (gather_mm) and Linear projections, the
+    MaybeQuantized::Original form -- unless quantize_dense = (group_size,
+    bits) asks to quantise them on load (try_into_quantized,
+    switch.rs:478-491).  A dense bf16 router computes in bf16 like the
+    reference's (nn.Linear); an f32 one in f32."""
     config = read_config(model_dir)
     tc = text_config(config)
     qc = QuantizationConfig.from_config(config)
@@ -151,12 +152,10 @@ def qwen35_moe_block(model_dir, layer: int, device, quantize_dense=None):
 
     def qlinear(module, cls, expert_dims):
         if not lt.quantised(module):
-            w = lt.get(f"{module}.weight")
+            w = lt.get(f"{module}.weight").to(dev, torch.bfloat16)
             if quantize_dense is None:
-                raise MlxrMoeError(f"weights: {raw}{module} is dense; pass quantize_dense="
-                                   "(group_size, bits) to quantise it on load")
+                return nn.Linear(w) if cls is nn.QuantizedLinear else nn.SwitchLinear(w)
             gs, bits = quantize_dense
-            w = w.to(dev, torch.bfloat16)
             if cls is nn.QuantizedLinear:
                 return cls.try_from_linear(w, gs, bits)
             return cls.try_from_switch_linear(w, gs, bits)
@@ -179,11 +178,18 @@ def qwen35_moe_block(model_dir, layer: int, device, quantize_dense=None):
         shared = nn.SwigluMlp(qlinear("shared_expert.gate_proj", L, 2),
                               qlinear("shared_expert.up_proj", L, 2),
                               qlinear("shared_expert.down_proj", L, 2))
-    quant_router = lt.quantised("gate")
-    if quant_router:
-        gate = qlinear("gate", nn.QuantizedLinear, 2)
+    f32_router = not lt.quantised("gate") and lt.get("gate.weight").dtype == torch.float32
+    if not f32_router:
+        # QuantizedLinear, or bf16 Linear (quantize_dense quantises the
+        # expert and shared-expert projections only; a dense router stays
+        # a bf16 Linear)
+        def router(module):
+            if lt.quantised(module):
+                return qlinear(module, nn.QuantizedLinear, 2)
+            return nn.Linear(lt.get(f"{module}.weight").to(dev, torch.bfloat16))
+        gate = router("gate")
         if shared is not None:
-            sgate = qlinear("shared_expert_gate", nn.QuantizedLinear, 2)
+            sgate = router("shared_expert_gate")
     else:
         gate = lt.get("gate.weight").to(dev, torch.float32)
         if shared is not None:

@@ -110,10 +110,11 @@ def test_read_back_quantised_layer(pkg, orc, tmp_path, shards):
         assert np.array_equal(lin.biases.reshape(bi.shape).view(torch.int16).numpy().view(np.uint16), bi)
 
 
-def test_hf_packed_experts_split_and_quantised_on_load(pkg, tmp_path):
+def test_hf_packed_experts_split_and_loaded_dense(pkg, tmp_path):
     """mlp.experts.gate_up_proj [E, 2H, D] (an unconverted checkpoint) splits
-    along axis 1 into gate and up (mlxr-convert/src/qwen3_5.rs:96-147);
-    dense experts are refused unless quantize_dense asks to quantise them."""
+    along axis 1 into gate and up (mlxr-convert/src/qwen3_5.rs:96-147); the
+    dense experts load as bf16 SwitchLinears (gather_mm) and the bf16 router
+    as a Linear (a bf16 block, as the reference computes it)."""
     E, d, H = 4, 256, 128
     g = torch.Generator().manual_seed(1)
     gu = (torch.randn((E, 2 * H, d), generator=g) * 0.02).to(torch.bfloat16)
@@ -125,5 +126,15 @@ def test_hf_packed_experts_split_and_quantised_on_load(pkg, tmp_path):
     lt = pkg.loader.LayerTensors(tmp_path / "hf", 0)
     assert torch.equal(lt.get("switch_mlp.gate_proj.weight"), gu[:, :H])
     assert torch.equal(lt.get("switch_mlp.up_proj.weight"), gu[:, H:])
-    with pytest.raises(pkg.MlxrMoeError):
-        pkg.loader.qwen35_moe_block(tmp_path / "hf", 0, "cpu")
+    blk = pkg.loader.qwen35_moe_block(tmp_path / "hf", 0, "cpu")
+    m = blk.switch_mlp
+    assert all(isinstance(x, pkg.nn.SwitchLinear) for x in (m.gate_proj, m.up_proj, m.down_proj))
+    assert torch.equal(m.gate_proj.weight, gu[:, :H]) and torch.equal(m.up_proj.weight, gu[:, H:])
+    assert torch.equal(m.down_proj.weight, dn)
+    assert isinstance(blk.gate_weight, pkg.nn.Linear) and blk.quantised_router
+    assert blk.out_dtype == torch.bfloat16 and blk.shared_expert is None
+    # an f32 router stays the f32 Linear path
+    t[p + "gate.weight"] = t[p + "gate.weight"].float()
+    _write_checkpoint(tmp_path / "hf32", t, {"text_config": {"num_experts_per_tok": 2}})
+    blk = pkg.loader.qwen35_moe_block(tmp_path / "hf32", 0, "cpu")
+    assert not blk.quantised_router and blk.gate_weight.dtype == torch.float32
