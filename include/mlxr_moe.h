@@ -353,6 +353,37 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
                            float* topk_w, void* workspace,
                            size_t workspace_size, mlxr_moe_stream stream);
 
+/* fast::rms_norm as RmsNorm::forward calls it (crates/mlxr/src/layers/
+ * normalization.rs:272-276; gemma4's router, crates/mlxr-lm/src/gemma4/
+ * text/text.rs:640): x bf16 [T, d], weight bf16 [d] -> out bf16 [T, d],
+ *   out_j = bf16(w_j * bf16(x_j * r)),  r = 1 / sqrt(sum_j x_j^2 / d + eps)
+ * (the normalised value in the input dtype, then the weight product, MLX's
+ * rounding points; the sum of squares in a fixed 64-lane order).  d % 4 ==
+ * 0, x 8-byte aligned. */
+int mlxr_moe_rms_norm(const void* x, int64_t T, int64_t d, const void* weight,
+                      float eps, void* out, mlxr_moe_stream stream);
+
+/* The MoE half of a Qwen3.5 / Qwen3.6 decoder layer (DecoderLayer::forward,
+ * crates/mlxr-lm/src/qwen3_5/text/layer.rs:134-138):
+ *   out = h + block(rms_norm(h, norm_weight, eps))
+ * h bf16 [T, d] (the residual stream after attention); norm_weight bf16 [d],
+ * post_attention_layernorm.weight as the model holds it (after the loader's
+ * +1.0 shift of non-mlx-format checkpoints, crates/mlxr-lm/src/qwen3_5/text/
+ * weights.rs:147-165); eps = rms_norm_eps.  out as mlxr_moe_block_forward's:
+ * f32 with the f32 router (bf16 h + f32 promotes), bf16 with a bf16 router
+ * (bf16(h + mlp_out)).  The norm is one kernel before the block and the
+ * residual add rides in the block's combine.  Workspace:
+ * mlxr_moe_block_residual_workspace_size (the block's plus the normed rows);
+ * its status word is the block's (mlxr_moe_workspace_status). */
+size_t mlxr_moe_block_residual_workspace_size(const mlxr_moe_block* block,
+                                              int64_t T);
+int mlxr_moe_block_forward_residual(const mlxr_moe_block* block,
+                                    const void* norm_weight, float eps,
+                                    const void* h, int64_t T, void* out,
+                                    int32_t* topk_idx, float* topk_w,
+                                    void* workspace, size_t workspace_size,
+                                    mlxr_moe_stream stream);
+
 /* Device status word of a workspace used by gather_qmm / dispatch /
  * switch_glu / block calls: 0 = all indices in range, 1 = some index out of
  * range.  Synchronises `stream`.  Returns the status or -1 on error. */
@@ -363,8 +394,9 @@ int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,
  * models with criterion, crates/mlxr-lm/benches/lm_decode.rs): while
  * `kernel` is armed, each launch of that kernel is bracketed by HIP events
  * on the stream it is launched on.  Names: "router_logits", "router_topk",
- * "dispatch", "qgemm_gated", "qgemm_down", "combine", and the shared
- * expert's GEMMs "shared_gated", "shared_down".  NULL disarms.  Not
+ * "dispatch", "qgemm_gated", "qgemm_down", "combine", the shared
+ * expert's GEMMs "shared_gated", "shared_down", and "rms_norm".  NULL
+ * disarms.  Not
  * for use while the stream is being captured into a graph. */
 int mlxr_moe_profile_start(const char* kernel);
 /* Waits for the armed kernel's last launch, returns the number of launches

@@ -130,6 +130,10 @@ SIGNATURES = {
         c_int, [POINTER(GemmaRouter), P, c_int64, P, P, P, c_size_t, P]),
     "mlxr_moe_block_workspace_size": (c_size_t, [POINTER(Block), c_int64]),
     "mlxr_moe_block_forward": (c_int, [POINTER(Block), P, c_int64, P, P, P, P, c_size_t, P]),
+    "mlxr_moe_rms_norm": (c_int, [P, c_int64, c_int64, P, c_float, P, P]),
+    "mlxr_moe_block_residual_workspace_size": (c_size_t, [POINTER(Block), c_int64]),
+    "mlxr_moe_block_forward_residual": (
+        c_int, [POINTER(Block), P, c_float, P, c_int64, P, P, P, P, c_size_t, P]),
     "mlxr_moe_workspace_status": (c_int, [P, c_size_t, P]),
     "mlxr_moe_gather_qmm_tiled": (c_int, [c_int64, c_int64]),
     "mlxr_moe_profile_start": (c_int, [c_char_p]),

@@ -451,8 +451,22 @@ int mlxr_moe_combine(const void* y, const float* w, int64_t T, int64_t K,
   return finish(from_hip(
       launch_combine(static_cast<const uint16_t*>(y), w, false, T, K, d,
                      static_cast<const uint16_t*>(shared_y), shared_logit, 1,
-                     out, false, as_stream(stream)),
+                     nullptr, out, false, as_stream(stream)),
       "combine"));
+}
+
+int mlxr_moe_rms_norm(const void* x, int64_t T, int64_t d, const void* weight,
+                      float eps, void* out, mlxr_moe_stream stream) {
+  if (T < 0 || d <= 0) return fail("rms_norm: bad shape");
+  if (d % 4) return fail("rms_norm: d must be a multiple of 4");
+  if (!(eps >= 0.0f)) return fail("rms_norm: eps must be >= 0");
+  if (T && (!x || !weight || !out)) return fail("rms_norm: null array");
+  if (!aligned(x, 8)) return fail("rms_norm: x must be 8-byte aligned");
+  return finish(from_hip(
+      launch_rms_norm(static_cast<const uint16_t*>(x), T, d,
+                      static_cast<const uint16_t*>(weight), eps,
+                      static_cast<uint16_t*>(out), as_stream(stream)),
+      "rms_norm"));
 }
 
 size_t mlxr_moe_switch_glu_workspace_size(const mlxr_moe_switch_glu* ffn,
@@ -748,11 +762,71 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
                           topk_w, c, s));
 }
 
+size_t mlxr_moe_block_residual_workspace_size(const mlxr_moe_block* block,
+                                              int64_t T) {
+  if (!block) return 0;
+  Carve c(nullptr);
+  c.take<int32_t>(1);
+  c.take<uint16_t>(T * block->hidden_size);  // the normed rows
+  nn::Qwen35MoeBlock::plan(c, *block, T);
+  return c.off;
+}
+
+int mlxr_moe_block_forward_residual(const mlxr_moe_block* block,
+                                    const void* norm_weight, float eps,
+                                    const void* h, int64_t T, void* out,
+                                    int32_t* topk_idx, float* topk_w,
+                                    void* workspace, size_t workspace_size,
+                                    mlxr_moe_stream stream) {
+  if (!block) return fail("block_residual: null module");
+  nn::Qwen35MoeBlock m(*block);
+  Status st = m.validate();
+  if (!st.ok) return finish(st);
+  if (T < 0) return fail("block_residual: bad T");
+  if (!(eps >= 0.0f)) return fail("block_residual: eps must be >= 0");
+  if (T && (!h || !out || !norm_weight)) return fail("block_residual: null array");
+  if (!aligned(h, 16) || !aligned(out, 16) || !aligned(block->gate_weight, 16) ||
+      (block->shared_expert_gate_weight &&
+       !aligned(block->shared_expert_gate_weight, 16)))
+    return fail("block_residual: h, out and router weights must be 16-byte "
+                "aligned");
+  const size_t rq_align = block->gate_q.bits == 16 ? 8 : 4;
+  if (!aligned(block->gate_q.weight, rq_align) ||
+      !aligned(block->shared_expert_gate_q.weight, rq_align) ||
+      !aligned(block->gate_q.scales, 2) || !aligned(block->gate_q.biases, 2) ||
+      !aligned(block->shared_expert_gate_q.scales, 2) ||
+      !aligned(block->shared_expert_gate_q.biases, 2))
+    return fail("block_residual: quantised router words must be 4-byte "
+                "(bf16 weights 8-byte) and its scales and biases 2-byte "
+                "aligned");
+  if (workspace_size < mlxr_moe_block_residual_workspace_size(block, T))
+    return fail("workspace too small: need " +
+                std::to_string(mlxr_moe_block_residual_workspace_size(block, T)) +
+                " bytes, got " + std::to_string(workspace_size));
+  if (T == 0) return 0;
+  if (!workspace || !aligned(workspace, 256))
+    return fail("workspace must be non-NULL and 256-byte aligned");
+  hipStream_t s = as_stream(stream);
+  Carve c(workspace);
+  c.take<int32_t>(1);  // status word, cleared by the routing kernel
+  uint16_t* normed = c.take<uint16_t>(T * block->hidden_size);
+  const uint16_t* hb = static_cast<const uint16_t*>(h);
+  // post_attention_layernorm (layer.rs:137), then the block with the
+  // residual add (layer.rs:138) in its combine
+  st = from_hip(launch_rms_norm(hb, T, block->hidden_size,
+                                static_cast<const uint16_t*>(norm_weight), eps,
+                                normed, s),
+                "post_attention_layernorm");
+  if (!st.ok) return finish(st);
+  return finish(m.forward(normed, T, out, topk_idx, topk_w, c, s, hb));
+}
+
 int mlxr_moe_profile_start(const char* kernel) {
   static const char* const kNames[] = {"router_logits", "router_topk",
                                        "dispatch",      "qgemm_gated",
                                        "qgemm_down",    "combine",
-                                       "shared_gated",  "shared_down"};
+                                       "shared_gated",  "shared_down",
+                                       "rms_norm"};
   if (kernel && *kernel) {
     bool known = false;
     for (const char* n : kNames) known = known || std::strcmp(n, kernel) == 0;

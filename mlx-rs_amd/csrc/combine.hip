@@ -10,6 +10,10 @@
 // bf16 and so is every op: w * y rounded to bf16, the sum over k in f32
 // rounded to bf16, shared = bf16(y_s * bf16(sigmoid(sg))), out =
 // bf16(shared + routed).
+// With a residual h (bf16 [T, d]) the decoder layer's add after the block
+// (DecoderLayer::forward, crates/mlxr-lm/src/qwen3_5/text/layer.rs:138)
+// follows in the same pass: out = h + mlp_out, f32 (bf16 + f32 promotes) or
+// bf16(h + bf16(mlp_out)) in the bf16 chain.
 // HBM-bound elementwise pass: 8 outputs per thread, 16 B loads of y.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -22,7 +26,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
     const uint16_t* __restrict__ y, const WT* __restrict__ w, int T, int K,
     int d, const uint16_t* __restrict__ shared_y,
     const float* __restrict__ shared_logit, int64_t shared_ld,
-    void* __restrict__ out) {
+    const uint16_t* __restrict__ residual, void* __restrict__ out) {
   const int t = blockIdx.y;
   const int n0 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (t >= T || n0 >= d) return;
@@ -72,6 +76,19 @@ __global__ __launch_bounds__(256) void combine_kernel(
       acc[2 * j + 1] = __fadd_rn(hi, acc[2 * j + 1]);
     }
   }
+  if (residual) {
+    const u32x4_t v =
+        *reinterpret_cast<const u32x4_t*>(residual + (int64_t)t * d + n0);
+    const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // h + mlp_out, with mlp_out in its own dtype first
+      const float m0 = BF16 ? bf16_round(acc[2 * j]) : acc[2 * j];
+      const float m1 = BF16 ? bf16_round(acc[2 * j + 1]) : acc[2 * j + 1];
+      acc[2 * j] = __fadd_rn(__uint_as_float(pk[j] << 16), m0);
+      acc[2 * j + 1] = __fadd_rn(__uint_as_float(pk[j] & 0xffff0000u), m1);
+    }
+  }
   if (BF16) {
     uint32_t pk[4];
 #pragma unroll
@@ -92,8 +109,8 @@ __global__ __launch_bounds__(256) void combine_kernel(
 hipError_t launch_combine(const uint16_t* y, const void* w, bool w_bf16,
                           int64_t T, int64_t K, int64_t d,
                           const uint16_t* shared_y, const float* shared_logit,
-                          int64_t shared_ld, void* out, bool bf16,
-                          hipStream_t s) {
+                          int64_t shared_ld, const uint16_t* residual,
+                          void* out, bool bf16, hipStream_t s) {
   if (T == 0) return hipSuccess;
   if (w_bf16 && !bf16) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((d / 8 + 255) / 256), (unsigned)T);
@@ -102,13 +119,13 @@ hipError_t launch_combine(const uint16_t* y, const void* w, bool w_bf16,
   const uint16_t* wh = static_cast<const uint16_t*>(w);
   if (w_bf16)
     combine_kernel<true, uint16_t><<<grid, 256, 0, s>>>(
-        y, wh, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, out);
+        y, wh, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, residual, out);
   else if (bf16)
     combine_kernel<true, float><<<grid, 256, 0, s>>>(
-        y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, out);
+        y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, residual, out);
   else
     combine_kernel<false, float><<<grid, 256, 0, s>>>(
-        y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, out);
+        y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, residual, out);
   return hipGetLastError();
 }
 

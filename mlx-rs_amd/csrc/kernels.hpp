@@ -70,7 +70,8 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
 hipError_t launch_router_topk(const float* logits, int64_t ld, int64_t T,
                               int64_t E, int64_t K, bool bf16, int32_t* idx,
                               float* wts, int32_t* status, hipStream_t s);
-// out bf16 [T, d] = fast::rms_norm(x, w, eps) (gemma4's router prologue)
+// out bf16 [T, d] = fast::rms_norm(x, w, eps) (gemma4's router prologue,
+// the decoder layer's post-attention norm)
 hipError_t launch_rms_norm(const uint16_t* x, int64_t T, int64_t d,
                            const uint16_t* w, float eps, uint16_t* out,
                            hipStream_t s);
@@ -222,11 +223,12 @@ hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
 // -------------------------------------------------------------- combine.hip
 // out f32 [T, d], or bf16 when bf16 (the routing weights are then bf16
 // values and every op rounds to bf16).  w is f32 [T, K], or bf16 when
-// w_bf16 (only with a bf16 out).
+// w_bf16 (only with a bf16 out).  residual (bf16 [T, d], optional) is added
+// last: out = residual + the combine's result in its own dtype.
 hipError_t launch_combine(const uint16_t* y, const void* w, bool w_bf16,
                           int64_t T, int64_t K, int64_t d,
                           const uint16_t* shared_y, const float* shared_logit,
-                          int64_t shared_ld, void* out, bool bf16,
-                          hipStream_t s);
+                          int64_t shared_ld, const uint16_t* residual,
+                          void* out, bool bf16, hipStream_t s);
 
 }  // namespace mlxr_moe

@@ -338,7 +338,8 @@ Status SwitchFfn::forward_with_combine(
   Status st = forward(x, T, indices, K, y, ws, status, s);
   if (!st.ok) return st;
   return from_hip(launch_combine(y, weights, w_bf16, T, K, sw_.d, shared_y,
-                                 shared_logit, shared_ld, out, w_bf16, s),
+                                 shared_logit, shared_ld, nullptr, out, w_bf16,
+                                 s),
                   "combine");
 }
 
@@ -411,7 +412,7 @@ void Qwen35MoeBlock::plan(Carve& ws, const mlxr_moe_block& b, int64_t T) {
 // the expert dispatch), [shared expert], gate/up, down, combine.
 Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
                                int32_t* topk_idx, float* topk_w, Carve& ws,
-                               hipStream_t s) const {
+                               hipStream_t s, const uint16_t* residual) const {
   const int64_t d = b_.hidden_size, E = b_.num_experts;
   const int64_t K = b_.num_experts_per_tok;
   const bool shared = has_shared();
@@ -460,8 +461,8 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
   st = mlp.experts(x, T, K, db, y, ws, s);
   if (!st.ok) return st;
   return from_hip(launch_combine(y, wts, false, T, K, d, sy,
-                                 shared ? logits + E : nullptr, ld, out, bf16,
-                                 s),
+                                 shared ? logits + E : nullptr, ld, residual,
+                                 out, bf16, s),
                   "combine");
 }
 

@@ -376,7 +376,8 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(
 }
 
 // fast::rms_norm as gemma4's router applies it (Router::forward,
-// crates/mlxr-lm/src/gemma4/text/text.rs:640): out_j = bf16(w_j *
+// crates/mlxr-lm/src/gemma4/text/text.rs:640) and as RmsNorm::forward does
+// (crates/mlxr/src/layers/normalization.rs:272-276): out_j = bf16(w_j *
 // bf16(x_j * r)), r = 1 / sqrt(sum_j x_j^2 / d + eps) -- MLX's rounding
 // points (the normalised value in the input dtype, then the weight
 // product) -- with the sum of squares in the router's lane order (fmaf over
@@ -508,6 +509,7 @@ hipError_t launch_rms_norm(const uint16_t* x, int64_t T, int64_t d,
                            const uint16_t* w, float eps, uint16_t* out,
                            hipStream_t s) {
   if (T == 0) return hipSuccess;
+  ProfileScope prof("rms_norm", s);
   rms_norm_kernel<<<(unsigned)((T + 3) / 4), 256, 0, s>>>(x, (int)T, (int)d, w,
                                                           eps, out);
   return hipGetLastError();

@@ -8,6 +8,8 @@ Follows the reference's loader for the keys this path uses:
                           with a `.scales` sibling is a QuantizedLinear's)
   QuantizationConfig      crates/mlxr-lm/src/quantization.rs:20-101
                           (body group_size / bits, per-path overrides)
+  post_attention_layernorm weights.rs:33-42, 119-165 (+1.0 in the
+                          weight's dtype unless the shard says format "mlx")
   the packed HF expert tensor `mlp.experts.gate_up_proj [E, 2H, D]`, split
   along axis 1 into `switch_mlp.{gate,up}_proj` as mlxr-convert does
   (crates/mlxr-convert/src/qwen3_5.rs:96-147).
@@ -125,6 +127,36 @@ class LayerTensors:
         return self.t[name]
 
 
+def is_mlx_format(path) -> bool:
+    """The shard's header metadata says format "mlx": its norm weights
+    already carry the +1.0 shift (weights.rs:45-70)."""
+    from safetensors import safe_open
+
+    with safe_open(str(path), framework="pt") as f:
+        meta = f.metadata() or {}
+    return meta.get("format") == "mlx"
+
+
+def post_attention_layernorm(model_dir, layer: int, device):
+    """nn.RmsNorm of decoder layer `layer`'s post_attention_layernorm (the
+    norm before the MoE block, layer.rs:137), eps = rms_norm_eps; the weight
+    gets the +1.0 centring shift in its own dtype unless its shard is
+    mlx-format (weights.rs:147-165)."""
+    from safetensors import safe_open
+
+    want = f"language_model.model.layers.{layer}.post_attention_layernorm.weight"
+    tc = text_config(read_config(model_dir))
+    for path in list_shards(model_dir):
+        with safe_open(str(path), framework="pt") as f:
+            for k in f.keys():
+                if sanitize_key(k) == want:
+                    w = f.get_tensor(k)
+                    if not is_mlx_format(path) and w.ndim == 1 and w.is_floating_point():
+                        w = w + torch.ones((), dtype=w.dtype)
+                    return nn.RmsNorm(w.to(device), float(tc.get("rms_norm_eps", 1e-6)))
+    raise MlxrMoeError(f"weights: {want} is missing")
+
+
 def _u32_as_i32(t: torch.Tensor) -> torch.Tensor:
     # packed codes are stored as U32; the kernels read the same bits as int32
     return t.view(torch.int32) if t.dtype == torch.uint32 else t.to(torch.int32)
@@ -198,4 +230,4 @@ def qwen35_moe_block(model_dir, layer: int, device, quantize_dense=None):
 
 
 __all__ = ["list_shards", "sanitize_key", "QuantizationConfig", "read_config", "text_config",
-           "LayerTensors", "qwen35_moe_block"]
+           "LayerTensors", "qwen35_moe_block", "is_mlx_format", "post_attention_layernorm"]

@@ -1,6 +1,7 @@
 """mlxr-lm MoE modules over the gfx950 C ABI.
 
     SwitchLinear           crates/mlxr-lm/src/nn/switch.rs:49-94 (dense)
+    RmsNorm                crates/mlxr/src/layers/normalization.rs:254-276
     Linear                 crates/mlxr/src/layers/linear.rs (dense, bf16)
     QuantizedSwitchLinear  crates/mlxr-lm/src/nn/switch.rs:115-168
     QuantizedLinear        crates/mlxr/src/layers/quantized.rs:214-379
@@ -504,5 +505,60 @@ class Qwen35MoeBlock:
         self.last_indices, self.last_weights = idx, wts
         self.last_workspace = workspace
         return out.reshape(tuple(x.shape[:-1]) + (d,))
+
+    __call__ = forward
+
+    def residual_workspace_size(self, T: int) -> int:
+        return C.lib().mlxr_moe_block_residual_workspace_size(ctypes.byref(self._desc), T)
+
+    def forward_residual(self, h, norm: "RmsNorm", out=None, workspace=None,
+                         keep_routing=True):
+        """The decoder layer's MoE half (layer.rs:134-138): h + self(norm(h)),
+        the norm (post_attention_layernorm) one kernel before the block and
+        the add fused into its combine.  h bf16 [..., d]; out f32 (bf16 with
+        a bf16 router)."""
+        d = h.shape[-1]
+        h2 = h.reshape(-1, d).contiguous()
+        T, K = h2.shape[0], self.num_experts_per_tok
+        if out is None:
+            out = torch.empty((T, d), dtype=self.out_dtype, device=h.device)
+        elif out.dtype != self.out_dtype:
+            raise MlxrMoeError(f"out must be {self.out_dtype}")
+        if workspace is None:
+            workspace = ops.workspace(self.residual_workspace_size(T), h.device)
+        idx = wts = None
+        if keep_routing:
+            idx = torch.empty((T, K), dtype=torch.int32, device=h.device)
+            wts = torch.empty((T, K), dtype=torch.float32, device=h.device)
+        C.check(C.lib().mlxr_moe_block_forward_residual(
+            ctypes.byref(self._desc), _ptr(norm.weight), norm.eps, _ptr(h2), T, _ptr(out),
+            _ptr(idx), _ptr(wts), _ptr(workspace), workspace.numel(), ops._stream(h)))
+        self.last_indices, self.last_weights = idx, wts
+        self.last_workspace = workspace
+        return out.reshape(tuple(h.shape[:-1]) + (d,))
+
+
+class RmsNorm:
+    """layers::RmsNorm (crates/mlxr/src/layers/normalization.rs:254-276):
+    fast::rms_norm(x, weight, eps), bf16.  The weight is the one the model
+    holds (a Qwen3.5 checkpoint's +1.0 shift already applied by the
+    loader)."""
+
+    def __init__(self, weight, eps: float = 1e-6):
+        if weight.ndim != 1:
+            raise MlxrMoeError("RmsNorm weight must be [d]")
+        self.weight = weight.to(torch.bfloat16).contiguous()
+        self.eps = float(eps)
+
+    def forward(self, x):
+        d = x.shape[-1]
+        if d != self.weight.numel():
+            raise MlxrMoeError("RmsNorm: last dim does not match the weight")
+        x2 = x.reshape(-1, d).contiguous()
+        ops._dev(x2, self.weight)
+        out = torch.empty_like(x2, dtype=torch.bfloat16)
+        C.check(C.lib().mlxr_moe_rms_norm(_ptr(x2), x2.shape[0], d, _ptr(self.weight), self.eps,
+                                          _ptr(out), ops._stream(x)))
+        return out.reshape(x.shape)
 
     __call__ = forward

@@ -868,3 +868,34 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
   free(sg);
   return 0;
 }
+
+/* The MoE half of a Qwen3.5 decoder layer (DecoderLayer::forward,
+ * crates/mlxr-lm/src/qwen3_5/text/layer.rs:134-138):
+ *   out = h + block(post_attention_layernorm(h))
+ * with the norm fast::rms_norm (orc_rms_norm) and the add in the block
+ * output's dtype: f32 = f32(h) + mlp_out, or bf16(h + mlp_out) with a bf16
+ * router. */
+int orc_block_forward_residual(const orc_block* blk, const uint16_t* norm_w,
+                               float eps, const uint16_t* h, int64_t T,
+                               void* out, int32_t* idx_out, float* w_out,
+                               int nthreads) {
+  const int64_t d = blk->hidden;
+  const int bf16 = blk->router_q.w != NULL;
+  uint16_t* normed = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * d));
+  void* m = malloc((bf16 ? 2 : 4) * (size_t)(T * d));
+  orc_rms_norm(h, T, d, norm_w, eps, normed);
+  const int rc = orc_block_forward(blk, normed, T, m, idx_out, w_out, nthreads);
+  if (rc == 0) {
+    for (int64_t i = 0; i < T * d; ++i) {
+      const float hv = orc_bf16_to_f32(h[i]);
+      if (bf16)
+        ((uint16_t*)out)[i] =
+            orc_f32_to_bf16(hv + orc_bf16_to_f32(((const uint16_t*)m)[i]));
+      else
+        ((float*)out)[i] = hv + ((const float*)m)[i];
+    }
+  }
+  free(normed);
+  free(m);
+  return rc;
+}

@@ -191,6 +191,14 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
                       void* out, int32_t* idx_out, float* w_out,
                       int nthreads);
 
+/* out = h + orc_block_forward(orc_rms_norm(h, norm_w, eps)) (DecoderLayer::
+ * forward, qwen3_5/text/layer.rs:134-138): f32 out (f32(h) + mlp_out), or
+ * bf16 with a bf16 router (bf16(h + mlp_out)).  Returns 0 or -1. */
+int orc_block_forward_residual(const orc_block* blk, const uint16_t* norm_w,
+                               float eps, const uint16_t* h, int64_t T,
+                               void* out, int32_t* idx_out, float* w_out,
+                               int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -328,7 +328,13 @@ def _ql(t):
     return _QL(*(None if a is None else a.ctypes.data for a in t))
 
 
-def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
+def block_forward_residual(p: dict, norm_w, eps, h, nthreads=1, tiled=(False, False)):
+    """out = h + block(rms_norm(h, norm_w, eps)) (layer.rs:134-138), with
+    block_forward's parameters.  Returns (out, idx, weights)."""
+    return block_forward(p, h, nthreads, tiled, residual=(norm_w, eps))
+
+
+def block_forward(p: dict, x, nthreads=1, tiled=(False, False), residual=None):
     """p: numpy block parameters -- d, E, K, f, fs, bits, group_size,
     router_w, router_b (or None), gate/up/down = (wq, scales, biases),
     shared_gate/shared_up/shared_down, shared_gate_w (None when fs == 0).
@@ -368,8 +374,14 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False)):
     out = np.zeros((T, p["d"]), np.uint16 if rq is not None else np.float32)
     idx = np.zeros((T, p["K"]), np.int32)
     w = np.zeros((T, p["K"]), np.float32)
-    rc = lib().orc_block_forward(ctypes.byref(blk), _p(x), c_int64(T), _p(out), _p(idx), _p(w),
-                                 c_int(nthreads))
+    if residual is not None:
+        nw = c(residual[0], np.uint16)
+        rc = lib().orc_block_forward_residual(ctypes.byref(blk), _p(nw), c_float(residual[1]),
+                                              _p(x), c_int64(T), _p(out), _p(idx), _p(w),
+                                              c_int(nthreads))
+    else:
+        rc = lib().orc_block_forward(ctypes.byref(blk), _p(x), c_int64(T), _p(out), _p(idx),
+                                     _p(w), c_int(nthreads))
     if rc:
         raise ValueError("orc_block_forward rejected the arguments")
     return out, idx, w
@@ -379,7 +391,7 @@ __all__ = ["build", "lib", "f32_to_bf16", "bf16_to_f32", "quantize", "dequantize
            "router_logits", "router_topk", "router_logits_q", "router_topk_bf16", "dispatch",
            "gather_qmm", "gather_mm", "swiglu", "combine", "combine_bf16", "geglu", "rms_norm", "gemma_router",
            "packed_switch_glu",
-           "block_forward", "POINTER", "c_float", "c_uint16", "c_uint32"]
+           "block_forward", "block_forward_residual", "POINTER", "c_float", "c_uint16", "c_uint32"]
 
 
 # ------------------------------------------------------- torch adapters

@@ -179,6 +179,51 @@ def test_dense_block_equals_dequantised_4bit_block(pkg, dev):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("cfg,T", [("c2", 64), ("c6", 1), ("c6", 64), ("c6", 512),
+                                   ("c8", 64)])
+def test_block_residual_parity(pkg, orc, dev, cfg, T):
+    """The decoder layer's MoE half, out = h + block(rms_norm(h))
+    (layer.rs:134-138), through mlxr_moe_block_forward_residual: routing
+    bit-exact against the oracle, out within the block tolerance (on the
+    block's part) plus one step of out's dtype; and bit-identical to the
+    same three steps run as separate GPU calls."""
+    bw = weights(pkg, cfg, dev)
+    c = bw.cfg
+    h = pkg.workloads.make_x(c, T, dev, seed=T + 1)
+    g = torch.Generator(device=dev).manual_seed(T)
+    nw = (1 + 0.1 * torch.randn(c.d, generator=g, device=dev)).to(torch.bfloat16)
+    norm = pkg.nn.RmsNorm(nw, 1e-6)
+    block = bw.block()
+    print(f"  block_residual {c.name} T={T}", flush=True)
+    out = block.forward_residual(h, norm)
+    idx = block.last_indices.clone()
+    # the same steps as separate calls
+    m = block(norm(h))
+    assert torch.equal(block.last_indices, idx)
+    sep = (h + m) if c.router_bits else (h.float() + m)
+    assert torch.equal(out, sep)
+    tiled = (pkg.ops.gather_qmm_tiled(T * c.K, c.E), pkg.ops.gather_qmm_tiled(T, 1))
+    p = orc.block_params(bw)
+    ref, ridx, rw = orc.block_forward_residual(p, orc.to_np(nw), 1e-6, orc.to_np(h),
+                                               nthreads=16, tiled=tiled)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    mref, _, _ = orc.block_forward(p, orc.rms_norm(orc.to_np(h), orc.to_np(nw), 1e-6),
+                                   nthreads=16, tiled=tiled)
+    if c.router_bits:
+        got, ref = orc.bf16_to_f32(orc.to_np(out)), orc.bf16_to_f32(ref)
+        mref = orc.bf16_to_f32(mref)
+    else:
+        got = out.cpu().numpy()
+    got, ref = got.astype(np.float64), ref.astype(np.float64)
+    rms = np.sqrt(np.mean(mref.astype(np.float64) ** 2))
+    a = np.abs(ref)
+    step = 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - (7 if c.router_bits else 23))
+    diff = np.abs(got - ref)
+    print(f"  max|err| {diff.max():.3e}  block rms {rms:.3e}", flush=True)
+    assert np.all(diff <= 2e-2 * rms + step)
+    assert pkg.ops.workspace_status(block.last_workspace) == 0
+
+
 def test_block_token_permutation_equivariance(pkg, dev):
     """At full c2 size: permuting tokens permutes output rows bit for bit,
     and repeated runs are bit-identical (size-independent properties)."""

@@ -345,6 +345,18 @@ def test_router_topk_bf16_linear_bit_exact(pkg, orc, dev, T, E):
     assert np.array_equal(wts.cpu().numpy(), rw)
 
 
+# ------------------------------------------------------- rms_norm
+@pytest.mark.parametrize("T,d", [(1, 2048), (37, 2048), (300, 4096), (5, 516)])
+def test_rms_norm_bit_exact(pkg, orc, dev, T, d):
+    """fast::rms_norm (layers/normalization.rs:272-276): bit for bit
+    against the oracle."""
+    rng = np.random.default_rng(T + d)
+    x = _bf16(orc, (3 * rng.standard_normal((T, d))).astype(np.float32), dev)
+    w = _bf16(orc, (1 + 0.2 * rng.standard_normal(d)).astype(np.float32), dev)
+    got = pkg.nn.RmsNorm(w, 1e-6)(x)
+    assert np.array_equal(_np(orc, got), orc.rms_norm(_np(orc, x), _np(orc, w), 1e-6))
+
+
 # -------------------------------------------------------- combine
 def test_combine_bit_exact(pkg, orc, dev):
     rng = np.random.default_rng(13)

@@ -41,19 +41,19 @@ def test_quantization_overrides_of_the_shipped_config(pkg):
         assert q.for_path(p + "shared_expert.down_proj") == (64, 4)
 
 
-def _write_checkpoint(d: Path, tensors: dict, config: dict, shards=1):
+def _write_checkpoint(d: Path, tensors: dict, config: dict, shards=1, fmt="mlx"):
     d.mkdir(parents=True, exist_ok=True)
     (d / "config.json").write_text(json.dumps(config))
     keys = sorted(tensors)
     if shards == 1:
         safetensors_torch.save_file(tensors, str(d / "model.safetensors"),
-                                    metadata={"format": "mlx"})
+                                    metadata={"format": fmt})
         return
     weight_map = {}
     for s in range(shards):
         name = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
         part = {k: tensors[k] for k in keys[s::shards]}
-        safetensors_torch.save_file(part, str(d / name), metadata={"format": "mlx"})
+        safetensors_torch.save_file(part, str(d / name), metadata={"format": fmt})
         weight_map.update({k: name for k in part})
     (d / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
 
@@ -138,3 +138,21 @@ def test_hf_packed_experts_split_and_loaded_dense(pkg, tmp_path):
     _write_checkpoint(tmp_path / "hf32", t, {"text_config": {"num_experts_per_tok": 2}})
     blk = pkg.loader.qwen35_moe_block(tmp_path / "hf32", 0, "cpu")
     assert not blk.quantised_router and blk.gate_weight.dtype == torch.float32
+
+
+@pytest.mark.parametrize("fmt", ["mlx", "pt"])
+def test_post_attention_layernorm_shift(pkg, tmp_path, fmt):
+    """weights.rs:147-165: a non-mlx-format checkpoint's norm weight gets
+    +1.0 in its own dtype (bf16 here: 0.5 -> 1.5, 2^-9 -> 1.0 after
+    rounding); an mlx-format one is taken as stored.  eps is rms_norm_eps."""
+    p = "model.language_model.layers.3."
+    w = torch.tensor([0.5, -0.25, 2.0 ** -9, 3.0], dtype=torch.bfloat16)
+    t = {p + "post_attention_layernorm.weight": w,
+         p + "input_layernorm.weight": torch.zeros(4, dtype=torch.bfloat16)}
+    _write_checkpoint(tmp_path / fmt, t, {"text_config": {"rms_norm_eps": 1e-5}}, fmt=fmt)
+    norm = pkg.loader.post_attention_layernorm(tmp_path / fmt, 3, "cpu")
+    assert norm.eps == pytest.approx(1e-5)
+    want = w if fmt == "mlx" else torch.tensor([1.5, 0.75, 1.0, 4.0], dtype=torch.bfloat16)
+    assert torch.equal(norm.weight, want)
+    with pytest.raises(pkg.MlxrMoeError):
+        pkg.loader.post_attention_layernorm(tmp_path / fmt, 2, "cpu")

@@ -677,3 +677,36 @@ def test_packed_switch_glu_dense_equals_split_composition(orc):
         u = orc.gather_mm(xs, np.ascontiguousarray(gu[:, H:]), ids)
         y = orc.gather_mm(fn(g, u), dn, ids).reshape(T, K, d)
         assert np.array_equal(out, orc.combine(y, w))
+
+
+# ------------------------------------------- the decoder layer's MoE half
+@pytest.mark.parametrize("router_bits", [0, 8])
+def test_block_residual_zero_norm_is_identity(orc, router_bits):
+    """layer.rs:134-138 with a zero norm weight: the block sees zero rows,
+    whose expert outputs are zero (no biases), so out = h exactly -- f32(h)
+    with the f32 router, h itself in the bf16 chain."""
+    p, h = _c1_params(orc, fs=256, router_bits=router_bits)
+    out, _, _ = orc.block_forward_residual(p, np.zeros(p["d"], np.uint16), 1e-6, h)
+    if router_bits:
+        assert out.dtype == np.uint16 and np.array_equal(out, h)
+    else:
+        assert np.array_equal(out, orc.bf16_to_f32(h))
+
+
+@pytest.mark.parametrize("router_bits", [0, 8])
+def test_block_residual_equals_norm_block_add(orc, router_bits):
+    """The fused tail equals its op sequence: post_attention_layernorm
+    (fast::rms_norm), the block, and the add in the block output's dtype
+    (bf16 + f32 promotes; bf16 + bf16 rounds to bf16)."""
+    rng = np.random.default_rng(70)
+    p, h = _c1_params(orc, fs=256, router_bits=router_bits)
+    nw = orc.f32_to_bf16((1.0 + 0.1 * rng.standard_normal(p["d"])).astype(np.float32))
+    out, idx, w = orc.block_forward_residual(p, nw, 1e-6, h)
+    m, idx2, w2 = orc.block_forward(p, orc.rms_norm(h, nw, 1e-6))
+    assert np.array_equal(idx, idx2) and np.array_equal(w, w2)
+    hf = orc.bf16_to_f32(h)
+    if router_bits:
+        want = orc.f32_to_bf16((hf + orc.bf16_to_f32(m)).astype(np.float32))
+    else:
+        want = (hf + m).astype(np.float32)
+    assert np.array_equal(out, want)
