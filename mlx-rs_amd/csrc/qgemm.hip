@@ -64,6 +64,10 @@ constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
 #ifndef MLXR_STREAM_MAX_NB
 #define MLXR_STREAM_MAX_NB 2
 #endif
+// ... and of the gated kernel (1 or 2)
+#ifndef MLXR_STREAM_GATED_NB
+#define MLXR_STREAM_GATED_NB 1
+#endif
 #ifndef MLXR_STREAM_SLOTS
 #define MLXR_STREAM_SLOTS 512
 #endif
@@ -737,7 +741,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     // staged as few times as the GPU allows
     const int64_t per_tile = a.N / (16 * kWaves);
     int nb = 1;
-    for (int c = a.gated ? 1 : MLXR_STREAM_MAX_NB; c > 1; --c)
+    for (int c = a.gated ? MLXR_STREAM_GATED_NB : MLXR_STREAM_MAX_NB; c > 1; --c)
       if (per_tile % c == 0 && max_items * (per_tile / c) >= kStreamSlots) {
         nb = c;
         break;
@@ -752,6 +756,11 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
 #define MLXR_QS(B, G, D, NB) \
   qgemm_stream_kernel<B, G, D, NB><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n)
     if (a.bits == 4) {
+#if MLXR_STREAM_GATED_NB > 1
+      if (a.gated && nb == 2)
+        MLXR_QS(4, true, MLXR_STREAM_DEPTH4, 2);
+      else
+#endif
       if (a.gated)
         MLXR_QS(4, true, MLXR_STREAM_DEPTH4, 1);
       else if (nb == 2)
@@ -759,6 +768,11 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
       else
         MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 1);
     } else {
+#if MLXR_STREAM_GATED_NB > 1
+      if (a.gated && nb == 2)
+        MLXR_QS(8, true, MLXR_STREAM_DEPTH8, 2);
+      else
+#endif
       if (a.gated)
         MLXR_QS(8, true, MLXR_STREAM_DEPTH8, 1);
       else if (nb == 2)

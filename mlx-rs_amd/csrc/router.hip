@@ -424,6 +424,20 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
   }
 }
 
+// Launch shape for 16 < T <= MLXR_RL_TILED_T (experts and tokens per wave,
+// 256-wide steps of loads in flight); the LDS-tiled kernel above that.
+#ifndef MLXR_RL_MID_EB
+#define MLXR_RL_MID_EB 2
+#endif
+#ifndef MLXR_RL_MID_TB
+#define MLXR_RL_MID_TB 4
+#endif
+#ifndef MLXR_RL_MID_U
+#define MLXR_RL_MID_U 4
+#endif
+#ifndef MLXR_RL_TILED_T
+#define MLXR_RL_TILED_T 256
+#endif
 template <int BITS>
 void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
                           const RouterWeights& w, const float* bias, int64_t E,
@@ -440,8 +454,8 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     MLXR_RL(1, 1, 8);
   else if (T <= 16)
     MLXR_RL(1, 2, 8);
-  else if (T <= 256)
-    MLXR_RL(2, 4, 4);
+  else if (T <= MLXR_RL_TILED_T)
+    MLXR_RL(MLXR_RL_MID_EB, MLXR_RL_MID_TB, MLXR_RL_MID_U);
   else
     router_logits_tiled_kernel<BITS>
         <<<dim3((unsigned)((e_tot + kRtCol - 1) / kRtCol),
