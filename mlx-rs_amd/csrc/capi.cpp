@@ -91,7 +91,7 @@ int run_gather(const char* op, const void* x, int64_t x_batch, int64_t M,
                int64_t B, void* out, void* workspace, size_t workspace_size,
                hipStream_t s) {
   const std::string o(op);
-  if (!rhs_indices) return fail(o + ": rhs_indices are required");
+  if (!rhs_indices && B > 0) return fail(o + ": rhs_indices are required");
   if (E <= 0 || E > kMaxExperts)
     return fail(o + ": num_experts must be in [1, " +
                 std::to_string(kMaxExperts) + "]");
@@ -111,7 +111,7 @@ int run_gather(const char* op, const void* x, int64_t x_batch, int64_t M,
     return fail(o + ": x must be under 2 GB");  // the M-tiled kernel's buffer
   if (N * K * bits / 8 >= ((int64_t)1 << 31))
     return fail(o + ": one expert's weights must be under 2 GB");
-  if (!x || !w || !out) return fail(o + ": null array");
+  if (B > 0 && (!x || !w || !out)) return fail(o + ": null array");
   if (!aligned(x, 16) || !aligned(w, 16))
     return fail(o + ": x and w must be 16-byte aligned");
   Carve plan(nullptr);

@@ -83,9 +83,9 @@ bool use_prefill_path(int64_t rows, int64_t experts, int bits) {
   // rows makes four gate/up tiles).
   if (bits == 16)
     return rows >= (int64_t)MLXR_DENSE_TILED_ROWS * experts && rows >= 512;
-  // the M-tiled kernel pays once the experts average 32 rows and there are
-  // rows enough for its tiles to spread over the GPU
-  return rows >= 32 * experts && rows >= 512;
+  // the M-tiled kernel pays once the experts average MLXR_QUANT_TILED_ROWS
+  // rows and there are rows enough for its tiles to spread over the GPU
+  return rows >= (int64_t)MLXR_QUANT_TILED_ROWS * experts && rows >= 512;
 }
 
 namespace {

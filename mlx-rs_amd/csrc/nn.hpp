@@ -57,6 +57,9 @@ namespace nn {
 // here the choice is about GEMM shape, not sorting, which always happens).
 // Dense bf16 GEMMs (bits 16) switch at MLXR_DENSE_TILED_ROWS rows per
 // expert.
+#ifndef MLXR_QUANT_TILED_ROWS
+#define MLXR_QUANT_TILED_ROWS 32
+#endif
 #ifndef MLXR_DENSE_TILED_ROWS
 #define MLXR_DENSE_TILED_ROWS 2
 #endif

@@ -123,11 +123,15 @@ namespace tile256 {
 #undef MLXR_PF_WAVES_N
 #undef MLXR_PF_REGBUF
 }  // namespace tile256
+// register buffers of the 128-row tile (2 or 3 groups of loads in flight)
+#ifndef MLXR_PF128_REGBUF
+#define MLXR_PF128_REGBUF 2
+#endif
 namespace tile128 {
 #define MLXR_PF_TILE_ROWS 128
 #define MLXR_PF_MBLOCKS 2
 #define MLXR_PF_WAVES_N 4
-#define MLXR_PF_REGBUF 2
+#define MLXR_PF_REGBUF MLXR_PF128_REGBUF
 // two stages (96 KB) leave room for the scales and biases of K up to 4096
 #define MLXR_PF_STAGES 2
 #include "prefill_tile.inc"

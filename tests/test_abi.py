@@ -160,6 +160,9 @@ def test_gather_mm_rejects_unsupported(pkg):
     assert call(bt=0) == -1 and "b_transposed" in _err(pkg)
     assert call(b_dt=C.FLOAT32) == -1 and "bf16" in _err(pkg)
     assert call() == -1 and "rhs_indices" in _err(pkg)
+    assert lib.mlxr_moe_gather_mm(None, C.BFLOAT16, 1, 1, 128, None, C.BFLOAT16, 4, 64, 1, None,
+                                  None, 0, 0, None, C.BFLOAT16, None, 0, None) == -1
+    assert "workspace" in _err(pkg)  # B = 0 needs no indices, only the (small) workspace
     assert call(K=96, rhs=8) == -1 and "multiples of 64" in _err(pkg)
     assert call(K=8192, rhs=8) == -1 and "K above" in _err(pkg)
     assert lib.mlxr_moe_gather_mm_workspace_size(8, 1, 4) == \

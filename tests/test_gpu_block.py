@@ -224,6 +224,19 @@ def test_block_residual_parity(pkg, orc, dev, cfg, T):
     assert pkg.ops.workspace_status(block.last_workspace) == 0
 
 
+@pytest.mark.parametrize("cfg", ["c6", "c8"])
+def test_block_residual_and_norm_empty_input(pkg, dev, cfg):
+    """T = 0 through the layer-tail entry and the norm: empty outputs, no
+    error, nothing launched that reads the input."""
+    bw = weights(pkg, cfg, dev)
+    d = bw.cfg.d
+    h = torch.empty((0, d), dtype=torch.bfloat16, device=dev)
+    norm = pkg.nn.RmsNorm(torch.ones(d, dtype=torch.bfloat16, device=dev))
+    out = bw.block().forward_residual(h, norm)
+    assert tuple(out.shape) == (0, d)
+    assert tuple(norm(h).shape) == (0, d)
+
+
 def test_block_token_permutation_equivariance(pkg, dev):
     """At full c2 size: permuting tokens permutes output rows bit for bit,
     and repeated runs are bit-identical (size-independent properties)."""

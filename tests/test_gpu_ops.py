@@ -311,6 +311,24 @@ def test_gather_mm_moe_shapes(pkg, orc, dev, T, K, E, N, Kd):
            orc.bf16_to_f32(want).reshape(T * K, N), (T, K, E, N, Kd))
 
 
+def test_gather_mm_edge_cases(pkg, orc, dev):
+    """Empty index lists give empty outputs; an out-of-range expert id
+    leaves its rows zero and sets the workspace status (the reference raises
+    at eval time instead); the other rows are unaffected."""
+    rng = np.random.default_rng(45)
+    w = _bf16(orc, (0.05 * rng.standard_normal((4, 64, 128))).astype(np.float32), dev)
+    x = _bf16(orc, rng.standard_normal((3, 1, 128)).astype(np.float32), dev)
+    empty = pkg.ops.gather_mm(x, w, None, torch.zeros((0, 1), dtype=torch.int32, device=dev))
+    assert tuple(empty.shape) == (0, 1, 1, 64)
+    idx = torch.tensor([1, 9, 2], dtype=torch.int32, device=dev)
+    got = pkg.ops.gather_mm(x, w, None, idx)
+    assert pkg.ops.workspace_status(got._mlxr_workspace) == 1
+    assert torch.all(got[1] == 0)
+    ok = pkg.ops.gather_mm(x[[0, 2]], w, None, idx[[0, 2]])
+    assert pkg.ops.workspace_status(ok._mlxr_workspace) == 0
+    assert torch.equal(got[[0, 2]], ok)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_gather_mm_is_tiled_gather_qmm_of_dequant(pkg, orc, dev, bits):
     """quantization.rs:344-421: gather_qmm(x, w) == gather_mm(x,
