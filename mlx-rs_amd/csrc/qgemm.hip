@@ -59,8 +59,8 @@ namespace {
 #define MLXR_STREAM_TT4_ROWS 4
 #endif
 constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
-// 16-channel blocks per wave of the down kernel, at most (1 or 2); the
-// gated kernel moves twice the bytes per step and keeps one
+// 16-channel blocks per wave of the down kernel, at most (1, 2 or 4; the
+// launcher halves it until the grid keeps every slot busy)
 #ifndef MLXR_STREAM_MAX_NB
 #define MLXR_STREAM_MAX_NB 2
 #endif
@@ -583,11 +583,17 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   // The loop issues the same loads every super-step (past the end they
   // repeat the last step, a cache hit) and holds no stores, so the
   // compiler can wait for exactly the oldest ring slot.  Steps past the
-  // end multiply zeros.  With two blocks per wave the first block's sums
-  // move to `first` when its last step is done.
-  f32x4_t acc[NM], first[NM];
+  // end multiply zeros.  With several blocks per wave each block's sums
+  // move to done[block] when its last step is done (selects, so the
+  // accumulators stay in registers).
+  constexpr int ND = NB > 1 ? NB - 1 : 1;
+  f32x4_t acc[NM], done[ND][NM];
 #pragma unroll
-  for (int m = 0; m < NM; ++m) acc[m] = first[m] = zero;
+  for (int m = 0; m < NM; ++m) {
+    acc[m] = zero;
+#pragma unroll
+    for (int b = 0; b < ND; ++b) done[b][m] = zero;
+  }
   const uint32_t one_v = 0x3F803F80u;
   // x operand source of this lane: its row's token chunk in its group's
   // codes, or the zero block off the diagonal / past the tokens
@@ -640,15 +646,20 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
         for (int r = 0; r < 4; ++r)
           acc[m][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(cb, X[r], acc[m][r]));
       }
-      if constexpr (NB == 2) {
-        const bool done0 = live && bi == 0 && ss == ssteps - 1;
+      if constexpr (NB > 1) {
+        const bool last = live && ss == ssteps - 1 && bi < NB - 1;
+#pragma unroll
+        for (int b = 0; b < NB - 1; ++b) {
+          const bool fin = last && bi == b;
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) done[b][m][r] = fin ? acc[m][r] : done[b][m][r];
+        }
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            first[m][r] = done0 ? acc[m][r] : first[m][r];
-            acc[m][r] = done0 ? 0.0f : acc[m][r];
-          }
+          for (int r = 0; r < 4; ++r) acc[m][r] = last ? 0.0f : acc[m][r];
       }
     }
   }
@@ -660,7 +671,9 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
     f32x4_t tot[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      tot[m] = (NB == 2 && bi == 0) ? first[m] : acc[m];
+      tot[m] = acc[m];
+#pragma unroll
+      for (int b = 0; b < NB - 1; ++b) tot[m] = bi == b ? done[b][m] : tot[m];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if constexpr (TT == 4) tot[m][r] += __shfl_xor(tot[m][r], 16, 64);
@@ -741,7 +754,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     // staged as few times as the GPU allows
     const int64_t per_tile = a.N / (16 * kWaves);
     int nb = 1;
-    for (int c = a.gated ? MLXR_STREAM_GATED_NB : MLXR_STREAM_MAX_NB; c > 1; --c)
+    for (int c = a.gated ? MLXR_STREAM_GATED_NB : MLXR_STREAM_MAX_NB; c > 1; c >>= 1)
       if (per_tile % c == 0 && max_items * (per_tile / c) >= kStreamSlots) {
         nb = c;
         break;
@@ -763,6 +776,10 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
 #endif
       if (a.gated)
         MLXR_QS(4, true, MLXR_STREAM_DEPTH4, 1);
+#if MLXR_STREAM_MAX_NB >= 4
+      else if (nb == 4)
+        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 4);
+#endif
       else if (nb == 2)
         MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 2);
       else
@@ -775,6 +792,10 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
 #endif
       if (a.gated)
         MLXR_QS(8, true, MLXR_STREAM_DEPTH8, 1);
+#if MLXR_STREAM_MAX_NB >= 4
+      else if (nb == 4)
+        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, 4);
+#endif
       else if (nb == 2)
         MLXR_QS(8, false, MLXR_STREAM_DEPTH8, 2);
       else

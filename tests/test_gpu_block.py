@@ -310,6 +310,9 @@ def test_checkpoint_round_trip_forward(pkg, orc, dev, tmp_path):
     put("shared_expert.down_proj", se.down_proj, True)
     put("gate", bw.gate_w, True)
     put("shared_expert_gate", bw.shared_gate_w, True)
+    g = torch.Generator(device=dev).manual_seed(9)
+    norm_w = (1 + 0.1 * torch.randn(cfg.d, generator=g, device=dev)).to(torch.bfloat16)
+    t["model.language_model.layers.5.post_attention_layernorm.weight"] = norm_w.cpu()
     d = tmp_path / "ck"
     d.mkdir()
     save_file(t, str(d / "model.safetensors"), metadata={"format": "mlx"})
@@ -317,9 +320,16 @@ def test_checkpoint_round_trip_forward(pkg, orc, dev, tmp_path):
          "language_model.model.layers.5.mlp.gate": {"group_size": 64, "bits": 8},
          "language_model.model.layers.5.mlp.shared_expert_gate": {"group_size": 64, "bits": 8}}
     (d / "config.json").write_text(json.dumps({"quantization": q,
-                                               "text_config": {"num_experts_per_tok": 2}}))
+                                               "text_config": {"num_experts_per_tok": 2,
+                                                               "rms_norm_eps": 1e-6}}))
     loaded = pkg.loader.qwen35_moe_block(d, 5, dev)
     x = W.make_x(cfg, 40, dev, seed=3)
     print("  checkpoint round trip T=40", flush=True)
     assert torch.equal(loaded(x), bw.block()(x))
     check_block(pkg, orc, bw, x)
+    # the layer tail from the same checkpoint (mlx format: the norm weight as
+    # stored)
+    norm = pkg.loader.post_attention_layernorm(d, 5, dev)
+    assert torch.equal(norm.weight, norm_w)
+    assert torch.equal(loaded.forward_residual(x, norm),
+                       bw.block().forward_residual(x, pkg.nn.RmsNorm(norm_w, 1e-6)))
