@@ -172,7 +172,7 @@ extern "C" {
 
 const char* mlxr_moe_last_error(void) { return g_last_error.c_str(); }
 
-int mlxr_moe_version(void) { return 200; }
+int mlxr_moe_version(void) { return 300; }
 
 int mlxr_moe_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
                       mlxr_moe_optional_int group_size,
