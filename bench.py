@@ -37,8 +37,11 @@ def parse():
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
                     help="replay one captured HIP graph per step, or launch eagerly")
     ap.add_argument("--sweep", default="c2:1,c2:8,c2:32,c3:512,c3:2048,c3:4096,c4:64,c4:2048,"
-                    "c5:32,c5:512,c6:64,c6:2048,c7:64,c7:2048,c8:64,c8:2048",
-                    help="extra cfg:T points timed after the headline ('' for none)")
+                    "c5:32,c5:512,c6:64,c6:2048,c6:64:res,c6:2048:res,c7:64,c7:2048,c8:64,"
+                    "c8:2048",
+                    help="extra cfg:T points timed after the headline ('' for none); "
+                         "cfg:T:res times the decoder layer's MoE half (RMSNorm, block, "
+                         "residual add)")
     ap.add_argument("--sweep-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound of the CPU-baseline sample (0 skips it)")
@@ -69,18 +72,27 @@ def host_cores() -> int:
 
 
 class Runner:
-    """One block at one T: eager or graph-replay steps on the current stream."""
+    """One block at one T: eager or graph-replay steps on the current stream.
+    residual: the decoder layer's MoE half instead (post-attention RMSNorm,
+    the block, the residual add: Qwen35MoeBlock.forward_residual)."""
 
-    def __init__(self, pkg, bw, T, dev, launch):
+    def __init__(self, pkg, bw, T, dev, launch, residual=False):
         import torch
         self.torch = torch
         self.T = T
         self.block = bw.block()
         self.x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
         self.out = torch.empty((T, bw.cfg.d), dtype=self.block.out_dtype, device=dev)
-        self.ws = pkg.ops.workspace(self.block.workspace_size(T), dev)
+        self.norm = None
+        if residual:
+            g = torch.Generator(device=dev).manual_seed(T)
+            w = (1 + 0.1 * torch.randn(bw.cfg.d, generator=g, device=dev)).to(torch.bfloat16)
+            self.norm = pkg.nn.RmsNorm(w, 1e-6)
+            self.ws = pkg.ops.workspace(self.block.residual_workspace_size(T), dev)
+        else:
+            self.ws = pkg.ops.workspace(self.block.workspace_size(T), dev)
         # one routed run: distinct experts for the byte count
-        self.block(self.x, out=self.out, workspace=self.ws, keep_routing=True)
+        self.run(keep_routing=True)
         torch.cuda.synchronize()
         self.idx = self.block.last_indices.clone()
         self.ref = self.out.clone()
@@ -106,8 +118,15 @@ class Runner:
                 self.eager()
                 torch.cuda.synchronize()
 
+    def run(self, keep_routing):
+        if self.norm is not None:
+            self.block.forward_residual(self.x, self.norm, out=self.out, workspace=self.ws,
+                                        keep_routing=keep_routing)
+        else:
+            self.block(self.x, out=self.out, workspace=self.ws, keep_routing=keep_routing)
+
     def eager(self):
-        self.block(self.x, out=self.out, workspace=self.ws, keep_routing=False)
+        self.run(keep_routing=False)
 
     def step(self):
         if self.graph is not None:
@@ -244,18 +263,20 @@ def main():
     sweep = []
     banks = {cfg.name: bw}
     for item in [s for s in args.sweep.split(",") if s]:
-        cname, tt = item.split(":")
-        tt = int(tt)
+        parts = item.split(":")
+        cname, tt = parts[0], int(parts[1])
+        res = len(parts) > 2 and parts[2] == "res"
         c2 = W.CONFIGS[cname]
         if c2.name not in banks:
             banks[c2.name] = W.make_weights(c2, dev)
-        r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch)
+        r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch, residual=res)
         s2 = r2.timed(args.sweep_steps, 5)
         U2 = W.distinct(r2.idx)
         # both rates for every point: the decode sizes and the small prefills
         # (c3 T=512, c4 T=2048, c5 T=512: arithmetic intensity below the
         # ridge) are HBM-bound, the large prefills MFMA-bound
-        ent = dict(config=c2.name, T=tt, tokens_per_s=round(tt / s2, 1),
+        ent = dict(config=c2.name + (" layer tail" if res else ""), T=tt,
+                   tokens_per_s=round(tt / s2, 1),
                    us_per_step=round(s2 * 1e6, 2), distinct_experts=U2,
                    block_hbm_gbs=round(W.algorithmic_bytes(c2, tt, U2) / s2 / 1e9, 1),
                    block_tflops=round(W.algorithmic_flops(c2, tt) / s2 / 1e12, 2))

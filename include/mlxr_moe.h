@@ -359,7 +359,7 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
  *   out_j = bf16(w_j * bf16(x_j * r)),  r = 1 / sqrt(sum_j x_j^2 / d + eps)
  * (the normalised value in the input dtype, then the weight product, MLX's
  * rounding points; the sum of squares in a fixed 64-lane order).  d % 4 ==
- * 0, x 8-byte aligned. */
+ * 0, x and out 8-byte aligned. */
 int mlxr_moe_rms_norm(const void* x, int64_t T, int64_t d, const void* weight,
                       float eps, void* out, mlxr_moe_stream stream);
 

@@ -461,7 +461,8 @@ int mlxr_moe_rms_norm(const void* x, int64_t T, int64_t d, const void* weight,
   if (d % 4) return fail("rms_norm: d must be a multiple of 4");
   if (!(eps >= 0.0f)) return fail("rms_norm: eps must be >= 0");
   if (T && (!x || !weight || !out)) return fail("rms_norm: null array");
-  if (!aligned(x, 8)) return fail("rms_norm: x must be 8-byte aligned");
+  if (!aligned(x, 8) || !aligned(out, 8))
+    return fail("rms_norm: x and out must be 8-byte aligned");
   return finish(from_hip(
       launch_rms_norm(static_cast<const uint16_t*>(x), T, d,
                       static_cast<const uint16_t*>(weight), eps,

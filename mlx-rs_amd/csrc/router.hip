@@ -399,9 +399,18 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   }
   const float ss = wave_sum_butterfly(acc);
   const float r = 1.0f / sqrtf(ss / (float)d + eps);
+  // the output in the same 4-element pieces: 8-byte loads of x and stores
   uint16_t* orow = out + (int64_t)t * d;
-  for (int j = lane; j < d; j += 64)
-    orow[j] = f32_to_bf16(bf16_to_f32(w[j]) * bf16_round(bf16_to_f32(xr[j]) * r));
+  for (int j0 = 4 * lane; j0 < d; j0 += 256) {
+    const uint2 u = *reinterpret_cast<const uint2*>(xr + j0);
+    const float v[4] = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                        __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      o[c] = f32_to_bf16(bf16_to_f32(w[j0 + c]) * bf16_round(v[c] * r));
+    *reinterpret_cast<uint2*>(orow + j0) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+  }
 }
 
 // gemma4's router top-k (wave_topk GEMMA): one wave per token; bf16 weights.
