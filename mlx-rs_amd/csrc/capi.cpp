@@ -619,13 +619,12 @@ int mlxr_moe_gemma_router_forward(const mlxr_moe_gemma_router* r,
                         nullptr,
                         nullptr}
         : RouterWeights{16, r->proj_weight, nullptr, nullptr, nullptr, nullptr, nullptr};
-  st = from_hip(launch_rms_norm(static_cast<const uint16_t*>(x), T, d,
-                                static_cast<const uint16_t*>(r->norm_weight),
-                                r->eps, normed, s),
-                "gemma_router rms_norm");
-  if (st.ok)
-    st = from_hip(launch_router_logits(normed, T, d, rw, nullptr, E, scores, E, s),
-                  "gemma_router scores");
+  // RMSNorm folded into the score kernel (the normalised rows land in
+  // `normed`)
+  const RouterNorm nm{static_cast<const uint16_t*>(r->norm_weight), r->eps, normed};
+  st = from_hip(launch_router_logits(static_cast<const uint16_t*>(x), T, d, rw,
+                                     nullptr, E, scores, E, s, &nm),
+                "gemma_router scores");
   if (st.ok)
     st = from_hip(launch_gemma_topk(scores, E, T, E, K,
                                     static_cast<const uint16_t*>(r->per_expert_scale),
@@ -812,14 +811,11 @@ int mlxr_moe_block_forward_residual(const mlxr_moe_block* block,
   c.take<int32_t>(1);  // status word, cleared by the routing kernel
   uint16_t* normed = c.take<uint16_t>(T * block->hidden_size);
   const uint16_t* hb = static_cast<const uint16_t*>(h);
-  // post_attention_layernorm (layer.rs:137), then the block with the
-  // residual add (layer.rs:138) in its combine
-  st = from_hip(launch_rms_norm(hb, T, block->hidden_size,
-                                static_cast<const uint16_t*>(norm_weight), eps,
-                                normed, s),
-                "post_attention_layernorm");
-  if (!st.ok) return finish(st);
-  return finish(m.forward(normed, T, out, topk_idx, topk_w, c, s, hb));
+  // post_attention_layernorm (layer.rs:137) folded into the router's
+  // logits kernel, which writes the normalised rows for the experts; the
+  // residual add (layer.rs:138) rides in the combine
+  const RouterNorm nm{static_cast<const uint16_t*>(norm_weight), eps, normed};
+  return finish(m.forward(hb, T, out, topk_idx, topk_w, c, s, hb, &nm));
 }
 
 int mlxr_moe_profile_start(const char* kernel) {

@@ -57,13 +57,22 @@ struct RouterWeights {
 inline RouterWeights router_weights_f32(const float* w, const float* w_extra) {
   return RouterWeights{0, w, nullptr, nullptr, w_extra, nullptr, nullptr};
 }
+// fast::rms_norm in front of the router: weight w [d] bf16, eps, and the
+// normalised rows out [T, d] bf16 (written for the experts that follow).
+struct RouterNorm {
+  const uint16_t* w;
+  float eps;
+  uint16_t* out;
+};
 // logits[t, e] for e < E (+ bias[e] when given, f32 weights only) and
 // column E from the extra row.  Quantised weights give bf16 logits (stored
-// as their f32 values).  ld = row stride of logits.
+// as their f32 values).  ld = row stride of logits.  With norm, the logits
+// of rms_norm(x) (and the normalised rows in norm->out), bit-identical to
+// launch_rms_norm followed by this call on its output.
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 const RouterWeights& w, const float* bias,
                                 int64_t E, float* logits, int64_t ld,
-                                hipStream_t s);
+                                hipStream_t s, const RouterNorm* norm = nullptr);
 // One wave per token; clears *status first when status != nullptr.  bf16:
 // the logits are bf16 and the selection is on their bf16 probabilities,
 // with bf16 weights (stored as f32).

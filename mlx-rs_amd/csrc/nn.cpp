@@ -412,7 +412,8 @@ void Qwen35MoeBlock::plan(Carve& ws, const mlxr_moe_block& b, int64_t T) {
 // the expert dispatch), [shared expert], gate/up, down, combine.
 Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
                                int32_t* topk_idx, float* topk_w, Carve& ws,
-                               hipStream_t s, const uint16_t* residual) const {
+                               hipStream_t s, const uint16_t* residual,
+                               const RouterNorm* norm) const {
   const int64_t d = b_.hidden_size, E = b_.num_experts;
   const int64_t K = b_.num_experts_per_tok;
   const bool shared = has_shared();
@@ -443,9 +444,10 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
                        static_cast<const uint16_t*>(sg.biases)};
   }
   Status st = from_hip(
-      launch_router_logits(x, T, d, rw, b_.gate_bias, E, logits, ld, s),
+      launch_router_logits(x, T, d, rw, b_.gate_bias, E, logits, ld, s, norm),
       "router logits");
   if (!st.ok) return st;
+  if (norm) x = norm->out;  // the experts read the normalised rows
   // softmax, argpartition top-k, renormalise (moe.rs:124-138) + gather_sort
   st = from_hip(launch_route(logits, ld, T, E, K, bf16, idx, wts,
                              prefill_tile_rows(T * K, E), db, s),

@@ -155,9 +155,12 @@ class Qwen35MoeBlock {
   // out f32 [T, d], bf16 with a quantised router; with residual (bf16
   // [T, d]) out = residual + the block's output (the decoder layer's add,
   // qwen3_5/text/layer.rs:138), fused into the combine
+  // With norm, x is the un-normalised input: the router normalises it and
+  // writes norm->out, which the experts then read.
   Status forward(const uint16_t* x, int64_t T, void* out, int32_t* topk_idx,
                  float* topk_w, Carve& ws, hipStream_t s,
-                 const uint16_t* residual = nullptr) const;
+                 const uint16_t* residual = nullptr,
+                 const RouterNorm* norm = nullptr) const;
   static void plan(Carve& ws, const mlxr_moe_block& b, int64_t T);
 
  private:

@@ -91,11 +91,17 @@ __device__ __forceinline__ float router_finish(float v, const float* bias,
 // One wave computes EB logit columns for up to TB tokens of a token block.
 // Router weights stream as float4 (16 B per lane), x as 4 bf16 (8 B); the
 // loads of U consecutive 256-wide steps are issued before their FMAs.
-template <int EB, int TB, int U, int BITS>
+// NORM: the logits of fast::rms_norm(x) instead (the norm in front of the
+// router folded in): each wave first takes the sum of squares of its tokens'
+// rows in rms_norm_kernel's lane order, then normalises every x element as
+// rms_norm_kernel does before its FMA, so the logits and the normalised rows
+// are bit-identical to the two-kernel sequence; the first wave of the first
+// expert block also writes the normalised rows (nm.out) for the experts.
+template <int EB, int TB, int U, int BITS, bool NORM>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
     const float* __restrict__ bias, int E, float* __restrict__ logits,
-    int64_t ld) {
+    int64_t ld, const RouterNorm nm) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int e_tot = E + (rw.w_extra ? 1 : 0);
@@ -116,11 +122,29 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   for (int q = 0; q < EB; ++q)
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt) acc[q][tt] = 0.0f;
+  float rs[TB];
+  const bool writer = NORM && nm.out && blockIdx.x == 0 && wave == 0;
+  if constexpr (NORM) {
+#pragma unroll
+    for (int tt = 0; tt < TB; ++tt) {
+      float a = 0.0f;
+      for (int j0 = 4 * lane; j0 < d; j0 += 256) {
+        const uint2 u = *reinterpret_cast<const uint2*>(xrow[tt] + j0);
+        const float v[4] = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                            __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) a = __builtin_fmaf(v[c], v[c], a);
+      }
+      const float ss = wave_sum_butterfly(a);
+      rs[tt] = 1.0f / sqrtf(ss / (float)d + nm.eps);
+    }
+  }
 
   const int steps = (d + 255) / 256;
   for (int i0 = 0; i0 < steps; i0 += U) {
     float4 wv[U][EB];
     uint2 xv[U][TB];
+    uint2 nwv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = 4 * lane + 256 * (i0 + u);
@@ -133,12 +157,31 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
       for (int tt = 0; tt < TB; ++tt)
         xv[u][tt] = in ? *reinterpret_cast<const uint2*>(xrow[tt] + j)
                        : make_uint2(0u, 0u);
+      nwv[u] = make_uint2(0u, 0u);
+      if constexpr (NORM)
+        nwv[u] = in ? *reinterpret_cast<const uint2*>(nm.w + j) : make_uint2(0u, 0u);
     }
     // elements past d contribute fmaf(0, 0, acc) = acc exactly
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int tt = 0; tt < TB; ++tt) {
+        if constexpr (NORM) {
+          // out_j = bf16(w_j * bf16(x_j * r)), as rms_norm_kernel
+          const uint2 xw = xv[u][tt], nw = nwv[u];
+          const uint32_t o0 = f32_to_bf16(__uint_as_float(nw.x << 16) *
+                                          bf16_round(__uint_as_float(xw.x << 16) * rs[tt]));
+          const uint32_t o1 = f32_to_bf16(__uint_as_float(nw.x & 0xffff0000u) *
+                                          bf16_round(__uint_as_float(xw.x & 0xffff0000u) * rs[tt]));
+          const uint32_t o2 = f32_to_bf16(__uint_as_float(nw.y << 16) *
+                                          bf16_round(__uint_as_float(xw.y << 16) * rs[tt]));
+          const uint32_t o3 = f32_to_bf16(__uint_as_float(nw.y & 0xffff0000u) *
+                                          bf16_round(__uint_as_float(xw.y & 0xffff0000u) * rs[tt]));
+          xv[u][tt] = make_uint2(o0 | (o1 << 16), o2 | (o3 << 16));
+          const int j = 4 * lane + 256 * (i0 + u);
+          if (writer && tt < nt && j < d)
+            *reinterpret_cast<uint2*>(nm.out + (int64_t)(t0 + tt) * d + j) = xv[u][tt];
+        }
         const float x0 = __uint_as_float(xv[u][tt].x << 16);
         const float x1 = __uint_as_float(xv[u][tt].x & 0xffff0000u);
         const float x2 = __uint_as_float(xv[u][tt].y << 16);
@@ -447,30 +490,54 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 #ifndef MLXR_RL_TILED_T
 #define MLXR_RL_TILED_T 256
 #endif
+// most tokens for which the norm in front of the router is folded into it
+#ifndef MLXR_RL_NORM_MAX_T
+#define MLXR_RL_NORM_MAX_T 2
+#endif
 template <int BITS>
 void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
                           const RouterWeights& w, const float* bias, int64_t E,
-                          float* logits, int64_t ld, hipStream_t s) {
+                          float* logits, int64_t ld, const RouterNorm* norm,
+                          hipStream_t s) {
   const int64_t e_tot = E + (w.w_extra ? 1 : 0);
+  const RouterNorm nm = norm ? *norm : RouterNorm{nullptr, 0.0f, nullptr};
   // Enough waves to have every CU pulling router weights at small T, and
   // register reuse of both operands (EB experts x TB tokens) at large T.
-#define MLXR_RL(EB, TB, U)                                                   \
-  router_logits_kernel<EB, TB, U, BITS>                                      \
+#define MLXR_RL_N(EB, TB, U, N)                                              \
+  router_logits_kernel<EB, TB, U, BITS, N>                                   \
       <<<dim3((unsigned)((e_tot + 4 * EB - 1) / (4 * EB)),                   \
               (unsigned)((T + TB - 1) / TB)),                                \
-         256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld)
-  if (T <= 2)
+         256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld, nm)
+#define MLXR_RL(EB, TB, U)           \
+  if (norm)                          \
+    MLXR_RL_N(EB, TB, U, true);      \
+  else                               \
+    MLXR_RL_N(EB, TB, U, false)
+  // The folded norm pays only while the launch it saves outweighs its
+  // repetition (every expert block of a token block normalises the same
+  // rows).  Measured on the c6 layer tail against the separate norm pass:
+  // T = 1 3 us and T = 2 1.3 us faster, T = 8 2 us and T = 16 8 us
+  // slower (c7's router: T = 1 2 us faster).  Above MLXR_RL_NORM_MAX_T
+  // tokens the norm is its own pass.
+  if (norm && T > MLXR_RL_NORM_MAX_T) {
+    launch_rms_norm(x, T, d, norm->w, norm->eps, norm->out, s);
+    x = norm->out;
+    norm = nullptr;
+  }
+  if (T <= 2) {
     MLXR_RL(1, 1, 8);
-  else if (T <= 16)
+  } else if (T <= 16) {
     MLXR_RL(1, 2, 8);
-  else if (T <= MLXR_RL_TILED_T)
-    MLXR_RL(MLXR_RL_MID_EB, MLXR_RL_MID_TB, MLXR_RL_MID_U);
-  else
+  } else if (T <= MLXR_RL_TILED_T) {
+    MLXR_RL_N(MLXR_RL_MID_EB, MLXR_RL_MID_TB, MLXR_RL_MID_U, false);
+  } else {
     router_logits_tiled_kernel<BITS>
         <<<dim3((unsigned)((e_tot + kRtCol - 1) / kRtCol),
                 (unsigned)((T + kRtTok - 1) / kRtTok)),
            256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld);
+  }
 #undef MLXR_RL
+#undef MLXR_RL_N
 }
 
 template <bool BF16>
@@ -500,19 +567,20 @@ void router_topk_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 const RouterWeights& w, const float* bias,
                                 int64_t E, float* logits, int64_t ld,
-                                hipStream_t s) {
+                                hipStream_t s, const RouterNorm* norm) {
   if (T == 0) return hipSuccess;
   if (w.bits != 0 && w.bits != 4 && w.bits != 8 && w.bits != 16)
     return hipErrorInvalidValue;
+  if (norm && (!norm->w || !norm->out || d % 4)) return hipErrorInvalidValue;
   ProfileScope prof("router_logits", s);
   if (w.bits == 16)
-    router_logits_launch<16>(x, T, d, w, bias, E, logits, ld, s);
+    router_logits_launch<16>(x, T, d, w, bias, E, logits, ld, norm, s);
   else if (w.bits == 8)
-    router_logits_launch<8>(x, T, d, w, bias, E, logits, ld, s);
+    router_logits_launch<8>(x, T, d, w, bias, E, logits, ld, norm, s);
   else if (w.bits == 4)
-    router_logits_launch<4>(x, T, d, w, bias, E, logits, ld, s);
+    router_logits_launch<4>(x, T, d, w, bias, E, logits, ld, norm, s);
   else
-    router_logits_launch<0>(x, T, d, w, bias, E, logits, ld, s);
+    router_logits_launch<0>(x, T, d, w, bias, E, logits, ld, norm, s);
   return hipGetLastError();
 }
 
