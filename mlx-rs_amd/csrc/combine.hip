@@ -18,6 +18,11 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// threads per workgroup (64 or 256)
+#ifndef MLXR_COMBINE_THREADS
+#define MLXR_COMBINE_THREADS 64
+#endif
+
 namespace mlxr_moe {
 namespace {
 
@@ -28,7 +33,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
     const float* __restrict__ shared_logit, int64_t shared_ld,
     const uint16_t* __restrict__ residual, void* __restrict__ out) {
   const int t = blockIdx.y;
-  const int n0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  const int n0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (t >= T || n0 >= d) return;
   float acc[8];
 #pragma unroll
@@ -113,18 +118,21 @@ hipError_t launch_combine(const uint16_t* y, const void* w, bool w_bf16,
                           void* out, bool bf16, hipStream_t s) {
   if (T == 0) return hipSuccess;
   if (w_bf16 && !bf16) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((d / 8 + 255) / 256), (unsigned)T);
+  // one-wave workgroups: a decode batch's rows spread over every CU (with
+  // 256-thread groups T = 64 rows of d = 2048 filled a quarter of them)
+  constexpr int kThreads = MLXR_COMBINE_THREADS;
+  const dim3 grid((unsigned)((d / 8 + kThreads - 1) / kThreads), (unsigned)T);
   ProfileScope prof("combine", s);
   const float* wf = static_cast<const float*>(w);
   const uint16_t* wh = static_cast<const uint16_t*>(w);
   if (w_bf16)
-    combine_kernel<true, uint16_t><<<grid, 256, 0, s>>>(
+    combine_kernel<true, uint16_t><<<grid, kThreads, 0, s>>>(
         y, wh, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, residual, out);
   else if (bf16)
-    combine_kernel<true, float><<<grid, 256, 0, s>>>(
+    combine_kernel<true, float><<<grid, kThreads, 0, s>>>(
         y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, residual, out);
   else
-    combine_kernel<false, float><<<grid, 256, 0, s>>>(
+    combine_kernel<false, float><<<grid, kThreads, 0, s>>>(
         y, wf, (int)T, (int)K, (int)d, shared_y, shared_logit, shared_ld, residual, out);
   return hipGetLastError();
 }
