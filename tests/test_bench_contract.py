@@ -1,0 +1,46 @@
+"""bench.py's contract on the CPU: one GPU only, the options the driver
+passes, and the algorithmic byte counts the roofline divides by."""
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _run(*args):
+    return subprocess.run([sys.executable, str(ROOT / "bench.py"), *args], cwd=ROOT,
+                          capture_output=True, text=True, timeout=120)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = _run("--gpus", "2", "--steps", "1", "--warmup", "0")
+    assert r.returncode == 2
+    assert "one MI355X" in r.stderr and r.stdout == ""
+
+
+def test_help_lists_the_driver_options_and_the_sweep_forms():
+    r = _run("--help")
+    assert r.returncode == 0
+    for opt in ("--gpus", "--steps", "--warmup", "--sweep", "--cpu-seconds"):
+        assert opt in r.stdout
+    assert "cfg:T:res" in r.stdout
+
+
+def test_algorithmic_bytes(pkg):
+    """Decode bytes per block forward (the distinct experts' weights, the
+    router, x in, out, routing): 4-bit at 0.5 + 4/64 bytes per weight,
+    dense bf16 at 2, with the router at its own width."""
+    W = pkg.workloads
+    c2, c8 = W.CONFIGS["c2"], W.CONFIGS["c8"]
+    T, U = 64, 126
+    want2 = (U * 3 * c2.f * c2.d * (0.5 + 4 / 64) + c2.E * c2.d * 4
+             + T * c2.d * 2 + T * c2.d * 4 + T * c2.K * 8)
+    assert W.algorithmic_bytes(c2, T, U) == int(want2)
+    U8 = 218
+    want8 = (U8 * 3 * c8.f * c8.d * 2 + c8.E * c8.d * 2 + 3 * c8.fs * c8.d * 2 + c8.d * 2
+             + T * c8.d * 2 + T * c8.d * 2 + T * c8.K * 8)
+    assert W.algorithmic_bytes(c8, T, U8) == int(want8)
+    assert W.weight_bytes_per_element(c8) == 2.0
+    assert W.weight_bytes_per_element(c2) == pytest.approx(0.5625)
