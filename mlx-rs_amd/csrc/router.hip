@@ -528,7 +528,10 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     MLXR_RL(1, 1, 8);
   } else if (T <= 16) {
     MLXR_RL(1, 2, 8);
-  } else if (T <= MLXR_RL_TILED_T) {
+  } else if (T <= MLXR_RL_TILED_T || d % 8 ||
+             (reinterpret_cast<uintptr_t>(x) & 15)) {
+    // (the tiled kernel stages x in 16-byte chunks of 8 values: whole
+    // chunks only, so rows of a multiple of 8 values, 16-byte aligned)
     MLXR_RL_N(MLXR_RL_MID_EB, MLXR_RL_MID_TB, MLXR_RL_MID_U, false);
   } else {
     router_logits_tiled_kernel<BITS>

@@ -153,6 +153,29 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+def _check_x(name: str, x, d: int, dtype=torch.bfloat16):
+    """x must be a `dtype` tensor whose last dim is d: the C ABI reads
+    T * d elements of that type.  (Callers check the device after every
+    shape check.)"""
+    if x.dtype != dtype:
+        raise MlxrMoeError(f"{name}: x must be {dtype}, got {x.dtype}")
+    if x.ndim < 1 or x.shape[-1] != d:
+        raise MlxrMoeError(f"{name}: x last dim must be {d}, got {tuple(x.shape)}")
+
+
+def _check_out(name: str, out, T: int, d: int, dtype, device):
+    """A caller's out must hold exactly T x d elements of `dtype`,
+    contiguously, on the inputs' device (the kernels write T * d of them)."""
+    if out.dtype != dtype:
+        raise MlxrMoeError(f"{name}: out must be {dtype}, got {out.dtype}")
+    if out.numel() != T * d or (out.ndim and out.shape[-1] != d):
+        raise MlxrMoeError(f"{name}: out must have shape ({T}, {d}), got {tuple(out.shape)}")
+    if not out.is_contiguous():
+        raise MlxrMoeError(f"{name}: out must be contiguous")
+    if out.device != device:
+        raise MlxrMoeError(f"{name}: out must be on {device}, got {out.device}")
+
+
 class SplitSwitchFfn:
     """SplitSwitchFfn<SwigluActivation>: gate_proj, up_proj [E, f, d],
     down_proj [E, d, f]; all three QuantizedSwitchLinear or all three dense
@@ -178,6 +201,8 @@ class SplitSwitchFfn:
 
     def _prep(self, x, indices):
         d = self.gate_proj.input_dims
+        _check_x("SplitSwitchFfn", x, d)
+        ops._dev(x, indices)
         x2 = x.reshape(-1, d).contiguous()
         K = indices.shape[-1]
         idx = indices.reshape(-1, K).to(torch.int32).contiguous()
@@ -203,6 +228,7 @@ class SplitSwitchFfn:
         """sum_k weights * expert_k(x) -> f32 [..., d] (switch.rs:446-474)."""
         x2, idx, K = self._prep(x, indices)
         T, d = x2.shape
+        ops._dev(x, weights)
         w = weights.reshape(-1, K).to(torch.float32).contiguous()
         out = torch.empty((T, d), dtype=torch.float32, device=x.device)
         lib = C.lib()
@@ -244,6 +270,8 @@ class PackedSwitchFfn:
 
     def _prep(self, x, indices):
         d = self.gate_up_proj.input_dims
+        _check_x("PackedSwitchFfn", x, d)
+        ops._dev(x, indices)
         x2 = x.reshape(-1, d).contiguous()
         K = indices.shape[-1]
         idx = indices.reshape(-1, K).to(torch.int32).contiguous()
@@ -276,8 +304,11 @@ class PackedSwitchFfn:
         if not bf16:
             w = w.to(torch.float32)
         odt = torch.bfloat16 if bf16 else torch.float32
+        ops._dev(x, weights)
         if out is None:
             out = torch.empty((T, d), dtype=odt, device=x.device)
+        else:
+            _check_out("PackedSwitchFfn", out, T, d, odt, x.device)
         if workspace is None:
             workspace = ops.workspace(self.workspace_size(T, K), x.device)
         C.check(C.lib().mlxr_moe_packed_switch_glu_forward(
@@ -324,7 +355,9 @@ class GemmaRouter:
 
     def forward(self, x, idx=None, weights=None, workspace=None):
         """x bf16 [..., d] -> (indices int32 [..., K], weights bf16 [..., K])."""
-        d = x.shape[-1]
+        d = self.hidden_size
+        _check_x("GemmaRouter", x, d)
+        ops._dev(x)
         x2 = x.reshape(-1, d).contiguous()
         T, K = x2.shape[0], self.top_k
         if idx is None:
@@ -361,7 +394,9 @@ class GemmaMoe:
         return ((a + 255) // 256) * 256 + self.experts.workspace_size(T, self.router.top_k)
 
     def forward(self, x, out=None, workspace=None, keep_routing=True):
-        d = x.shape[-1]
+        d = self.router.hidden_size
+        _check_x("GemmaMoe", x, d)
+        ops._dev(x)
         x2 = x.reshape(-1, d).contiguous()
         T, K = x2.shape[0], self.router.top_k
         if workspace is None:
@@ -457,6 +492,7 @@ class Qwen35MoeBlock:
         self.shared_expert = shared_expert
         self.num_experts_per_tok = num_experts_per_tok
         self.out_dtype = torch.bfloat16 if self.quantised_router else torch.float32
+        self.hidden_size = d
         f = switch_mlp.gate_proj.output_dims
         se = shared_expert
         self._desc = C.Block(
@@ -480,7 +516,9 @@ class Qwen35MoeBlock:
     def forward(self, x, out=None, workspace=None, keep_routing=True):
         """Qwen35MoeBlock::forward (moe.rs:116-146): x bf16 [..., d] ->
         [..., d], f32 (bf16 with a quantised router)."""
-        d = x.shape[-1]
+        d = self.hidden_size
+        _check_x("Qwen35MoeBlock", x, d)
+        ops._dev(x)
         x2 = x.reshape(-1, d)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
@@ -488,8 +526,10 @@ class Qwen35MoeBlock:
         K = self.num_experts_per_tok
         if out is None:
             out = torch.empty((T, d), dtype=self.out_dtype, device=x.device)
-        elif out.dtype != self.out_dtype:
-            raise MlxrMoeError(f"out must be {self.out_dtype}")
+        else:
+            _check_out("Qwen35MoeBlock", out, T, d, self.out_dtype, x.device)
+        if workspace is not None:
+            ops._dev(x, workspace)
         if workspace is None:
             need = self.workspace_size(T)
             if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
@@ -517,13 +557,20 @@ class Qwen35MoeBlock:
         the norm (post_attention_layernorm) one kernel before the block and
         the add fused into its combine.  h bf16 [..., d]; out f32 (bf16 with
         a bf16 router)."""
-        d = h.shape[-1]
+        d = self.hidden_size
+        _check_x("Qwen35MoeBlock.forward_residual", h, d)
+        if norm.weight.numel() != d:
+            raise MlxrMoeError(f"forward_residual: the norm weight must have {d} elements, "
+                               f"got {norm.weight.numel()}")
+        ops._dev(h, norm.weight)
         h2 = h.reshape(-1, d).contiguous()
         T, K = h2.shape[0], self.num_experts_per_tok
         if out is None:
             out = torch.empty((T, d), dtype=self.out_dtype, device=h.device)
-        elif out.dtype != self.out_dtype:
-            raise MlxrMoeError(f"out must be {self.out_dtype}")
+        else:
+            _check_out("Qwen35MoeBlock.forward_residual", out, T, d, self.out_dtype, h.device)
+        if workspace is not None:
+            ops._dev(h, workspace)
         if workspace is None:
             workspace = ops.workspace(self.residual_workspace_size(T), h.device)
         idx = wts = None
@@ -554,6 +601,7 @@ class RmsNorm:
         d = x.shape[-1]
         if d != self.weight.numel():
             raise MlxrMoeError("RmsNorm: last dim does not match the weight")
+        _check_x("RmsNorm", x, d)
         x2 = x.reshape(-1, d).contiguous()
         ops._dev(x2, self.weight)
         out = torch.empty_like(x2, dtype=torch.bfloat16)

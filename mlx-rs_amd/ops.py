@@ -66,6 +66,29 @@ def _as_u32(idx: torch.Tensor) -> torch.Tensor:
     return idx.to(torch.int32).contiguous()
 
 
+def _check_x_batch(name: str, x_batch_shape, idx_shape):
+    """Without lhs indices the kernels take x's batch b as b // (B // x_batch)
+    (B = the index count): right for x's batch shape equal to the index
+    shape's leading axes followed by singletons (x [.., T, 1, 1, K] against
+    indices [.., T, top_k], or one x batch for all).  Other broadcasts (a
+    leading singleton against a larger index axis) would pick wrong rows:
+    they are rejected."""
+    xs = list(x_batch_shape)
+    while len(xs) > len(idx_shape) and xs[0] == 1:
+        xs.pop(0)
+    ok = len(xs) <= len(idx_shape)
+    if ok:
+        pad = [1] * (len(idx_shape) - len(xs)) + xs
+        j = 0
+        while j < len(pad) and pad[j] == idx_shape[j]:
+            j += 1
+        ok = all(p == 1 for p in pad[j:])
+    if not ok:
+        raise MlxrMoeError(
+            f"{name}: x batch shape {tuple(x_batch_shape)} must be the indices' leading axes "
+            f"{tuple(idx_shape)} followed by singletons (or pass lhs_indices)")
+
+
 def quantize(w: torch.Tensor, group_size=None, bits=None):
     """(w_q, scales, biases) of MLX affine quantisation along the last axis.
     w_q is int32 storage of mlx's uint32 words."""
@@ -113,9 +136,11 @@ def gather_qmm(x, w, scales, biases=None, lhs_indices=None, rhs_indices=None,
     x [..., M, K] bf16; w [E, N, K*bits/32]; output rhs_indices.shape +
     [M, N].  Without lhs_indices, x's batch broadcasts over the trailing
     index axis (x [.., T, 1, 1, K] against indices [.., T, top_k])."""
-    _dev(x, w, scales, biases, lhs_indices, rhs_indices)
     if rhs_indices is None:
         raise MlxrMoeError("gather_qmm: rhs_indices are required")
+    if lhs_indices is None and rhs_indices.numel():
+        _check_x_batch("gather_qmm", x.shape[:-2], tuple(rhs_indices.shape))
+    _dev(x, w, scales, biases, lhs_indices, rhs_indices)
     b = DEFAULT_BITS if bits is None else bits
     x = x.contiguous()
     M, K = x.shape[-2], x.shape[-1]
@@ -151,9 +176,11 @@ def gather_mm(a, b, lhs_indices=None, rhs_indices=None, sorted_indices=False,
     swap_axes(weight, -1, -2), the same memory).  a [..., M, K] bf16; output
     rhs_indices.shape + [M, N] bf16, f32 accumulation.  Without lhs_indices,
     a's batch broadcasts over the trailing index axis."""
-    _dev(a, b, lhs_indices, rhs_indices)
     if rhs_indices is None:
         raise MlxrMoeError("gather_mm: rhs_indices are required")
+    if lhs_indices is None and rhs_indices.numel():
+        _check_x_batch("gather_mm", a.shape[:-2], tuple(rhs_indices.shape))
+    _dev(a, b, lhs_indices, rhs_indices)
     if not b_transposed:
         raise MlxrMoeError("gather_mm: only b stored [E, N, K] (b_transposed) is supported")
     if b.ndim != 3:

@@ -60,6 +60,38 @@ def check_gemma(pkg, orc, bw, x, nthreads=16):
     assert pkg.ops.workspace_status(block.last_workspace) == 0
 
 
+def _step(a):
+    """One bf16 step (ulp) at each value of a (0 at 0)."""
+    a = np.abs(np.asarray(a, np.float64))
+    return np.where(a > 0, 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - 7), 0.0)
+
+
+def flip_allowance(pkg, orc, bw, x, ridx, rw, tiled, nthreads=16):
+    """Per-element bound on what one-step flips of the block's bf16
+    intermediates can move the f32 output by: sum_k |w_k| step(y_k) +
+    sigmoid(g) step(y_s), from the oracle's own y [T, K, d] and shared y_s.
+    Two implementations of the same op sequence whose f32 sums run in
+    different orders round a small fraction of those bf16 values to
+    neighbouring steps; at large T some fall on the largest values, and one
+    step of a shared-expert output near 0.5 alone is ~2% of the block's RMS."""
+    cfg, p = bw.cfg, orc.block_params(bw)
+    T = x.shape[0]
+    xs = orc.to_np(x)[:, None, :]
+    ids = ridx.reshape(-1)
+    gq = lambda a, t, i, tl: orc.gather_qmm(a, *t, i, bits=cfg.bits, nthreads=nthreads,  # noqa
+                                            tiled=tl)
+    a = orc.swiglu(gq(xs, p["gate"], ids, tiled[0]), gq(xs, p["up"], ids, tiled[0]))
+    y = orc.bf16_to_f32(gq(a, p["down"], ids, tiled[0])).reshape(T, cfg.K, -1)
+    bound = np.einsum("tk,tkd->td", np.abs(rw.astype(np.float64)), _step(y))
+    if cfg.fs:
+        z = np.zeros(T, np.int32)
+        sa = orc.swiglu(gq(xs, p["shared_gate"], z, tiled[1]), gq(xs, p["shared_up"], z, tiled[1]))
+        ys = orc.bf16_to_f32(gq(sa, p["shared_down"], z, tiled[1])).reshape(T, -1)
+        sl = orc.router_logits(orc.to_np(x), p["shared_gate_w"])[:, 0].astype(np.float64)
+        bound += (1.0 / (1.0 + np.exp(-sl)))[:, None] * _step(ys)
+    return bound
+
+
 def check_block(pkg, orc, bw, x, nthreads=16):
     if bw.cfg.layout == "gemma":
         return check_gemma(pkg, orc, bw, x, nthreads)
@@ -91,8 +123,21 @@ def check_block(pkg, orc, bw, x, nthreads=16):
         a = np.abs(ref.astype(np.float64))
         ulp = np.where(a > 0, 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - 7), 0.0)
         assert np.all(diff <= 2e-2 * rms + ulp)
-    else:
-        assert err <= 2e-2 * rms
+    elif err > 2e-2 * rms:
+        # Past the bar only through one-step flips of bf16 intermediates:
+        # at most 1e-4 of the elements, each within the bar plus the step
+        # bound of the branch values it sums (the oracle's own).
+        over = diff > 2e-2 * rms
+        allow = flip_allowance(pkg, orc, bw, x, ridx, rw, tiled, nthreads)
+        print(f"  {int(over.sum())} of {over.size} elements past 2e-2*rms; "
+              f"max excess / flip bound {((diff - 2e-2 * rms) / allow)[over].max():.2f}",
+              flush=True)
+        assert over.sum() <= 1e-4 * over.size
+        assert np.all(diff <= 2e-2 * rms + allow)
+    # the bulk of the elements sit well inside the bar
+    q = np.quantile(diff, 0.999)
+    print(f"  p99.9 |err| / rms {q / rms:.2e}", flush=True)
+    assert q <= 1e-2 * rms
     assert pkg.ops.workspace_status(block.last_workspace) == 0
     return out, block
 
@@ -126,11 +171,14 @@ def test_c1_golden_fixture(pkg, orc, dev):
         assert np.array_equal(orc.to_np(sc), p[name][1])
 
 
-@pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 8), ("c2", 64), ("c5", 32),
-                                   ("c4", 1), ("c4", 64), ("c3", 512), ("c6", 1), ("c6", 64),
+@pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 8), ("c2", 32), ("c2", 64),
+                                   ("c5", 32), ("c5", 512), ("c4", 1), ("c4", 64), ("c4", 2048),
+                                   ("c3", 512), ("c3", 2048), ("c3", 4096), ("c6", 1), ("c6", 64),
                                    ("c6", 512), ("c7", 1), ("c7", 64), ("c7", 512),
                                    ("c8", 1), ("c8", 64), ("c8", 512)])
 def test_block_parity(pkg, orc, dev, cfg, T):
+    """Every BASELINE.json configuration at every token count the bench
+    reports (c1-c5), plus the Qwen3.6 (c6, c8) and gemma4 (c7) layouts."""
     bw = weights(pkg, cfg, dev)
     x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
     check_block(pkg, orc, bw, x)
@@ -279,6 +327,52 @@ def test_switch_glu_forward_matches_composition(pkg, orc, dev):
     ref = orc.combine(ya, w.cpu().numpy())
     rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
     assert np.abs(out.cpu().numpy() - ref).max() <= 2e-2 * rms
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_switch_glu_tall_prefill_tile(pkg, orc, dev, bits):
+    """The 256-row M-tiles of the prefill GEMMs (taken when the experts
+    average 192 rows or more: here 4096 rows over 16 experts), gated
+    (gate/up with the SwiGLU epilogue) and down, against the oracle's tiled
+    gather_qmm numerics, one expert much fuller than the rest."""
+    W = pkg.workloads
+    cfg = W.MoEConfig("tall_tile", d=512, E=16, K=2, f=512, bits=bits, tokens=(2048,))
+    bw = W.make_weights(cfg, dev)
+    T = 2048
+    assert T * cfg.K >= 192 * cfg.E and pkg.ops.gather_qmm_tiled(T * cfg.K, cfg.E)
+    x = W.make_x(cfg, T, dev, seed=21)
+    g = torch.Generator().manual_seed(21)
+    idx = torch.stack([torch.randperm(cfg.E, generator=g)[:cfg.K] for _ in range(T)]).int()
+    idx[: T // 2, 0] = 5  # expert 5: ~1100 rows, several tiles and a ragged last one
+    idx[: T // 2, 1] = torch.where(idx[: T // 2, 1] == 5, 6, idx[: T // 2, 1])
+    idx = idx.to(dev)
+    w = torch.rand((T, cfg.K), generator=g).to(dev)
+    print(f"  tall prefill tile bits={bits}", flush=True)
+    mlp = bw.switch_mlp
+    y = mlp.forward(x, idx)
+    out = mlp.forward_with_combine(x, idx, w)
+    p = orc.block_params(bw)
+    xs = orc.to_np(x)[:, None, :]
+    ids = idx.cpu().numpy().reshape(-1)
+    ga = orc.gather_qmm(xs, *p["gate"], ids, bits=bits, nthreads=16, tiled=True)
+    ua = orc.gather_qmm(xs, *p["up"], ids, bits=bits, nthreads=16, tiled=True)
+    ya = orc.gather_qmm(orc.swiglu(ga, ua), *p["down"], ids, bits=bits, nthreads=16,
+                        tiled=True).reshape(T, cfg.K, -1)
+    yf = orc.bf16_to_f32(ya).astype(np.float64)
+    rms = np.sqrt(np.mean(yf ** 2))
+    dy = np.abs(orc.bf16_to_f32(orc.to_np(y)).reshape(yf.shape) - yf)
+    print(f"  max|y err| {dy.max():.3e}  rms {rms:.3e}  "
+          f"{int((dy > 2e-2 * rms).sum())} of {dy.size} past 2e-2*rms", flush=True)
+    # bf16 y: one step of the oracle's value where the two f32 sums round
+    # apart (a step of a value past ~3 RMS is itself 2e-2 * RMS)
+    assert np.all(dy <= 2e-2 * rms + _step(yf))
+    assert (dy > 2e-2 * rms).sum() <= 1e-4 * dy.size
+    ref = orc.combine(ya, w.cpu().numpy())
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    do = np.abs(out.cpu().numpy() - ref)
+    flips = np.einsum("tk,tkd->td", np.abs(w.cpu().numpy().astype(np.float64)), _step(yf))
+    assert np.all(do <= 2e-2 * rms + flips)
+    assert (do > 2e-2 * rms).sum() <= 1e-4 * do.size
 
 
 def test_checkpoint_round_trip_forward(pkg, orc, dev, tmp_path):

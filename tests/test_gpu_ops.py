@@ -60,10 +60,17 @@ def test_quantize_full_expert_bank_bit_exact(pkg, orc, dev):
 
 # --------------------------------------------------------- router
 @pytest.mark.parametrize("T,d,E,K", [(16, 512, 8, 2), (1, 2048, 128, 8), (64, 2048, 128, 8),
-                                     (64, 2048, 512, 10), (300, 4096, 128, 8)])
+                                     (64, 2048, 512, 10), (300, 4096, 128, 8),
+                                     (300, 2052, 128, 8)])
 def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
     rng = np.random.default_rng(T * 7 + E)
-    x = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev)
+    print(f"  router_topk T={T} d={d} E={E} K={K}", flush=True)
+    # x is the head of a buffer whose tail holds NaN bits: a kernel that
+    # read past the last row (or past a row into the next) would turn a
+    # logit into NaN
+    buf = torch.full((T * d + 64,), float("nan"), dtype=torch.bfloat16, device=dev)
+    buf[:T * d] = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev).reshape(-1)
+    x = buf[:T * d].view(T, d)
     w = torch.from_numpy((rng.standard_normal((E, d)) * 0.02).astype(np.float32)).to(dev)
     idx, wts = pkg.ops.router_topk(x, w, K)
     lg = orc.router_logits(_np(orc, x), w.cpu().numpy())
@@ -96,7 +103,7 @@ def test_router_topk_quantized_bit_exact(pkg, orc, dev, T, d, E, K, bits):
 
 @pytest.mark.parametrize("T,d,E,K,bits", [(1, 2048, 128, 8, 16), (40, 2048, 128, 8, 16),
                                           (300, 2048, 128, 8, 16), (33, 2048, 256, 8, 8),
-                                          (7, 512, 8, 2, 16)])
+                                          (7, 512, 8, 2, 16), (300, 516, 64, 4, 16)])
 def test_gemma_router_bit_exact(pkg, orc, dev, T, d, E, K, bits):
     """gemma4 Router::forward (text.rs:621-665): RMSNorm, bf16 (or 8-bit)
     projection, top-K of the bf16 scores, softmax of the K scores times
@@ -218,7 +225,9 @@ def test_gather_qmm_reference_cases(pkg, orc, dev, bits):
     (16, 2, 8, 256, 512, 4), (32, 8, 128, 1536, 4096, 8), (7, 10, 512, 512, 2048, 4),
     (300, 8, 16, 128, 256, 4), (40, 1, 2, 64, 64, 8),
     # many rows per expert: the M-tiled prefill kernel, ragged last tiles
-    (1024, 4, 8, 256, 512, 8), (600, 8, 32, 384, 1024, 4)])
+    (1024, 4, 8, 256, 512, 8), (600, 8, 32, 384, 1024, 4),
+    # 256-row M-tiles (experts averaging >= 192 rows)
+    (2048, 2, 16, 256, 512, 4), (2048, 2, 16, 320, 1024, 8)])
 def test_gather_qmm_moe_unsorted_shapes(pkg, orc, dev, T, K, E, N, Kd, bits):
     """x [T, 1, 1, Kd] against indices [T, K] -> [T, K, 1, N]."""
     wq, sc, bi = _qbank(pkg, orc, E, N, Kd, bits, dev, T + E)

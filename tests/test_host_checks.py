@@ -1,0 +1,78 @@
+"""Host-side argument checks of the Python mirrors: shapes, dtypes and
+devices are rejected before any pointer reaches the C ABI (no GPU needed:
+every case here fails before a kernel could run)."""
+import pytest
+import torch
+
+
+def _tiny_block(pkg, d=128, E=4, f=64, K=2):
+    nn = pkg.nn
+    q = lambda out, inp: nn.QuantizedSwitchLinear(  # noqa: E731
+        torch.zeros((E, out, inp // 8), dtype=torch.int32),
+        torch.zeros((E, out, inp // 64), dtype=torch.bfloat16),
+        torch.zeros((E, out, inp // 64), dtype=torch.bfloat16), 64, 4)
+    mlp = nn.SplitSwitchFfn(q(f, d), q(f, d), q(d, f))
+    return nn.Qwen35MoeBlock(torch.zeros((E, d)), mlp, K)
+
+
+@pytest.mark.parametrize("xs,idx", [((), (5, 2)), ((5, 1), (5, 2)), ((1,), (5, 2)),
+                                    ((5, 2), (5, 2)), ((3, 1, 1), (3, 4, 2)),
+                                    ((1, 5, 1), (5, 2)), ((3, 4, 1), (3, 4, 2))])
+def test_x_batch_forms_accepted(pkg, xs, idx):
+    pkg.ops._check_x_batch("gather_qmm", xs, idx)
+
+
+@pytest.mark.parametrize("xs,idx", [((1, 3), (2, 3)), ((2,), (2, 3)), ((1, 2), (3, 2)),
+                                    ((4, 1), (5, 2)), ((2, 5, 1), (5, 2))])
+def test_x_batch_forms_rejected(pkg, xs, idx):
+    """A leading singleton broadcast against a larger index axis (MLX would
+    take x row b % 3; the kernels' b // (B / x_batch) would not)."""
+    with pytest.raises(pkg.MlxrMoeError, match="batch shape"):
+        pkg.ops._check_x_batch("gather_qmm", xs, idx)
+
+
+def test_gather_qmm_rejects_broadcast_before_launch(pkg):
+    x = torch.zeros((1, 3, 1, 64), dtype=torch.bfloat16)
+    idx = torch.zeros((2, 3), dtype=torch.int32)
+    with pytest.raises(pkg.MlxrMoeError, match="batch shape"):
+        pkg.ops.gather_qmm(x, torch.zeros((4, 64, 8), dtype=torch.int32),
+                           torch.zeros((4, 64, 1), dtype=torch.bfloat16),
+                           torch.zeros((4, 64, 1), dtype=torch.bfloat16), None, idx)
+    with pytest.raises(pkg.MlxrMoeError, match="batch shape"):
+        pkg.ops.gather_mm(x, torch.zeros((4, 64, 64), dtype=torch.bfloat16), None, idx)
+
+
+def test_block_rejects_wrong_x_before_launch(pkg):
+    blk = _tiny_block(pkg)
+    with pytest.raises(pkg.MlxrMoeError, match="must be torch.bfloat16"):
+        blk.forward(torch.zeros((3, 128), dtype=torch.float32))
+    with pytest.raises(pkg.MlxrMoeError, match="last dim must be 128"):
+        blk.forward(torch.zeros((3, 64), dtype=torch.bfloat16))
+    with pytest.raises(pkg.MlxrMoeError, match="ROCm device"):
+        blk.forward(torch.zeros((3, 128), dtype=torch.bfloat16))
+    norm = pkg.nn.RmsNorm(torch.ones(64))
+    with pytest.raises(pkg.MlxrMoeError, match="norm weight must have 128"):
+        blk.forward_residual(torch.zeros((3, 128), dtype=torch.bfloat16), norm)
+    with pytest.raises(pkg.MlxrMoeError, match="must be torch.bfloat16"):
+        blk.forward_residual(torch.zeros((3, 128), dtype=torch.float16), norm)
+    with pytest.raises(pkg.MlxrMoeError, match="must be torch.bfloat16"):
+        blk.switch_mlp.forward(torch.zeros((3, 128)), torch.zeros((3, 2), dtype=torch.int32))
+    with pytest.raises(pkg.MlxrMoeError, match="must be torch.bfloat16"):
+        pkg.nn.RmsNorm(torch.ones(128)).forward(torch.zeros((3, 128)))
+
+
+def test_out_checks(pkg):
+    chk = pkg.nn._check_out
+    dev = torch.device("cpu")
+    chk("b", torch.empty((3, 128)), 3, 128, torch.float32, dev)
+    chk("b", torch.empty((1, 3, 128)), 3, 128, torch.float32, dev)
+    with pytest.raises(pkg.MlxrMoeError, match="must be torch.float32"):
+        chk("b", torch.empty((3, 128), dtype=torch.bfloat16), 3, 128, torch.float32, dev)
+    with pytest.raises(pkg.MlxrMoeError, match=r"shape \(3, 128\)"):
+        chk("b", torch.empty((2, 128)), 3, 128, torch.float32, dev)
+    with pytest.raises(pkg.MlxrMoeError, match=r"shape \(3, 128\)"):
+        chk("b", torch.empty((128, 3)), 3, 128, torch.float32, dev)
+    with pytest.raises(pkg.MlxrMoeError, match="contiguous"):
+        chk("b", torch.empty((128, 3)).t(), 3, 128, torch.float32, dev)
+    with pytest.raises(pkg.MlxrMoeError, match="must be on"):
+        chk("b", torch.empty((3, 128), device="meta"), 3, 128, torch.float32, dev)

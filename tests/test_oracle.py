@@ -103,6 +103,59 @@ def test_quantize_bf16_storage_round_trip(orc):
     assert np.all(np.abs(wh - wf) <= bound)
 
 
+def test_quantize_edge_snap_closed_form(orc):
+    """MLX's affine recipe on a hand-computed group (4 bits, n_bins 15):
+    max 1.0, min m with (1 - m) = 15 / 7.7, so the unsnapped scale is
+    s0 = -(1 - m) / 15 and edge / s0 = -7.7.  The edge snaps to the
+    nearest code, q0 = -8 (a truncation would give -7), so the stored
+    scale is exactly 1 / -8 = -0.125 and the bias the edge, 1.0."""
+    w = np.zeros((1, 64), np.float32)
+    m = np.float32(1.0) - np.float32(15.0 / 7.7)
+    w[0, 0] = 1.0
+    w[0, 1] = m
+    w[0, 2:] = np.linspace(m, 1.0, 62, dtype=np.float32)
+    s0 = -((np.float32(1.0) - m) / np.float32(15.0))
+    assert -7.71 < np.float32(1.0) / s0 < -7.69  # the fraction rint and trunc split on
+    wq, sc, bi = orc.quantize(w, 64, 4, bf16=False)
+    assert sc[0, 0] == np.float32(-0.125) and bi[0, 0] == np.float32(1.0)
+    codes = (wq[0, :, None] >> (np.arange(8, dtype=np.uint32) * 4)) & 15
+    codes = codes.reshape(-1)
+    # the edge is code 0; the far end (m - 1) / -0.125 = 15.58 clamps to 15
+    assert codes[0] == 0 and codes[1] == 15
+    # and a negative edge: the same group mirrored snaps to +8 with bias -1
+    wq, sc, bi = orc.quantize(-w, 64, 4, bf16=False)
+    assert sc[0, 0] == np.float32(0.125) and bi[0, 0] == np.float32(-1.0)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantize_edge_snaps_to_nearest_code(orc, bits):
+    """For every group, q0 = bias / scale is the integer nearest to
+    edge / s0, with s0 = -+max((max - min) / n_bins, 1e-7) the unsnapped
+    scale (sign towards the smaller-magnitude end), both in f32.  Groups are
+    drawn so edge / s0 spans many fractions, both sides of one half."""
+    rng = np.random.default_rng(11 + bits)
+    n_bins = np.float32((1 << bits) - 1)
+    rows = 512
+    hi = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    lo = -hi * rng.uniform(0.0, 1.0, rows).astype(np.float32)
+    sign = np.where(rng.random(rows) < 0.5, 1.0, -1.0).astype(np.float32)
+    w = (rng.uniform(0, 1, (rows, 64)).astype(np.float32) * (hi - lo)[:, None] + lo[:, None])
+    w[:, 0], w[:, 1] = hi, lo
+    w *= sign[:, None]
+    wq, sc, bi = orc.quantize(w, 64, bits, bf16=False)
+    wmax, wmin = w.max(1), w.min(1)
+    neg = np.abs(wmin) > np.abs(wmax)
+    s0 = np.maximum((wmax - wmin) / n_bins, np.float32(1e-7)).astype(np.float32)
+    s0 = np.where(neg, s0, -s0).astype(np.float32)
+    edge = np.where(neg, wmin, wmax).astype(np.float32)
+    ratio = (edge / s0).astype(np.float64)
+    frac = np.abs(ratio - np.trunc(ratio))
+    assert (frac > 0.5).sum() > 50 and (frac < 0.5).sum() > 50
+    q0 = np.rint(bi[:, 0].astype(np.float64) / sc[:, 0].astype(np.float64))
+    assert np.all(np.abs(q0 - ratio) <= 0.5)
+    assert np.array_equal(bi[:, 0], edge)
+
+
 def test_quantize_rejects_bad_args(orc):
     with pytest.raises(ValueError):
         orc.quantize(np.zeros((2, 64), np.float32), 64, 3, bf16=False)
@@ -237,6 +290,84 @@ def test_combine_bf16_per_op_rounding(orc):
     routed = orc.bf16_to_f32(orc.combine_bf16(y, w)).astype(np.float64)
     mag = np.einsum("tk,tkd->td", np.abs(w), np.abs(orc.bf16_to_f32(y))).astype(np.float64)
     assert np.all(np.abs(routed - orc.combine(y, w)) <= (K + 1) * 2.0 ** -8 * mag)
+
+
+def test_shared_gate_closed_forms(orc):
+    """The shared branch is y_s * sigmoid(g) (moe.rs:118-120,145).  At
+    g = 0 the gate is exactly 1/2, at g = 40 it is 1 in f32 and at g = -40
+    it is ~4e-18, so out = routed + y_s / 2, routed + y_s and routed, each
+    exact in f32 (halving is exact); the bf16 combine the same with each
+    sum rounded once to bf16."""
+    rng = np.random.default_rng(5)
+    T, K, d = 3, 4, 64
+    y = orc.f32_to_bf16(rng.standard_normal((T, K, d)).astype(np.float32))
+    w = rng.random((T, K)).astype(np.float32)
+    sy = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    ys = orc.bf16_to_f32(sy)
+    routed = orc.combine(y, w)
+    assert np.all(routed != 0)
+    sl = np.array([0.0, 40.0, -40.0], np.float32)
+    got = orc.combine(y, w, sy, sl)
+    assert np.array_equal(got[0], (routed[0] + np.float32(0.5) * ys[0]).astype(np.float32))
+    assert np.array_equal(got[1], (routed[1] + ys[1]).astype(np.float32))
+    assert np.array_equal(got[2], routed[2])
+    # bf16 weights: out = bf16(bf16(y_s * gate) + bf16(routed sum))
+    bf = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(np.asarray(a, np.float32)))
+    wb = bf(w)
+    rb = orc.bf16_to_f32(orc.combine_bf16(y, wb))
+    gotb = orc.bf16_to_f32(orc.combine_bf16(y, wb, sy, sl))
+    assert np.array_equal(gotb[0], bf(rb[0] + bf(np.float32(0.5) * ys[0])))
+    assert np.array_equal(gotb[1], bf(rb[1] + ys[1]))
+    assert np.array_equal(gotb[2], rb[2])
+    # sigma(ln 3) = 3/4: within one f32 rounding of the gate
+    g = np.array([np.log(3.0)] * T, np.float32)
+    d3 = orc.combine(y, w, sy, g).astype(np.float64) - routed
+    assert np.allclose(d3, 0.75 * ys, rtol=2e-6, atol=1e-6 * np.abs(routed).max())
+
+
+@pytest.mark.parametrize("router_bits", [0, 8])
+def test_block_shared_branch_fp64(orc, router_bits):
+    """A block with a shared expert minus the same block without it (same
+    router, so the same routing) is sigmoid(x . g_s) * shared(x), checked
+    against an fp64 evaluation: the dequantised shared weights, matmuls
+    and the sigmoid in double, no intermediate roundings.  The bound
+    covers the bf16 rounding points of the reference's op sequence
+    (gather_qmm outputs, SwiGLU, the gate) on the f32 router, and the
+    bf16 output on the quantised one."""
+    p, x = _c1_params(orc, fs=256, router_bits=router_bits)
+    out1, idx1, w1 = orc.block_forward(p, x)
+    p0 = dict(p)
+    for k in ("shared_gate", "shared_up", "shared_down", "shared_gate_w", "shared_gate_q"):
+        p0.pop(k, None)
+    p0["fs"] = 0
+    out0, idx0, w0 = orc.block_forward(p0, x)
+    assert np.array_equal(idx0, idx1) and np.array_equal(w0, w1)
+    if router_bits:
+        out1, out0 = orc.bf16_to_f32(out1), orc.bf16_to_f32(out0)
+    got = out1.astype(np.float64) - out0.astype(np.float64)
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    deq = lambda t: orc.bf16_to_f32(orc.dequantize(*t, 64, 4))[0].astype(np.float64)
+    g = xf @ deq(p["shared_gate"]).T
+    u = xf @ deq(p["shared_up"]).T
+    ys = ((g / (1.0 + np.exp(-g))) * u) @ deq(p["shared_down"]).T
+    if router_bits:
+        gw = orc.dequantize(*p["shared_gate_q"], 64, 8, out_bf16=False)
+        sl = xf @ gw.astype(np.float64)[0]
+    else:
+        sl = xf @ p["shared_gate_w"].astype(np.float64)[0]
+    gate = 1.0 / (1.0 + np.exp(-sl))
+    assert np.all((gate > 0.05) & (gate < 0.95)) and np.ptp(gate) > 0.3
+    want = gate[:, None] * ys
+    rms = np.sqrt(np.mean(want ** 2))
+    # The bf16 roundings are unbiased noise: about 0.4% of the RMS on
+    # average, a few percent at the worst of 8192 elements.  A bf16 out
+    # (quantised router) adds up to one bf16 step of the routed part.
+    err = np.abs(got - want)
+    assert err.mean() <= 1e-2 * rms
+    assert np.all(err <= 8e-2 * rms + (2.0 ** -7 * np.abs(out0) if router_bits else 0.0))
+    # an ungated branch, or a constant gate of 1/2, is far outside
+    assert np.abs(ys - want).mean() > 10 * 1e-2 * rms
+    assert np.abs(0.5 * ys - want).mean() > 10 * 1e-2 * rms
 
 
 # ------------------------------------------------------------ dispatch
