@@ -353,6 +353,23 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
                            float* topk_w, void* workspace,
                            size_t workspace_size, mlxr_moe_stream stream);
 
+/* mlxr_moe_block_forward for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference (MLX allocates its
+ * intermediates itself).  Same arguments, results and checks, without the
+ * workspace: the scratch is a device array inside the library, one per GPU,
+ * of mlxr_moe_noalloc_scratch_size() bytes (MLXR_MOE_NOALLOC_SCRATCH_BYTES),
+ * held until the process ends.  A T whose block workspace
+ * (mlxr_moe_block_workspace_size) exceeds it is rejected with an error.
+ * Nothing is allocated.  Calls that overlap on one GPU share the array and
+ * race: serialise them (one stream, or events).  The status word of the
+ * last call is not readable through mlxr_moe_workspace_status. */
+#define MLXR_MOE_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
+size_t mlxr_moe_noalloc_scratch_size(void);
+int mlxr_moe_block_forward_noalloc(const mlxr_moe_block* block, const void* x,
+                                   int64_t T, void* out, int32_t* topk_idx,
+                                   float* topk_w, mlxr_moe_stream stream);
+
 /* fast::rms_norm as RmsNorm::forward calls it (crates/mlxr/src/layers/
  * normalization.rs:272-276; gemma4's router, crates/mlxr-lm/src/gemma4/
  * text/text.rs:640): x bf16 [T, d], weight bf16 [d] -> out bf16 [T, d],

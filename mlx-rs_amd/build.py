@@ -33,6 +33,7 @@ SOURCES = [
     "nn.cpp",
     "profile.cpp",
     "capi.cpp",
+    "noalloc.hip",
 ]
 
 COMMON = [

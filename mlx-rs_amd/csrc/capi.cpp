@@ -25,6 +25,13 @@ int fail(const std::string& msg) {
 
 int finish(const Status& st) { return st.ok ? 0 : fail(st.what); }
 
+}  // namespace
+
+// The thread-local error of the C ABI, for entry points in other sources.
+int mlxr_moe::capi_fail(const std::string& msg) { return fail(msg); }
+
+namespace {
+
 hipStream_t as_stream(mlxr_moe_stream s) {
   return reinterpret_cast<hipStream_t>(s);
 }
@@ -172,7 +179,7 @@ extern "C" {
 
 const char* mlxr_moe_last_error(void) { return g_last_error.c_str(); }
 
-int mlxr_moe_version(void) { return 300; }
+int mlxr_moe_version(void) { return 301; }
 
 int mlxr_moe_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
                       mlxr_moe_optional_int group_size,

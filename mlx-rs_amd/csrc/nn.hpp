@@ -41,6 +41,9 @@ struct Status {
   static Status error(std::string m) { return Status{false, std::move(m)}; }
 };
 
+// Sets the C ABI's thread-local error (mlxr_moe_last_error) and returns -1.
+int capi_fail(const std::string& msg);
+
 Status check_qlinear(const mlxr_moe_qlinear& q, int64_t experts, int64_t out,
                      int64_t in, const char* name);
 Status from_hip(hipError_t e, const char* where);

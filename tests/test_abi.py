@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(pkg):
     missing = [s for s in declared_symbols() if not hasattr(lib, s)]
     assert not missing
     assert sorted(pkg._capi.SIGNATURES) == declared_symbols()
-    assert pkg._capi.lib().mlxr_moe_version() == 300
+    assert pkg._capi.lib().mlxr_moe_version() == 301
 
 
 def _err(pkg):

@@ -76,3 +76,22 @@ def test_out_checks(pkg):
         chk("b", torch.empty((128, 3)).t(), 3, 128, torch.float32, dev)
     with pytest.raises(pkg.MlxrMoeError, match="must be on"):
         chk("b", torch.empty((3, 128), device="meta"), 3, 128, torch.float32, dev)
+
+
+def test_noalloc_refuses_oversize_on_host(pkg):
+    """The no-alloc block forward refuses a T whose workspace exceeds the
+    library's scratch array before touching the device (host pointers
+    here are never dereferenced)."""
+    import ctypes
+    blk = _tiny_block(pkg)
+    lib, C = pkg._capi.lib(), pkg._capi
+    cap = lib.mlxr_moe_noalloc_scratch_size()
+    T = 1
+    while blk.workspace_size(T) <= cap:
+        T *= 2
+    x = torch.zeros(16, dtype=torch.bfloat16)
+    rc = lib.mlxr_moe_block_forward_noalloc(ctypes.byref(blk.descriptor()), x.data_ptr(), T,
+                                            x.data_ptr(), None, None, None)
+    assert rc == -1 and "scratch" in C.last_error() and str(T) in C.last_error()
+    assert lib.mlxr_moe_block_forward_noalloc(None, None, 1, None, None, None, None) == -1
+    assert "null module" in C.last_error()
