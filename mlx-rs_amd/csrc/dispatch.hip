@@ -51,11 +51,15 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_rank_kernel(
   if (ok && r == 0) tab[wave * E + id] = (uint16_t)__popcll(match);
   __syncthreads();
   for (int e = tid; e < E; e += kDispatchBlock) {
+    // the 16 wave counts read at once, their exclusive prefix written back
+    int c[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) c[w] = tab[w * E + e];
     int run = 0;
+#pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const int c = tab[w * E + e];
       tab[w * E + e] = (uint16_t)run;
-      run += c;
+      run += c[w];
     }
     block_hist[(int64_t)blockIdx.x * E + e] = run;
   }

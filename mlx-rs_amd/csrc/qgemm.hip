@@ -74,6 +74,7 @@ constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
 // workgroups resident at once (2 per CU on 256 CUs)
 constexpr int64_t kStreamSlots = MLXR_STREAM_SLOTS;
 
+
 // Reorder 8 consecutive bf16 x values to the code order that unpack4 emits:
 // element j of the fragment holds x[perm(j)], perm = 0,4,1,5,2,6,3,7.
 __device__ __forceinline__ u32x4_t perm4(u32x4_t v) {
@@ -428,7 +429,8 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
 template <int BITS, bool GATED, int TT, int D, int NB>
 __device__ __forceinline__ void stream_body(const QGemmArgs& a,
                                             const int32_t* rec, int4 wk,
-                                            int tile, char* smem) {
+                                            int4 fr0, int4 fr1, int tile,
+                                            char* smem) {
   constexpr int nb = NB;
   static_assert(kWorkRows <= 8, "an item of a >4-row expert fits TT = 8");
   constexpr int NM = GATED ? 2 : 1;
@@ -489,14 +491,69 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
       for (int i = 0; i < NL; ++i) r.w[m][i] = wp[i];
     }
   };
-  Ring ring[R];
+  // Prologue.  Loads retire in issue order, so what the staging waits for
+  // is issued first: the x rows (L2 hits, shared by every tile of the
+  // item), then the wave's scales and biases, then the first D weight
+  // super-steps.  Staging x waits for the x loads alone, the barrier
+  // follows, and the weights' memory round trip overlaps both.  Every load
+  // is issued by every thread (indices clamped, the extra copies dropped):
+  // a load under a branch would make the compiler's wait counts cover the
+  // loads issued after it as well.
+
+  // x rows of the item's tokens, from the record's flat rows (fetched with
+  // its header; a row_map lookup issues every load before the first use)
+  int64_t xr[TT];
+  {
+    const int fl[8] = {fr0.x, fr0.y, fr0.z, fr0.w, fr1.x, fr1.y, fr1.z, fr1.w};
+    int32_t rm[TT];
+    if (!a.x_by_slot && a.row_map) {
 #pragma unroll
-  for (int j = 0; j < D; ++j) load(ring[j], min(j, total - 1));
+      for (int t = 0; t < TT; ++t) rm[t] = a.row_map[t < nt ? fl[t] : fl[0]];
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      int64_t r = 0;
+      if (t < nt)
+        r = a.x_by_slot ? row0 + t : (a.row_map ? rm[t] : fl[t] / a.row_div);
+      xr[t] = r;
+    }
+  }
+  // thread k8 holds elements 8*k8..8*k8+7 of every token; the token sums X
+  // of each 64-wide group come from the 8 threads sharing it
+  const int per_row = K >> 3;
+  auto load_x = [&](int k8, u32x4_t (&v)[TT]) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+      v[t] = *reinterpret_cast<const u32x4_t*>(a.x + xr[t] * a.x_ld + 8 * k8);
+  };
+  auto stage_x = [&](int k8, const u32x4_t (&v)[TT]) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const u32x4_t vt = t < nt ? v[t] : zq;
+      float sx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sx += __uint_as_float(vt[j] << 16) + __uint_as_float(vt[j] & 0xffff0000u);
+      sx += __shfl_xor(sx, 1, 64);
+      sx += __shfl_xor(sx, 2, 64);
+      sx += __shfl_xor(sx, 4, 64);
+      if ((k8 & 7) == 0) Xl[(k8 >> 3) * TT + t] = sx;
+      u32x4_t w = vt;
+      if constexpr (BITS == 4) w = perm4(w);
+      *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = w;
+    }
+  };
+  const int k8 = threadIdx.x;
+  const bool x_in = k8 < per_row;
+  u32x4_t xv[TT];
+  load_x(min(k8, per_row - 1), xv);
+  MLXR_SCHED_BARRIER();  // issue order is retire order: x first
 
   // Scales and biases of this wave's blocks: 16 rows x groups bf16 per
-  // block and array, contiguous in memory, copied to LDS with 16-byte loads
-  // (the hot loop then reads its two values per step from LDS): a per-step
-  // 2-byte load per lane would touch 16 cache lines for 128 useful bytes.
+  // block and array, contiguous in memory, copied to the wave's own LDS
+  // region with 16-byte loads (the hot loop then reads its two values per
+  // step from LDS): a per-step 2-byte load per lane would touch 16 cache
+  // lines for 128 useful bytes.
   const int sbn = nb * 16 * groups;  // bf16 per array
   const int sbv = sbn >> 3;          // 16-byte vectors per array
   uint16_t* sbl = reinterpret_cast<uint16_t*>(sb_base) + (size_t)wave * NA * sbn;
@@ -509,76 +566,42 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   }
   u32x4_t sv[NA];
   const bool s_in = lane < sbv;
+  const int sl = min(lane, sbv - 1);
 #pragma unroll
   for (int i = 0; i < NA; ++i)
-    sv[i] = s_in ? *reinterpret_cast<const u32x4_t*>(sbsrc[i] + 8 * lane) : zq;
+    sv[i] = *reinterpret_cast<const u32x4_t*>(sbsrc[i] + 8 * sl);
+  MLXR_SCHED_BARRIER();
 
-  // x rows of the item's tokens, from the record
-  int64_t xr[TT];
+  Ring ring[R];
 #pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    int64_t r = 0;
-    if (t < nt) {
-      const int slot = row0 + t;
-      const int flat = rec[4 + t];
-      r = a.x_by_slot ? slot : (a.row_map ? a.row_map[flat] : flat / a.row_div);
-    }
-    xr[t] = r;
-  }
-  // thread k8 holds elements 8*k8..8*k8+7 of every token; the token sums X
-  // of each 64-wide group come from the 8 threads sharing it
-  const int per_row = K >> 3;
-  auto load_x = [&](int k8, u32x4_t (&v)[TT]) {
-#pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      v[t] = zq;
-      if (t < nt)
-        v[t] = *reinterpret_cast<const u32x4_t*>(a.x + xr[t] * a.x_ld + 8 * k8);
-    }
-  };
-  auto stage_x = [&](int k8, const u32x4_t (&v)[TT]) {
-#pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      float sx = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        sx += __uint_as_float(v[t][j] << 16) + __uint_as_float(v[t][j] & 0xffff0000u);
-      sx += __shfl_xor(sx, 1, 64);
-      sx += __shfl_xor(sx, 2, 64);
-      sx += __shfl_xor(sx, 4, 64);
-      if ((k8 & 7) == 0) Xl[(k8 >> 3) * TT + t] = sx;
-      u32x4_t w = v[t];
-      if constexpr (BITS == 4) w = perm4(w);
-      *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = w;
-    }
-  };
-  {
-    // first chunk: every load above is in flight before the first store
-    const int k8 = threadIdx.x;
+  for (int j = 0; j < D; ++j) load(ring[j], min(j, total - 1));
+  MLXR_SCHED_BARRIER();
+
+  if (x_in) stage_x(k8, xv);  // per_row is a multiple of 8: whole octets
+  // the rest of x (input dims above 64 * 8 * waves)
+  for (int c8 = k8 + blockDim.x; c8 < per_row; c8 += blockDim.x) {
     u32x4_t v[TT];
-    const bool x_in = k8 < per_row;
-    if (x_in) load_x(k8, v);
-    if (s_in) {
-#pragma unroll
-      for (int i = 0; i < NA; ++i)
-        *reinterpret_cast<u32x4_t*>(sbl + i * sbn + 8 * lane) = sv[i];
-    }
-    if (x_in) stage_x(k8, v);  // per_row is a multiple of 8: whole octets
+    load_x(c8, v);
+    stage_x(c8, v);
   }
-  // the rest (input dims above 64 * 8 * waves, or long scale rows)
+  if (threadIdx.x == 0) *reinterpret_cast<u32x4_t*>(zero_blk) = zq;
+  __syncthreads();
+  // the scales (issued before the weights) -> this wave's region; only
+  // this wave reads it
+  if (s_in) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+      *reinterpret_cast<u32x4_t*>(sbl + i * sbn + 8 * lane) = sv[i];
+  }
   for (int i = lane + 64; i < sbv; i += 64) {
 #pragma unroll
     for (int j = 0; j < NA; ++j)
       *reinterpret_cast<u32x4_t*>(sbl + j * sbn + 8 * i) =
           *reinterpret_cast<const u32x4_t*>(sbsrc[j] + 8 * i);
   }
-  for (int k8 = threadIdx.x + blockDim.x; k8 < per_row; k8 += blockDim.x) {
-    u32x4_t v[TT];
-    load_x(k8, v);
-    stage_x(k8, v);
-  }
-  if (threadIdx.x == 0) *reinterpret_cast<u32x4_t*>(zero_blk) = zq;
-  __syncthreads();
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // The loop issues the same loads every super-step (past the end they
   // repeat the last step, a cache hit) and holds no stores, so the
@@ -700,6 +723,16 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   }
 }
 
+// Ring depth of the 8-token form (half the bytes per super-step of the
+// 4-token form): twice the 4-token depth unless set.
+#ifdef MLXR_STREAM_DEPTH_TT8
+template <int D>
+constexpr int kTT8Depth = MLXR_STREAM_DEPTH_TT8;
+#else
+template <int D>
+constexpr int kTT8Depth = 2 * D;
+#endif
+
 // Tokens per pass follow the expert's row count: 4 (GG = 4) for experts
 // with at most MLXR_STREAM_TT4_ROWS rows, else 8 (GG = 2).  LDS is sized
 // for 8.
@@ -710,16 +743,20 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
   const int ai = blockIdx.x / tiles_n, tile = blockIdx.x - ai * tiles_n;
   const int n_act = *a.num_work;
   const int32_t* rec = a.work + (int64_t)kWorkInts * ai;
+  // the whole 48-byte record at once: header and the 8 flat rows (records
+  // are 16-byte aligned)
   const int4 wk = *reinterpret_cast<const int4*>(rec);
+  const int4 fr0 = *reinterpret_cast<const int4*>(rec + 4);
+  const int4 fr1 = *reinterpret_cast<const int4*>(rec + 8);
   if (ai >= n_act) return;
   // The MFMA form follows the expert's row count (not the item's), so every
   // token of an expert is summed in the same order, wherever its item
   // boundaries fall.  The 8-token form moves half the bytes per super-step:
   // twice the depth.
   if (wk.w <= MLXR_STREAM_TT4_ROWS)
-    stream_body<BITS, GATED, 4, D, NB>(a, rec, wk, tile, smem);
+    stream_body<BITS, GATED, 4, D, NB>(a, rec, wk, fr0, fr1, tile, smem);
   else
-    stream_body<BITS, GATED, 8, 2 * D, NB>(a, rec, wk, tile, smem);
+    stream_body<BITS, GATED, 8, kTT8Depth<D>, NB>(a, rec, wk, fr0, fr1, tile, smem);
 }
 
 }  // namespace
@@ -760,11 +797,11 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
         break;
       }
     const int tiles_n = (int)(per_tile / nb);
+    const size_t sb_lds = (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
+    const dim3 grid((unsigned)(max_items * tiles_n));
     const size_t lds =
         (((size_t)kMaxTT * (a.K + 8) * 2 + 16 + (size_t)groups * kMaxTT * 4 + 15) &
-         ~size_t(15)) +
-        (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
-    const dim3 grid((unsigned)(max_items * tiles_n));
+         ~size_t(15)) + sb_lds;
     ProfileScope prof(profile, s);
 #define MLXR_QS(B, G, D, NB) \
   qgemm_stream_kernel<B, G, D, NB><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n)

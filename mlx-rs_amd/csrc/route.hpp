@@ -1,7 +1,7 @@
 // Device routines shared by the router and the dispatch kernels:
-//   wave_topk       top-K of one token's logits on one wave (radix select on
-//                   order-preserving keys, ballots only), softmax and the
-//                   renormalised top-K weights;
+//   wave_topk       top-K of one token's logits on one wave (K rounds of a
+//                   wave maximum of order-preserving keys, ties to the lower
+//                   id), softmax and the renormalised top-K weights;
 //   block_dispatch  stable counting sort of up to 1024 expert ids held in
 //                   LDS by one 1024-thread workgroup.
 #pragma once
@@ -18,7 +18,50 @@ __device__ __forceinline__ uint32_t float_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Per-wave scratch for wave_topk: the K selected (key, id) pairs.
+// Original float of an order-preserving key (-0 maps back to +0).
+__device__ __forceinline__ float key_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// DPP lane moves within 16-lane rows (no LDS): quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror; row_shr:n; row_bcast:15/31.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, false);
+}
+
+// Maximum over the wave of v, uniform: within each row by DPP, then the
+// four row results through scalar registers.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp<0xB1>(v));
+  v = max(v, dpp<0x4E>(v));
+  v = max(v, dpp<0x141>(v));
+  v = max(v, dpp<0x140>(v));
+  const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0),
+                         (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+  const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32),
+                         (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+  return max(a, b);
+}
+
+// Inclusive prefix sum over the wave (integers): row scans by DPP shifts,
+// then rows 1-3 add the running totals of the rows before them.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += dpp<0x111>(v);
+  v += dpp<0x112>(v);
+  v += dpp<0x114>(v);
+  v += dpp<0x118>(v);
+  v += dpp<0x142, 0xa>(v);
+  v += dpp<0x143, 0xc>(v);
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Per-wave scratch for wave_topk (unused by the selection below; kept for
+// the callers' LDS layout).
 struct TopkScratch {
   uint32_t key[64];
   int32_t id[64];
@@ -49,7 +92,6 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
                           TopkScratch* sc, int* out_id, float* out_w,
                           const uint16_t* __restrict__ pes = nullptr) {
   const int lane = threadIdx.x & 63;
-  const uint64_t below = (1ull << lane) - 1ull;
   float v[SLOTS];
   uint32_t key[SLOTS];
 #pragma unroll
@@ -79,107 +121,86 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s)
     key[s] = lane + 64 * s < E ? float_key(v[s]) : 0u;  // 0: below every real key
-  // theta = largest key with at least K keys >= theta (the K-th largest)
-  uint32_t theta = 0u;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = theta | (1u << b);
-    int cnt = 0;
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) cnt += __popcll(__ballot(key[s] >= cand));
-    if (cnt >= K) theta = cand;
-  }
-  // keys above theta, then the lowest-id keys equal to theta
-  int left = K;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) left -= __popcll(__ballot(key[s] > theta));
-  int base = 0;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    const uint64_t eq = __ballot(key[s] == theta);
-    const int take = min(__popcll(eq), left);
-    left -= take;
-    const bool sel =
-        key[s] > theta || (key[s] == theta && __popcll(eq & below) < take);
-    const uint64_t sm = __ballot(sel);
-    if (sel) {
-      const int pos = base + __popcll(sm & below);
-      sc->key[pos] = key[s];
-      sc->id[pos] = lane + 64 * s;
-      sc->val[pos] = v[s];
-    }
-    base += __popcll(sm);
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // rank of each selected pair: larger key first, then lower id
-  int my_id = 0, rank = 0;
-  uint32_t my_key = 0u;
+  // K rounds: the largest remaining key, the lowest expert id among equal
+  // keys (ids ascend with the slot, then the lane); lane k keeps the k-th
+  // pick -- the selection order of argpartition(-K) with the order inside
+  // the partition defined (descending, ties to the lower id).
+  int my_id = 0;
   float my_val = 0.0f;
-  if (lane < K) {
-    my_key = sc->key[lane];
-    my_id = sc->id[lane];
-    my_val = sc->val[lane];
-    for (int j = 0; j < K; ++j) {
-      const uint32_t kj = sc->key[j];
-      const int ij = sc->id[j];
-      rank += (kj > my_key || (kj == my_key && ij < my_id)) ? 1 : 0;
+  (void)sc;
+  for (int k = 0; k < K; ++k) {
+    uint32_t m = key[0];
+#pragma unroll
+    for (int s = 1; s < SLOTS; ++s) m = max(m, key[s]);
+    const uint32_t M = wave_max_u32(m);
+    int sel = 0;
+    bool found = false;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      const uint64_t b = __ballot(key[s] == M);
+      if (!found && b) {
+        sel = 64 * s + (int)__builtin_ctzll(b);
+        found = true;
+      }
+    }
+    float vs = v[0];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      if (s == (sel >> 6)) vs = v[s];
+      if (s == (sel >> 6) && lane == (sel & 63)) key[s] = 0u;
+    }
+    vs = readlane_f(vs, sel & 63);
+    if (lane == k) {
+      my_id = sel;
+      my_val = vs;
     }
   }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane < K) {
-    sc->id[rank] = my_id;
-    sc->val[rank] = my_val;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int id = lane < K ? sc->id[lane] : 0;
+  const int id = lane < K ? my_id : 0;
+  const float top = readlane_f(my_val, 0);  // the largest selected value
   if constexpr (GEMMA) {
-    const float m = sc->val[0];
-    const float dk = lane < K ? bf16_round(sc->val[lane] - m) : 0.0f;
+    const float m = top;
+    const float dk = lane < K ? bf16_round(my_val - m) : 0.0f;
     const float ek = lane < K ? bf16_round((float)exp((double)dk)) : 0.0f;
     float S = 0.0f;
-    for (int k = 0; k < K; ++k) S += __shfl(ek, k, 64);
+    for (int k = 0; k < K; ++k) S += readlane_f(ek, k);
     const float pk = bf16_round(ek / bf16_round(S));
     *out_id = id;
     *out_w = lane < K ? bf16_round(pk * bf16_to_f32(pes[id])) : 0.0f;
     return;
   }
   if constexpr (BF16) {
-    const float p = lane < K ? sc->val[lane] : 0.0f;
+    const float p = lane < K ? my_val : 0.0f;
     float psum = 0.0f;
-    for (int k = 0; k < K; ++k) psum += __shfl(p, k, 64);
+    for (int k = 0; k < K; ++k) psum += readlane_f(p, k);
     *out_id = id;
     *out_w = bf16_round(p / bf16_round(psum));
     return;
   }
-  // the selected logits come from LDS: no dependent re-read of memory
-  const float m = sc->val[0];
+  const float m = top;
   float acc = 0.0f;
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s)
     if (lane + 64 * s < E) acc += expf(v[s] - m);
   const float S = wave_sum_butterfly(acc);
-  const float p = lane < K ? expf(sc->val[lane] - m) / S : 0.0f;
+  const float p = lane < K ? expf(my_val - m) / S : 0.0f;
   float psum = 0.0f;
-  for (int k = 0; k < K; ++k) psum += __shfl(p, k, 64);
+  for (int k = 0; k < K; ++k) psum += readlane_f(p, k);
   *out_id = id;
   *out_w = p / psum;
 }
 
-// LDS of block_dispatch: per-wave match counts, scan scratch, offsets.
+// LDS of block_dispatch: per-wave match counts [wave * E + expert], scan
+// scratch, offsets.
 struct DispatchScratch {
-  uint16_t tab[kDispatchBlock / 64][kMaxExperts];
+  uint16_t tab[(kDispatchBlock / 64) * kMaxExperts];
   int wsum[kDispatchBlock / 64 + 1][4];
   int off[kMaxExperts];
   int wpos[kMaxExperts];
 };
 
 // Exclusive scans of four ints per thread over a 1024-thread workgroup at
-// once: wave scans, then wave 0 scans the 16 wave totals.  Two barriers.
+// once: DPP wave scans, the wave totals through LDS (one barrier), and every
+// thread adds the totals of the waves before its own.
 __device__ __forceinline__ void block_exclusive_scan4(const int (&v)[4],
                                                       int (&ex)[4],
                                                       int (&total)[4],
@@ -188,58 +209,46 @@ __device__ __forceinline__ void block_exclusive_scan4(const int (&v)[4],
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int inc[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    inc[k] = v[k];
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(inc[k], o, 64);
-      if (lane >= o) inc[k] += u;
-    }
-  }
+  for (int k = 0; k < 4; ++k) inc[k] = (int)wave_incl_scan((uint32_t)v[k]);
   if (lane == 63) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) wsum[wave][k] = inc[k];
   }
   __syncthreads();
-  if (wave == 0) {
+  int pre[4] = {0, 0, 0, 0}, all[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int t = lane < kWaves ? wsum[lane][k] : 0;
-      int s = t;
-#pragma unroll
-      for (int o = 1; o < kWaves; o <<= 1) {
-        const int u = __shfl_up(s, o, 64);
-        if (lane >= o) s += u;
-      }
-      if (lane < kWaves) wsum[lane][k] = s - t;
-      if (lane == kWaves - 1) wsum[kWaves][k] = s;
+      const int t = wsum[w][k];
+      pre[k] += w < wave ? t : 0;
+      all[k] += t;
     }
   }
-  __syncthreads();
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    ex[k] = wsum[wave][k] + inc[k] - v[k];
-    total[k] = wsum[kWaves][k];
+    ex[k] = pre[k] + inc[k] - v[k];
+    total[k] = all[k];
   }
 }
 
 // Stable counting sort of ids[0..n) (n <= 1024, read by thread i) by expert
 // in [0, E): counts, offsets, the active-expert list, the work item records,
 // the M-tile list and sorted/inv, exactly the permutation of a stable
-// argsort.  Ids of -1 are
-// left out silently; other ids outside [0, E) are left out and flag
-// *status.  Every thread of the 1024-thread workgroup must call it.
+// argsort.  Ids of -1 are left out silently; other ids outside [0, E) are
+// left out and flag *status.  Every thread of the 1024-thread workgroup
+// must call it.  Three barriers.
 __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
                                const DispatchBuffers& b, DispatchScratch* ls) {
   constexpr int kWaves = kDispatchBlock / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < kWaves * E; i += kDispatchBlock)
-    ls->tab[i / E][i % E] = 0;
-  __syncthreads();
+  uint32_t* tab32 = reinterpret_cast<uint32_t*>(ls->tab);
+  for (int i = tid; i < (kWaves * E + 1) / 2; i += kDispatchBlock) tab32[i] = 0u;
   const bool valid = tid < n;
   const int id = valid ? id_in : -1;
   const bool ok = valid && id >= 0 && id < E;
   if (valid && !ok && id != -1) *b.status = 1;
+  // threads of this wave with the same id: ballots over the id bits
   uint64_t match = __ballot(ok);
   const int id_bits = E > 1 ? 32 - __clz(E - 1) : 0;
   for (int bit = 0; bit < id_bits; ++bit) {
@@ -248,14 +257,20 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
     match &= on ? bal : ~bal;
   }
   const int r = __popcll(match & ((1ull << lane) - 1ull));
-  if (ok && r == 0) ls->tab[wave][id] = (uint16_t)__popcll(match);
+  __syncthreads();  // the table is zero
+  if (ok && r == 0) ls->tab[wave * E + id] = (uint16_t)__popcll(match);
   __syncthreads();
+  // per expert: the 16 wave counts read at once, their exclusive prefix
+  // written back (the rank base of each wave), the total
   int cnt = 0;
   if (tid < E) {
+    int c[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) c[w] = ls->tab[w * E + tid];
+#pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const int c = ls->tab[w][tid];
-      ls->tab[w][tid] = (uint16_t)cnt;
-      cnt += c;
+      ls->tab[w * E + tid] = (uint16_t)cnt;
+      cnt += c[w];
     }
   }
   // one scan: row offsets, active experts, work items, M-tiles
@@ -266,10 +281,21 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
   block_exclusive_scan4({cnt, has, nw, nt}, ex, tot, ls->wsum);
   const int off = ex[0], apos = ex[1], wpos = ex[2], tpos = ex[3];
   if (tid < E) {
-    b.counts[tid] = cnt;
-    b.offsets[tid] = off;
     ls->off[tid] = off;
     ls->wpos[tid] = wpos;
+  }
+  __syncthreads();
+  if (ok) {
+    const int rank = ls->tab[wave * E + id] + r;
+    const int pos = ls->off[id] + rank;
+    b.sorted[pos] = tid;
+    b.inv[tid] = pos;
+    b.work[kWorkInts * (ls->wpos[id] + rank / kWorkRows) + 4 +
+           rank % kWorkRows] = tid;
+  }
+  if (tid < E) {
+    b.counts[tid] = cnt;
+    b.offsets[tid] = off;
   }
   if (has) b.active[apos] = tid;
   for (int j = 0; j < nw; ++j) {
@@ -288,15 +314,6 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
     *b.num_active = tot[1];
     *b.num_work = tot[2];
     *b.num_tiles = tot[3];
-  }
-  __syncthreads();
-  if (ok) {
-    const int rank = ls->tab[wave][id] + r;
-    const int pos = ls->off[id] + rank;
-    b.sorted[pos] = tid;
-    b.inv[tid] = pos;
-    b.work[kWorkInts * (ls->wpos[id] + rank / kWorkRows) + 4 +
-           rank % kWorkRows] = tid;
   }
 }
 
