@@ -86,8 +86,9 @@ __device__ __forceinline__ int upper_slot(const int* start, int n, int v) {
 // search).  The scatter into sorted/inv is dispatch_scatter_kernel.
 __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
     int n, int E, int nb, int tile_rows, DispatchBuffers b) {
-  __shared__ int s_off[kMaxExperts], s_wpos[kMaxExperts], s_tpos[kMaxExperts];
-  __shared__ int wsum[kWaves + 1][4];
+  __shared__ int s_off[kMaxExperts], s_wlong[kMaxExperts], s_wshort[kMaxExperts],
+      s_tpos[kMaxExperts];
+  __shared__ int wsum[kWaves + 1][kScanVals];
   const int tid = threadIdx.x;
   // exclusive prefix of each expert's column over the workgroups, 16 loads
   // in flight at a time (a load after a store of the same array would wait
@@ -107,19 +108,23 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
       }
     }
   }
-  // one scan: row offsets, active experts, work items, M-tiles
+  // one scan: row offsets, active experts, work items (long form first),
+  // M-tiles
   const int has = (tid < E && cnt > 0) ? 1 : 0;
-  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
+  int nw_long, nw_short;
+  work_counts(cnt, tid < E, nw_long, nw_short);
   const int nt = (tid < E) ? (cnt + tile_rows - 1) / tile_rows : 0;
-  int ex[4], tot[4];
-  block_exclusive_scan4({cnt, has, nw, nt}, ex, tot, wsum);
-  const int off = ex[0], wpos = ex[2], tpos = ex[3];
-  const int total = tot[0], n_work = tot[2], n_tiles = tot[3];
+  int ex[5], tot[5];
+  block_exclusive_scan<5>({cnt, has, nw_long, nw_short, nt}, ex, tot, wsum);
+  const int off = ex[0], tpos = ex[4];
+  const int wpos = nw_long ? ex[2] : tot[2] + ex[3];
+  const int total = tot[0], n_work = tot[2] + tot[3], n_tiles = tot[4];
   if (tid < E) {
     b.counts[tid] = cnt;
     b.offsets[tid] = off;
     s_off[tid] = off;
-    s_wpos[tid] = wpos;
+    s_wlong[tid] = ex[2];
+    s_wshort[tid] = tot[2] + ex[3];
     b.work_first[tid] = wpos;
     s_tpos[tid] = tpos;
   }
@@ -131,10 +136,12 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_scan_kernel(
     *b.num_tiles = n_tiles;
   }
   __syncthreads();
-  // experts with no rows share their start with the next: the search finds
-  // the last expert starting at or before the entry, which has rows
+  // experts with no items in a region share their start with the next: the
+  // search (the long-form region, then the rest) finds the last expert
+  // starting at or before the entry, which has items there
   for (int i = tid; i < n_work; i += kDispatchBlock) {
-    const int e = upper_slot(s_wpos, E, i), j = i - s_wpos[e];
+    const int* start = i < tot[2] ? s_wlong : s_wshort;
+    const int e = upper_slot(start, E, i), j = i - start[e];
     const int cnt_e = (e + 1 < E ? s_off[e + 1] : total) - s_off[e];
     int32_t* w = b.work + kWorkInts * i;
     w[0] = e;

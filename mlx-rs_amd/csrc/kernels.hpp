@@ -123,6 +123,14 @@ constexpr int kWorkRows = 8;
 // item's slots (unset past rows).  A GEMM workgroup learns its task, and
 // where its x rows live, from these 48 bytes without a dependent load.
 constexpr int kWorkInts = 4 + kWorkRows;
+// The streaming decode GEMM runs the items of experts with at most this many
+// rows in its 4-token MFMA form, the others in the 8-token form (longer per
+// item: the dispatch lists their items first, so the long workgroups start
+// in the first wave of the grid rather than making its tail).
+#ifndef MLXR_STREAM_TT4_ROWS
+#define MLXR_STREAM_TT4_ROWS 4
+#endif
+constexpr int kStreamTT4Rows = MLXR_STREAM_TT4_ROWS;
 int64_t dispatch_max_tiles(int64_t n, int64_t E, int tile_rows);
 // Bound on the work items of n flat rows over E experts.
 inline int64_t dispatch_max_work(int64_t n, int64_t E) {

@@ -54,10 +54,7 @@ namespace {
 #ifndef MLXR_SCHED_BARRIER
 #define MLXR_SCHED_BARRIER() __builtin_amdgcn_sched_barrier(0)
 #endif
-// experts with at most this many rows use the 4-token MFMA form
-#ifndef MLXR_STREAM_TT4_ROWS
-#define MLXR_STREAM_TT4_ROWS 4
-#endif
+
 constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
 // 16-channel blocks per wave of the down kernel, at most (1, 2 or 4; the
 // launcher halves it until the grid keeps every slot busy)
@@ -734,7 +731,7 @@ constexpr int kTT8Depth = 2 * D;
 #endif
 
 // Tokens per pass follow the expert's row count: 4 (GG = 4) for experts
-// with at most MLXR_STREAM_TT4_ROWS rows, else 8 (GG = 2).  LDS is sized
+// with at most kStreamTT4Rows rows, else 8 (GG = 2).  LDS is sized
 // for 8.
 template <int BITS, bool GATED, int D, int NB>
 __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
@@ -753,7 +750,7 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
   // token of an expert is summed in the same order, wherever its item
   // boundaries fall.  The 8-token form moves half the bytes per super-step:
   // twice the depth.
-  if (wk.w <= MLXR_STREAM_TT4_ROWS)
+  if (wk.w <= kStreamTT4Rows)
     stream_body<BITS, GATED, 4, D, NB>(a, rec, wk, fr0, fr1, tile, smem);
   else
     stream_body<BITS, GATED, 8, kTT8Depth<D>, NB>(a, rec, wk, fr0, fr1, tile, smem);

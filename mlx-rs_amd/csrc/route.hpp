@@ -11,6 +11,9 @@
 
 namespace mlxr_moe {
 
+// Values one block_exclusive_scan covers at most.
+constexpr int kScanVals = 5;
+
 // Order-preserving key of a float: larger float, larger key; -0 == +0.
 __device__ __forceinline__ uint32_t float_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -193,43 +196,57 @@ __device__ void wave_topk(const float* __restrict__ logits, int E, int K,
 // scratch, offsets.
 struct DispatchScratch {
   uint16_t tab[(kDispatchBlock / 64) * kMaxExperts];
-  int wsum[kDispatchBlock / 64 + 1][4];
+  int wsum[kDispatchBlock / 64 + 1][kScanVals];
   int off[kMaxExperts];
   int wpos[kMaxExperts];
 };
 
-// Exclusive scans of four ints per thread over a 1024-thread workgroup at
+// Exclusive scans of NV ints per thread over a 1024-thread workgroup at
 // once: DPP wave scans, the wave totals through LDS (one barrier), and every
 // thread adds the totals of the waves before its own.
-__device__ __forceinline__ void block_exclusive_scan4(const int (&v)[4],
-                                                      int (&ex)[4],
-                                                      int (&total)[4],
-                                                      int (*wsum)[4]) {
+template <int NV>
+__device__ __forceinline__ void block_exclusive_scan(const int (&v)[NV],
+                                                     int (&ex)[NV],
+                                                     int (&total)[NV],
+                                                     int (*wsum)[kScanVals]) {
+  static_assert(NV <= kScanVals, "scan scratch holds kScanVals values");
   constexpr int kWaves = kDispatchBlock / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc[4];
+  int inc[NV];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) inc[k] = (int)wave_incl_scan((uint32_t)v[k]);
+  for (int k = 0; k < NV; ++k) inc[k] = (int)wave_incl_scan((uint32_t)v[k]);
   if (lane == 63) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) wsum[wave][k] = inc[k];
+    for (int k = 0; k < NV; ++k) wsum[wave][k] = inc[k];
   }
   __syncthreads();
-  int pre[4] = {0, 0, 0, 0}, all[4] = {0, 0, 0, 0};
+  int pre[NV], all[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) pre[k] = all[k] = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < NV; ++k) {
       const int t = wsum[w][k];
       pre[k] += w < wave ? t : 0;
       all[k] += t;
     }
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < NV; ++k) {
     ex[k] = pre[k] + inc[k] - v[k];
     total[k] = all[k];
   }
+}
+
+// Work items per expert of cnt rows, listed long form first: the items of
+// experts above kStreamTT4Rows rows (the streaming GEMM's slower 8-token
+// form) take positions [0, total_long), the others follow.
+__device__ __forceinline__ void work_counts(int cnt, bool expert, int& nw_long,
+                                            int& nw_short) {
+  const int nw = expert ? (cnt + kWorkRows - 1) / kWorkRows : 0;
+  nw_long = cnt > kStreamTT4Rows ? nw : 0;
+  nw_short = cnt > kStreamTT4Rows ? 0 : nw;
 }
 
 // Stable counting sort of ids[0..n) (n <= 1024, read by thread i) by expert
@@ -273,13 +290,17 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
       cnt += c[w];
     }
   }
-  // one scan: row offsets, active experts, work items, M-tiles
+  // one scan: row offsets, active experts, work items (long form first),
+  // M-tiles
   const int has = (tid < E && cnt > 0) ? 1 : 0;
-  const int nw = tid < E ? (cnt + kWorkRows - 1) / kWorkRows : 0;
+  int nw_long, nw_short;
+  work_counts(cnt, tid < E, nw_long, nw_short);
+  const int nw = nw_long + nw_short;
   const int nt = tid < E ? (cnt + tile_rows - 1) / tile_rows : 0;
-  int ex[4], tot[4];
-  block_exclusive_scan4({cnt, has, nw, nt}, ex, tot, ls->wsum);
-  const int off = ex[0], apos = ex[1], wpos = ex[2], tpos = ex[3];
+  int ex[5], tot[5];
+  block_exclusive_scan<5>({cnt, has, nw_long, nw_short, nt}, ex, tot, ls->wsum);
+  const int off = ex[0], apos = ex[1], tpos = ex[4];
+  const int wpos = nw_long ? ex[2] : tot[2] + ex[3];
   if (tid < E) {
     ls->off[tid] = off;
     ls->wpos[tid] = wpos;
@@ -312,8 +333,8 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
   if (tid == 0) {
     b.offsets[E] = tot[0];
     *b.num_active = tot[1];
-    *b.num_work = tot[2];
-    *b.num_tiles = tot[3];
+    *b.num_work = tot[2] + tot[3];
+    *b.num_tiles = tot[4];
   }
 }
 

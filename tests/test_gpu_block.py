@@ -172,6 +172,7 @@ def test_c1_golden_fixture(pkg, orc, dev):
 
 
 @pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 8), ("c2", 32), ("c2", 64),
+                                   ("c2", 256),
                                    ("c5", 32), ("c5", 512), ("c4", 1), ("c4", 64), ("c4", 2048),
                                    ("c3", 512), ("c3", 2048), ("c3", 4096), ("c6", 1), ("c6", 64),
                                    ("c6", 512), ("c7", 1), ("c7", 64), ("c7", 512),

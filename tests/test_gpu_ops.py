@@ -227,7 +227,10 @@ def test_gather_qmm_reference_cases(pkg, orc, dev, bits):
     # many rows per expert: the M-tiled prefill kernel, ragged last tiles
     (1024, 4, 8, 256, 512, 8), (600, 8, 32, 384, 1024, 4),
     # 256-row M-tiles (experts averaging >= 192 rows)
-    (2048, 2, 16, 256, 512, 4), (2048, 2, 16, 320, 1024, 8)])
+    (2048, 2, 16, 256, 512, 4), (2048, 2, 16, 320, 1024, 8),
+    # more than 1024 ids (the multi-kernel dispatch) on the decode kernels:
+    # its work list, long-form items first
+    (200, 8, 128, 768, 2048, 4), (160, 8, 128, 256, 1024, 8)])
 def test_gather_qmm_moe_unsorted_shapes(pkg, orc, dev, T, K, E, N, Kd, bits):
     """x [T, 1, 1, Kd] against indices [T, K] -> [T, K, 1, N]."""
     wq, sc, bi = _qbank(pkg, orc, E, N, Kd, bits, dev, T + E)
