@@ -36,12 +36,13 @@ def parse():
     ap.add_argument("--tokens", type=int, default=64, help="T of the headline line")
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
                     help="replay one captured HIP graph per step, or launch eagerly")
-    ap.add_argument("--sweep", default="c2:1,c2:8,c2:32,c3:512,c3:2048,c3:4096,c4:64,c4:2048,"
-                    "c5:32,c5:512,c6:64,c6:2048,c6:64:res,c6:2048:res,c7:64,c7:2048,c8:64,"
-                    "c8:2048",
+    ap.add_argument("--sweep", default="c2:1,c2:1:cold,c2:8,c2:8:cold,c2:32,c2:32:cold,c3:512,"
+                    "c3:2048,c3:4096,c4:64,c4:2048,c5:32,c5:512,c6:64,c6:2048,c6:64:res,"
+                    "c6:2048:res,c7:64,c7:2048,c8:64,c8:2048",
                     help="extra cfg:T points timed after the headline ('' for none); "
                          "cfg:T:res times the decoder layer's MoE half (RMSNorm, block, "
-                         "residual add)")
+                         "residual add); cfg:T:cold rotates copies of the weights so "
+                         "every forward reads its experts from HBM")
     ap.add_argument("--sweep-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound of the CPU-baseline sample (0 skips it)")
@@ -64,23 +65,32 @@ def copy_calibration(mib: int) -> None:
 
 
 def host_cores() -> int:
+    """The cores this process may run on (its affinity mask), within an
+    OpenMP thread limit the host sets (OMP_NUM_THREADS)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+    lim = os.environ.get("OMP_NUM_THREADS", "")
+    if lim.isdigit() and int(lim) > 0:
+        n = min(n, int(lim))
+    return max(1, n)
 
 
 class Runner:
     """One block at one T: eager or graph-replay steps on the current stream.
     residual: the decoder layer's MoE half instead (post-attention RMSNorm,
-    the block, the residual add: Qwen35MoeBlock.forward_residual)."""
+    the block, the residual add: Qwen35MoeBlock.forward_residual).
+    banks: more copies of the weights in their own memory (a cold-cache
+    measurement, like a decoder whose every step reads another layer's
+    experts): one step is one forward on the next bank in turn."""
 
-    def __init__(self, pkg, bw, T, dev, launch, residual=False):
+    def __init__(self, pkg, bw, T, dev, launch, residual=False, banks=()):
         import torch
         self.torch = torch
         self.T = T
-        self.block = bw.block()
+        self.blocks = [b.block() for b in (bw, *banks)]
+        self.block = self.blocks[0]
         self.x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
         self.out = torch.empty((T, bw.cfg.d), dtype=self.block.out_dtype, device=dev)
         self.norm = None
@@ -118,15 +128,18 @@ class Runner:
                 self.eager()
                 torch.cuda.synchronize()
 
-    def run(self, keep_routing):
+    def run(self, keep_routing, block=None):
+        block = block or self.block
         if self.norm is not None:
-            self.block.forward_residual(self.x, self.norm, out=self.out, workspace=self.ws,
-                                        keep_routing=keep_routing)
+            block.forward_residual(self.x, self.norm, out=self.out, workspace=self.ws,
+                                   keep_routing=keep_routing)
         else:
-            self.block(self.x, out=self.out, workspace=self.ws, keep_routing=keep_routing)
+            block(self.x, out=self.out, workspace=self.ws, keep_routing=keep_routing)
 
     def eager(self):
-        self.run(keep_routing=False)
+        # one forward per bank (the graph holds them all)
+        for b in self.blocks:
+            self.run(keep_routing=False, block=b)
 
     def step(self):
         if self.graph is not None:
@@ -135,6 +148,7 @@ class Runner:
             self.eager()
 
     def timed(self, steps, warmup):
+        """Mean seconds per forward over `steps` steps."""
         torch = self.torch
         for _ in range(warmup):
             self.step()
@@ -143,7 +157,20 @@ class Runner:
         for _ in range(steps):
             self.step()
         torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / steps
+        return (time.perf_counter() - t0) / steps / len(self.blocks)
+
+    def median(self, steps):
+        """Median seconds per forward, each step bracketed by events on the
+        stream the forwards run on."""
+        torch = self.torch
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record()
+        for i in range(steps):
+            self.step()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        d = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        return d[steps // 2] / 1e3 / len(self.blocks)
 
     def kernel_time(self, pkg, kernel, steps):
         """Average duration (s) of `kernel` over `steps` eager forwards, from
@@ -193,6 +220,26 @@ def measured_traffic(workload: str, kernel: str):
     return data.get("kernels", {}).get(kernel, {}).get("traffic_bytes")
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cold_banks(W, bw, T, U):
+    """Copies of bw so that a bank is reused only after more than twice the
+    256 MB of MI355X's last-level (Infinity) cache has streamed through:
+    every forward then reads its experts from HBM."""
+    per_step = W.algorithmic_bytes(bw.cfg, T, U)
+    n = max(4, min(48, -(-2 * 256 * 2 ** 20 // max(per_step, 1)) + 1))
+    return [W.clone_weights(bw) for _ in range(n - 1)]
+
+
 def cpu_baseline(pkg, orc, bw, T, seconds, threads):
     """The oracle (plain C, OpenMP) on this host: whole block forwards of the
     same c-config at T tokens until `seconds` have passed (at least one)."""
@@ -210,7 +257,8 @@ def cpu_baseline(pkg, orc, bw, T, seconds, threads):
             break
     return dict(value=round(n * T / el, 2), unit="tokens/s", cores=threads, kind="port",
                 sample=f"{n} block forwards of {bw.cfg.name} at T={T} "
-                       f"({el:.1f} s, oracle/moe_oracle.c, {threads} OpenMP threads)")
+                       f"({el:.1f} s, oracle/moe_oracle.c -O3 -march=native, "
+                       f"{threads} OpenMP threads)")
 
 
 def main():
@@ -239,7 +287,19 @@ def main():
     sec = r.timed(args.steps, args.warmup)
     tok_s = T / sec
     block_bytes = W.algorithmic_bytes(cfg, T, U)
-    print(f"bench: {sec * 1e6:.1f} us/step, {tok_s:.0f} tokens/s", file=sys.stderr, flush=True)
+    med = r.median(args.steps)
+    print(f"bench: {sec * 1e6:.1f} us/step (median {med * 1e6:.1f}), {tok_s:.0f} tokens/s",
+          file=sys.stderr, flush=True)
+    # the same forward with the weights rotated over banks in their own
+    # memory: no step finds its experts in the caches
+    rc = Runner(pkg, bw, T, dev, args.launch, banks=cold_banks(W, bw, T, U))
+    sec_c = rc.timed(max(args.steps // len(rc.blocks), 10), 2)
+    cold = dict(tokens_per_s=round(T / sec_c, 1), us_per_step=round(sec_c * 1e6, 2),
+                us_per_step_median=round(rc.median(max(args.steps // len(rc.blocks), 10)) * 1e6, 2),
+                banks=len(rc.blocks), bank_bytes=W.bank_bytes(bw),
+                block_hbm_gbs=round(block_bytes / sec_c / 1e9, 1))
+    del rc
+    print(f"bench: cold {cold}", file=sys.stderr, flush=True)
 
     # dominant kernel: the fused gate/up gather_qmm
     kt, kn, kmin, kmax = r.kernel_time(pkg, "qgemm_gated", args.steps)
@@ -266,33 +326,50 @@ def main():
         parts = item.split(":")
         cname, tt = parts[0], int(parts[1])
         res = len(parts) > 2 and parts[2] == "res"
+        cold_pt = len(parts) > 2 and parts[2] == "cold"
         c2 = W.CONFIGS[cname]
         if c2.name not in banks:
             banks[c2.name] = W.make_weights(c2, dev)
         r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch, residual=res)
-        s2 = r2.timed(args.sweep_steps, 5)
         U2 = W.distinct(r2.idx)
+        if cold_pt:
+            r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch,
+                        banks=cold_banks(W, banks[c2.name], tt, U2))
+        steps2 = max(args.sweep_steps // len(r2.blocks), 10)
+        s2 = r2.timed(steps2, 2)
+        m2 = r2.median(steps2)
         # both rates for every point: the decode sizes and the small prefills
         # (c3 T=512, c4 T=2048, c5 T=512: arithmetic intensity below the
         # ridge) are HBM-bound, the large prefills MFMA-bound
-        ent = dict(config=c2.name + (" layer tail" if res else ""), T=tt,
-                   tokens_per_s=round(tt / s2, 1),
-                   us_per_step=round(s2 * 1e6, 2), distinct_experts=U2,
+        ent = dict(config=c2.name + (" layer tail" if res else "") + (" cold" if cold_pt else ""),
+                   T=tt, tokens_per_s=round(tt / s2, 1),
+                   us_per_step=round(s2 * 1e6, 2), us_per_step_median=round(m2 * 1e6, 2),
+                   distinct_experts=U2,
                    block_hbm_gbs=round(W.algorithmic_bytes(c2, tt, U2) / s2 / 1e9, 1),
-                   block_tflops=round(W.algorithmic_flops(c2, tt) / s2 / 1e12, 2))
+                   block_tflops=round(W.algorithmic_flops(c2, tt) / s2 / 1e12, 2),
+                   rows_per_expert=W.rows_per_expert(r2.idx, c2.E))
+        if cold_pt:
+            ent["banks"] = len(r2.blocks)
         sweep.append(ent)
         print(f"bench: sweep {ent}", file=sys.stderr, flush=True)
         del r2
 
     cpu = None
     if args.cpu_seconds > 0:
+        import tempfile
         orc = entry.load_oracle()
+        # the restatement compiled for this host's CPU, in a scratch dir
+        tmp = tempfile.mkdtemp(prefix="mlxr_oracle_")
+        orc.use_library(orc.build_native(tmp))
         threads = args.cpu_threads or host_cores()
         cpu = cpu_baseline(pkg, orc, bw, T, args.cpu_seconds, threads)
         # and on one core (a single-threaded run of the same restatement)
         one = cpu_baseline(pkg, orc, bw, T, args.cpu_seconds / 2, 1)
         cpu["value_1core"] = one["value"]
         cpu["sample_1core"] = one["sample"]
+        cpu["host"] = dict(cpu_model=cpu_model(), nproc=os.cpu_count(),
+                           affinity=len(os.sched_getaffinity(0)),
+                           omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
         print(f"bench: cpu baseline {cpu}", file=sys.stderr, flush=True)
 
     line = {
@@ -303,6 +380,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(sec * 1e3, 5),
+        "ms_per_step_median": round(med * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -312,7 +390,9 @@ def main():
                    "K": cfg.K, "f": cfg.f, "bits": cfg.bits, "group_size": cfg.group_size,
                    "distinct_experts": U, "launch": args.launch,
                    "block_algorithmic_bytes": block_bytes,
-                   "block_hbm_gbs": round(block_bytes / sec / 1e9, 1)},
+                   "block_hbm_gbs": round(block_bytes / sec / 1e9, 1),
+                   "rows_per_expert": W.rows_per_expert(r.idx, cfg.E)},
+        "cold": cold,
         "roofline": roof,
         "cpu_baseline": cpu,
         "sweep": sweep,

@@ -173,6 +173,62 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
     return BlockWeights(cfg, gate_w, gate_b, mlp, shared, sgw)
 
 
+def clone_weights(bw: BlockWeights) -> BlockWeights:
+    """The same weights in new device memory: another layer's bank for a
+    cold-cache measurement (every step reads weights no earlier step of
+    the cycle left in the caches)."""
+    def lin(x):
+        if x is None:
+            return None
+        if isinstance(x, torch.Tensor):
+            return x.clone()
+        if isinstance(x, nn.QuantizedLinear):
+            return nn.QuantizedLinear(x.weight[0].clone(), x.scales[0].clone(),
+                                      x.biases[0].clone(), x.group_size, x.bits)
+        if isinstance(x, nn.QuantizedSwitchLinear):
+            return nn.QuantizedSwitchLinear(x.weight.clone(), x.scales.clone(), x.biases.clone(),
+                                            x.group_size, x.bits)
+        if isinstance(x, nn.Linear):
+            return nn.Linear(x.weight[0].clone())
+        if isinstance(x, nn.SwitchLinear):
+            return nn.SwitchLinear(x.weight.clone())
+        raise TypeError(type(x))
+
+    m = bw.switch_mlp
+    if isinstance(m, nn.PackedSwitchFfn):
+        mlp = nn.PackedSwitchFfn(lin(m.gate_up_proj), lin(m.down_proj), m.activation)
+    else:
+        mlp = nn.SplitSwitchFfn(lin(m.gate_proj), lin(m.up_proj), lin(m.down_proj))
+    se = bw.shared_expert
+    shared = None if se is None else nn.SwigluMlp(lin(se.gate_proj), lin(se.up_proj),
+                                                 lin(se.down_proj))
+    gemma = None if bw.gemma is None else tuple(t.clone() for t in bw.gemma)
+    return BlockWeights(bw.cfg, lin(bw.gate_w), lin(bw.gate_b), mlp, shared,
+                        lin(bw.shared_gate_w), gemma)
+
+
+def bank_bytes(bw: BlockWeights) -> int:
+    """Device bytes of one bank's expert weights (what a layer holds)."""
+    m = bw.switch_mlp
+    lins = ([m.gate_up_proj, m.down_proj] if isinstance(m, nn.PackedSwitchFfn)
+            else [m.gate_proj, m.up_proj, m.down_proj])
+    tot = 0
+    for x in lins:
+        for t in (x.weight, getattr(x, "scales", None), getattr(x, "biases", None)):
+            if t is not None:
+                tot += t.numel() * t.element_size()
+    return tot
+
+
+def rows_per_expert(indices: torch.Tensor, E: int) -> dict:
+    """The realised load: rows each expert received (max, min over all E,
+    mean over the active ones, active count)."""
+    c = torch.bincount(indices.reshape(-1).long(), minlength=E).cpu()
+    act = c[c > 0]
+    return dict(max=int(c.max()), min=int(c.min()), active=int(act.numel()),
+                mean_active=round(float(act.float().mean()), 2) if act.numel() else 0.0)
+
+
 def algorithmic_bytes(cfg: MoEConfig, T: int, distinct_experts: int) -> int:
     """HBM bytes one block forward must move at decode: the packed weights,
     scales and biases of the distinct selected experts (3 projections), the
@@ -212,4 +268,5 @@ def expert_bytes_per_row(cfg: MoEConfig, K_dim: int) -> float:
 
 
 __all__ = ["MoEConfig", "CONFIGS", "make_x", "make_weights", "BlockWeights", "zipf_bias",
+           "clone_weights", "bank_bytes", "rows_per_expert",
            "algorithmic_bytes", "weight_bytes_per_element", "algorithmic_flops", "distinct", "math", "ops"]

@@ -23,7 +23,22 @@ def build() -> Path:
     return LIB
 
 
+def build_native(out_dir) -> Path:
+    """A copy of the oracle compiled for this host's CPU (-march=native) in
+    out_dir: the CPU baseline times it where it runs."""
+    out = Path(out_dir) / "liboracle_native.so"
+    subprocess.run(["make", "-s", "-C", str(HERE), f"NATIVE_OUT={out}", "native"], check=True)
+    return out
+
+
 _lib = None
+
+
+def use_library(path) -> None:
+    """Route every later oracle call through the library at `path` (built
+    from the same source, e.g. by build_native)."""
+    global _lib
+    _lib = ctypes.CDLL(str(path))
 
 
 def lib():
@@ -387,7 +402,7 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False), residual=None):
     return out, idx, w
 
 
-__all__ = ["build", "lib", "f32_to_bf16", "bf16_to_f32", "quantize", "dequantize",
+__all__ = ["build", "build_native", "use_library", "lib", "f32_to_bf16", "bf16_to_f32", "quantize", "dequantize",
            "router_logits", "router_topk", "router_logits_q", "router_topk_bf16", "dispatch",
            "gather_qmm", "gather_mm", "swiglu", "combine", "combine_bf16", "geglu", "rms_norm", "gemma_router",
            "packed_switch_glu",
