@@ -72,6 +72,12 @@ constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
 constexpr int64_t kStreamSlots = MLXR_STREAM_SLOTS;
 
 
+// quantisation groups of the input dim per wave and pass in the split-K
+// kernel (its waves split the input dim; more groups per wave, fewer waves)
+#ifndef MLXR_SPLITK_GROUPS
+#define MLXR_SPLITK_GROUPS 4
+#endif
+
 // Reorder 8 consecutive bf16 x values to the code order that unpack4 emits:
 // element j of the fragment holds x[perm(j)], perm = 0,4,1,5,2,6,3,7.
 __device__ __forceinline__ u32x4_t perm4(u32x4_t v) {
@@ -232,7 +238,10 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
   const int ai = item / tiles_n, tile = item - ai * tiles_n;
   const int n_act = *a.num_work;
   const int32_t* rec = a.work + (int64_t)kWorkInts * ai;
+  // the whole 48-byte record at once: header and the flat rows
   const int4 wk = *reinterpret_cast<const int4*>(rec);
+  const int4 fr0 = *reinterpret_cast<const int4*>(rec + 4);
+  const int4 fr1 = *reinterpret_cast<const int4*>(rec + 8);
   if (ai >= n_act) return;
   const int e = wk.x, row0 = wk.y, rows = wk.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -252,7 +261,10 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
     int64_t xrow = 0;
     if (tv) {
       const int slot = row0 + tok;
-      const int flat = rec[4 + tok];
+      // this lane's flat row from the record (tok < kWorkRows = 8)
+      const int f4 = (tok & 3) == 0 ? fr0.x : (tok & 3) == 1 ? fr0.y : (tok & 3) == 2 ? fr0.z : fr0.w;
+      const int f8 = (tok & 3) == 0 ? fr1.x : (tok & 3) == 1 ? fr1.y : (tok & 3) == 2 ? fr1.z : fr1.w;
+      const int flat = tok < 4 ? f4 : f8;
       xrow = a.x_by_slot ? slot : (a.row_map ? a.row_map[flat] : flat / a.row_div);
     }
     f32x4_t acc[CB][NM];
@@ -840,7 +852,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   }
   // waves along the input dim: two groups each per pass (one step at 4-bit,
   // two at 8-bit), up to 16 waves; more groups take several passes
-  constexpr int kGroupsPerWave = 2;
+  constexpr int kGroupsPerWave = MLXR_SPLITK_GROUPS;
   const int kw = std::min(16, (groups + kGroupsPerWave - 1) / kGroupsPerWave);
   // channel blocks per workgroup: as many as keep >= ~1024 workgroups, with
   // the partial sums of the blocks within 64 KB of LDS

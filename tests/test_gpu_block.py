@@ -267,6 +267,10 @@ def test_block_residual_parity(pkg, orc, dev, cfg, T):
     rms = np.sqrt(np.mean(mref.astype(np.float64) ** 2))
     a = np.abs(ref)
     step = 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - (7 if c.router_bits else 23))
+    if c.router_bits:
+        # the bf16 chain rounds twice: the block's output (where the two
+        # f32 sums can round to neighbouring bf16 values), then h + it
+        step = step + _step(mref)
     diff = np.abs(got - ref)
     print(f"  max|err| {diff.max():.3e}  block rms {rms:.3e}", flush=True)
     assert np.all(diff <= 2e-2 * rms + step)
