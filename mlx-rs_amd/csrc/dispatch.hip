@@ -14,6 +14,8 @@
 //         item records and M-tile list for the GEMMs, and the scatter into
 //         sorted/inv (and the flat rows of the work records).
 // Ids outside [0, E) are left out of every expert and flagged in *status.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "route.hpp"
@@ -213,6 +215,36 @@ __global__ __launch_bounds__(kDispatchBlock) void route_small_kernel(
                  tile_rows, b, &ls);
 }
 
+// Decode routing for at most 64 ids (T * K <= 64): one wave per token for
+// the top-K (blockDim = 64 * min(T, 16)), then wave 0 sorts the ids
+// (wave_dispatch: no LDS table, no scans).
+template <int SLOTS, bool BF16>
+__global__ __launch_bounds__(kDispatchBlock) void route_wave_kernel(
+    const float* __restrict__ logits, int64_t ld, int T, int E, int K,
+    int32_t* __restrict__ idx, float* __restrict__ wts, int tile_rows,
+    DispatchBuffers b) {
+  __shared__ TopkScratch sc[kDispatchBlock / 64];
+  __shared__ int ids[64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  if (threadIdx.x == 0) *b.status = 0;
+  for (int t = wave; t < T; t += waves) {
+    int id;
+    float wt;
+    wave_topk<SLOTS, BF16>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
+    if (lane < K) {
+      idx[(int64_t)t * K + lane] = id;
+      wts[(int64_t)t * K + lane] = wt;
+      ids[t * K + lane] = id;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int n = T * K;
+    wave_dispatch(lane < n ? ids[lane] : -1, n, E, tile_rows, b);
+  }
+}
+
 __global__ __launch_bounds__(256) void dispatch_identity_kernel(
     int n, int tile_rows, DispatchBuffers b) {
   const int tid = threadIdx.x;
@@ -306,9 +338,18 @@ void route_small_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
                         int64_t K, int32_t* idx, float* wts, int tile_rows,
                         const DispatchBuffers& b, hipStream_t s) {
   const int slots = (int)((E + 63) / 64);
+  // at most 64 ids: a wave per token and the one-wave sort
+  const bool one_wave = T * K <= 64;
+  const unsigned threads = one_wave ? 64u * (unsigned)std::min<int64_t>(T, 16) : kDispatchBlock;
 #define MLXR_RS(S)                                                         \
-  route_small_kernel<S, BF16><<<1, kDispatchBlock, 0, s>>>(                \
-      logits, ld, (int)T, (int)E, (int)K, idx, wts, tile_rows, b)
+  do {                                                                     \
+    if (one_wave)                                                          \
+      route_wave_kernel<S, BF16><<<1, threads, 0, s>>>(                    \
+          logits, ld, (int)T, (int)E, (int)K, idx, wts, tile_rows, b);     \
+    else                                                                   \
+      route_small_kernel<S, BF16><<<1, kDispatchBlock, 0, s>>>(            \
+          logits, ld, (int)T, (int)E, (int)K, idx, wts, tile_rows, b);     \
+  } while (0)
   if (slots <= 1)
     MLXR_RS(1);
   else if (slots <= 2)

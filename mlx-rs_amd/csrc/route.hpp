@@ -338,4 +338,96 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
   }
 }
 
+// The same sort for at most 64 ids, one per lane of one wave (lane i < n:
+// id_in), with no LDS and no barrier: an id's sorted position is the number
+// of ids below it plus the equal ids on lower lanes, and each expert's
+// first work item the items of the experts listed before it (long form
+// first), both summed over the distinct experts (one lane each) by a
+// uniform loop.  Writes every output block_dispatch writes.
+__device__ void wave_dispatch(int id_in, int n, int E, int tile_rows,
+                              const DispatchBuffers& b) {
+  const int lane = threadIdx.x & 63;
+  const bool valid = lane < n;
+  const int id = valid ? id_in : -1;
+  const bool ok = valid && id >= 0 && id < E;
+  if (valid && !ok && id != -1) *b.status = 1;
+  uint64_t match = __ballot(ok);
+  const int id_bits = E > 1 ? 32 - __clz(E - 1) : 0;
+  for (int bit = 0; bit < id_bits; ++bit) {
+    const bool on = ok && ((id >> bit) & 1);
+    const uint64_t bal = __ballot(on);
+    match &= on ? bal : ~bal;
+  }
+  const int r = __popcll(match & ((1ull << lane) - 1ull));  // rank among equals
+  const int c = ok ? __popcll(match) : 0;                   // the expert's rows
+  const bool lng = c > kStreamTT4Rows;
+  // over the distinct experts j (their first lanes): ids below this one,
+  // items listed before this expert's, experts and tiles below it, totals
+  int below = 0, item_base = 0, act = 0, tl = 0;
+  int tot_items = 0, tot_active = 0, tot_tiles = 0;
+  uint64_t leaders = __ballot(ok && r == 0);
+  while (leaders) {
+    const int j = (int)__builtin_ctzll(leaders);
+    leaders &= leaders - 1;
+    const int idj = __builtin_amdgcn_readlane(id, j);
+    const int cj = __builtin_amdgcn_readlane(c, j);
+    const int nwj = (cj + kWorkRows - 1) / kWorkRows;
+    const int ntj = (cj + tile_rows - 1) / tile_rows;
+    const bool lj = cj > kStreamTT4Rows;
+    const bool lower = idj < id;
+    below += lower ? cj : 0;
+    item_base += ((lj && !lng) || (lj == lng && lower)) ? nwj : 0;
+    act += lower ? 1 : 0;
+    tl += lower ? ntj : 0;
+    tot_items += nwj;
+    tot_active += 1;
+    tot_tiles += ntj;
+  }
+  if (ok) {
+    const int pos = below + r;
+    b.sorted[pos] = lane;
+    b.inv[lane] = pos;
+    b.work[kWorkInts * (item_base + r / kWorkRows) + 4 + r % kWorkRows] = lane;
+    if (r == 0) {
+      b.active[act] = id;
+      for (int j = 0; j * kWorkRows < c; ++j) {
+        int32_t* w = b.work + kWorkInts * (item_base + j);
+        w[0] = id;
+        w[1] = below + j * kWorkRows;
+        w[2] = min(kWorkRows, c - j * kWorkRows);
+        w[3] = c;
+      }
+      for (int j = 0; j * tile_rows < c; ++j) {
+        b.tiles[2 * (tl + j)] = id;
+        b.tiles[2 * (tl + j) + 1] = below + j * tile_rows;
+      }
+    }
+  }
+  // counts and offsets of every expert: lane l holds experts l + 64 s
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    int cnt = 0, off = 0;
+    uint64_t ls = __ballot(ok && r == 0);
+    while (ls) {
+      const int j = (int)__builtin_ctzll(ls);
+      ls &= ls - 1;
+      const int idj = __builtin_amdgcn_readlane(id, j);
+      const int cj = __builtin_amdgcn_readlane(c, j);
+      cnt += idj == e ? cj : 0;
+      off += idj < e ? cj : 0;
+    }
+    if (e < E) {
+      b.counts[e] = cnt;
+      b.offsets[e] = off;
+    }
+  }
+  const int tot_rows = __popcll(__ballot(ok));
+  if (lane == 0) {
+    b.offsets[E] = tot_rows;
+    *b.num_active = tot_active;
+    *b.num_work = tot_items;
+    *b.num_tiles = tot_tiles;
+  }
+}
+
 }  // namespace mlxr_moe
