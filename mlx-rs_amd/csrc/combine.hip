@@ -32,31 +32,51 @@ __global__ __launch_bounds__(256) void combine_kernel(
     int d, const uint16_t* __restrict__ shared_y,
     const float* __restrict__ shared_logit, int64_t shared_ld,
     const uint16_t* __restrict__ residual, void* __restrict__ out) {
+  constexpr int kBatch = 8;
   const int t = blockIdx.y;
   const int n0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (t >= T || n0 >= d) return;
+  // the shared row, its gate logit and the residual row are issued first
+  const u32x4_t zq = {0u, 0u, 0u, 0u};
+  const u32x4_t sv = shared_y ? *reinterpret_cast<const u32x4_t*>(
+                                    shared_y + (int64_t)t * d + n0)
+                              : zq;
+  const float slog = shared_y ? shared_logit[t * shared_ld] : 0.0f;
+  const u32x4_t rv = residual ? *reinterpret_cast<const u32x4_t*>(
+                                    residual + (int64_t)t * d + n0)
+                              : zq;
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    float wk;
-    if constexpr (sizeof(WT) == 2)
-      wk = bf16_to_f32(w[(int64_t)t * K + k]);
-    else
-      wk = w[(int64_t)t * K + k];
-    const u32x4_t v =
-        *reinterpret_cast<const u32x4_t*>(y + ((int64_t)t * K + k) * d + n0);
-    const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
+  // eight rows' loads in flight at once (indices clamped, so every load is
+  // in bounds and none sits under a branch), then the k-ordered sum
+  for (int k0 = 0; k0 < K; k0 += kBatch) {
+    u32x4_t v[kBatch];
+    float wk[kBatch];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float lo = __fmul_rn(wk, __uint_as_float(pk[j] << 16));
-      float hi = __fmul_rn(wk, __uint_as_float(pk[j] & 0xffff0000u));
-      if (BF16) {
-        lo = bf16_round(lo);
-        hi = bf16_round(hi);
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t r = (int64_t)t * K + min(k0 + i, K - 1);
+      v[i] = *reinterpret_cast<const u32x4_t*>(y + r * d + n0);
+      if constexpr (sizeof(WT) == 2)
+        wk[i] = bf16_to_f32(w[r]);
+      else
+        wk[i] = w[r];
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (k0 + i >= K) break;
+      const uint32_t pk[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float lo = __fmul_rn(wk[i], __uint_as_float(pk[j] << 16));
+        float hi = __fmul_rn(wk[i], __uint_as_float(pk[j] & 0xffff0000u));
+        if (BF16) {
+          lo = bf16_round(lo);
+          hi = bf16_round(hi);
+        }
+        acc[2 * j] = __fadd_rn(acc[2 * j], lo);
+        acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], hi);
       }
-      acc[2 * j] = __fadd_rn(acc[2 * j], lo);
-      acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], hi);
     }
   }
   if (BF16) {
@@ -64,11 +84,9 @@ __global__ __launch_bounds__(256) void combine_kernel(
     for (int j = 0; j < 8; ++j) acc[j] = bf16_round(acc[j]);
   }
   if (shared_y) {
-    float gate = 1.0f / (1.0f + expf(-shared_logit[t * shared_ld]));
+    float gate = 1.0f / (1.0f + expf(-slog));
     if (BF16) gate = bf16_round(gate);
-    const u32x4_t v =
-        *reinterpret_cast<const u32x4_t*>(shared_y + (int64_t)t * d + n0);
-    const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t pk[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float lo = __fmul_rn(__uint_as_float(pk[j] << 16), gate);
@@ -82,9 +100,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
     }
   }
   if (residual) {
-    const u32x4_t v =
-        *reinterpret_cast<const u32x4_t*>(residual + (int64_t)t * d + n0);
-    const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t pk[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // h + mlp_out, with mlp_out in its own dtype first

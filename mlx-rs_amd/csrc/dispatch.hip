@@ -217,13 +217,13 @@ __global__ __launch_bounds__(kDispatchBlock) void route_small_kernel(
 
 // Decode routing for at most 64 ids (T * K <= 64): one wave per token for
 // the top-K (blockDim = 64 * min(T, 16)), then wave 0 sorts the ids
-// (wave_dispatch: no LDS table, no scans).
+// (wave_dispatch: ballots and one scan of the expert table, no barrier).
 template <int SLOTS, bool BF16>
 __global__ __launch_bounds__(kDispatchBlock) void route_wave_kernel(
     const float* __restrict__ logits, int64_t ld, int T, int E, int K,
     int32_t* __restrict__ idx, float* __restrict__ wts, int tile_rows,
     DispatchBuffers b) {
-  __shared__ TopkScratch sc[kDispatchBlock / 64];
+  __shared__ WaveDispatchScratch ls;
   __shared__ int ids[64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
@@ -231,7 +231,7 @@ __global__ __launch_bounds__(kDispatchBlock) void route_wave_kernel(
   for (int t = wave; t < T; t += waves) {
     int id;
     float wt;
-    wave_topk<SLOTS, BF16>(logits + (int64_t)t * ld, E, K, &sc[wave], &id, &wt);
+    wave_topk<SLOTS, BF16>(logits + (int64_t)t * ld, E, K, nullptr, &id, &wt);
     if (lane < K) {
       idx[(int64_t)t * K + lane] = id;
       wts[(int64_t)t * K + lane] = wt;
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(kDispatchBlock) void route_wave_kernel(
   __syncthreads();
   if (wave == 0) {
     const int n = T * K;
-    wave_dispatch(lane < n ? ids[lane] : -1, n, E, tile_rows, b);
+    wave_dispatch(lane < n ? ids[lane] : -1, n, E, tile_rows, b, &ls);
   }
 }
 

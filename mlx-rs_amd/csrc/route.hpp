@@ -59,6 +59,10 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
@@ -338,14 +342,25 @@ __device__ void block_dispatch(int id_in, int n, int E, int tile_rows,
   }
 }
 
+// LDS of wave_dispatch: per expert its row count, first sorted slot and
+// first work item.
+struct WaveDispatchScratch {
+  int cnt[kMaxExperts];
+  int pos[kMaxExperts];
+  int item[kMaxExperts];
+};
+
 // The same sort for at most 64 ids, one per lane of one wave (lane i < n:
-// id_in), with no LDS and no barrier: an id's sorted position is the number
-// of ids below it plus the equal ids on lower lanes, and each expert's
-// first work item the items of the experts listed before it (long form
-// first), both summed over the distinct experts (one lane each) by a
-// uniform loop.  Writes every output block_dispatch writes.
+// id_in), with no barrier.  Equal ids meet by ballots over the id bits (an
+// id's rank among equals, the expert's row count); the expert table is
+// then scanned 64 experts per pass (DPP prefix sums of packed per-expert
+// fields: rows, active, M-tiles, long-form items; and short-form items),
+// which gives every expert's first sorted slot and first work item (the
+// long-form items first, in expert order, then the short).  Writes every
+// output block_dispatch writes.
 __device__ void wave_dispatch(int id_in, int n, int E, int tile_rows,
-                              const DispatchBuffers& b) {
+                              const DispatchBuffers& b,
+                              WaveDispatchScratch* ls) {
   const int lane = threadIdx.x & 63;
   const bool valid = lane < n;
   const int id = valid ? id_in : -1;
@@ -360,73 +375,64 @@ __device__ void wave_dispatch(int id_in, int n, int E, int tile_rows,
   }
   const int r = __popcll(match & ((1ull << lane) - 1ull));  // rank among equals
   const int c = ok ? __popcll(match) : 0;                   // the expert's rows
-  const bool lng = c > kStreamTT4Rows;
-  // over the distinct experts j (their first lanes): ids below this one,
-  // items listed before this expert's, experts and tiles below it, totals
-  int below = 0, item_base = 0, act = 0, tl = 0;
-  int tot_items = 0, tot_active = 0, tot_tiles = 0;
-  uint64_t leaders = __ballot(ok && r == 0);
-  while (leaders) {
-    const int j = (int)__builtin_ctzll(leaders);
-    leaders &= leaders - 1;
-    const int idj = __builtin_amdgcn_readlane(id, j);
-    const int cj = __builtin_amdgcn_readlane(c, j);
-    const int nwj = (cj + kWorkRows - 1) / kWorkRows;
-    const int ntj = (cj + tile_rows - 1) / tile_rows;
-    const bool lj = cj > kStreamTT4Rows;
-    const bool lower = idj < id;
-    below += lower ? cj : 0;
-    item_base += ((lj && !lng) || (lj == lng && lower)) ? nwj : 0;
-    act += lower ? 1 : 0;
-    tl += lower ? ntj : 0;
-    tot_items += nwj;
-    tot_active += 1;
-    tot_tiles += ntj;
-  }
-  if (ok) {
-    const int pos = below + r;
-    b.sorted[pos] = lane;
-    b.inv[lane] = pos;
-    b.work[kWorkInts * (item_base + r / kWorkRows) + 4 + r % kWorkRows] = lane;
-    if (r == 0) {
-      b.active[act] = id;
-      for (int j = 0; j * kWorkRows < c; ++j) {
-        int32_t* w = b.work + kWorkInts * (item_base + j);
-        w[0] = id;
-        w[1] = below + j * kWorkRows;
-        w[2] = min(kWorkRows, c - j * kWorkRows);
-        w[3] = c;
-      }
-      for (int j = 0; j * tile_rows < c; ++j) {
-        b.tiles[2 * (tl + j)] = id;
-        b.tiles[2 * (tl + j) + 1] = below + j * tile_rows;
-      }
-    }
-  }
-  // counts and offsets of every expert: lane l holds experts l + 64 s
+  const bool leader = ok && r == 0;
+  // long-form items over all experts: the short-form items start after them
+  const uint32_t wl_own =
+      leader && c > kStreamTT4Rows ? (uint32_t)((c + kWorkRows - 1) / kWorkRows) : 0u;
+  const int tot_long = (int)readlane_u32(wave_incl_scan(wl_own), 63);
+  for (int e = lane; e < E; e += 64) ls->cnt[e] = 0;
+  if (leader) ls->cnt[id] = c;
+  // packed exclusive prefixes: rows | active << 8 | tiles << 16 |
+  // long items << 24 (each total <= 64), and short items
+  uint32_t carry_a = 0u, carry_b = 0u;
   for (int e0 = 0; e0 < E; e0 += 64) {
     const int e = e0 + lane;
-    int cnt = 0, off = 0;
-    uint64_t ls = __ballot(ok && r == 0);
-    while (ls) {
-      const int j = (int)__builtin_ctzll(ls);
-      ls &= ls - 1;
-      const int idj = __builtin_amdgcn_readlane(id, j);
-      const int cj = __builtin_amdgcn_readlane(c, j);
-      cnt += idj == e ? cj : 0;
-      off += idj < e ? cj : 0;
-    }
+    const int ce = e < E ? ls->cnt[e] : 0;
+    const int nw = (ce + kWorkRows - 1) / kWorkRows;
+    const int nt = (ce + tile_rows - 1) / tile_rows;
+    const bool lng = ce > kStreamTT4Rows;
+    const uint32_t pa = (uint32_t)ce | (ce > 0 ? 1u << 8 : 0u) |
+                        ((uint32_t)nt << 16) | (lng ? (uint32_t)nw << 24 : 0u);
+    const uint32_t pb = lng ? 0u : (uint32_t)nw;
+    const uint32_t ia = wave_incl_scan(pa), ib = wave_incl_scan(pb);
+    const uint32_t xa = ia - pa + carry_a, xb = ib - pb + carry_b;
+    carry_a += readlane_u32(ia, 63);
+    carry_b += readlane_u32(ib, 63);
+    const int off = (int)(xa & 0xffu);
     if (e < E) {
-      b.counts[e] = cnt;
+      b.counts[e] = ce;
       b.offsets[e] = off;
     }
+    if (ce > 0) {
+      const int first = lng ? (int)(xa >> 24) : tot_long + (int)xb;
+      ls->pos[e] = off;
+      ls->item[e] = first;
+      b.active[(xa >> 8) & 0xffu] = e;
+      for (int j = 0; j < nw; ++j) {
+        int32_t* w = b.work + kWorkInts * (first + j);
+        w[0] = e;
+        w[1] = off + j * kWorkRows;
+        w[2] = min(kWorkRows, ce - j * kWorkRows);
+        w[3] = ce;
+      }
+      const int tb = (int)((xa >> 16) & 0xffu);
+      for (int j = 0; j < nt; ++j) {
+        b.tiles[2 * (tb + j)] = e;
+        b.tiles[2 * (tb + j) + 1] = off + j * tile_rows;
+      }
+    }
   }
-  const int tot_rows = __popcll(__ballot(ok));
+  if (ok) {
+    const int pos = ls->pos[id] + r;
+    b.sorted[pos] = lane;
+    b.inv[lane] = pos;
+    b.work[kWorkInts * (ls->item[id] + r / kWorkRows) + 4 + r % kWorkRows] = lane;
+  }
   if (lane == 0) {
-    b.offsets[E] = tot_rows;
-    *b.num_active = tot_active;
-    *b.num_work = tot_items;
-    *b.num_tiles = tot_tiles;
+    b.offsets[E] = (int)(carry_a & 0xffu);
+    *b.num_active = (int)((carry_a >> 8) & 0xffu);
+    *b.num_work = tot_long + (int)carry_b;
+    *b.num_tiles = (int)((carry_a >> 16) & 0xffu);
   }
 }
 
