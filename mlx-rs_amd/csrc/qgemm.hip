@@ -39,8 +39,12 @@ namespace {
 // Launch shape of the streaming kernel: (experts x 16-channel blocks) from
 // which it runs, waves per workgroup, super-steps of loads in flight at 4-
 // and 8-bit.
+// (measured at T = 1..4: the streaming kernel's time is nearly flat in the
+// blocks there, ~11.8 us for c2/c4 gate/up, while the split-K kernel's
+// grows with the bytes: 10.1 us at 8 experts x 512 channels (288 blocks),
+// 13.7 at 10 x 512 (352) and 8 x 768 (432))
 #ifndef MLXR_STREAM_MIN_BLOCKS
-#define MLXR_STREAM_MIN_BLOCKS 2048
+#define MLXR_STREAM_MIN_BLOCKS 320
 #endif
 #ifndef MLXR_STREAM_WAVES
 #define MLXR_STREAM_WAVES 4
