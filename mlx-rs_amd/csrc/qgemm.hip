@@ -72,6 +72,10 @@ constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
 #ifndef MLXR_STREAM_SLOTS
 #define MLXR_STREAM_SLOTS 512
 #endif
+// largest grid that K-slices may make (one workgroup per slot)
+#ifndef MLXR_STREAM_KS_GRID
+#define MLXR_STREAM_KS_GRID 512
+#endif
 // workgroups resident at once (2 per CU on 256 CUs)
 constexpr int64_t kStreamSlots = MLXR_STREAM_SLOTS;
 
@@ -439,7 +443,7 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
 // lane loads 16*GG codes of its group (16 B per load).  Lanes that feed
 // zeros read a zero block in LDS.  The GG partial sums of a token meet by
 // cross-lane adds at the end.
-template <int BITS, bool GATED, int TT, int D, int NB>
+template <int BITS, bool GATED, int TT, int D, int NB, int KS>
 __device__ __forceinline__ void stream_body(const QGemmArgs& a,
                                             const int32_t* rec, int4 wk,
                                             int4 fr0, int4 fr1, int tile,
@@ -454,16 +458,21 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   constexpr int NL = CPL * BITS / 128;  // 16-byte loads per lane
   constexpr int NMF = CPL / 8;          // MFMAs per super-step
   constexpr int WPG = 2 * BITS;         // packed words per row and group
-  const int waves = blockDim.x >> 6;
+  // KS waves share each set of blocks, one K-slice each (KS > 1 for small
+  // grids: more, shorter waves); their sums meet in LDS at the end
+  const int waves = (blockDim.x >> 6) / KS;  // channel waves
   // items of experts with at most 4 rows run with TT = 4, the others with
   // TT = 8 >= kWorkRows: an item is always one pass
   const int e = wk.x, row0 = wk.y, nt = min(wk.z, TT);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave_id = threadIdx.x >> 6;
+  const int wave = wave_id / KS, kq = wave_id % KS;  // channel wave, K-slice
   const int n = lane & 15, q = lane >> 4;
   const int gq = q / LPG, sq = q % LPG;  // this lane's group, its part
   const int K = a.K, groups = K >> 6;
   const int ssteps = groups / GG;  // the host runs this kernel when GG | groups
-  const int total = nb * ssteps;   // super-steps of this wave, all blocks
+  const int ssk = ssteps / KS;     // ... and KS | ssteps: steps per slice
+  const int s0 = kq * ssk;         // this wave's first step of each block
+  const int total = nb * ssk;      // super-steps of this wave, all blocks
   // LDS: x [TT][K + 8] bf16 (rows padded 16 B), 16 B zero block,
   // X [groups][TT] f32, then per wave its scales and biases
   const int xs = K + 8;
@@ -495,7 +504,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   }
   const int64_t blk_rows = (int64_t)16 * groups;  // row stride of a block
   auto load = [&](Ring& r, int gs) {
-    const int bi = gs / ssteps, ss = gs - bi * ssteps;
+    const int bi = gs / ssk, ss = s0 + gs - bi * ssk;
     const int64_t go = bi * blk_rows + ss * GG;  // group offset
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
@@ -569,7 +578,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   // lines for 128 useful bytes.
   const int sbn = nb * 16 * groups;  // bf16 per array
   const int sbv = sbn >> 3;          // 16-byte vectors per array
-  uint16_t* sbl = reinterpret_cast<uint16_t*>(sb_base) + (size_t)wave * NA * sbn;
+  uint16_t* sbl = reinterpret_cast<uint16_t*>(sb_base) + (size_t)wave_id * NA * sbn;
   const uint16_t* sbsrc[NA];
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
@@ -642,7 +651,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
       load(ring[(j + D) % R], min(gs + D, total - 1));
       const Ring& cur = ring[j];
       const bool live = gs < total;
-      const int bi = gs / ssteps, ss = gs - bi * ssteps;
+      const int bi = gs / ssk, ls = gs - bi * ssk, ss = s0 + ls;
       const int g = ss * GG + gq;
       const bool on = diag && live;
       const char* xp = on ? xsrc + (size_t)(64 * g) * 2 : zero_blk;
@@ -683,7 +692,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
           acc[m][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(cb, X[r], acc[m][r]));
       }
       if constexpr (NB > 1) {
-        const bool last = live && ss == ssteps - 1 && bi < NB - 1;
+        const bool last = live && ls == ssk - 1 && bi < NB - 1;
 #pragma unroll
         for (int b = 0; b < NB - 1; ++b) {
           const bool fin = last && bi == b;
@@ -701,7 +710,24 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   }
   // Each token's GG group partials sit on lanes 16*(TT/4) apart: a
   // butterfly over those lanes sums them, and lanes q < TT/4 write tokens
-  // 4q..4q+3 of channel n.
+  // 4q..4q+3 of channel n.  With K-slices the KS waves' sums of a block
+  // meet in LDS (after the x region is no longer read) and the slice-0
+  // wave adds them in slice order.
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(
+      sb_base + (((size_t)(blockDim.x >> 6) * NA * nb * 16 * groups * 2 + 15) & ~size_t(15)));
+  if constexpr (KS > 1) {
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        f32x4_t t = acc[m];
+#pragma unroll
+        for (int b = 0; b < NB - 1; ++b) t = bi == b ? done[b][m] : t;
+        red[((wave_id * NB + bi) * NM + m) * 64 + lane] = t;
+      }
+    __syncthreads();
+    if (kq != 0) return;
+  }
 #pragma unroll
   for (int bi = 0; bi < NB; ++bi) {
     f32x4_t tot[NM];
@@ -710,6 +736,11 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
       tot[m] = acc[m];
 #pragma unroll
       for (int b = 0; b < NB - 1; ++b) tot[m] = bi == b ? done[b][m] : tot[m];
+      if constexpr (KS > 1) {
+#pragma unroll
+        for (int k = 1; k < KS; ++k)
+          tot[m] += red[(((wave_id + k) * NB + bi) * NM + m) * 64 + lane];
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if constexpr (TT == 4) tot[m][r] += __shfl_xor(tot[m][r], 16, 64);
@@ -749,7 +780,7 @@ constexpr int kTT8Depth = 2 * D;
 // Tokens per pass follow the expert's row count: 4 (GG = 4) for experts
 // with at most kStreamTT4Rows rows, else 8 (GG = 2).  LDS is sized
 // for 8.
-template <int BITS, bool GATED, int D, int NB>
+template <int BITS, bool GATED, int D, int NB, int KS>
 __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
     QGemmArgs a, int tiles_n) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -767,9 +798,9 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
   // boundaries fall.  The 8-token form moves half the bytes per super-step:
   // twice the depth.
   if (wk.w <= kStreamTT4Rows)
-    stream_body<BITS, GATED, 4, D, NB>(a, rec, wk, fr0, fr1, tile, smem);
+    stream_body<BITS, GATED, 4, D, NB, KS>(a, rec, wk, fr0, fr1, tile, smem);
   else
-    stream_body<BITS, GATED, 8, kTT8Depth<D>, NB>(a, rec, wk, fr0, fr1, tile, smem);
+    stream_body<BITS, GATED, 8, kTT8Depth<D>, NB, KS>(a, rec, wk, fr0, fr1, tile, smem);
 }
 
 }  // namespace
@@ -809,15 +840,38 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
         nb = c;
         break;
       }
-    const int tiles_n = (int)(per_tile / nb);
+    // K-slices: a small grid (few items, one block per wave) splits each
+    // block's input dim over ks waves of a workgroup, so more and shorter
+    // waves run at once (the super-steps of either MFMA form divide
+    // evenly), as long as the grid stays within one workgroup per slot
+    // (two per CU, or one where the LDS allows only one)
     const size_t sb_lds = (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
-    const dim3 grid((unsigned)(max_items * tiles_n));
-    const size_t lds =
+    const size_t base_lds =
         (((size_t)kMaxTT * (a.K + 8) * 2 + 16 + (size_t)groups * kMaxTT * 4 + 15) &
-         ~size_t(15)) + sb_lds;
+         ~size_t(15)) + ((sb_lds + 15) & ~size_t(15));
+    const size_t red_lds = (size_t)kWaves * (a.gated ? 2 : 1) * 64 * 16;
+    const int64_t slots = (kStreamSlots / 2) * (base_lds + red_lds <= 80 * 1024 ? 2 : 1);
+    int ks = 1;
+    if (nb == 1)
+      for (int c = std::min(4, kWaves); c > 1; c >>= 1)
+        if ((groups / 4) % c == 0 &&
+            max_items * (a.N / (16 * (kWaves / c))) <= std::min<int64_t>(slots, MLXR_STREAM_KS_GRID)) {
+          ks = c;
+          break;
+        }
+    const int tiles_n = (int)(a.N / (16 * (kWaves / ks)) / nb);
+    const dim3 grid((unsigned)(max_items * tiles_n));
+    const size_t lds = base_lds + (ks > 1 ? red_lds : 0);
     ProfileScope prof(profile, s);
-#define MLXR_QS(B, G, D, NB) \
-  qgemm_stream_kernel<B, G, D, NB><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n)
+#define MLXR_QS(B, G, D, NB)                                                  \
+  do {                                                                        \
+    if (ks == 4)                                                              \
+      qgemm_stream_kernel<B, G, D, 1, 4><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n); \
+    else if (ks == 2)                                                         \
+      qgemm_stream_kernel<B, G, D, 1, 2><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n); \
+    else                                                                      \
+      qgemm_stream_kernel<B, G, D, NB, 1><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n); \
+  } while (0)
     if (a.bits == 4) {
 #if MLXR_STREAM_GATED_NB > 1
       if (a.gated && nb == 2)
