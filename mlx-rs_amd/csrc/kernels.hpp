@@ -223,10 +223,15 @@ int prefill_tile_rows(int64_t rows, int64_t experts);
 // weights (bits 16) take the split-K decode kernel or the M-tiled one.
 // `profile` names the launch for ProfileScope (default "qgemm_gated" or
 // "qgemm_down"; the shared expert's GEMMs are "shared_gated" /
-// "shared_down").
+// "shared_down").  `shared` folds a second problem into the same decode
+// launch: the block's shared expert, whose shared_rows rows are the tokens
+// in order (its work items are made in the kernel, no dispatch); it must
+// have a's N, K, bits and mode, and prefill must be false.
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s,
-                        const char* profile = nullptr);
+                        const char* profile = nullptr,
+                        const QGemmArgs* shared = nullptr,
+                        int64_t shared_rows = 0);
 
 // ---------------------------------------------------------------- prefill.hip
 // x_rows bounds the rows of x the GEMM reads; tile_rows is the M-tile height

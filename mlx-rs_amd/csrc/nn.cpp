@@ -173,6 +173,17 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
                   "shared_expert down");
 }
 
+SharedFold SwigluMlp::fold(Carve ws, int64_t T, uint16_t* y) const {
+  (void)carve_dispatch(ws, T, 1, nullptr);  // (unused when folded)
+  SharedFold f{};
+  f.gate = qw(gate_);
+  f.up = qw(up_);
+  f.down = qw(down_);
+  f.act = ws.take<uint16_t>(T * gate_.output_dims);
+  f.y = y;
+  return f;
+}
+
 // ----------------------------------------------------------- switch FFNs
 SplitSwitchFfn::SplitSwitchFfn(const mlxr_moe_switch_glu& w) : w_(w) {
   sw_.gate = qw(w.gate_proj);
@@ -271,9 +282,15 @@ Status SwitchFfn::forward(const uint16_t* x, int64_t T, const int32_t* indices,
 // switch.rs:305-307, is the H-row offset of the up half), down gather_qmm
 // whose rows land at their flat (t, k) position (scatter_unsort,
 // switch.rs:437-439).
+bool SwitchFfn::can_fold(const SwigluMlp& m, int64_t T, int64_t K) const {
+  return m.bits() == sw_.bits && m.hidden() == sw_.f && sw_.bits != 16 &&
+         !use_prefill_path(T * K, sw_.E, sw_.bits) &&
+         !use_prefill_path(T, 1, m.bits());
+}
+
 Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
                           const DispatchBuffers& db, uint16_t* y, Carve& ws,
-                          hipStream_t s) const {
+                          hipStream_t s, const SharedFold* fold) const {
   const int64_t d = sw_.d, f = sw_.f, E = sw_.E;
   const int64_t n = T * K;
   uint16_t* act = ws.take<uint16_t>(n * f);
@@ -306,7 +323,20 @@ Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   g.out = act;
   g.out_ld = f;
   g.gated = true;
-  Status st = from_hip(launch_qgemm(g, n, max_items, prefill, s),
+  // the folded shared expert: every token once, x rows by slot, SwiGLU
+  QGemmArgs g2 = g;
+  if (fold) {
+    g2.row_div = 1;
+    g2.x_by_slot = true;
+    g2.w0 = fold->gate;
+    g2.w1 = fold->up;
+    g2.E = 1;
+    g2.e_rows = (int32_t)f;
+    g2.act = kActSwiglu;
+    g2.out = fold->act;
+  }
+  Status st = from_hip(launch_qgemm(g, n, max_items, prefill, s, nullptr,
+                                    fold ? &g2 : nullptr, fold ? T : 0),
                        "switch_mlp gate/up");
   if (!st.ok) return st;
   QGemmArgs h = g;
@@ -323,7 +353,17 @@ Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
   h.out_ld = d;
   h.out_by_flat = true;
   h.gated = false;
-  return from_hip(launch_qgemm(h, n, max_items, prefill, s),
+  QGemmArgs h2 = h;
+  if (fold) {
+    h2.x = fold->act;
+    h2.x_rows = T;
+    h2.w0 = fold->down;
+    h2.E = 1;
+    h2.out = fold->y;
+    h2.out_by_flat = false;
+  }
+  return from_hip(launch_qgemm(h, n, max_items, prefill, s, nullptr,
+                               fold ? &h2 : nullptr, fold ? T : 0),
                   "switch_mlp down");
 }
 
@@ -453,14 +493,18 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
                              prefill_tile_rows(T * K, E), db, s),
                 "router top-k / dispatch");
   if (!st.ok) return st;
-  if (shared) {
-    st = SwigluMlp(b_.shared_gate_proj, b_.shared_up_proj,
-                   b_.shared_down_proj)
-             .forward(x, T, sy, shared_ws, status, s);
+  const SplitSwitchFfn mlp(b_.switch_mlp);
+  const SwigluMlp smlp(b_.shared_gate_proj, b_.shared_up_proj,
+                       b_.shared_down_proj);
+  // on the decode kernels the shared expert rides in the routed launches
+  const bool fold = shared && mlp.can_fold(smlp, T, K);
+  if (shared && !fold) {
+    st = smlp.forward(x, T, sy, shared_ws, status, s);
     if (!st.ok) return st;
   }
-  const SplitSwitchFfn mlp(b_.switch_mlp);
-  st = mlp.experts(x, T, K, db, y, ws, s);
+  SharedFold sf{};
+  if (fold) sf = smlp.fold(shared_ws, T, sy);
+  st = mlp.experts(x, T, K, db, y, ws, s, fold ? &sf : nullptr);
   if (!st.ok) return st;
   return from_hip(launch_combine(y, wts, false, T, K, d, sy,
                                  shared ? logits + E : nullptr, ld, residual,

@@ -68,6 +68,14 @@ namespace nn {
 #endif
 bool use_prefill_path(int64_t rows, int64_t experts, int bits = 4);
 
+// A shared expert folded into the routed decode GEMM launches (its gate/up
+// and down run as the second problem of the same launches).
+struct SharedFold {
+  QWeights gate, up, down;
+  uint16_t* act;  // [T, f] its activations
+  uint16_t* y;    // [T, d] its output
+};
+
 class SwigluMlp {
  public:
   SwigluMlp(const mlxr_moe_qlinear& gate, const mlxr_moe_qlinear& up,
@@ -78,6 +86,11 @@ class SwigluMlp {
   Status forward(const uint16_t* x, int64_t T, uint16_t* y, Carve& ws,
                  int32_t* status, hipStream_t s) const;
   static void plan(Carve& ws, int64_t T, int64_t d, int64_t f);
+  // The fold of this MLP into the routed launches, with its activations in
+  // its own workspace region (plan order) and output y.
+  SharedFold fold(Carve ws, int64_t T, uint16_t* y) const;
+  int bits() const { return gate_.bits; }
+  int64_t hidden() const { return gate_.output_dims; }
 
  private:
   mlxr_moe_qlinear gate_, up_, down_;
@@ -101,10 +114,14 @@ class SwitchFfn {
   Status forward(const uint16_t* x, int64_t T, const int32_t* indices,
                  int64_t K, uint16_t* y, Carve& ws, int32_t* status,
                  hipStream_t s) const;
-  // The expert products given a dispatch of the T*K flat ids.
+  // The expert products given a dispatch of the T*K flat ids; with `fold`,
+  // the shared expert's products in the same launches.
   Status experts(const uint16_t* x, int64_t T, int64_t K,
                  const DispatchBuffers& db, uint16_t* y, Carve& ws,
-                 hipStream_t s) const;
+                 hipStream_t s, const SharedFold* fold = nullptr) const;
+  // Whether a SwiGLU shared expert can fold into this FFN's launches at T
+  // tokens: both on the decode kernels, same bits and hidden size.
+  bool can_fold(const SwigluMlp& m, int64_t T, int64_t K) const;
   // forward_with_combine: out [T, d] = sum_k w * y (+ shared branch); f32
   // weights give an f32 out, bf16 weights (w_bf16) a bf16 out.
   Status forward_with_combine(const uint16_t* x, int64_t T,

@@ -234,23 +234,15 @@ __device__ __forceinline__ void group_terms(uint32_t s16, uint32_t b16,
 // i+1 are in flight.  The kw partial sums of each block meet in LDS and one
 // wave writes the block.  Lane l: token / channel l%16, quarter l/16.
 template <int BITS, bool GATED, int SPW, int CB>
-__global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
-                                                            int tiles_n) {
+__device__ __forceinline__ void decode_body(const QGemmArgs& a, int tile,
+                                            const int32_t* rec, int4 wk,
+                                            int4 fr0, int4 fr1) {
   extern __shared__ f32x4_t red[];  // [kw][CB][NM][64]
   constexpr int NM = GATED ? 2 : 1;
   constexpr int GPS = BITS == 4 ? 2 : 1;
   constexpr int GW = SPW * GPS;          // groups per wave per pass
   constexpr int NX = BITS == 4 ? 4 : 2;  // x fragments per step
   const int kw = blockDim.x >> 6;
-  const int item = blockIdx.x;
-  const int ai = item / tiles_n, tile = item - ai * tiles_n;
-  const int n_act = *a.num_work;
-  const int32_t* rec = a.work + (int64_t)kWorkInts * ai;
-  // the whole 48-byte record at once: header and the flat rows
-  const int4 wk = *reinterpret_cast<const int4*>(rec);
-  const int4 fr0 = *reinterpret_cast<const int4*>(rec + 4);
-  const int4 fr1 = *reinterpret_cast<const int4*>(rec + 8);
-  if (ai >= n_act) return;
   const int e = wk.x, row0 = wk.y, rows = wk.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
@@ -417,6 +409,49 @@ __global__ __launch_bounds__(1024) void qgemm_decode_kernel(QGemmArgs a,
     }
     __syncthreads();
   }
+}
+
+// The unit of workgroup blockIdx.x: a work item of the routed problem `a`
+// (its record, fetched whole: header and flat rows), or, from units1 on,
+// an item of a folded second problem -- the block's shared expert, every
+// token's row once: item i is rows 8i..8i+7 of `rows2` in token order, its
+// record made here (expert 0, the rows' own slots, no dispatch).  Returns
+// false for an idle workgroup (past the routed problem's items).
+struct Unit {
+  const int32_t* rec;
+  int4 wk, fr0, fr1;
+  int tile;
+  bool shared;
+};
+__device__ __forceinline__ bool decode_unit(const QGemmArgs& a, int tiles_n,
+                                            int units1, int rows2, Unit& u) {
+  u.shared = (int)blockIdx.x >= units1;
+  const int v = u.shared ? (int)blockIdx.x - units1 : (int)blockIdx.x;
+  const int ai = v / tiles_n;
+  u.tile = v - ai * tiles_n;
+  // (the routed record is read unconditionally, item 0's for a shared unit)
+  u.rec = a.work + (int64_t)kWorkInts * (u.shared ? 0 : ai);
+  u.wk = *reinterpret_cast<const int4*>(u.rec);
+  u.fr0 = *reinterpret_cast<const int4*>(u.rec + 4);
+  u.fr1 = *reinterpret_cast<const int4*>(u.rec + 8);
+  const int n_act = *a.num_work;
+  if (u.shared) {
+    const int r0 = kWorkRows * ai;
+    u.wk = make_int4(0, r0, min(kWorkRows, rows2 - r0), rows2);
+    u.fr0 = make_int4(r0, r0 + 1, r0 + 2, r0 + 3);
+    u.fr1 = make_int4(r0 + 4, r0 + 5, r0 + 6, r0 + 7);
+    return true;
+  }
+  return ai < n_act;
+}
+
+template <int BITS, bool GATED, int SPW, int CB>
+__global__ __launch_bounds__(1024) void qgemm_decode_kernel(
+    QGemmArgs a, int tiles_n, QGemmArgs a2, int units1, int rows2) {
+  Unit u;
+  if (!decode_unit(a, tiles_n, units1, rows2, u)) return;
+  decode_body<BITS, GATED, SPW, CB>(u.shared ? a2 : a, u.tile, u.rec, u.wk,
+                                    u.fr0, u.fr1);
 }
 
 // Streaming decode GEMM for many (work item, channel tile) units.  One
@@ -782,34 +817,37 @@ constexpr int kTT8Depth = 2 * D;
 // for 8.
 template <int BITS, bool GATED, int D, int NB, int KS>
 __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
-    QGemmArgs a, int tiles_n) {
+    QGemmArgs a, int tiles_n, QGemmArgs a2, int units1, int rows2) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int ai = blockIdx.x / tiles_n, tile = blockIdx.x - ai * tiles_n;
-  const int n_act = *a.num_work;
-  const int32_t* rec = a.work + (int64_t)kWorkInts * ai;
-  // the whole 48-byte record at once: header and the 8 flat rows (records
-  // are 16-byte aligned)
-  const int4 wk = *reinterpret_cast<const int4*>(rec);
-  const int4 fr0 = *reinterpret_cast<const int4*>(rec + 4);
-  const int4 fr1 = *reinterpret_cast<const int4*>(rec + 8);
-  if (ai >= n_act) return;
+  Unit u;
+  if (!decode_unit(a, tiles_n, units1, rows2, u)) return;
+  const QGemmArgs& A = u.shared ? a2 : a;
   // The MFMA form follows the expert's row count (not the item's), so every
   // token of an expert is summed in the same order, wherever its item
   // boundaries fall.  The 8-token form moves half the bytes per super-step:
   // twice the depth.
-  if (wk.w <= kStreamTT4Rows)
-    stream_body<BITS, GATED, 4, D, NB, KS>(a, rec, wk, fr0, fr1, tile, smem);
+  if (u.wk.w <= kStreamTT4Rows)
+    stream_body<BITS, GATED, 4, D, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1, u.tile, smem);
   else
-    stream_body<BITS, GATED, 8, kTT8Depth<D>, NB, KS>(a, rec, wk, fr0, fr1, tile, smem);
+    stream_body<BITS, GATED, 8, kTT8Depth<D>, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1,
+                                                      u.tile, smem);
 }
 
 }  // namespace
 
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s,
-                        const char* profile) {
-  if (max_items <= 0) return hipSuccess;
+                        const char* profile, const QGemmArgs* shared,
+                        int64_t shared_rows) {
   if (!profile) profile = a.gated ? "qgemm_gated" : "qgemm_down";
+  // a folded second problem (decode only): the same projection shape and
+  // format, its items after the routed ones in the same grid
+  const int64_t items2 = shared ? (shared_rows + kWorkRows - 1) / kWorkRows : 0;
+  if (shared && (prefill || shared->N != a.N || shared->K != a.K ||
+                 shared->bits != a.bits || shared->gated != a.gated))
+    return hipErrorInvalidValue;
+  if (max_items + items2 <= 0) return hipSuccess;
+  const QGemmArgs& b = shared ? *shared : a;
   // the M-tiled kernel reads x through a buffer of x's own rows (gathered
   // rows may lie anywhere in it: gather_mm / gather_qmm with lhs indices)
   const int64_t x_rows = a.x_rows > 0 ? a.x_rows : total_rows;
@@ -826,9 +864,12 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
   };
   const bool sb16 = a16(a.w0.scales) && a16(a.w0.biases) &&
-                    (!a.gated || (a16(a.w1.scales) && a16(a.w1.biases)));
+                    (!a.gated || (a16(a.w1.scales) && a16(a.w1.biases))) &&
+                    a16(b.w0.scales) && a16(b.w0.biases) &&
+                    (!b.gated || (a16(b.w1.scales) && a16(b.w1.biases)));
+  const int64_t all_items = max_items + items2;
   // (dense bf16 weights, bits 16, take the split-K kernel below)
-  if (a.bits != 16 && max_items * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0 &&
+  if (a.bits != 16 && all_items * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0 &&
       groups % 4 == 0 && sb16) {
     constexpr int kWaves = MLXR_STREAM_WAVES, kMaxTT = 8;
     // blocks per wave: about one workgroup per slot (two per CU), so x is
@@ -836,7 +877,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     const int64_t per_tile = a.N / (16 * kWaves);
     int nb = 1;
     for (int c = a.gated ? MLXR_STREAM_GATED_NB : MLXR_STREAM_MAX_NB; c > 1; c >>= 1)
-      if (per_tile % c == 0 && max_items * (per_tile / c) >= kStreamSlots) {
+      if (per_tile % c == 0 && all_items * (per_tile / c) >= kStreamSlots) {
         nb = c;
         break;
       }
@@ -855,22 +896,27 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     if (nb == 1)
       for (int c = std::min(4, kWaves); c > 1; c >>= 1)
         if ((groups / 4) % c == 0 &&
-            max_items * (a.N / (16 * (kWaves / c))) <= std::min<int64_t>(slots, MLXR_STREAM_KS_GRID)) {
+            all_items * (a.N / (16 * (kWaves / c))) <= std::min<int64_t>(slots, MLXR_STREAM_KS_GRID)) {
           ks = c;
           break;
         }
     const int tiles_n = (int)(a.N / (16 * (kWaves / ks)) / nb);
-    const dim3 grid((unsigned)(max_items * tiles_n));
+    const int units1 = (int)(max_items * tiles_n);
+    const dim3 grid((unsigned)(all_items * tiles_n));
     const size_t lds = base_lds + (ks > 1 ? red_lds : 0);
+    const int rows2 = (int)shared_rows;
     ProfileScope prof(profile, s);
-#define MLXR_QS(B, G, D, NB)                                                  \
-  do {                                                                        \
-    if (ks == 4)                                                              \
-      qgemm_stream_kernel<B, G, D, 1, 4><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n); \
-    else if (ks == 2)                                                         \
-      qgemm_stream_kernel<B, G, D, 1, 2><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n); \
-    else                                                                      \
-      qgemm_stream_kernel<B, G, D, NB, 1><<<grid, 64 * kWaves, lds, s>>>(a, tiles_n); \
+#define MLXR_QS(B, G, D, NB)                                              \
+  do {                                                                    \
+    if (ks == 4)                                                          \
+      qgemm_stream_kernel<B, G, D, 1, 4>                                  \
+          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, rows2);  \
+    else if (ks == 2)                                                     \
+      qgemm_stream_kernel<B, G, D, 1, 2>                                  \
+          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, rows2);  \
+    else                                                                  \
+      qgemm_stream_kernel<B, G, D, NB, 1>                                 \
+          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, rows2);  \
   } while (0)
     if (a.bits == 4) {
 #if MLXR_STREAM_GATED_NB > 1
@@ -920,41 +966,43 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   // (the gated kernel keeps one block: two would spill under the 128-VGPR
   // budget of 16-wave workgroups)
   for (int c = 4; c > 1 && !a.gated; c >>= 1)
-    if (nblk % c == 0 && max_items * (nblk / c) >= 1024 &&
+    if (nblk % c == 0 && all_items * (nblk / c) >= 1024 &&
         kw * c * nm <= 64) {
       cb = c;
       break;
     }
   const int tiles_n = nblk / cb;
   const size_t lds = (size_t)kw * cb * nm * 64 * sizeof(f32x4_t);
-  const dim3 grid((unsigned)(max_items * tiles_n));
+  const int units1 = (int)(max_items * tiles_n);
+  const int rows2 = (int)shared_rows;
+  const dim3 grid((unsigned)(all_items * tiles_n));
   const dim3 block((unsigned)(64 * kw));
   ProfileScope prof(profile, s);
 #define MLXR_QG(B, G, SPW)                                                  \
   do {                                                                      \
     if (cb == 4)                                                            \
       qgemm_decode_kernel<B, G, SPW, 4>                                     \
-          <<<grid, block, lds, s>>>(a, tiles_n);                            \
+          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);                            \
     else if (cb == 2)                                                       \
       qgemm_decode_kernel<B, G, SPW, 2>                                     \
-          <<<grid, block, lds, s>>>(a, tiles_n);                            \
+          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);                            \
     else                                                                    \
       qgemm_decode_kernel<B, G, SPW, 1>                                     \
-          <<<grid, block, lds, s>>>(a, tiles_n);                            \
+          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);                            \
   } while (0)
   if (a.bits == 16) {
     if (a.gated)
-      qgemm_decode_kernel<16, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n);
+      qgemm_decode_kernel<16, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);
     else
       MLXR_QG(16, false, 2);
   } else if (a.bits == 4) {
     if (a.gated)
-      qgemm_decode_kernel<4, true, 1, 1><<<grid, block, lds, s>>>(a, tiles_n);
+      qgemm_decode_kernel<4, true, 1, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);
     else
       MLXR_QG(4, false, 1);
   } else {
     if (a.gated)
-      qgemm_decode_kernel<8, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n);
+      qgemm_decode_kernel<8, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);
     else
       MLXR_QG(8, false, 2);
   }

@@ -520,7 +520,9 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
   // slower (c7's router: T = 1 2 us faster).  Above MLXR_RL_NORM_MAX_T
   // tokens the norm is its own pass.
   if (norm && T > MLXR_RL_NORM_MAX_T) {
-    launch_rms_norm(x, T, d, norm->w, norm->eps, norm->out, s);
+    // (a failed launch stays the runtime's last error, which the caller
+    // returns after the logits launch)
+    (void)launch_rms_norm(x, T, d, norm->w, norm->eps, norm->out, s);
     x = norm->out;
     norm = nullptr;
   }
