@@ -6,11 +6,13 @@ fallback behind these functions.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32, c_int64,
                     c_size_t, c_void_p)
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libmlxr_moe.so"
+# MLXR_MOE_LIB: another build of the same sources (e.g. a host-sanitizer copy)
+LIB_PATH = Path(os.environ.get("MLXR_MOE_LIB", Path(__file__).resolve().parent / "libmlxr_moe.so"))
 
 FLOAT32 = 0
 BFLOAT16 = 1

@@ -7,6 +7,7 @@ import this module.  bf16 arrays are numpy uint16 bit patterns.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_uint16, c_uint32, c_void_p
 from pathlib import Path
@@ -14,7 +15,8 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "liboracle.so"
+# MLXR_ORACLE_LIB: another build of the same source (the sanitizer copy)
+LIB = Path(os.environ.get("MLXR_ORACLE_LIB", HERE / "liboracle.so"))
 F32, BF16 = 0, 1
 
 
