@@ -424,13 +424,15 @@ struct Unit {
   bool shared;
 };
 __device__ __forceinline__ bool decode_unit(const QGemmArgs& a, int tiles_n,
-                                            int units1, int rows2, Unit& u) {
+                                            int units1, int items1, int rows2,
+                                            Unit& u) {
   u.shared = (int)blockIdx.x >= units1;
   const int v = u.shared ? (int)blockIdx.x - units1 : (int)blockIdx.x;
   const int ai = v / tiles_n;
   u.tile = v - ai * tiles_n;
-  // (the routed record is read unconditionally, item 0's for a shared unit)
-  u.rec = a.work + (int64_t)kWorkInts * (u.shared ? 0 : ai);
+  // (the routed record is read unconditionally, item 0's for a shared
+  // unit)
+  u.rec = a.work + (int64_t)kWorkInts * (u.shared ? 0 : min(ai, items1 - 1));
   u.wk = *reinterpret_cast<const int4*>(u.rec);
   u.fr0 = *reinterpret_cast<const int4*>(u.rec + 4);
   u.fr1 = *reinterpret_cast<const int4*>(u.rec + 8);
@@ -447,9 +449,9 @@ __device__ __forceinline__ bool decode_unit(const QGemmArgs& a, int tiles_n,
 
 template <int BITS, bool GATED, int SPW, int CB>
 __global__ __launch_bounds__(1024) void qgemm_decode_kernel(
-    QGemmArgs a, int tiles_n, QGemmArgs a2, int units1, int rows2) {
+    QGemmArgs a, int tiles_n, QGemmArgs a2, int units1, int items1, int rows2) {
   Unit u;
-  if (!decode_unit(a, tiles_n, units1, rows2, u)) return;
+  if (!decode_unit(a, tiles_n, units1, items1, rows2, u)) return;
   decode_body<BITS, GATED, SPW, CB>(u.shared ? a2 : a, u.tile, u.rec, u.wk,
                                     u.fr0, u.fr1);
 }
@@ -578,10 +580,15 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   // thread k8 holds elements 8*k8..8*k8+7 of every token; the token sums X
   // of each 64-wide group come from the 8 threads sharing it
   const int per_row = K >> 3;
+  // (only the item's nt rows are read: the padding rows of the MFMA form
+  // stage zeros.  The branch is uniform, and these are the first loads of
+  // the workgroup, so every later wait counts only loads issued after them)
   auto load_x = [&](int k8, u32x4_t (&v)[TT]) {
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
-      v[t] = *reinterpret_cast<const u32x4_t*>(a.x + xr[t] * a.x_ld + 8 * k8);
+    for (int t = 0; t < TT; ++t) {
+      v[t] = zq;
+      if (t < nt) v[t] = *reinterpret_cast<const u32x4_t*>(a.x + xr[t] * a.x_ld + 8 * k8);
+    }
   };
   auto stage_x = [&](int k8, const u32x4_t (&v)[TT]) {
 #pragma unroll
@@ -817,10 +824,10 @@ constexpr int kTT8Depth = 2 * D;
 // for 8.
 template <int BITS, bool GATED, int D, int NB, int KS>
 __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
-    QGemmArgs a, int tiles_n, QGemmArgs a2, int units1, int rows2) {
+    QGemmArgs a, int tiles_n, QGemmArgs a2, int units1, int items1, int rows2) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   Unit u;
-  if (!decode_unit(a, tiles_n, units1, rows2, u)) return;
+  if (!decode_unit(a, tiles_n, units1, items1, rows2, u)) return;
   const QGemmArgs& A = u.shared ? a2 : a;
   // The MFMA form follows the expert's row count (not the item's), so every
   // token of an expert is summed in the same order, wherever its item
@@ -901,8 +908,9 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
           break;
         }
     const int tiles_n = (int)(a.N / (16 * (kWaves / ks)) / nb);
+    const int items1 = (int)max_items;
     const int units1 = (int)(max_items * tiles_n);
-    const dim3 grid((unsigned)(all_items * tiles_n));
+    const dim3 grid((unsigned)(units1 + items2 * tiles_n));
     const size_t lds = base_lds + (ks > 1 ? red_lds : 0);
     const int rows2 = (int)shared_rows;
     ProfileScope prof(profile, s);
@@ -910,13 +918,13 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   do {                                                                    \
     if (ks == 4)                                                          \
       qgemm_stream_kernel<B, G, D, 1, 4>                                  \
-          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, rows2);  \
+          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, items1, rows2);  \
     else if (ks == 2)                                                     \
       qgemm_stream_kernel<B, G, D, 1, 2>                                  \
-          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, rows2);  \
+          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, items1, rows2);  \
     else                                                                  \
       qgemm_stream_kernel<B, G, D, NB, 1>                                 \
-          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, rows2);  \
+          <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, items1, rows2);  \
   } while (0)
     if (a.bits == 4) {
 #if MLXR_STREAM_GATED_NB > 1
@@ -973,36 +981,37 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     }
   const int tiles_n = nblk / cb;
   const size_t lds = (size_t)kw * cb * nm * 64 * sizeof(f32x4_t);
+  const int items1 = (int)max_items;
   const int units1 = (int)(max_items * tiles_n);
   const int rows2 = (int)shared_rows;
-  const dim3 grid((unsigned)(all_items * tiles_n));
+  const dim3 grid((unsigned)(units1 + items2 * tiles_n));
   const dim3 block((unsigned)(64 * kw));
   ProfileScope prof(profile, s);
 #define MLXR_QG(B, G, SPW)                                                  \
   do {                                                                      \
     if (cb == 4)                                                            \
       qgemm_decode_kernel<B, G, SPW, 4>                                     \
-          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);                            \
+          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, items1, rows2);                            \
     else if (cb == 2)                                                       \
       qgemm_decode_kernel<B, G, SPW, 2>                                     \
-          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);                            \
+          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, items1, rows2);                            \
     else                                                                    \
       qgemm_decode_kernel<B, G, SPW, 1>                                     \
-          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);                            \
+          <<<grid, block, lds, s>>>(a, tiles_n, b, units1, items1, rows2);                            \
   } while (0)
   if (a.bits == 16) {
     if (a.gated)
-      qgemm_decode_kernel<16, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);
+      qgemm_decode_kernel<16, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, items1, rows2);
     else
       MLXR_QG(16, false, 2);
   } else if (a.bits == 4) {
     if (a.gated)
-      qgemm_decode_kernel<4, true, 1, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);
+      qgemm_decode_kernel<4, true, 1, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, items1, rows2);
     else
       MLXR_QG(4, false, 1);
   } else {
     if (a.gated)
-      qgemm_decode_kernel<8, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, rows2);
+      qgemm_decode_kernel<8, true, 2, 1><<<grid, block, lds, s>>>(a, tiles_n, b, units1, items1, rows2);
     else
       MLXR_QG(8, false, 2);
   }
