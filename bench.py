@@ -191,13 +191,18 @@ class Runner:
         return tot.value / n.value / 1e3, n.value, mn.value / 1e3, mx.value / 1e3
 
 
-def gated_bytes(cfg, T, U):
+def gated_bytes(cfg, T, U, shared_folded=False):
     """Algorithmic HBM bytes of one gate/up launch: the packed words plus
     bf16 scales and biases (or the dense bf16 weights) of the U distinct
     selected experts' gate and up rows (2*f*d weights each), x read once
-    (T*d bf16) and the activations written (T*K*f bf16)."""
+    (T*d bf16) and the activations written (T*K*f bf16); with the shared
+    expert folded into the launch (decode, same bits and hidden size) also
+    its gate and up rows (2*fs*d) and its activations (T*fs bf16)."""
     per_w = 2.0 if cfg.bits == 16 else cfg.bits / 8 + 4 / cfg.group_size
-    return int(U * 2 * cfg.f * cfg.d * per_w + T * cfg.d * 2 + T * cfg.K * cfg.f * 2)
+    b = U * 2 * cfg.f * cfg.d * per_w + T * cfg.d * 2 + T * cfg.K * cfg.f * 2
+    if shared_folded and cfg.fs:
+        b += 2 * cfg.fs * cfg.d * per_w + T * cfg.fs * 2
+    return int(b)
 
 
 def gated_flops(cfg, T):
@@ -305,7 +310,10 @@ def main():
     kt, kn, kmin, kmax = r.kernel_time(pkg, "qgemm_gated", args.steps)
     decode = T * cfg.K < 2048
     if decode:
-        traffic_alg = gated_bytes(cfg, T, U)
+        # (the block folds its shared expert into the decode launches when
+        # it has the experts' bits and hidden size)
+        folded = bool(cfg.fs) and cfg.fs == cfg.f and cfg.bits != 16
+        traffic_alg = gated_bytes(cfg, T, U, folded)
         achieved = traffic_alg / kt / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(achieved / HBM_PEAK_GBS, 4),

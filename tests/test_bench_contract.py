@@ -44,3 +44,16 @@ def test_algorithmic_bytes(pkg):
     assert W.algorithmic_bytes(c8, T, U8) == int(want8)
     assert W.weight_bytes_per_element(c8) == 2.0
     assert W.weight_bytes_per_element(c2) == pytest.approx(0.5625)
+
+
+def test_gated_bytes_with_folded_shared_expert(pkg):
+    """The gate/up launch's bytes: the routed experts' gate and up rows, x in,
+    activations out; the folded shared expert adds its own rows and
+    activations (c6: E=256, f = fs = 512, 4-bit)."""
+    import bench
+    c6 = pkg.workloads.CONFIGS["c6"]
+    T, U = 64, 219
+    per_w = 0.5 + 4 / 64
+    base = U * 2 * c6.f * c6.d * per_w + T * c6.d * 2 + T * c6.K * c6.f * 2
+    assert bench.gated_bytes(c6, T, U) == int(base)
+    assert bench.gated_bytes(c6, T, U, True) == int(base + 2 * c6.fs * c6.d * per_w + T * c6.fs * 2)
