@@ -138,7 +138,7 @@ int run_gather(const char* op, const void* x, int64_t x_batch, int64_t M,
                                    N, ids, xrow, ob, status, s),
                 (o + " prep").c_str());
   if (st.ok)
-    st = from_hip(launch_dispatch(ids, R, E, prefill_tile_rows(R, E), db, false, s),
+    st = from_hip(launch_dispatch(ids, R, E, prefill_tile_rows(R, E, bits), db, false, s),
                   (o + " dispatch").c_str());
   if (!st.ok) return finish(st);
   QGemmArgs a{};

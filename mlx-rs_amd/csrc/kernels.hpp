@@ -205,19 +205,22 @@ constexpr int32_t kActGeglu = 1;   // gelu_approx(g) * u  (gemma4 experts)
 // Largest input dim (K) of a projection: 8 waves x 8 groups of 64.
 constexpr int kMaxInputDims = 4096;
 // Prefill kernel M-tiles: 256 rows when the experts average at least
-// MLXR_PREFILL_TALL_ROWS rows, else 128 (prefill_tile_rows).  The dispatch
-// cuts its M-tile list with the same choice; tile lists are sized for the
-// shorter tiles.
+// MLXR_PREFILL_TALL_ROWS rows, 128 from MLXR_PREFILL_SHORT_ROWS (and always
+// for 8-bit weights), else 64 (prefill_tile_rows).  The dispatch cuts its M-tile list with the same
+// choice; tile lists are sized for the shortest tiles.
 #ifndef MLXR_PREFILL_TALL_ROWS
 #define MLXR_PREFILL_TALL_ROWS 192
+#endif
+#ifndef MLXR_PREFILL_SHORT_ROWS
+#define MLXR_PREFILL_SHORT_ROWS 64
 #endif
 // 1: the prefill GEMM keeps each tile's scales and biases in LDS (where they
 // fit) instead of loading them every K step
 #ifndef MLXR_PREFILL_SCALES_LDS
 #define MLXR_PREFILL_SCALES_LDS 1
 #endif
-constexpr int kPrefillMinTileRows = 128;
-int prefill_tile_rows(int64_t rows, int64_t experts);
+constexpr int kPrefillMinTileRows = 64;
+int prefill_tile_rows(int64_t rows, int64_t experts, int bits = 4);
 // max_items bounds the number of work items (dispatch_max_work); prefill
 // selects the M-tiled kernel (prefill.hip) where it applies.  Dense bf16
 // weights (bits 16) take the split-K decode kernel or the M-tiled one.

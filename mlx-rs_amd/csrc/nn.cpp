@@ -121,7 +121,7 @@ Status SwigluMlp::forward(const uint16_t* x, int64_t T, uint16_t* y,
   const int64_t d = gate_.input_dims, f = gate_.output_dims;
   const DispatchBuffers db = carve_dispatch(ws, T, 1, status);
   uint16_t* act = ws.take<uint16_t>(T * f);
-  Status st = from_hip(launch_dispatch_identity(T, prefill_tile_rows(T, 1), db, s),
+  Status st = from_hip(launch_dispatch_identity(T, prefill_tile_rows(T, 1, gate_.bits), db, s),
                        "shared_expert dispatch");
   if (!st.ok) return st;
   const bool prefill = use_prefill_path(T, 1, gate_.bits);
@@ -271,7 +271,7 @@ Status SwitchFfn::forward(const uint16_t* x, int64_t T, const int32_t* indices,
   const int64_t n = T * K;
   const DispatchBuffers db = carve_dispatch(ws, n, E, status);
   Status st = from_hip(
-      launch_dispatch(indices, n, E, prefill_tile_rows(n, E), db, false, s),
+      launch_dispatch(indices, n, E, prefill_tile_rows(n, E, sw_.bits), db, false, s),
       "switch_mlp dispatch");
   if (!st.ok) return st;
   return experts(x, T, K, db, y, ws, s);
@@ -490,7 +490,8 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
   if (norm) x = norm->out;  // the experts read the normalised rows
   // softmax, argpartition top-k, renormalise (moe.rs:124-138) + gather_sort
   st = from_hip(launch_route(logits, ld, T, E, K, bf16, idx, wts,
-                             prefill_tile_rows(T * K, E), db, s),
+                             prefill_tile_rows(T * K, E, b_.switch_mlp.gate_proj.bits),
+                             db, s),
                 "router top-k / dispatch");
   if (!st.ok) return st;
   const SplitSwitchFfn mlp(b_.switch_mlp);

@@ -107,10 +107,10 @@ __device__ __forceinline__ void dequant8(uint32_t w, float s, float b,
 
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
-// The two tile shapes.  Tall tiles (256 x 256, waves of 128 x 64) dequantise
-// each weight group for more rows and read fewer LDS bytes per MFMA; short
-// ones (128 x 256, waves of 64 x 64) waste less when the experts hold few
-// rows.  prefill_tile_rows picks one per call, and the dispatch cuts the
+// The tile shapes.  Tall tiles (256 x 256, waves of 128 x 64) dequantise
+// each weight group for more rows and read fewer LDS bytes per MFMA; shorter
+// ones (128 x 256, waves of 64 x 64; 64 x 256, waves of 32 x 64) waste less
+// when the experts hold few rows.  prefill_tile_rows picks one per call, and the dispatch cuts the
 // M-tiles to match.
 namespace tile256 {
 #define MLXR_PF_TILE_ROWS 256
@@ -141,13 +141,32 @@ namespace tile128 {
 #undef MLXR_PF_WAVES_N
 #undef MLXR_PF_REGBUF
 }  // namespace tile128
+// 64 x 256 tiles (waves of 32 x 64) for experts averaging under
+// MLXR_PREFILL_SHORT_ROWS rows: a 128-row tile there multiplies mostly
+// padding rows (2048 tokens, top 10 of 512 experts: 40 rows an expert).
+// 8-bit weights keep the 128-row tile: dequantising a wider group for half
+// the rows measured slower than the padding it saves.
+namespace tile64 {
+#define MLXR_PF_TILE_ROWS 64
+#define MLXR_PF_MBLOCKS 1
+#define MLXR_PF_WAVES_N 4
+#define MLXR_PF_REGBUF 2
+#define MLXR_PF_STAGES 2
+#include "prefill_tile.inc"
+#undef MLXR_PF_STAGES
+#undef MLXR_PF_TILE_ROWS
+#undef MLXR_PF_MBLOCKS
+#undef MLXR_PF_WAVES_N
+#undef MLXR_PF_REGBUF
+}  // namespace tile64
 
 }  // namespace
 
-int prefill_tile_rows(int64_t rows, int64_t experts) {
-  return rows >= (int64_t)MLXR_PREFILL_TALL_ROWS * (experts > 0 ? experts : 1)
-             ? tile256::kBM
-             : tile128::kBM;
+int prefill_tile_rows(int64_t rows, int64_t experts, int bits) {
+  const int64_t e = experts > 0 ? experts : 1;
+  if (rows >= (int64_t)MLXR_PREFILL_TALL_ROWS * e) return tile256::kBM;
+  if (rows >= (int64_t)MLXR_PREFILL_SHORT_ROWS * e || bits == 8) return tile128::kBM;
+  return tile64::kBM;
 }
 
 bool prefill_supported(const QGemmArgs& a, int64_t x_rows) {
@@ -165,6 +184,7 @@ hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 hipStream_t s, const char* profile) {
   if (tile_rows == tile256::kBM) return tile256::launch(a, x_rows, max_tiles, s, profile);
   if (tile_rows == tile128::kBM) return tile128::launch(a, x_rows, max_tiles, s, profile);
+  if (tile_rows == tile64::kBM) return tile64::launch(a, x_rows, max_tiles, s, profile);
   return hipErrorInvalidValue;
 }
 

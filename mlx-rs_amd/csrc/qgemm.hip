@@ -859,7 +859,7 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   // rows may lie anywhere in it: gather_mm / gather_qmm with lhs indices)
   const int64_t x_rows = a.x_rows > 0 ? a.x_rows : total_rows;
   if (prefill && prefill_supported(a, x_rows)) {
-    const int tile_rows = prefill_tile_rows(total_rows, a.E);
+    const int tile_rows = prefill_tile_rows(total_rows, a.E, a.bits);
     return launch_qgemm_prefill(a, x_rows, tile_rows,
                                 dispatch_max_tiles(total_rows, a.E, tile_rows), s, profile);
   }
