@@ -226,10 +226,12 @@ int prefill_tile_rows(int64_t rows, int64_t experts, int bits = 4);
 // weights (bits 16) take the split-K decode kernel or the M-tiled one.
 // `profile` names the launch for ProfileScope (default "qgemm_gated" or
 // "qgemm_down"; the shared expert's GEMMs are "shared_gated" /
-// "shared_down").  `shared` folds a second problem into the same decode
-// launch: the block's shared expert, whose shared_rows rows are the tokens
-// in order (its work items are made in the kernel, no dispatch); it must
-// have a's N, K, bits and mode, and prefill must be false.
+// "shared_down").  `shared` folds a second problem into the same launch:
+// the block's shared expert, whose shared_rows rows are the tokens in order
+// (its work items or M-tiles are made in the kernel, no dispatch); it must
+// have a's N, K, bits and mode.  (On the prefill path its tiles have the
+// routed problem's height: each output's sum runs in the same order at any
+// height.)
 hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         int64_t max_items, bool prefill, hipStream_t s,
                         const char* profile = nullptr,
@@ -239,11 +241,15 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
 // ---------------------------------------------------------------- prefill.hip
 // x_rows bounds the rows of x the GEMM reads; tile_rows is the M-tile height
 // the dispatch used (prefill_tile_rows); max_tiles bounds the M-tile list
-// (dispatch_max_tiles).
+// (dispatch_max_tiles).  shared (optional): a second problem of the same
+// projection shape and format with shared_rows rows by slot (the block's
+// shared expert), its M-tiles in the same launch.
 bool prefill_supported(const QGemmArgs& a, int64_t x_rows);
 hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 int tile_rows, int64_t max_tiles,
-                                hipStream_t s, const char* profile);
+                                hipStream_t s, const char* profile,
+                                const QGemmArgs* shared = nullptr,
+                                int64_t shared_rows = 0);
 
 // -------------------------------------------------------------- combine.hip
 // out f32 [T, d], or bf16 when bf16 (the routing weights are then bf16

@@ -283,9 +283,13 @@ Status SwitchFfn::forward(const uint16_t* x, int64_t T, const int32_t* indices,
 // whose rows land at their flat (t, k) position (scatter_unsort,
 // switch.rs:437-439).
 bool SwitchFfn::can_fold(const SwigluMlp& m, int64_t T, int64_t K) const {
-  return m.bits() == sw_.bits && m.hidden() == sw_.f && sw_.bits != 16 &&
-         !use_prefill_path(T * K, sw_.E, sw_.bits) &&
-         !use_prefill_path(T, 1, m.bits());
+  if (m.bits() != sw_.bits || m.hidden() != sw_.f) return false;
+  const bool routed_tiled = use_prefill_path(T * K, sw_.E, sw_.bits);
+  const bool shared_tiled = use_prefill_path(T, 1, m.bits());
+  // both on the decode kernels (quantised: the streaming kernel), or both
+  // on the M-tiled one
+  if (!routed_tiled && !shared_tiled) return sw_.bits != 16;
+  return routed_tiled && shared_tiled;
 }
 
 Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,

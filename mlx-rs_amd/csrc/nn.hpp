@@ -120,7 +120,8 @@ class SwitchFfn {
                  const DispatchBuffers& db, uint16_t* y, Carve& ws,
                  hipStream_t s, const SharedFold* fold = nullptr) const;
   // Whether a SwiGLU shared expert can fold into this FFN's launches at T
-  // tokens: both on the decode kernels, same bits and hidden size.
+  // tokens: same bits and hidden size, and both on the streaming decode
+  // kernel or both on the M-tiled one.
   bool can_fold(const SwigluMlp& m, int64_t T, int64_t K) const;
   // forward_with_combine: out [T, d] = sum_k w * y (+ shared branch); f32
   // weights give an f32 out, bf16 weights (w_bf16) a bf16 out.

@@ -181,10 +181,14 @@ bool prefill_supported(const QGemmArgs& a, int64_t x_rows) {
 
 hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 int tile_rows, int64_t max_tiles,
-                                hipStream_t s, const char* profile) {
-  if (tile_rows == tile256::kBM) return tile256::launch(a, x_rows, max_tiles, s, profile);
-  if (tile_rows == tile128::kBM) return tile128::launch(a, x_rows, max_tiles, s, profile);
-  if (tile_rows == tile64::kBM) return tile64::launch(a, x_rows, max_tiles, s, profile);
+                                hipStream_t s, const char* profile,
+                                const QGemmArgs* shared, int64_t shared_rows) {
+  if (tile_rows == tile256::kBM)
+    return tile256::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
+  if (tile_rows == tile128::kBM)
+    return tile128::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
+  if (tile_rows == tile64::kBM)
+    return tile64::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
   return hipErrorInvalidValue;
 }
 

@@ -847,10 +847,10 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         const char* profile, const QGemmArgs* shared,
                         int64_t shared_rows) {
   if (!profile) profile = a.gated ? "qgemm_gated" : "qgemm_down";
-  // a folded second problem (decode only): the same projection shape and
-  // format, its items after the routed ones in the same grid
+  // a folded second problem: the same projection shape and format, its
+  // items (or M-tiles) beside the routed ones in the same grid
   const int64_t items2 = shared ? (shared_rows + kWorkRows - 1) / kWorkRows : 0;
-  if (shared && (prefill || shared->N != a.N || shared->K != a.K ||
+  if (shared && (shared->N != a.N || shared->K != a.K ||
                  shared->bits != a.bits || shared->gated != a.gated))
     return hipErrorInvalidValue;
   if (max_items + items2 <= 0) return hipSuccess;
@@ -858,10 +858,12 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   // the M-tiled kernel reads x through a buffer of x's own rows (gathered
   // rows may lie anywhere in it: gather_mm / gather_qmm with lhs indices)
   const int64_t x_rows = a.x_rows > 0 ? a.x_rows : total_rows;
-  if (prefill && prefill_supported(a, x_rows)) {
+  if (prefill && prefill_supported(a, x_rows) &&
+      (!shared || prefill_supported(*shared, shared_rows))) {
     const int tile_rows = prefill_tile_rows(total_rows, a.E, a.bits);
     return launch_qgemm_prefill(a, x_rows, tile_rows,
-                                dispatch_max_tiles(total_rows, a.E, tile_rows), s, profile);
+                                dispatch_max_tiles(total_rows, a.E, tile_rows), s, profile,
+                                shared, shared_rows);
   }
   const int groups = a.K / 64;
   // Many (expert, block) items: the streaming kernel (one block per wave,
