@@ -542,10 +542,26 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     else
       MLXR_RL_N(MLXR_RL_MID_EB, MLXR_RL_MID_TB, MLXR_RL_MID_U, false);
   } else {
+    // A lone extra column (the shared expert's gate beside 16k experts)
+    // would add a round of whole column blocks: the tiled kernel takes the
+    // E expert columns and the per-wave kernel the extra one (the same
+    // lane order and butterfly, so the same bits).
+    const bool split = w.w_extra && e_tot % kRtCol == 1;
+    RouterWeights wm = w;
+    if (split) wm.w_extra = nullptr, wm.scales_extra = nullptr, wm.biases_extra = nullptr;
+    const int64_t cols = split ? E : e_tot;
     router_logits_tiled_kernel<BITS>
-        <<<dim3((unsigned)((e_tot + kRtCol - 1) / kRtCol),
+        <<<dim3((unsigned)((cols + kRtCol - 1) / kRtCol),
                 (unsigned)((T + kRtTok - 1) / kRtTok)),
-           256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld);
+           256, 0, s>>>(x, (int)T, (int)d, wm, bias, (int)E, logits, ld);
+    if (split) {
+      const RouterWeights we{w.bits, w.w_extra, w.scales_extra, w.biases_extra,
+                             nullptr, nullptr, nullptr};
+      constexpr int kTB = MLXR_RL_MID_TB;
+      router_logits_kernel<1, kTB, 2, BITS, false>
+          <<<dim3(1u, (unsigned)((T + kTB - 1) / kTB)), 256, 0, s>>>(
+              x, (int)T, (int)d, we, nullptr, 1, logits + E, ld, nm);
+    }
   }
 #undef MLXR_RL
 #undef MLXR_RL_N
