@@ -196,8 +196,8 @@ def gated_bytes(cfg, T, U, shared_folded=False):
     bf16 scales and biases (or the dense bf16 weights) of the U distinct
     selected experts' gate and up rows (2*f*d weights each), x read once
     (T*d bf16) and the activations written (T*K*f bf16); with the shared
-    expert folded into the launch (decode, same bits and hidden size) also
-    its gate and up rows (2*fs*d) and its activations (T*fs bf16)."""
+    expert folded into the launch (folds_shared) also its gate and up rows
+    (2*fs*d) and its activations (T*fs bf16)."""
     per_w = 2.0 if cfg.bits == 16 else cfg.bits / 8 + 4 / cfg.group_size
     b = U * 2 * cfg.f * cfg.d * per_w + T * cfg.d * 2 + T * cfg.K * cfg.f * 2
     if shared_folded and cfg.fs:
@@ -205,8 +205,32 @@ def gated_bytes(cfg, T, U, shared_folded=False):
     return int(b)
 
 
-def gated_flops(cfg, T):
-    return 4 * T * cfg.K * cfg.f * cfg.d
+def gated_flops(cfg, T, shared_folded=False):
+    """gate/up flops of one launch: 4*T*K*f*d, plus 4*T*fs*d with the
+    shared expert folded in."""
+    return 4 * T * (cfg.K * cfg.f + (cfg.fs if shared_folded and cfg.fs else 0)) * cfg.d
+
+
+def tiled_path(rows, experts, bits):
+    """Whether a grouped GEMM of `rows` rows over `experts` experts runs the
+    M-tiled kernel: nn::use_prefill_path (csrc/nn.cpp), with its thresholds
+    MLXR_QUANT_TILED_ROWS (32) and MLXR_DENSE_TILED_ROWS (2) rows per
+    expert (csrc/nn.hpp), and at least 512 rows."""
+    per = 2 if bits == 16 else 32
+    return rows >= per * experts and rows >= 512
+
+
+def folds_shared(cfg, T):
+    """Whether the block folds its shared expert into the routed launches
+    (SwitchFfn::can_fold, csrc/nn.cpp): same bits and hidden size, and both
+    on the streaming decode kernel (quantised) or both M-tiled."""
+    if not cfg.fs or cfg.fs != cfg.f:
+        return False
+    routed = tiled_path(T * cfg.K, cfg.E, cfg.bits)
+    shared = tiled_path(T, 1, cfg.bits)
+    if not routed and not shared:
+        return cfg.bits != 16
+    return routed and shared
 
 
 def measured_traffic(workload: str, kernel: str):
@@ -310,17 +334,14 @@ def main():
     kt, kn, kmin, kmax = r.kernel_time(pkg, "qgemm_gated", args.steps)
     decode = T * cfg.K < 2048
     if decode:
-        # (the block folds its shared expert into the decode launches when
-        # it has the experts' bits and hidden size)
-        folded = bool(cfg.fs) and cfg.fs == cfg.f and cfg.bits != 16
-        traffic_alg = gated_bytes(cfg, T, U, folded)
+        traffic_alg = gated_bytes(cfg, T, U, folds_shared(cfg, T))
         achieved = traffic_alg / kt / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(achieved / HBM_PEAK_GBS, 4),
                     traffic=measured_traffic(f"{cfg.name} T={T}", "qgemm_gated"),
                     algorithmic_bytes=traffic_alg)
     else:
-        achieved = gated_flops(cfg, T) / kt / 1e12
+        achieved = gated_flops(cfg, T, folds_shared(cfg, T)) / kt / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 2), peak=BF16_PEAK_TFLOPS,
                     unit="TFLOP/s", frac=round(achieved / BF16_PEAK_TFLOPS, 4), traffic=None)
     roof.update(kernel="qgemm_gated", kernel_us=round(kt * 1e6, 2), launches=kn,
