@@ -513,9 +513,7 @@ int mlxr_moe_switch_glu_forward(const mlxr_moe_switch_glu* ffn, const void* x,
   hipStream_t s = as_stream(stream);
   Carve c(workspace);
   int32_t* status = c.take<int32_t>(1);
-  st = from_hip(launch_zero_status(status, s), "switch_glu status");
-  if (st.ok)
-    st = m.forward_with_combine(static_cast<const uint16_t*>(x), T, indices,
+  st = m.forward_with_combine(static_cast<const uint16_t*>(x), T, indices,
                                 weights, false, K, out, nullptr, nullptr, 0,
                                 c, status, s);
   return finish(st);
@@ -544,9 +542,7 @@ int mlxr_moe_switch_glu_experts(const mlxr_moe_switch_glu* ffn, const void* x,
   Carve c(workspace);
   int32_t* status = c.take<int32_t>(1);
   c.take<uint16_t>(T * K * d);  // the combine's y slot, unused here
-  st = from_hip(launch_zero_status(status, s), "switch_glu status");
-  if (st.ok)
-    st = m.forward(static_cast<const uint16_t*>(x), T, indices, K,
+  st = m.forward(static_cast<const uint16_t*>(x), T, indices, K,
                    static_cast<uint16_t*>(y), c, status, s);
   return finish(st);
 }
@@ -694,9 +690,7 @@ int mlxr_moe_packed_switch_glu_forward(const mlxr_moe_packed_switch_glu* ffn,
   hipStream_t s = as_stream(stream);
   Carve c(workspace);
   int32_t* status = c.take<int32_t>(1);
-  st = from_hip(launch_zero_status(status, s), "packed_switch_glu status");
-  if (st.ok)
-    st = m.forward_with_combine(static_cast<const uint16_t*>(x), T, indices,
+  st = m.forward_with_combine(static_cast<const uint16_t*>(x), T, indices,
                                 weights, weights_dtype == MLXR_MOE_BFLOAT16, K,
                                 out, nullptr, nullptr, 0, c, status, s);
   return finish(st);
@@ -718,9 +712,7 @@ int mlxr_moe_packed_switch_glu_experts(const mlxr_moe_packed_switch_glu* ffn,
   Carve c(workspace);
   int32_t* status = c.take<int32_t>(1);
   c.take<uint16_t>(T * K * m.weights().d);  // the combine's y slot, unused
-  st = from_hip(launch_zero_status(status, s), "packed_switch_glu status");
-  if (st.ok)
-    st = m.forward(static_cast<const uint16_t*>(x), T, indices, K,
+  st = m.forward(static_cast<const uint16_t*>(x), T, indices, K,
                    static_cast<uint16_t*>(y), c, status, s);
   return finish(st);
 }

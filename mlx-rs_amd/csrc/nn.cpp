@@ -270,8 +270,9 @@ Status SwitchFfn::forward(const uint16_t* x, int64_t T, const int32_t* indices,
   const int64_t E = sw_.E;
   const int64_t n = T * K;
   const DispatchBuffers db = carve_dispatch(ws, n, E, status);
+  // (the dispatch clears *status first: no launch of its own for that)
   Status st = from_hip(
-      launch_dispatch(indices, n, E, prefill_tile_rows(n, E, sw_.bits), db, false, s),
+      launch_dispatch(indices, n, E, prefill_tile_rows(n, E, sw_.bits), db, true, s),
       "switch_mlp dispatch");
   if (!st.ok) return st;
   return experts(x, T, K, db, y, ws, s);

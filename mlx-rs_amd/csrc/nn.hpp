@@ -110,7 +110,8 @@ struct SwitchWeights {
 // The forward shared by both expert layouts (switch.rs:417-474).
 class SwitchFfn {
  public:
-  // forward: y bf16 [T, K, d] per-expert outputs.
+  // forward: y bf16 [T, K, d] per-expert outputs; clears *status first
+  // (in its dispatch launch).
   Status forward(const uint16_t* x, int64_t T, const int32_t* indices,
                  int64_t K, uint16_t* y, Carve& ws, int32_t* status,
                  hipStream_t s) const;

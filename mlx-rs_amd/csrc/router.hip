@@ -418,6 +418,10 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(
     out[row * n + i] = expf(r[i] - mx) / sum;
 }
 
+// rows the norm holds in registers (up to kMaxRmsDims values): 4 values
+// per lane per 256-wide piece
+constexpr int kRmsPieces = 16;
+constexpr int kMaxRmsDims = 256 * kRmsPieces;
 // fast::rms_norm as gemma4's router applies it (Router::forward,
 // crates/mlxr-lm/src/gemma4/text/text.rs:640) and as RmsNorm::forward does
 // (crates/mlxr/src/layers/normalization.rs:272-276): out_j = bf16(w_j *
@@ -432,22 +436,61 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const uint16_t* xr = x + (int64_t)t * d;
+  uint16_t* orow = out + (int64_t)t * d;
+  const auto piece = [](uint2 u, float (&v)[4]) {
+    v[0] = __uint_as_float(u.x << 16);
+    v[1] = __uint_as_float(u.x & 0xffff0000u);
+    v[2] = __uint_as_float(u.y << 16);
+    v[3] = __uint_as_float(u.y & 0xffff0000u);
+  };
+  if (d <= kMaxRmsDims && (reinterpret_cast<uintptr_t>(w) & 7) == 0) {
+    // the row's 4-element pieces stay in registers between the two passes,
+    // and the weight's load with them (8-byte pieces)
+    uint2 xv[kRmsPieces], wv[kRmsPieces];
+#pragma unroll
+    for (int i = 0; i < kRmsPieces; ++i) {
+      const int j0 = 4 * lane + 256 * i;
+      xv[i] = j0 < d ? *reinterpret_cast<const uint2*>(xr + j0) : make_uint2(0u, 0u);
+      wv[i] = j0 < d ? *reinterpret_cast<const uint2*>(w + j0) : make_uint2(0u, 0u);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRmsPieces; ++i) {
+      float v[4];
+      piece(xv[i], v);
+      // (pieces past d are zeros: adding 0*0 leaves the sum as it is)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(v[c], v[c], acc);
+    }
+    const float ss = wave_sum_butterfly(acc);
+    const float r = 1.0f / sqrtf(ss / (float)d + eps);
+#pragma unroll
+    for (int i = 0; i < kRmsPieces; ++i) {
+      const int j0 = 4 * lane + 256 * i;
+      float v[4], g[4];
+      piece(xv[i], v);
+      piece(wv[i], g);
+      uint32_t o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = f32_to_bf16(g[c] * bf16_round(v[c] * r));
+      if (j0 < d)
+        *reinterpret_cast<uint2*>(orow + j0) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    }
+    return;
+  }
+  // wider rows (or a weight not 8-byte aligned): x read twice, w by element
   float acc = 0.0f;
   for (int j0 = 4 * lane; j0 < d; j0 += 256) {
-    const uint2 u = *reinterpret_cast<const uint2*>(xr + j0);
-    const float v[4] = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                        __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+    float v[4];
+    piece(*reinterpret_cast<const uint2*>(xr + j0), v);
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(v[c], v[c], acc);
   }
   const float ss = wave_sum_butterfly(acc);
   const float r = 1.0f / sqrtf(ss / (float)d + eps);
-  // the output in the same 4-element pieces: 8-byte loads of x and stores
-  uint16_t* orow = out + (int64_t)t * d;
   for (int j0 = 4 * lane; j0 < d; j0 += 256) {
-    const uint2 u = *reinterpret_cast<const uint2*>(xr + j0);
-    const float v[4] = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                        __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+    float v[4];
+    piece(*reinterpret_cast<const uint2*>(xr + j0), v);
     uint32_t o[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)

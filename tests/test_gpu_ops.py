@@ -376,10 +376,11 @@ def test_router_topk_bf16_linear_bit_exact(pkg, orc, dev, T, E):
 
 
 # ------------------------------------------------------- rms_norm
-@pytest.mark.parametrize("T,d", [(1, 2048), (37, 2048), (300, 4096), (5, 516)])
+@pytest.mark.parametrize("T,d", [(1, 2048), (37, 2048), (300, 4096), (5, 516), (3, 6148)])
 def test_rms_norm_bit_exact(pkg, orc, dev, T, d):
     """fast::rms_norm (layers/normalization.rs:272-276): bit for bit
-    against the oracle."""
+    against the oracle (rows held in registers up to d = 4096; d = 6148
+    takes the two-pass loop)."""
     rng = np.random.default_rng(T + d)
     x = _bf16(orc, (3 * rng.standard_normal((T, d))).astype(np.float32), dev)
     w = _bf16(orc, (1 + 0.2 * rng.standard_normal(d)).astype(np.float32), dev)
