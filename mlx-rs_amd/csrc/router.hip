@@ -219,15 +219,22 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 // lane sums of a logit are added in the butterfly's pairwise tree (lanes
 // l and l^32 first, ... l and l^1 last) -- by one lane reading them from
 // LDS rather than by six shuffles on every lane.  Same bits.
-constexpr int kRtTok = 32, kRtCol = 16, kRtWaveTok = 8;
-template <int BITS>
+// kRtCol experts x 4 * WT tokens per workgroup (WT tokens per wave: 8, or
+// 4 where 8 would leave CUs idle)
+constexpr int kRtCol = 16;
+template <int BITS, int WT>
 __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
     const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
     const float* __restrict__ bias, int E, float* __restrict__ logits,
     int64_t ld) {
-  // 32 KB: the step's x [32][256] bf16 and w [16][256] f32; afterwards the
-  // lane sums [wave][32 logits][64 lanes] f32, 32 logits at a time
-  __shared__ __attribute__((aligned(16))) char lds[kRtTok * 256 * 2 + kRtCol * 256 * 4];
+  constexpr int kRtTok = 4 * WT, kRtWaveTok = WT;
+  constexpr int XK = kRtTok / 8;  // 16-byte x chunks per thread per step
+  constexpr int CPR = 32 / WT;    // columns per round of the final sums
+  static_assert(WT == 4 || WT == 8, "tokens per wave");
+  // the step's x [kRtTok][256] bf16 and w [16][256] f32; afterwards the
+  // lane sums [wave][32 logits][64 lanes] f32 (32 KB), 32 logits at a time
+  constexpr int kStageBytes = kRtTok * 256 * 2 + kRtCol * 256 * 4;
+  __shared__ __attribute__((aligned(16))) char lds[kStageBytes > 32768 ? kStageBytes : 32768];
   uint16_t (*xs)[256] = reinterpret_cast<uint16_t (*)[256]>(lds);
   float (*ws)[256] = reinterpret_cast<float (*)[256]>(lds + kRtTok * 256 * 2);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -241,25 +248,30 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
   // this thread's staging chunks: x rows id/32 (8 bf16 at (id%32)*8), w rows
   // id/64 (4 weights at (id%64)*4, dequantised to f32 on the way to LDS),
   // id = tid + 256k; zeros past d / T / e_tot
-  const uint16_t* xp[4];
+  const uint16_t* xp[XK];
   WRow wp[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < XK; ++k) {
     const int id = tid + 256 * k;
     const int t = t0 + (id >> 5);
     xp[k] = t < T ? x + (int64_t)t * d + (id & 31) * 8 : nullptr;
-    wp[k] = router_row<BITS>(rw, e0 + (id >> 6), E, d);
   }
-  u32x4_t xr[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wp[k] = router_row<BITS>(rw, e0 + ((tid + 256 * k) >> 6), E, d);
+  u32x4_t xr[XK];
   float4 wr[4];
   auto fetch = [&](int i) {
     const int j0 = 256 * i;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < XK; ++k) {
       const int id = tid + 256 * k;
       xr[k] = (xp[k] && j0 + (id & 31) * 8 < d)
                   ? *reinterpret_cast<const u32x4_t*>(xp[k] + j0)
                   : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int id = tid + 256 * k;
       wr[k] = (wp[k].w && j0 + (id & 63) * 4 < d)
                   ? router_w4<BITS>(wp[k], j0 + (id & 63) * 4)
                   : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -269,9 +281,13 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
   fetch(0);
   for (int i = 0; i < steps; ++i) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < XK; ++k) {
       const int id = tid + 256 * k;
       *reinterpret_cast<u32x4_t*>(&xs[id >> 5][(id & 31) * 8]) = xr[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int id = tid + 256 * k;
       *reinterpret_cast<float4*>(&ws[id >> 6][(id & 63) * 4]) = wr[k];
     }
     __syncthreads();
@@ -300,13 +316,13 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
     }
     __syncthreads();
   }
-  // lane sums -> logits, 32 logits (4 columns x 8 tokens) per round; each
-  // wave uses its own quarter of the LDS, logit i's row swizzled by i
+  // lane sums -> logits, 32 logits (CPR columns x WT tokens) per round;
+  // each wave uses its own quarter of the LDS, logit i's row swizzled by i
   float* red = reinterpret_cast<float*>(lds) + wave * 32 * 64;
 #pragma unroll
-  for (int q0 = 0; q0 < kRtCol; q0 += 4) {
+  for (int q0 = 0; q0 < kRtCol; q0 += CPR) {
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq)
+    for (int qq = 0; qq < CPR; ++qq)
 #pragma unroll
       for (int tt = 0; tt < kRtWaveTok; ++tt)
         red[(qq * kRtWaveTok + tt) * 64 + (lane ^ (qq * kRtWaveTok + tt))] =
@@ -593,10 +609,17 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     RouterWeights wm = w;
     if (split) wm.w_extra = nullptr, wm.scales_extra = nullptr, wm.biases_extra = nullptr;
     const int64_t cols = split ? E : e_tot;
-    router_logits_tiled_kernel<BITS>
-        <<<dim3((unsigned)((cols + kRtCol - 1) / kRtCol),
-                (unsigned)((T + kRtTok - 1) / kRtTok)),
-           256, 0, s>>>(x, (int)T, (int)d, wm, bias, (int)E, logits, ld);
+    // 8 tokens per wave, or 4 where 8 would make fewer workgroups than
+    // the GPU's 2 x 256 slots (c3 T=512: 128 workgroups)
+    const int64_t cb = (cols + kRtCol - 1) / kRtCol;
+    if (cb * ((T + 31) / 32) >= 512)
+      router_logits_tiled_kernel<BITS, 8>
+          <<<dim3((unsigned)cb, (unsigned)((T + 31) / 32)), 256, 0, s>>>(
+              x, (int)T, (int)d, wm, bias, (int)E, logits, ld);
+    else
+      router_logits_tiled_kernel<BITS, 4>
+          <<<dim3((unsigned)cb, (unsigned)((T + 15) / 16)), 256, 0, s>>>(
+              x, (int)T, (int)d, wm, bias, (int)E, logits, ld);
     if (split) {
       const RouterWeights we{w.bits, w.w_extra, w.scales_extra, w.biases_extra,
                              nullptr, nullptr, nullptr};
