@@ -13,13 +13,13 @@
 // bf16(fmaf(code, scale, bias)) -- into LDS, where every wave of the
 // workgroup reuses them.
 //
-// Workgroup: 8 waves, kWM x kWN = 2 x 4; tile kBM rows x kBN = 256 columns
-// (the gated kernel's columns are 128 gate channels then the same 128 up
-// channels, so each wave holds matching gate and up sums for the SwiGLU
-// epilogue).  Two tile heights (prefill_tile.inc is built once per shape):
-// 256 rows, each wave 128 x 64 outputs as 4 x 2 blocks of
-// v_mfma_f32_32x32x16_bf16, or 128 rows, each wave 64 x 64 as 2 x 2 blocks
-// (K = 16 per instruction, four per group).  A tall tile spreads the
+// Workgroup: kWM x kWN waves (2 x 4, or 2 x 2 in the narrow forms); tile
+// kBM rows x kBN = 64 kWN columns (the gated kernel's columns are gate
+// channels then the same up channels, so each wave holds matching gate and
+// up sums for the SwiGLU epilogue).  Tile heights 256, 128 and 64 rows
+// (prefill_tile.inc is built once per shape): each wave 128 x 64, 64 x 64
+// or 32 x 64 outputs as blocks of v_mfma_f32_32x32x16_bf16 (K = 16 per
+// instruction, four per group).  A tall tile spreads the
 // dequantisation (the VALU cost, about three instructions per weight) over
 // more rows; waves whose rows lie past the expert's last row skip their
 // MFMAs.  Global loads are raw buffer loads with the K step in the scalar
@@ -159,6 +159,40 @@ namespace tile64 {
 #undef MLXR_PF_WAVES_N
 #undef MLXR_PF_REGBUF
 }  // namespace tile64
+// Narrow forms: 128 columns, 4 waves of 64 x 64 (128 rows) or 32 x 64 (64
+// rows), two stages: 80 and 64 KB of LDS with the scales, so two
+// workgroups share a CU and one's barrier waits and staging overlap the
+// other's MFMAs (the 8-wave tiles fill a CU alone).  Measured against the
+// 256-column tiles: c7 T=2048 gate/up 234 to 205 µs, c6 T=2048 176 to 164
+// (down 109 to 103), c3 T=2048 191 to 184; 64 rows, gate/up: c4 T=2048
+// 291 to 258, c3 T=512 126 to 118.  Not for 8-bit weights (c5 T=512
+// gate/up 463 to 670) or the 64-row down GEMMs (c4 T=2048 135 to 141).
+namespace tile128n {
+#define MLXR_PF_TILE_ROWS 128
+#define MLXR_PF_MBLOCKS 2
+#define MLXR_PF_WAVES_N 2
+#define MLXR_PF_REGBUF 2
+#define MLXR_PF_STAGES 2
+#include "prefill_tile.inc"
+#undef MLXR_PF_STAGES
+#undef MLXR_PF_TILE_ROWS
+#undef MLXR_PF_MBLOCKS
+#undef MLXR_PF_WAVES_N
+#undef MLXR_PF_REGBUF
+}  // namespace tile128n
+namespace tile64n {
+#define MLXR_PF_TILE_ROWS 64
+#define MLXR_PF_MBLOCKS 1
+#define MLXR_PF_WAVES_N 2
+#define MLXR_PF_REGBUF 2
+#define MLXR_PF_STAGES 2
+#include "prefill_tile.inc"
+#undef MLXR_PF_STAGES
+#undef MLXR_PF_TILE_ROWS
+#undef MLXR_PF_MBLOCKS
+#undef MLXR_PF_WAVES_N
+#undef MLXR_PF_REGBUF
+}  // namespace tile64n
 
 }  // namespace
 
@@ -185,6 +219,11 @@ hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
                                 const QGemmArgs* shared, int64_t shared_rows) {
   if (tile_rows == tile256::kBM)
     return tile256::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
+  // (the dispatch's M-tiles fix the height; the width is the launch's own)
+  if (tile_rows == tile128::kBM && a.bits != 8)
+    return tile128n::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
+  if (tile_rows == tile64::kBM && a.gated)
+    return tile64n::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
   if (tile_rows == tile128::kBM)
     return tile128::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
   if (tile_rows == tile64::kBM)
