@@ -228,6 +228,9 @@ def test_gather_qmm_reference_cases(pkg, orc, dev, bits):
     (1024, 4, 8, 256, 512, 8), (600, 8, 32, 384, 1024, 4),
     # 256-row M-tiles (experts averaging >= 192 rows)
     (2048, 2, 16, 256, 512, 4), (2048, 2, 16, 320, 1024, 8),
+    # 128-row narrow tiles (128 columns) with a half last N-tile, and
+    # 64-row tiles (256 columns) with a quarter last N-tile
+    (1200, 4, 32, 320, 512, 4), (1024, 4, 100, 320, 512, 4),
     # more than 1024 ids (the multi-kernel dispatch) on the decode kernels:
     # its work list, long-form items first
     (200, 8, 128, 768, 2048, 4), (160, 8, 128, 256, 1024, 8)])
