@@ -214,9 +214,9 @@ def gated_flops(cfg, T, shared_folded=False):
 def tiled_path(rows, experts, bits):
     """Whether a grouped GEMM of `rows` rows over `experts` experts runs the
     M-tiled kernel: nn::use_prefill_path (csrc/nn.cpp), with its thresholds
-    MLXR_QUANT_TILED_ROWS (32) and MLXR_DENSE_TILED_ROWS (2) rows per
+    MLXR_QUANT_TILED_ROWS (16) and MLXR_DENSE_TILED_ROWS (2) rows per
     expert (csrc/nn.hpp), and at least 512 rows."""
-    per = 2 if bits == 16 else 32
+    per = 2 if bits == 16 else 16
     return rows >= per * experts and rows >= 512
 
 

@@ -59,9 +59,12 @@ namespace nn {
 // switches to its sorted path at T*K >= SORT_THRESHOLD = 2048, switch.rs:40;
 // here the choice is about GEMM shape, not sorting, which always happens).
 // Dense bf16 GEMMs (bits 16) switch at MLXR_DENSE_TILED_ROWS rows per
-// expert.
+// expert.  Measured for the quantised ones (graph steps): at 16 rows per
+// expert the tile kernel wins (c6 T=512 391 to 262 µs, c2 T=256 219 to
+// 175, c5 T=256 1055 to 676); at 8-10 it does not (c2 T=160 169 to 171,
+// c6 T=320 260 to 273, c2 T=128 141 to 162).
 #ifndef MLXR_QUANT_TILED_ROWS
-#define MLXR_QUANT_TILED_ROWS 32
+#define MLXR_QUANT_TILED_ROWS 16
 #endif
 #ifndef MLXR_DENSE_TILED_ROWS
 #define MLXR_DENSE_TILED_ROWS 2

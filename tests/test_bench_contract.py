@@ -61,15 +61,15 @@ def test_gated_bytes_with_folded_shared_expert(pkg):
 
 def test_shared_expert_fold_rule(pkg):
     """The bench's copy of the library's fold rule: c6 folds at T=64 (both
-    streaming) and T=2048 (both M-tiled), not at T=512 (routed rows on the
-    streaming kernel, the shared expert's 512 rows M-tiled); dense c8 folds
-    only M-tiled; c3 has no shared expert.  The folded gate/up launch's
-    flops count the shared expert's rows."""
+    streaming) and T=512 and 2048 (both M-tiled); c4 not at T=512 (routed
+    rows on the streaming kernel, 10 per expert; the shared expert's 512
+    rows M-tiled); dense c8 folds only M-tiled; c3 has no shared expert.
+    The folded gate/up launch's flops count the shared expert's rows."""
     import bench
     C = pkg.workloads.CONFIGS
-    c6, c8 = C["c6"], C["c8"]
+    c4, c6, c8 = C["c4"], C["c6"], C["c8"]
     assert bench.folds_shared(c6, 64) and bench.folds_shared(c6, 2048)
-    assert not bench.folds_shared(c6, 512)
+    assert bench.folds_shared(c6, 512) and not bench.folds_shared(c4, 512)
     assert not bench.folds_shared(c8, 64) and bench.folds_shared(c8, 2048)
     assert not bench.folds_shared(C["c3"], 4096)
     assert bench.tiled_path(2048 * c6.K, c6.E, c6.bits) == bool(pkg.ops.gather_qmm_tiled(2048 * c6.K, c6.E))

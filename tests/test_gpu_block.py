@@ -174,13 +174,16 @@ def test_c1_golden_fixture(pkg, orc, dev):
 # Besides the bench points: T = 2, 3, 5 on the streaming kernel with
 # K-slices (4, 2, 1 of them as the grid grows), c5 T=1 and 4 (8-bit
 # K-slices), c4/c6 at T = 3 and 9 (the folded shared expert with a partial
-# item of rows; 9 > 8 rows: two shared items).  c4 and c6 at T = 2048 fold
-# the shared expert into the M-tiled launches (c8: dense weights), c6 at
-# T = 512 does not (its routed GEMMs stay on the streaming kernel).
+# item of rows; 9 > 8 rows: two shared items).  c4 and c6 at T = 2048 and
+# c6 at T = 512 fold the shared expert into the M-tiled launches (c8: dense
+# weights); c4 at T = 512 does not (10 routed rows per expert stay on the
+# streaming kernel, the shared expert's 512 rows are M-tiled).  c2 at
+# T = 256 is M-tiled from 16 rows per expert.
 @pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 2), ("c2", 3), ("c2", 5),
                                    ("c2", 8), ("c2", 32), ("c2", 64), ("c2", 256),
                                    ("c5", 1), ("c5", 4), ("c5", 32), ("c5", 512),
-                                   ("c4", 1), ("c4", 3), ("c4", 9), ("c4", 64), ("c4", 2048),
+                                   ("c4", 1), ("c4", 3), ("c4", 9), ("c4", 64), ("c4", 512),
+                                   ("c4", 2048),
                                    ("c3", 512), ("c3", 2048), ("c3", 4096),
                                    ("c6", 1), ("c6", 3), ("c6", 9), ("c6", 64),
                                    ("c6", 512), ("c6", 2048), ("c7", 1), ("c7", 64),
