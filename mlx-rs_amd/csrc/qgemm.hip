@@ -63,7 +63,13 @@ constexpr int64_t kStreamMinBlocks = MLXR_STREAM_MIN_BLOCKS;
 // 16-channel blocks per wave of the down kernel, at most (1, 2 or 4; the
 // launcher halves it until the grid keeps every slot busy)
 #ifndef MLXR_STREAM_MAX_NB
-#define MLXR_STREAM_MAX_NB 2
+#define MLXR_STREAM_MAX_NB 4
+#endif
+// four blocks per wave only while the grid stays this many times the slots
+// (many small items: c4 T=512 down 157 to 141 µs, c6 T=320 91 to 85; with
+// 4x the slots c2 T=128 down went 45.8 to 50.0)
+#ifndef MLXR_STREAM_NB4_GRIDS
+#define MLXR_STREAM_NB4_GRIDS 8
 #endif
 // ... and of the gated kernel (1 or 2)
 #ifndef MLXR_STREAM_GATED_NB
@@ -886,7 +892,8 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     const int64_t per_tile = a.N / (16 * kWaves);
     int nb = 1;
     for (int c = a.gated ? MLXR_STREAM_GATED_NB : MLXR_STREAM_MAX_NB; c > 1; c >>= 1)
-      if (per_tile % c == 0 && all_items * (per_tile / c) >= kStreamSlots) {
+      if (per_tile % c == 0 &&
+          all_items * (per_tile / c) >= kStreamSlots * (c >= 4 ? MLXR_STREAM_NB4_GRIDS : 1)) {
         nb = c;
         break;
       }
