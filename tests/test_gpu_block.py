@@ -178,9 +178,11 @@ def test_c1_golden_fixture(pkg, orc, dev):
 # c6 at T = 512 fold the shared expert into the M-tiled launches (c8: dense
 # weights); c4 at T = 512 does not (10 routed rows per expert stay on the
 # streaming kernel, the shared expert's 512 rows are M-tiled).  c2 at
-# T = 256 is M-tiled from 16 rows per expert.
+# T = 256 (16 rows per expert) and c5 at T = 256 are M-tiled, c2 at T = 240
+# (15) is not.
 @pytest.mark.parametrize("cfg,T", [("c1", 16), ("c2", 1), ("c2", 2), ("c2", 3), ("c2", 5),
-                                   ("c2", 8), ("c2", 32), ("c2", 64), ("c2", 256),
+                                   ("c2", 8), ("c2", 32), ("c2", 64), ("c2", 240),
+                                   ("c2", 256), ("c5", 256),
                                    ("c5", 1), ("c5", 4), ("c5", 32), ("c5", 512),
                                    ("c4", 1), ("c4", 3), ("c4", 9), ("c4", 64), ("c4", 512),
                                    ("c4", 2048),
