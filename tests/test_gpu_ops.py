@@ -1,4 +1,6 @@
 """GPU parity of the op-level entry points against the CPU oracle."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -147,6 +149,35 @@ def test_packed_swiglu_equals_split(pkg, dev, T):
     print(f"  packed vs split T={T}", flush=True)
     assert torch.equal(packed.forward(x, idx), m.forward(x, idx))
     assert torch.equal(packed.forward_with_combine(x, idx, w), m.forward_with_combine(x, idx, w))
+
+
+@pytest.mark.parametrize("T", [6, 600])
+def test_switch_status_cleared_per_call(pkg, orc, dev, T):
+    """The switch FFN's dispatch clears the workspace status itself: an
+    out-of-range expert id sets it to 1, and the next call with valid ids on
+    the same workspace reads 0 again, with T*K below (one dispatch kernel)
+    and above 1024 flat rows (the multi-kernel dispatch)."""
+    E, d, f, K = 8, 256, 128, 2
+    qs = [_qbank(pkg, orc, E, n, k, 4, dev, seed) for seed, (n, k) in
+          enumerate([(f, d), (f, d), (d, f)])]
+    sw = pkg.nn.SplitSwitchFfn(*[pkg.nn.QuantizedSwitchLinear(*q, 64, 4) for q in qs])
+    g = torch.Generator().manual_seed(T)
+    x = (torch.randn((T, d), generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    good = torch.randint(0, E, (T, K), generator=g, dtype=torch.int32).to(dev)
+    bad = good.clone()
+    bad[T // 2, 1] = E + 3
+    print(f"  switch status T={T}", flush=True)
+    sw.forward(x, bad)
+    ws = sw.last_workspace
+    assert pkg.ops.workspace_status(ws) == 1
+    want = sw.forward(x, good)
+    C, lib = pkg._capi, pkg._capi.lib()
+    y = torch.empty((T, K, d), dtype=torch.bfloat16, device=dev)
+    C.check(lib.mlxr_moe_switch_glu_experts(
+        ctypes.byref(sw.descriptor()), x.data_ptr(), T, good.data_ptr(), K, y.data_ptr(),
+        ws.data_ptr(), ws.numel(), pkg.ops._stream(x)))
+    assert pkg.ops.workspace_status(ws) == 0
+    assert torch.equal(y, want)
 
 
 def test_router_ties_pick_lower_ids(pkg, dev):
