@@ -4,7 +4,10 @@
 
 One step is one Qwen35MoeBlock forward (router -> dispatch -> grouped
 quantised expert GEMMs -> combine) over T synthetic tokens, weights and
-inputs already resident in HBM.  Prints ONE JSON line: tokens/s through the
+inputs already resident in HBM.  Steps run as replays of a captured HIP
+graph holding several forwards (--forwards-per-graph, as a decoder's step
+graph holds one block per layer); the same forward alone in its graph is
+reported beside it.  Prints ONE JSON line: tokens/s through the
 block, the dominant kernel's roofline (algorithmic bytes or FLOPs per launch
 over its average launch time, from HIP events recorded on the stream it runs
 on) and the CPU oracle timed on this host's cores on a bounded sample.
@@ -43,6 +46,11 @@ def parse():
                          "cfg:T:res times the decoder layer's MoE half (RMSNorm, block, "
                          "residual add); cfg:T:cold rotates copies of the weights so "
                          "every forward reads its experts from HBM")
+    ap.add_argument("--forwards-per-graph", type=int, default=8,
+                    help="forwards of the block one captured graph holds (warm graph "
+                         "replays; a decoder's step graph holds one block per layer, so "
+                         "the replay's own launch cost is shared); the headline uses the "
+                         "largest count up to this that divides --steps")
     ap.add_argument("--sweep-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound of the CPU-baseline sample (0 skips it)")
@@ -83,13 +91,15 @@ class Runner:
     the block, the residual add: Qwen35MoeBlock.forward_residual).
     banks: more copies of the weights in their own memory (a cold-cache
     measurement, like a decoder whose every step reads another layer's
-    experts): one step is one forward on the next bank in turn."""
+    experts): one step is one forward on the next bank in turn.
+    repeat: the forwards of one graph replay (or eager step) run the same
+    weights this many times over (with banks: the bank cycle, repeated)."""
 
-    def __init__(self, pkg, bw, T, dev, launch, residual=False, banks=()):
+    def __init__(self, pkg, bw, T, dev, launch, residual=False, banks=(), repeat=1):
         import torch
         self.torch = torch
         self.T = T
-        self.blocks = [b.block() for b in (bw, *banks)]
+        self.blocks = [b.block() for b in (bw, *banks)] * max(1, repeat)
         self.block = self.blocks[0]
         self.x = pkg.workloads.make_x(bw.cfg, T, dev, seed=T)
         self.out = torch.empty((T, bw.cfg.d), dtype=self.block.out_dtype, device=dev)
@@ -311,14 +321,29 @@ def main():
     print(f"bench: {cfg.name} T={T} on {torch.cuda.get_device_name(dev)}", file=sys.stderr,
           flush=True)
     bw = W.make_weights(cfg, dev)
-    r = Runner(pkg, bw, T, dev, args.launch)
+    # forwards per graph replay: the largest count up to the option that
+    # divides --steps, so that exactly --steps forwards are timed
+    fpg = 1
+    if args.launch == "graph":
+        fpg = max(c for c in range(1, max(1, args.forwards_per_graph) + 1)
+                  if args.steps % c == 0)
+    r = Runner(pkg, bw, T, dev, args.launch, repeat=fpg)
     U = W.distinct(r.idx)
-    sec = r.timed(args.steps, args.warmup)
+    sec = r.timed(args.steps // fpg, max(1, args.warmup // fpg))
     tok_s = T / sec
     block_bytes = W.algorithmic_bytes(cfg, T, U)
-    med = r.median(args.steps)
-    print(f"bench: {sec * 1e6:.1f} us/step (median {med * 1e6:.1f}), {tok_s:.0f} tokens/s",
-          file=sys.stderr, flush=True)
+    med = r.median(args.steps // fpg)
+    print(f"bench: {sec * 1e6:.1f} us/step (median {med * 1e6:.1f}), {tok_s:.0f} tokens/s, "
+          f"{fpg} forwards per graph", file=sys.stderr, flush=True)
+    # the same forward alone in its graph (the replay's launch cost on every
+    # forward)
+    sec1 = None
+    if fpg > 1:
+        r1 = Runner(pkg, bw, T, dev, args.launch)
+        sec1 = r1.timed(args.steps, args.warmup)
+        del r1
+        print(f"bench: one forward per graph {sec1 * 1e6:.1f} us/step", file=sys.stderr,
+              flush=True)
     # the same forward with the weights rotated over banks in their own
     # memory: no step finds its experts in the caches
     rc = Runner(pkg, bw, T, dev, args.launch, banks=cold_banks(W, bw, T, U))
@@ -359,7 +384,8 @@ def main():
         c2 = W.CONFIGS[cname]
         if c2.name not in banks:
             banks[c2.name] = W.make_weights(c2, dev)
-        r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch, residual=res)
+        fpg2 = max(1, args.forwards_per_graph) if args.launch == "graph" else 1
+        r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch, residual=res, repeat=fpg2)
         U2 = W.distinct(r2.idx)
         if cold_pt:
             r2 = Runner(pkg, banks[c2.name], tt, dev, args.launch,
@@ -376,7 +402,8 @@ def main():
                    distinct_experts=U2,
                    block_hbm_gbs=round(W.algorithmic_bytes(c2, tt, U2) / s2 / 1e9, 1),
                    block_tflops=round(W.algorithmic_flops(c2, tt) / s2 / 1e12, 2),
-                   rows_per_expert=W.rows_per_expert(r2.idx, c2.E))
+                   rows_per_expert=W.rows_per_expert(r2.idx, c2.E),
+                   forwards_per_graph=len(r2.blocks))
         if cold_pt:
             ent["banks"] = len(r2.blocks)
         sweep.append(ent)
@@ -418,9 +445,13 @@ def main():
         "config": {"workload": f"{cfg.name} T={T}", "tokens": T, "d": cfg.d, "E": cfg.E,
                    "K": cfg.K, "f": cfg.f, "bits": cfg.bits, "group_size": cfg.group_size,
                    "distinct_experts": U, "launch": args.launch,
+                   "forwards_per_graph": fpg,
                    "block_algorithmic_bytes": block_bytes,
                    "block_hbm_gbs": round(block_bytes / sec / 1e9, 1),
                    "rows_per_expert": W.rows_per_expert(r.idx, cfg.E)},
+        "one_forward_per_graph": (None if sec1 is None else
+                                  {"us_per_step": round(sec1 * 1e6, 2),
+                                   "tokens_per_s": round(T / sec1, 1)}),
         "cold": cold,
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -55,6 +55,31 @@ namespace {
 #ifndef MLXR_STREAM_DEPTH8
 #define MLXR_STREAM_DEPTH8 1
 #endif
+// ... of the 8-token form (half the bytes per super-step: twice the depth)
+#ifndef MLXR_STREAM_DEPTH4_TT8
+#define MLXR_STREAM_DEPTH4_TT8 (2 * MLXR_STREAM_DEPTH4)
+#endif
+#ifndef MLXR_STREAM_DEPTH8_TT8
+#define MLXR_STREAM_DEPTH8_TT8 (2 * MLXR_STREAM_DEPTH8)
+#endif
+// ... and of the gated kernels (gate and up: two rows of loads per step).
+// The 4-bit gated 8-token form keeps three super-steps in flight: a ring
+// of four slots divides its 16 super-steps at K = 2048 (with three slots two
+// zero steps follow the last one).  Measured (event means, c2 T=8/32/64,
+// c4 T=64, c6 T=64): gate/up 0.3-1% faster; depth 3 for the 4-token form
+// was 2-12% slower.
+#ifndef MLXR_STREAM_DEPTH4G
+#define MLXR_STREAM_DEPTH4G MLXR_STREAM_DEPTH4
+#endif
+#ifndef MLXR_STREAM_DEPTH4G_TT8
+#define MLXR_STREAM_DEPTH4G_TT8 3
+#endif
+#ifndef MLXR_STREAM_DEPTH8G
+#define MLXR_STREAM_DEPTH8G MLXR_STREAM_DEPTH8
+#endif
+#ifndef MLXR_STREAM_DEPTH8G_TT8
+#define MLXR_STREAM_DEPTH8G_TT8 (2 * MLXR_STREAM_DEPTH8G)
+#endif
 #ifndef MLXR_SCHED_BARRIER
 #define MLXR_SCHED_BARRIER() __builtin_amdgcn_sched_barrier(0)
 #endif
@@ -815,20 +840,10 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   }
 }
 
-// Ring depth of the 8-token form (half the bytes per super-step of the
-// 4-token form): twice the 4-token depth unless set.
-#ifdef MLXR_STREAM_DEPTH_TT8
-template <int D>
-constexpr int kTT8Depth = MLXR_STREAM_DEPTH_TT8;
-#else
-template <int D>
-constexpr int kTT8Depth = 2 * D;
-#endif
-
 // Tokens per pass follow the expert's row count: 4 (GG = 4) for experts
 // with at most kStreamTT4Rows rows, else 8 (GG = 2).  LDS is sized
 // for 8.
-template <int BITS, bool GATED, int D, int NB, int KS>
+template <int BITS, bool GATED, int D, int D8, int NB, int KS>
 __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
     QGemmArgs a, int tiles_n, QGemmArgs a2, int units1, int items1, int rows2) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -837,13 +852,12 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
   const QGemmArgs& A = u.shared ? a2 : a;
   // The MFMA form follows the expert's row count (not the item's), so every
   // token of an expert is summed in the same order, wherever its item
-  // boundaries fall.  The 8-token form moves half the bytes per super-step:
-  // twice the depth.
+  // boundaries fall.  Ring depths: D super-steps of the 4-token form in
+  // flight, D8 of the 8-token form (half the bytes per super-step).
   if (u.wk.w <= kStreamTT4Rows)
     stream_body<BITS, GATED, 4, D, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1, u.tile, smem);
   else
-    stream_body<BITS, GATED, 8, kTT8Depth<D>, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1,
-                                                      u.tile, smem);
+    stream_body<BITS, GATED, 8, D8, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1, u.tile, smem);
 }
 
 }  // namespace
@@ -923,50 +937,50 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
     const size_t lds = base_lds + (ks > 1 ? red_lds : 0);
     const int rows2 = (int)shared_rows;
     ProfileScope prof(profile, s);
-#define MLXR_QS(B, G, D, NB)                                              \
+#define MLXR_QS(B, G, D, D8, NB)                                          \
   do {                                                                    \
     if (ks == 4)                                                          \
-      qgemm_stream_kernel<B, G, D, 1, 4>                                  \
+      qgemm_stream_kernel<B, G, D, D8, 1, 4>                              \
           <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, items1, rows2);  \
     else if (ks == 2)                                                     \
-      qgemm_stream_kernel<B, G, D, 1, 2>                                  \
+      qgemm_stream_kernel<B, G, D, D8, 1, 2>                              \
           <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, items1, rows2);  \
     else                                                                  \
-      qgemm_stream_kernel<B, G, D, NB, 1>                                 \
+      qgemm_stream_kernel<B, G, D, D8, NB, 1>                             \
           <<<grid, 64 * kWaves, lds, s>>>(a, tiles_n, b, units1, items1, rows2);  \
   } while (0)
     if (a.bits == 4) {
 #if MLXR_STREAM_GATED_NB > 1
       if (a.gated && nb == 2)
-        MLXR_QS(4, true, MLXR_STREAM_DEPTH4, 2);
+        MLXR_QS(4, true, MLXR_STREAM_DEPTH4G, MLXR_STREAM_DEPTH4G_TT8, 2);
       else
 #endif
       if (a.gated)
-        MLXR_QS(4, true, MLXR_STREAM_DEPTH4, 1);
+        MLXR_QS(4, true, MLXR_STREAM_DEPTH4G, MLXR_STREAM_DEPTH4G_TT8, 1);
 #if MLXR_STREAM_MAX_NB >= 4
       else if (nb == 4)
-        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 4);
+        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, MLXR_STREAM_DEPTH4_TT8, 4);
 #endif
       else if (nb == 2)
-        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 2);
+        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, MLXR_STREAM_DEPTH4_TT8, 2);
       else
-        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, 1);
+        MLXR_QS(4, false, MLXR_STREAM_DEPTH4, MLXR_STREAM_DEPTH4_TT8, 1);
     } else {
 #if MLXR_STREAM_GATED_NB > 1
       if (a.gated && nb == 2)
-        MLXR_QS(8, true, MLXR_STREAM_DEPTH8, 2);
+        MLXR_QS(8, true, MLXR_STREAM_DEPTH8G, MLXR_STREAM_DEPTH8G_TT8, 2);
       else
 #endif
       if (a.gated)
-        MLXR_QS(8, true, MLXR_STREAM_DEPTH8, 1);
+        MLXR_QS(8, true, MLXR_STREAM_DEPTH8G, MLXR_STREAM_DEPTH8G_TT8, 1);
 #if MLXR_STREAM_MAX_NB >= 4
       else if (nb == 4)
-        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, 4);
+        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, MLXR_STREAM_DEPTH8_TT8, 4);
 #endif
       else if (nb == 2)
-        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, 2);
+        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, MLXR_STREAM_DEPTH8_TT8, 2);
       else
-        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, 1);
+        MLXR_QS(8, false, MLXR_STREAM_DEPTH8, MLXR_STREAM_DEPTH8_TT8, 1);
     }
 #undef MLXR_QS
     return hipGetLastError();
