@@ -68,14 +68,9 @@ __global__ __launch_bounds__(256) void combine_kernel(
       const uint32_t pk[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float lo = __fmul_rn(wk[i], __uint_as_float(pk[j] << 16));
-        float hi = __fmul_rn(wk[i], __uint_as_float(pk[j] & 0xffff0000u));
-        if (BF16) {
-          lo = bf16_round(lo);
-          hi = bf16_round(hi);
-        }
-        acc[2 * j] = __fadd_rn(acc[2 * j], lo);
-        acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], hi);
+        acc[2 * j] = combine_add<BF16>(acc[2 * j], wk[i], __uint_as_float(pk[j] << 16));
+        acc[2 * j + 1] =
+            combine_add<BF16>(acc[2 * j + 1], wk[i], __uint_as_float(pk[j] & 0xffff0000u));
       }
     }
   }
@@ -84,30 +79,21 @@ __global__ __launch_bounds__(256) void combine_kernel(
     for (int j = 0; j < 8; ++j) acc[j] = bf16_round(acc[j]);
   }
   if (shared_y) {
-    float gate = 1.0f / (1.0f + expf(-slog));
-    if (BF16) gate = bf16_round(gate);
+    const float gate = combine_gate<BF16>(slog);
     const uint32_t pk[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float lo = __fmul_rn(__uint_as_float(pk[j] << 16), gate);
-      float hi = __fmul_rn(__uint_as_float(pk[j] & 0xffff0000u), gate);
-      if (BF16) {
-        lo = bf16_round(lo);
-        hi = bf16_round(hi);
-      }
-      acc[2 * j] = __fadd_rn(lo, acc[2 * j]);
-      acc[2 * j + 1] = __fadd_rn(hi, acc[2 * j + 1]);
+      acc[2 * j] = combine_shared<BF16>(acc[2 * j], __uint_as_float(pk[j] << 16), gate);
+      acc[2 * j + 1] =
+          combine_shared<BF16>(acc[2 * j + 1], __uint_as_float(pk[j] & 0xffff0000u), gate);
     }
   }
   if (residual) {
     const uint32_t pk[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      // h + mlp_out, with mlp_out in its own dtype first
-      const float m0 = BF16 ? bf16_round(acc[2 * j]) : acc[2 * j];
-      const float m1 = BF16 ? bf16_round(acc[2 * j + 1]) : acc[2 * j + 1];
-      acc[2 * j] = __fadd_rn(__uint_as_float(pk[j] << 16), m0);
-      acc[2 * j + 1] = __fadd_rn(__uint_as_float(pk[j] & 0xffff0000u), m1);
+      acc[2 * j] = combine_residual<BF16>(acc[2 * j], __uint_as_float(pk[j] << 16));
+      acc[2 * j + 1] = combine_residual<BF16>(acc[2 * j + 1], __uint_as_float(pk[j] & 0xffff0000u));
     }
   }
   if (BF16) {

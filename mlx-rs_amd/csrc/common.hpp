@@ -74,6 +74,39 @@ __device__ __forceinline__ uint16_t gated_act_bf16(int act, float g, float u) {
   return act == 1 ? geglu_bf16(g, u) : swiglu_bf16(g, u);
 }
 
+// The combine's arithmetic for one output element
+// (combine_with_weights, crates/mlxr-lm/src/nn/switch.rs:223-234: w * y
+// promoted to f32, summed over k in order; the block's shared branch,
+// qwen3_5/text/moe.rs:117-120,145; the decoder layer's residual add,
+// layer.rs:138).  BF16: the quantised router's bf16 chain, every op rounded
+// to bf16.  A sum is combine_add over k = 0..K-1 from 0, bf16-rounded (BF16),
+// then combine_shared, then combine_residual.  Every kernel that combines
+// uses these, so they agree bit for bit.
+template <bool BF16>
+__device__ __forceinline__ float combine_add(float acc, float w, float y) {
+  float p = __fmul_rn(w, y);
+  if (BF16) p = bf16_round(p);
+  return __fadd_rn(acc, p);
+}
+template <bool BF16>
+__device__ __forceinline__ float combine_gate(float logit) {
+  float g = 1.0f / (1.0f + expf(-logit));
+  if (BF16) g = bf16_round(g);
+  return g;
+}
+template <bool BF16>
+__device__ __forceinline__ float combine_shared(float acc, float sy, float gate) {
+  float p = __fmul_rn(sy, gate);
+  if (BF16) p = bf16_round(p);
+  return __fadd_rn(p, acc);
+}
+template <bool BF16>
+__device__ __forceinline__ float combine_residual(float acc, float h) {
+  // h + mlp_out, with mlp_out in its own dtype first
+  const float m = BF16 ? bf16_round(acc) : acc;
+  return __fadd_rn(h, m);
+}
+
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
   // v += v[l ^ m] for m = 32, 16, 8, 4, 2, 1: every lane ends with the
   // same bits, and the CPU restatement reproduces the association.

@@ -238,6 +238,34 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
                         const QGemmArgs* shared = nullptr,
                         int64_t shared_rows = 0);
 
+// The combine of a single token folded into its down GEMM
+// (launch_qgemm_down_combine): the routing weights [K] (f32, or bf16 with
+// w_bf16), the shared expert's row [d] when it ran apart (a folded one
+// comes from the same launch), its gate logit (null: no shared branch), the
+// residual row [d] or null, and the output row [d] (bf16 when bf16, else
+// f32) -- the arguments of launch_combine at T = 1.
+struct DownCombine {
+  const void* w;
+  bool w_bf16;
+  const uint16_t* shared_y;
+  const float* shared_logit;
+  const uint16_t* residual;
+  void* out;
+  bool bf16;
+};
+
+// The down GEMM of ONE token (K routed rows, and the folded shared
+// expert's row when `shared` is given) with the combine in the same launch:
+// one workgroup per 16 output channels runs every row's item (the streaming
+// kernel's per-item work, the same K-slices, so each y value is the one the
+// separate down launch writes), keeps the bf16 rows in LDS and sums them in
+// k order.  Sets *done = false, launching nothing, where the streaming
+// kernel would not run the down launch or the rows do not fit one
+// workgroup; the caller then launches the down GEMM and the combine.
+hipError_t launch_qgemm_down_combine(const QGemmArgs& a, int64_t K, int64_t max_items,
+                                     const QGemmArgs* shared, const DownCombine& c,
+                                     hipStream_t s, bool* done);
+
 // ---------------------------------------------------------------- prefill.hip
 // x_rows bounds the rows of x the GEMM reads; tile_rows is the M-tile height
 // the dispatch used (prefill_tile_rows); max_tiles bounds the M-tile list

@@ -5,6 +5,12 @@
 
 #include <algorithm>
 
+// The single-token combine in the down launch (0: always the separate
+// combine launch)
+#ifndef MLXR_DOWN_COMBINE
+#define MLXR_DOWN_COMBINE 1
+#endif
+
 namespace mlxr_moe {
 
 Status from_hip(hipError_t e, const char* where) {
@@ -295,7 +301,9 @@ bool SwitchFfn::can_fold(const SwigluMlp& m, int64_t T, int64_t K) const {
 
 Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
                           const DispatchBuffers& db, uint16_t* y, Carve& ws,
-                          hipStream_t s, const SharedFold* fold) const {
+                          hipStream_t s, const SharedFold* fold,
+                          const DownCombine* dc, bool* combined) const {
+  if (combined) *combined = false;
   const int64_t d = sw_.d, f = sw_.f, E = sw_.E;
   const int64_t n = T * K;
   uint16_t* act = ws.take<uint16_t>(n * f);
@@ -366,6 +374,16 @@ Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
     h2.E = 1;
     h2.out = fold->y;
     h2.out_by_flat = false;
+  }
+  if (MLXR_DOWN_COMBINE && dc && T == 1 && !prefill) {
+    bool done = false;
+    st = from_hip(launch_qgemm_down_combine(h, K, max_items, fold ? &h2 : nullptr, *dc, s,
+                                            &done),
+                  "switch_mlp down + combine");
+    if (!st.ok || done) {
+      if (combined) *combined = done;
+      return st;
+    }
   }
   return from_hip(launch_qgemm(h, n, max_items, prefill, s, nullptr,
                                fold ? &h2 : nullptr, fold ? T : 0),
@@ -510,8 +528,12 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
   }
   SharedFold sf{};
   if (fold) sf = smlp.fold(shared_ws, T, sy);
-  st = mlp.experts(x, T, K, db, y, ws, s, fold ? &sf : nullptr);
-  if (!st.ok) return st;
+  // one token: the combine rides in the down launch where it can
+  const DownCombine dc{wts, false, sy, shared ? logits + E : nullptr, residual, out, bf16};
+  bool combined = false;
+  st = mlp.experts(x, T, K, db, y, ws, s, fold ? &sf : nullptr, T == 1 ? &dc : nullptr,
+                   &combined);
+  if (!st.ok || combined) return st;
   return from_hip(launch_combine(y, wts, false, T, K, d, sy,
                                  shared ? logits + E : nullptr, ld, residual,
                                  out, bf16, s),

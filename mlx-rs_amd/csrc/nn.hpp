@@ -119,10 +119,14 @@ class SwitchFfn {
                  int64_t K, uint16_t* y, Carve& ws, int32_t* status,
                  hipStream_t s) const;
   // The expert products given a dispatch of the T*K flat ids; with `fold`,
-  // the shared expert's products in the same launches.
+  // the shared expert's products in the same launches.  With `dc` at T = 1
+  // the combine runs in the down launch where it can
+  // (launch_qgemm_down_combine): *combined says whether it did (y is then
+  // not written).
   Status experts(const uint16_t* x, int64_t T, int64_t K,
                  const DispatchBuffers& db, uint16_t* y, Carve& ws,
-                 hipStream_t s, const SharedFold* fold = nullptr) const;
+                 hipStream_t s, const SharedFold* fold = nullptr,
+                 const DownCombine* dc = nullptr, bool* combined = nullptr) const;
   // Whether a SwiGLU shared expert can fold into this FFN's launches at T
   // tokens: same bits and hidden size, and both on the streaming decode
   // kernel or both on the M-tiled one.

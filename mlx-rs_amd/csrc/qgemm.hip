@@ -515,7 +515,8 @@ template <int BITS, bool GATED, int TT, int D, int NB, int KS>
 __device__ __forceinline__ void stream_body(const QGemmArgs& a,
                                             const int32_t* rec, int4 wk,
                                             int4 fr0, int4 fr1, int tile,
-                                            char* smem) {
+                                            char* smem, int ltid, int lthreads,
+                                            uint16_t* yl, int yrow_off) {
   constexpr int nb = NB;
   static_assert(kWorkRows <= 8, "an item of a >4-row expert fits TT = 8");
   constexpr int NM = GATED ? 2 : 1;
@@ -528,11 +529,11 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   constexpr int WPG = 2 * BITS;         // packed words per row and group
   // KS waves share each set of blocks, one K-slice each (KS > 1 for small
   // grids: more, shorter waves); their sums meet in LDS at the end
-  const int waves = (blockDim.x >> 6) / KS;  // channel waves
+  const int waves = (lthreads >> 6) / KS;  // channel waves
   // items of experts with at most 4 rows run with TT = 4, the others with
   // TT = 8 >= kWorkRows: an item is always one pass
   const int e = wk.x, row0 = wk.y, nt = min(wk.z, TT);
-  const int lane = threadIdx.x & 63, wave_id = threadIdx.x >> 6;
+  const int lane = ltid & 63, wave_id = ltid >> 6;
   const int wave = wave_id / KS, kq = wave_id % KS;  // channel wave, K-slice
   const int n = lane & 15, q = lane >> 4;
   const int gq = q / LPG, sq = q % LPG;  // this lane's group, its part
@@ -638,7 +639,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
       *reinterpret_cast<u32x4_t*>(xl + (size_t)t * xs + 8 * k8) = w;
     }
   };
-  const int k8 = threadIdx.x;
+  const int k8 = ltid;
   const bool x_in = k8 < per_row;
   u32x4_t xv[TT];
   load_x(min(k8, per_row - 1), xv);
@@ -674,12 +675,12 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
 
   if (x_in) stage_x(k8, xv);  // per_row is a multiple of 8: whole octets
   // the rest of x (input dims above 64 * 8 * waves)
-  for (int c8 = k8 + blockDim.x; c8 < per_row; c8 += blockDim.x) {
+  for (int c8 = k8 + lthreads; c8 < per_row; c8 += lthreads) {
     u32x4_t v[TT];
     load_x(c8, v);
     stage_x(c8, v);
   }
-  if (threadIdx.x == 0) *reinterpret_cast<u32x4_t*>(zero_blk) = zq;
+  if (ltid == 0) *reinterpret_cast<u32x4_t*>(zero_blk) = zq;
   __syncthreads();
   // the scales (issued before the weights) -> this wave's region; only
   // this wave reads it
@@ -787,7 +788,7 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
   // meet in LDS (after the x region is no longer read) and the slice-0
   // wave adds them in slice order.
   f32x4_t* red = reinterpret_cast<f32x4_t*>(
-      sb_base + (((size_t)(blockDim.x >> 6) * NA * nb * 16 * groups * 2 + 15) & ~size_t(15)));
+      sb_base + (((size_t)(lthreads >> 6) * NA * nb * 16 * groups * 2 + 15) & ~size_t(15)));
   if constexpr (KS > 1) {
 #pragma unroll
     for (int bi = 0; bi < NB; ++bi)
@@ -832,7 +833,10 @@ __device__ __forceinline__ void stream_body(const QGemmArgs& a,
                 gated_act_bf16(a.act, bf16_round(tot[0][r]), bf16_round(tot[1][r]));
           } else {
             const int64_t orow = a.out_by_flat ? rec[4 + t] : slot;
-            a.out[orow * a.out_ld + ch] = f32_to_bf16(tot[0][r]);
+            if (yl)  // the single-token down + combine: rows stay in LDS
+              yl[(orow + yrow_off) * 16 + n] = f32_to_bf16(tot[0][r]);
+            else
+              a.out[orow * a.out_ld + ch] = f32_to_bf16(tot[0][r]);
           }
         }
       }
@@ -855,9 +859,175 @@ __global__ __launch_bounds__(64 * MLXR_STREAM_WAVES) void qgemm_stream_kernel(
   // boundaries fall.  Ring depths: D super-steps of the 4-token form in
   // flight, D8 of the 8-token form (half the bytes per super-step).
   if (u.wk.w <= kStreamTT4Rows)
-    stream_body<BITS, GATED, 4, D, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1, u.tile, smem);
+    stream_body<BITS, GATED, 4, D, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1, u.tile, smem,
+                                           threadIdx.x, blockDim.x, nullptr, 0);
   else
-    stream_body<BITS, GATED, 8, D8, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1, u.tile, smem);
+    stream_body<BITS, GATED, 8, D8, NB, KS>(A, u.rec, u.wk, u.fr0, u.fr1, u.tile, smem,
+                                            threadIdx.x, blockDim.x, nullptr, 0);
+}
+
+// q ? b : c, field by field: every field a scalar select, so the chosen
+// set stays in registers (selecting the whole struct by reference or value
+// copies both argument sets to private memory)
+__device__ __forceinline__ QWeights pick_w(bool q, const QWeights& b, const QWeights& c) {
+  return QWeights{q ? b.w : c.w, q ? b.scales : c.scales, q ? b.biases : c.biases};
+}
+__device__ __forceinline__ QGemmArgs pick_args(bool q, const QGemmArgs& b, const QGemmArgs& c) {
+  QGemmArgs r;
+  r.x = q ? b.x : c.x;
+  r.x_ld = q ? b.x_ld : c.x_ld;
+  r.x_rows = q ? b.x_rows : c.x_rows;
+  r.row_map = q ? b.row_map : c.row_map;
+  r.row_div = q ? b.row_div : c.row_div;
+  r.x_by_slot = q ? b.x_by_slot : c.x_by_slot;
+  r.offsets = q ? b.offsets : c.offsets;
+  r.active = q ? b.active : c.active;
+  r.num_active = q ? b.num_active : c.num_active;
+  r.work = q ? b.work : c.work;
+  r.num_work = q ? b.num_work : c.num_work;
+  r.tiles = q ? b.tiles : c.tiles;
+  r.num_tiles = q ? b.num_tiles : c.num_tiles;
+  r.sorted = q ? b.sorted : c.sorted;
+  r.w0 = pick_w(q, b.w0, c.w0);
+  r.w1 = pick_w(q, b.w1, c.w1);
+  r.E = q ? b.E : c.E;
+  r.N = q ? b.N : c.N;
+  r.K = q ? b.K : c.K;
+  r.bits = q ? b.bits : c.bits;
+  r.e_rows = q ? b.e_rows : c.e_rows;
+  r.act = q ? b.act : c.act;
+  r.out = q ? b.out : c.out;
+  r.out_ld = q ? b.out_ld : c.out_ld;
+  r.out_by_flat = q ? b.out_by_flat : c.out_by_flat;
+  r.gated = q ? b.gated : c.gated;
+  return r;
+}
+
+// The down GEMM of one token and its combine (launch_qgemm_down_combine).
+// Workgroup = 16 output channels (blockIdx.x); its waves come in groups of
+// KS, one group per row: the K routed rows (work items 0..K-1 of the
+// dispatch, one row each) and, from K on, the folded shared expert's row.
+// Each group runs the streaming kernel's item work (the 4-token MFMA form,
+// KS K-slices) in its own LDS region and leaves its bf16 row values in LDS
+// (row k at its flat row k, the shared row at K); after a barrier 16
+// threads sum them in k order with the combine's arithmetic.
+template <int BITS, int KS, bool BF16, typename WT>
+__global__ __launch_bounds__(1024) void qgemm_down_combine_kernel(
+    QGemmArgs a, QGemmArgs a2, int K, int nsub, int sub_lds, DownCombine c) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int L = 64 * KS;
+  constexpr int D = BITS == 4 ? MLXR_STREAM_DEPTH4 : MLXR_STREAM_DEPTH8;
+  // (the group is uniform over a wave: said so, the choice of argument
+  // set stays in scalar registers)
+  const int sub = __builtin_amdgcn_readfirstlane((int)threadIdx.x / L);
+  const int ltid = threadIdx.x - sub * L;
+  const bool sh = sub >= K;
+  uint16_t* yl = reinterpret_cast<uint16_t*>(smem + (size_t)nsub * sub_lds);
+  // rows no item writes read as zeros (the groups' first barrier publishes
+  // these stores)
+  if ((int)threadIdx.x < nsub * 2)
+    reinterpret_cast<u32x4_t*>(yl)[threadIdx.x] = u32x4_t{0u, 0u, 0u, 0u};
+  const int32_t* rec = a.work + (int64_t)kWorkInts * (sh ? 0 : sub);
+  int4 wk = *reinterpret_cast<const int4*>(rec);
+  int4 fr0 = *reinterpret_cast<const int4*>(rec + 4);
+  int4 fr1 = *reinterpret_cast<const int4*>(rec + 8);
+  if (sh) {
+    // the shared expert's one row: slot 0, no dispatch
+    wk = make_int4(0, 0, 1, 1);
+    fr0 = make_int4(0, 1, 2, 3);
+    fr1 = make_int4(4, 5, 6, 7);
+  } else if (sub >= *a.num_work) {
+    wk = make_int4(0, 0, 0, 0);  // no such item: no rows (expert 0's loads)
+  }
+  const QGemmArgs A = pick_args(sh, a2, a);
+  stream_body<BITS, false, 4, D, 1, KS>(A, rec, wk, fr0, fr1, (int)blockIdx.x,
+                                        smem + (size_t)sub * sub_lds, ltid, L, yl,
+                                        sh ? K : 0);
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int n = threadIdx.x, ch = (int)blockIdx.x * 16 + n;
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k) {
+      float w;
+      if constexpr (sizeof(WT) == 2)
+        w = bf16_to_f32(static_cast<const uint16_t*>(c.w)[k]);
+      else
+        w = static_cast<const float*>(c.w)[k];
+      acc = combine_add<BF16>(acc, w, bf16_to_f32(yl[k * 16 + n]));
+    }
+    if (BF16) acc = bf16_round(acc);
+    if (c.shared_logit) {
+      const float sy = bf16_to_f32(nsub > K ? yl[K * 16 + n] : c.shared_y[ch]);
+      acc = combine_shared<BF16>(acc, sy, combine_gate<BF16>(c.shared_logit[0]));
+    }
+    if (c.residual) acc = combine_residual<BF16>(acc, bf16_to_f32(c.residual[ch]));
+    if (BF16)
+      static_cast<uint16_t*>(c.out)[ch] = f32_to_bf16(acc);
+    else
+      static_cast<float*>(c.out)[ch] = acc;
+  }
+}
+
+}  // namespace
+
+namespace {
+
+// Whether the streaming kernel runs a decode launch of `all_items` work
+// items (routed and folded): quantised weights, enough (item, block) units,
+// whole 64-channel tiles, groups in fours, 16-byte aligned scales and biases.
+bool stream_eligible(const QGemmArgs& a, const QGemmArgs& b, int64_t all_items) {
+  const auto a16 = [](const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+  };
+  const bool sb16 = a16(a.w0.scales) && a16(a.w0.biases) &&
+                    (!a.gated || (a16(a.w1.scales) && a16(a.w1.biases))) &&
+                    a16(b.w0.scales) && a16(b.w0.biases) &&
+                    (!b.gated || (a16(b.w1.scales) && a16(b.w1.biases)));
+  const int groups = a.K / 64;
+  return a.bits != 16 && all_items * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0 &&
+         groups % 4 == 0 && sb16;
+}
+
+// Launch shape of the streaming kernel: 16-channel blocks per wave (nb),
+// K-slices (ks), channel tiles per item and the LDS of one workgroup.
+struct StreamShape {
+  int nb, ks, tiles_n;
+  size_t lds;
+};
+StreamShape stream_shape(const QGemmArgs& a, int64_t all_items) {
+  constexpr int kWaves = MLXR_STREAM_WAVES, kMaxTT = 8;
+  const int groups = a.K / 64;
+  // blocks per wave: about one workgroup per slot (two per CU), so x is
+  // staged as few times as the GPU allows
+  const int64_t per_tile = a.N / (16 * kWaves);
+  int nb = 1;
+  for (int c = a.gated ? MLXR_STREAM_GATED_NB : MLXR_STREAM_MAX_NB; c > 1; c >>= 1)
+    if (per_tile % c == 0 &&
+        all_items * (per_tile / c) >= kStreamSlots * (c >= 4 ? MLXR_STREAM_NB4_GRIDS : 1)) {
+      nb = c;
+      break;
+    }
+  // K-slices: a small grid (few items, one block per wave) splits each
+  // block's input dim over ks waves of a workgroup, so more and shorter
+  // waves run at once (the super-steps of either MFMA form divide
+  // evenly), as long as the grid stays within one workgroup per slot
+  // (two per CU, or one where the LDS allows only one)
+  const size_t sb_lds = (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
+  const size_t base_lds =
+      (((size_t)kMaxTT * (a.K + 8) * 2 + 16 + (size_t)groups * kMaxTT * 4 + 15) &
+       ~size_t(15)) + ((sb_lds + 15) & ~size_t(15));
+  const size_t red_lds = (size_t)kWaves * (a.gated ? 2 : 1) * 64 * 16;
+  const int64_t slots = (kStreamSlots / 2) * (base_lds + red_lds <= 80 * 1024 ? 2 : 1);
+  int ks = 1;
+  if (nb == 1)
+    for (int c = std::min(4, kWaves); c > 1; c >>= 1)
+      if ((groups / 4) % c == 0 &&
+          all_items * (a.N / (16 * (kWaves / c))) <= std::min<int64_t>(slots, MLXR_STREAM_KS_GRID)) {
+        ks = c;
+        break;
+      }
+  const int tiles_n = (int)(a.N / (16 * (kWaves / ks)) / nb);
+  return StreamShape{nb, ks, tiles_n, base_lds + (ks > 1 ? red_lds : 0)};
 }
 
 }  // namespace
@@ -889,52 +1059,16 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
   // Many (expert, block) items: the streaming kernel (one block per wave,
   // x in LDS, a ring of weight loads).  Few: the split-K kernel below, which
   // spreads each block over up to 16 waves.
-  const auto a16 = [](const void* p) {
-    return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
-  };
-  const bool sb16 = a16(a.w0.scales) && a16(a.w0.biases) &&
-                    (!a.gated || (a16(a.w1.scales) && a16(a.w1.biases))) &&
-                    a16(b.w0.scales) && a16(b.w0.biases) &&
-                    (!b.gated || (a16(b.w1.scales) && a16(b.w1.biases)));
   const int64_t all_items = max_items + items2;
   // (dense bf16 weights, bits 16, take the split-K kernel below)
-  if (a.bits != 16 && all_items * (a.N / 16) >= kStreamMinBlocks && a.N % 64 == 0 &&
-      groups % 4 == 0 && sb16) {
-    constexpr int kWaves = MLXR_STREAM_WAVES, kMaxTT = 8;
-    // blocks per wave: about one workgroup per slot (two per CU), so x is
-    // staged as few times as the GPU allows
-    const int64_t per_tile = a.N / (16 * kWaves);
-    int nb = 1;
-    for (int c = a.gated ? MLXR_STREAM_GATED_NB : MLXR_STREAM_MAX_NB; c > 1; c >>= 1)
-      if (per_tile % c == 0 &&
-          all_items * (per_tile / c) >= kStreamSlots * (c >= 4 ? MLXR_STREAM_NB4_GRIDS : 1)) {
-        nb = c;
-        break;
-      }
-    // K-slices: a small grid (few items, one block per wave) splits each
-    // block's input dim over ks waves of a workgroup, so more and shorter
-    // waves run at once (the super-steps of either MFMA form divide
-    // evenly), as long as the grid stays within one workgroup per slot
-    // (two per CU, or one where the LDS allows only one)
-    const size_t sb_lds = (size_t)kWaves * (a.gated ? 2 : 1) * 2 * nb * 16 * groups * 2;
-    const size_t base_lds =
-        (((size_t)kMaxTT * (a.K + 8) * 2 + 16 + (size_t)groups * kMaxTT * 4 + 15) &
-         ~size_t(15)) + ((sb_lds + 15) & ~size_t(15));
-    const size_t red_lds = (size_t)kWaves * (a.gated ? 2 : 1) * 64 * 16;
-    const int64_t slots = (kStreamSlots / 2) * (base_lds + red_lds <= 80 * 1024 ? 2 : 1);
-    int ks = 1;
-    if (nb == 1)
-      for (int c = std::min(4, kWaves); c > 1; c >>= 1)
-        if ((groups / 4) % c == 0 &&
-            all_items * (a.N / (16 * (kWaves / c))) <= std::min<int64_t>(slots, MLXR_STREAM_KS_GRID)) {
-          ks = c;
-          break;
-        }
-    const int tiles_n = (int)(a.N / (16 * (kWaves / ks)) / nb);
+  if (stream_eligible(a, b, all_items)) {
+    constexpr int kWaves = MLXR_STREAM_WAVES;
+    const StreamShape sh = stream_shape(a, all_items);
+    const int nb = sh.nb, ks = sh.ks, tiles_n = sh.tiles_n;
+    const size_t lds = sh.lds;
     const int items1 = (int)max_items;
     const int units1 = (int)(max_items * tiles_n);
     const dim3 grid((unsigned)(units1 + items2 * tiles_n));
-    const size_t lds = base_lds + (ks > 1 ? red_lds : 0);
     const int rows2 = (int)shared_rows;
     ProfileScope prof(profile, s);
 #define MLXR_QS(B, G, D, D8, NB)                                          \
@@ -1039,6 +1173,61 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
       MLXR_QG(8, false, 2);
   }
 #undef MLXR_QG
+  return hipGetLastError();
+}
+
+hipError_t launch_qgemm_down_combine(const QGemmArgs& a, int64_t K, int64_t max_items,
+                                     const QGemmArgs* shared, const DownCombine& c,
+                                     hipStream_t s, bool* done) {
+  *done = false;
+  const QGemmArgs& b = shared ? *shared : a;
+  if (a.gated || (a.bits != 4 && a.bits != 8) || K < 1 ||
+      (shared && (shared->N != a.N || shared->K != a.K || shared->bits != a.bits ||
+                  shared->gated)) ||
+      (c.w_bf16 && !c.bf16) || (shared && !c.shared_logit))
+    return hipSuccess;
+  const int64_t items2 = shared ? 1 : 0;
+  const int64_t all_items = max_items + items2;
+  // (the group of row k reads work record k: the list holds K records)
+  if (max_items < K || !stream_eligible(a, b, all_items)) return hipSuccess;
+  // the separate down launch's K-slices, so every y value is the same
+  const int ks = stream_shape(a, all_items).ks;
+  const int nsub = (int)K + (int)items2;
+  if (ks > 2 || nsub * ks > 16) return hipSuccess;
+  const int groups = a.K / 64;
+  const size_t sub_lds =
+      (((size_t)4 * (a.K + 8) * 2 + 16 + (size_t)groups * 4 * 4 + 15) & ~size_t(15)) +
+      (((size_t)ks * 2 * 16 * groups * 2 + 15) & ~size_t(15)) +
+      (ks > 1 ? (size_t)ks * 64 * 16 : 0);
+  const size_t lds = (size_t)nsub * sub_lds + (size_t)nsub * 32;
+  if (lds > 160 * 1024) return hipSuccess;
+  const dim3 grid((unsigned)(a.N / 16)), block((unsigned)(64 * ks * nsub));
+  ProfileScope prof("qgemm_down", s);
+#define MLXR_DC(B, KS_)                                                                   \
+  do {                                                                                    \
+    if (c.w_bf16)                                                                         \
+      qgemm_down_combine_kernel<B, KS_, true, uint16_t>                                   \
+          <<<grid, block, lds, s>>>(a, b, (int)K, nsub, (int)sub_lds, c);                 \
+    else if (c.bf16)                                                                      \
+      qgemm_down_combine_kernel<B, KS_, true, float>                                      \
+          <<<grid, block, lds, s>>>(a, b, (int)K, nsub, (int)sub_lds, c);                 \
+    else                                                                                  \
+      qgemm_down_combine_kernel<B, KS_, false, float>                                     \
+          <<<grid, block, lds, s>>>(a, b, (int)K, nsub, (int)sub_lds, c);                 \
+  } while (0)
+  if (a.bits == 4) {
+    if (ks == 2)
+      MLXR_DC(4, 2);
+    else
+      MLXR_DC(4, 1);
+  } else {
+    if (ks == 2)
+      MLXR_DC(8, 2);
+    else
+      MLXR_DC(8, 1);
+  }
+#undef MLXR_DC
+  *done = true;
   return hipGetLastError();
 }
 

@@ -319,6 +319,20 @@ def test_block_token_permutation_equivariance(pkg, dev):
     assert torch.equal(c, a[perm])
 
 
+@pytest.mark.parametrize("cfg", ["c2", "c5"])
+def test_single_token_combine_in_down_launch(pkg, dev, cfg):
+    """At T = 1 the block sums the routed rows inside its down launch; the
+    output equals, bit for bit, the separate down GEMM and combine launches
+    of the same routing (SplitSwitchFfn.forward_with_combine)."""
+    bw = weights(pkg, cfg, dev)
+    block = bw.block()
+    for seed in (11, 12, 13):
+        x = pkg.workloads.make_x(bw.cfg, 1, dev, seed=seed)
+        out = block(x).clone()
+        ref = bw.switch_mlp.forward_with_combine(x, block.last_indices, block.last_weights)
+        assert out.dtype == ref.dtype and torch.equal(out, ref), seed
+
+
 def test_switch_glu_forward_matches_composition(pkg, orc, dev):
     """SplitSwitchFfn::forward (per-expert rows) and forward_with_combine
     against the oracle composition of gather_qmm / swiglu / combine."""
