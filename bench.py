@@ -356,7 +356,7 @@ def main():
     print(f"bench: cold {cold}", file=sys.stderr, flush=True)
 
     # dominant kernel: the fused gate/up gather_qmm
-    kt, kn, kmin, kmax = r.kernel_time(pkg, "qgemm_gated", args.steps)
+    kt, kn, kmin, kmax = r.kernel_time(pkg, "qgemm_gated", max(1, args.steps // fpg))
     decode = T * cfg.K < 2048
     if decode:
         traffic_alg = gated_bytes(cfg, T, U, folds_shared(cfg, T))

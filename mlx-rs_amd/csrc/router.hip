@@ -546,6 +546,12 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 #ifndef MLXR_RL_MID_U
 #define MLXR_RL_MID_U 4
 #endif
+// ... and with one expert per wave (4 steps in flight: c2 T=32 logits
+// 9.1 to 8.4 us, T=64 9.6 to 9.2, c6 T=64 12.9 to 12.6 against 2; 8 slower
+// at c6)
+#ifndef MLXR_RL_MID_U1
+#define MLXR_RL_MID_U1 4
+#endif
 #ifndef MLXR_RL_TILED_T
 #define MLXR_RL_TILED_T 256
 #endif
@@ -597,7 +603,7 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     // there: c2 T=64 10.0 -> 9.7 us, c6 15.3 -> 12.8; wider routers keep
     // two per wave)
     if (e_tot <= 4 * 64 + 1)
-      MLXR_RL_N(1, MLXR_RL_MID_TB, 2, false);
+      MLXR_RL_N(1, MLXR_RL_MID_TB, MLXR_RL_MID_U1, false);
     else
       MLXR_RL_N(MLXR_RL_MID_EB, MLXR_RL_MID_TB, MLXR_RL_MID_U, false);
   } else {
