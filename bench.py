@@ -72,6 +72,15 @@ def copy_calibration(mib: int) -> None:
     print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 20}), flush=True)
 
 
+def graph_forwards(steps: int, cap: int, launch: str) -> int:
+    """Forwards one graph replay holds: the largest count up to `cap` that
+    divides `steps`, so that exactly `steps` forwards are timed (1 for
+    eager launches)."""
+    if launch != "graph":
+        return 1
+    return max(c for c in range(1, max(1, cap) + 1) if steps % c == 0)
+
+
 def host_cores() -> int:
     """The cores this process may run on (its affinity mask), within an
     OpenMP thread limit the host sets (OMP_NUM_THREADS)."""
@@ -321,12 +330,7 @@ def main():
     print(f"bench: {cfg.name} T={T} on {torch.cuda.get_device_name(dev)}", file=sys.stderr,
           flush=True)
     bw = W.make_weights(cfg, dev)
-    # forwards per graph replay: the largest count up to the option that
-    # divides --steps, so that exactly --steps forwards are timed
-    fpg = 1
-    if args.launch == "graph":
-        fpg = max(c for c in range(1, max(1, args.forwards_per_graph) + 1)
-                  if args.steps % c == 0)
+    fpg = graph_forwards(args.steps, args.forwards_per_graph, args.launch)
     r = Runner(pkg, bw, T, dev, args.launch, repeat=fpg)
     U = W.distinct(r.idx)
     sec = r.timed(args.steps // fpg, max(1, args.warmup // fpg))

@@ -23,9 +23,26 @@ def test_more_than_one_gpu_exits_with_a_message():
 def test_help_lists_the_driver_options_and_the_sweep_forms():
     r = _run("--help")
     assert r.returncode == 0
-    for opt in ("--gpus", "--steps", "--warmup", "--sweep", "--cpu-seconds"):
+    for opt in ("--gpus", "--steps", "--warmup", "--sweep", "--cpu-seconds",
+                "--forwards-per-graph"):
         assert opt in r.stdout
     assert "cfg:T:res" in r.stdout
+
+
+def test_forwards_per_graph_divide_the_steps():
+    """Graph replays hold the largest count of forwards up to the option
+    that divides --steps, so exactly --steps forwards are timed."""
+    import bench
+    assert bench.graph_forwards(200, 8, "graph") == 8
+    assert bench.graph_forwards(5, 8, "graph") == 5
+    assert bench.graph_forwards(9, 8, "graph") == 3
+    assert bench.graph_forwards(7, 8, "graph") == 7
+    assert bench.graph_forwards(13, 8, "graph") == 1
+    assert bench.graph_forwards(200, 8, "eager") == 1
+    assert bench.graph_forwards(200, 0, "graph") == 1
+    for steps in range(1, 60):
+        f = bench.graph_forwards(steps, 8, "graph")
+        assert steps % f == 0 and 1 <= f <= 8
 
 
 def test_algorithmic_bytes(pkg):
