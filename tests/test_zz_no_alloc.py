@@ -1,9 +1,10 @@
 """mlxr_moe_block_forward_noalloc (the block forward whose scratch is the
 library's own per-GPU device array) against mlxr_moe_block_forward with a
 caller workspace, through the C ABI: the same kernels on the same values,
-so outputs and routing are bit-identical.  Two calls in a row, the second
-with fewer tokens (the array keeps the first call's contents), and a T
-whose workspace exceeds the array is refused on the host."""
+so outputs and routing are bit-identical.  Calls in a row, each with
+fewer tokens than the last (the array keeps the previous call's contents;
+T = 1 takes the down launch that carries the combine), and a T whose
+workspace exceeds the array is refused on the host."""
 import ctypes
 
 import pytest
@@ -32,7 +33,7 @@ def test_noalloc_block_equals_workspace_block(pkg, dev, cfg):
     block = bw.block()
     lib = pkg._capi.lib()
     assert lib.mlxr_moe_noalloc_scratch_size() == 32 * 1024 * 1024
-    for T in (64, 8):
+    for T in (64, 8, 1):
         print(f"  noalloc {cfg} T={T}", flush=True)
         x = W.make_x(bw.cfg, T, dev, seed=100 + T)
         assert block.workspace_size(T) <= lib.mlxr_moe_noalloc_scratch_size()
