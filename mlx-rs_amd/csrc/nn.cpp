@@ -272,7 +272,8 @@ void SwitchFfn::plan(Carve& ws, int64_t T, int64_t K, int64_t d, int64_t f,
 // products.
 Status SwitchFfn::forward(const uint16_t* x, int64_t T, const int32_t* indices,
                           int64_t K, uint16_t* y, Carve& ws, int32_t* status,
-                          hipStream_t s) const {
+                          hipStream_t s, const DownCombine* dc, bool* combined) const {
+  if (combined) *combined = false;
   const int64_t E = sw_.E;
   const int64_t n = T * K;
   const DispatchBuffers db = carve_dispatch(ws, n, E, status);
@@ -281,7 +282,7 @@ Status SwitchFfn::forward(const uint16_t* x, int64_t T, const int32_t* indices,
       launch_dispatch(indices, n, E, prefill_tile_rows(n, E, sw_.bits), db, true, s),
       "switch_mlp dispatch");
   if (!st.ok) return st;
-  return experts(x, T, K, db, y, ws, s);
+  return experts(x, T, K, db, y, ws, s, nullptr, dc, combined);
 }
 
 // The expert products given the dispatch: gate and up gather_qmm fused with
@@ -398,8 +399,12 @@ Status SwitchFfn::forward_with_combine(
     const float* shared_logit, int64_t shared_ld, Carve& ws, int32_t* status,
     hipStream_t s) const {
   uint16_t* y = ws.take<uint16_t>(T * K * sw_.d);
-  Status st = forward(x, T, indices, K, y, ws, status, s);
-  if (!st.ok) return st;
+  // one token: the combine rides in the down launch where it can
+  const DownCombine dc{weights, w_bf16, shared_y, shared_y ? shared_logit : nullptr, nullptr,
+                       out, w_bf16};
+  bool combined = false;
+  Status st = forward(x, T, indices, K, y, ws, status, s, T == 1 ? &dc : nullptr, &combined);
+  if (!st.ok || combined) return st;
   return from_hip(launch_combine(y, weights, w_bf16, T, K, sw_.d, shared_y,
                                  shared_logit, shared_ld, nullptr, out, w_bf16,
                                  s),

@@ -115,9 +115,11 @@ class SwitchFfn {
  public:
   // forward: y bf16 [T, K, d] per-expert outputs; clears *status first
   // (in its dispatch launch).
+  // With `dc`, as experts().
   Status forward(const uint16_t* x, int64_t T, const int32_t* indices,
                  int64_t K, uint16_t* y, Carve& ws, int32_t* status,
-                 hipStream_t s) const;
+                 hipStream_t s, const DownCombine* dc = nullptr,
+                 bool* combined = nullptr) const;
   // The expert products given a dispatch of the T*K flat ids; with `fold`,
   // the shared expert's products in the same launches.  With `dc` at T = 1
   // the combine runs in the down launch where it can

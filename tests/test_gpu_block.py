@@ -321,16 +321,21 @@ def test_block_token_permutation_equivariance(pkg, dev):
 
 @pytest.mark.parametrize("cfg", ["c2", "c5"])
 def test_single_token_combine_in_down_launch(pkg, dev, cfg):
-    """At T = 1 the block sums the routed rows inside its down launch; the
-    output equals, bit for bit, the separate down GEMM and combine launches
-    of the same routing (SplitSwitchFfn.forward_with_combine)."""
+    """At T = 1 the block and SplitSwitchFfn.forward_with_combine sum the
+    routed rows inside their down launch; both equal, bit for bit, the
+    separate launches of the same routing: the per-expert rows
+    (SplitSwitchFfn.forward) and the combine op."""
     bw = weights(pkg, cfg, dev)
     block = bw.block()
     for seed in (11, 12, 13):
         x = pkg.workloads.make_x(bw.cfg, 1, dev, seed=seed)
         out = block(x).clone()
-        ref = bw.switch_mlp.forward_with_combine(x, block.last_indices, block.last_weights)
+        idx, w = block.last_indices.clone(), block.last_weights.clone()
+        y = bw.switch_mlp.forward(x, idx)
+        ref = pkg.ops.combine(y.reshape(1, bw.cfg.K, bw.cfg.d), w.reshape(1, bw.cfg.K))
         assert out.dtype == ref.dtype and torch.equal(out, ref), seed
+        fused = bw.switch_mlp.forward_with_combine(x, idx, w)
+        assert torch.equal(fused, ref), seed
 
 
 def test_switch_glu_forward_matches_composition(pkg, orc, dev):
