@@ -243,7 +243,10 @@ hipError_t launch_qgemm(const QGemmArgs& a, int64_t total_rows,
 // w_bf16), the shared expert's row [d] when it ran apart (a folded one
 // comes from the same launch), its gate logit (null: no shared branch), the
 // residual row [d] or null, and the output row [d] (bf16 when bf16, else
-// f32) -- the arguments of launch_combine at T = 1.
+// f32) -- the arguments of launch_combine at T = 1.  `distinct`: the K ids
+// name K different experts (the block's own top-K), so every work item holds
+// one row; otherwise (caller indices) an expert may take several rows and
+// its item then runs in the 8-token form, as in the separate down launch.
 struct DownCombine {
   const void* w;
   bool w_bf16;
@@ -252,6 +255,7 @@ struct DownCombine {
   const uint16_t* residual;
   void* out;
   bool bf16;
+  bool distinct;
 };
 
 // The down GEMM of ONE token (K routed rows, and the folded shared

@@ -4,6 +4,7 @@
 #include "nn.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 // The single-token combine in the down launch (0: always the separate
 // combine launch)
@@ -95,6 +96,15 @@ bool use_prefill_path(int64_t rows, int64_t experts, int bits) {
 }
 
 namespace {
+
+// MLXR_MOE_DOWN_COMBINE=0 in the environment sends one token through the
+// separate down and combine launches as well (bit-identical; read at every
+// call, so a test can compare the two forms in one process).
+bool down_combine_on() {
+  if (!MLXR_DOWN_COMBINE) return false;
+  const char* v = std::getenv("MLXR_MOE_DOWN_COMBINE");
+  return !(v && v[0] == '0');
+}
 
 QWeights qw(const mlxr_moe_qlinear& q) {
   return QWeights{q.weight, static_cast<const uint16_t*>(q.scales),
@@ -376,7 +386,7 @@ Status SwitchFfn::experts(const uint16_t* x, int64_t T, int64_t K,
     h2.out = fold->y;
     h2.out_by_flat = false;
   }
-  if (MLXR_DOWN_COMBINE && dc && T == 1 && !prefill) {
+  if (dc && T == 1 && !prefill && down_combine_on()) {
     bool done = false;
     st = from_hip(launch_qgemm_down_combine(h, K, max_items, fold ? &h2 : nullptr, *dc, s,
                                             &done),
@@ -400,8 +410,9 @@ Status SwitchFfn::forward_with_combine(
     hipStream_t s) const {
   uint16_t* y = ws.take<uint16_t>(T * K * sw_.d);
   // one token: the combine rides in the down launch where it can
+  // (caller indices may name one expert several times)
   const DownCombine dc{weights, w_bf16, shared_y, shared_y ? shared_logit : nullptr, nullptr,
-                       out, w_bf16};
+                       out, w_bf16, false};
   bool combined = false;
   Status st = forward(x, T, indices, K, y, ws, status, s, T == 1 ? &dc : nullptr, &combined);
   if (!st.ok || combined) return st;
@@ -534,7 +545,9 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
   SharedFold sf{};
   if (fold) sf = smlp.fold(shared_ws, T, sy);
   // one token: the combine rides in the down launch where it can
-  const DownCombine dc{wts, false, sy, shared ? logits + E : nullptr, residual, out, bf16};
+  // (top-K picks K different experts: one row per work item)
+  const DownCombine dc{wts, false, sy, shared ? logits + E : nullptr, residual, out, bf16,
+                       true};
   bool combined = false;
   st = mlp.experts(x, T, K, db, y, ws, s, fold ? &sf : nullptr, T == 1 ? &dc : nullptr,
                    &combined);

@@ -905,18 +905,22 @@ __device__ __forceinline__ QGemmArgs pick_args(bool q, const QGemmArgs& b, const
 
 // The down GEMM of one token and its combine (launch_qgemm_down_combine).
 // Workgroup = 16 output channels (blockIdx.x); its waves come in groups of
-// KS, one group per row: the K routed rows (work items 0..K-1 of the
-// dispatch, one row each) and, from K on, the folded shared expert's row.
-// Each group runs the streaming kernel's item work (the 4-token MFMA form,
-// KS K-slices) in its own LDS region and leaves its bf16 row values in LDS
-// (row k at its flat row k, the shared row at K); after a barrier 16
-// threads sum them in k order with the combine's arithmetic.
-template <int BITS, int KS, bool BF16, typename WT>
+// KS, one group per work item: the routed items (at most K: items 0..K-1
+// of the dispatch) and, from K on, the folded shared expert's row.  Each
+// group runs the streaming kernel's item work (KS K-slices, the MFMA form of
+// the separate launch: 4 tokens, or 8 for an expert of more than
+// kStreamTT4Rows rows when LONG) in its own LDS region and leaves its bf16
+// row values in LDS (flat row k at row k, the shared row at K); after a
+// barrier 16 threads sum them in k order with the combine's arithmetic.
+// Without LONG the caller guarantees one row per item (K distinct
+// experts).  Both MFMA forms pass the same barriers.
+template <int BITS, int KS, bool BF16, typename WT, bool LONG>
 __global__ __launch_bounds__(1024) void qgemm_down_combine_kernel(
     QGemmArgs a, QGemmArgs a2, int K, int nsub, int sub_lds, DownCombine c) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int L = 64 * KS;
   constexpr int D = BITS == 4 ? MLXR_STREAM_DEPTH4 : MLXR_STREAM_DEPTH8;
+  constexpr int D8 = BITS == 4 ? MLXR_STREAM_DEPTH4_TT8 : MLXR_STREAM_DEPTH8_TT8;
   // (the group is uniform over a wave: said so, the choice of argument
   // set stays in scalar registers)
   const int sub = __builtin_amdgcn_readfirstlane((int)threadIdx.x / L);
@@ -940,9 +944,14 @@ __global__ __launch_bounds__(1024) void qgemm_down_combine_kernel(
     wk = make_int4(0, 0, 0, 0);  // no such item: no rows (expert 0's loads)
   }
   const QGemmArgs A = pick_args(sh, a2, a);
-  stream_body<BITS, false, 4, D, 1, KS>(A, rec, wk, fr0, fr1, (int)blockIdx.x,
-                                        smem + (size_t)sub * sub_lds, ltid, L, yl,
-                                        sh ? K : 0);
+  if (LONG && wk.w > kStreamTT4Rows)
+    stream_body<BITS, false, 8, D8, 1, KS>(A, rec, wk, fr0, fr1, (int)blockIdx.x,
+                                           smem + (size_t)sub * sub_lds, ltid, L, yl,
+                                           sh ? K : 0);
+  else
+    stream_body<BITS, false, 4, D, 1, KS>(A, rec, wk, fr0, fr1, (int)blockIdx.x,
+                                          smem + (size_t)sub * sub_lds, ltid, L, yl,
+                                          sh ? K : 0);
   __syncthreads();
   if (threadIdx.x < 16) {
     const int n = threadIdx.x, ch = (int)blockIdx.x * 16 + n;
@@ -1195,25 +1204,36 @@ hipError_t launch_qgemm_down_combine(const QGemmArgs& a, int64_t K, int64_t max_
   const int nsub = (int)K + (int)items2;
   if (ks > 2 || nsub * ks > 16) return hipSuccess;
   const int groups = a.K / 64;
+  // an expert can take more than kStreamTT4Rows of the K rows only when the
+  // ids may repeat: then its item runs in the 8-token form, LDS sized for it
+  const bool long_items = !c.distinct && K > kStreamTT4Rows;
+  const size_t tt = long_items ? 8 : 4;
   const size_t sub_lds =
-      (((size_t)4 * (a.K + 8) * 2 + 16 + (size_t)groups * 4 * 4 + 15) & ~size_t(15)) +
+      ((tt * (a.K + 8) * 2 + 16 + (size_t)groups * tt * 4 + 15) & ~size_t(15)) +
       (((size_t)ks * 2 * 16 * groups * 2 + 15) & ~size_t(15)) +
       (ks > 1 ? (size_t)ks * 64 * 16 : 0);
   const size_t lds = (size_t)nsub * sub_lds + (size_t)nsub * 32;
   if (lds > 160 * 1024) return hipSuccess;
   const dim3 grid((unsigned)(a.N / 16)), block((unsigned)(64 * ks * nsub));
   ProfileScope prof("qgemm_down", s);
-#define MLXR_DC(B, KS_)                                                                   \
+#define MLXR_DC2(B, KS_, LG)                                                              \
   do {                                                                                    \
     if (c.w_bf16)                                                                         \
-      qgemm_down_combine_kernel<B, KS_, true, uint16_t>                                   \
+      qgemm_down_combine_kernel<B, KS_, true, uint16_t, LG>                               \
           <<<grid, block, lds, s>>>(a, b, (int)K, nsub, (int)sub_lds, c);                 \
     else if (c.bf16)                                                                      \
-      qgemm_down_combine_kernel<B, KS_, true, float>                                      \
+      qgemm_down_combine_kernel<B, KS_, true, float, LG>                                  \
           <<<grid, block, lds, s>>>(a, b, (int)K, nsub, (int)sub_lds, c);                 \
     else                                                                                  \
-      qgemm_down_combine_kernel<B, KS_, false, float>                                     \
+      qgemm_down_combine_kernel<B, KS_, false, float, LG>                                 \
           <<<grid, block, lds, s>>>(a, b, (int)K, nsub, (int)sub_lds, c);                 \
+  } while (0)
+#define MLXR_DC(B, KS_)              \
+  do {                               \
+    if (long_items)                  \
+      MLXR_DC2(B, KS_, true);        \
+    else                             \
+      MLXR_DC2(B, KS_, false);       \
   } while (0)
   if (a.bits == 4) {
     if (ks == 2)
@@ -1227,6 +1247,7 @@ hipError_t launch_qgemm_down_combine(const QGemmArgs& a, int64_t K, int64_t max_
       MLXR_DC(8, 1);
   }
 #undef MLXR_DC
+#undef MLXR_DC2
   *done = true;
   return hipGetLastError();
 }
