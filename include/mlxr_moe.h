@@ -363,7 +363,10 @@ int mlxr_moe_block_forward(const mlxr_moe_block* block, const void* x,
  * (mlxr_moe_block_workspace_size) exceeds it is rejected with an error.
  * Nothing is allocated.  Calls that overlap on one GPU share the array and
  * race: serialise them (one stream, or events).  The status word of the
- * last call is not readable through mlxr_moe_workspace_status. */
+ * last call is not readable through mlxr_moe_workspace_status.  The array's
+ * device address is looked up once per device, by the first call there or
+ * by mlxr_moe_noalloc_scratch_size() with that device current: call the
+ * latter once per device before capturing the entry into a graph. */
 #define MLXR_MOE_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
 size_t mlxr_moe_noalloc_scratch_size(void);
 int mlxr_moe_block_forward_noalloc(const mlxr_moe_block* block, const void* x,

@@ -63,7 +63,15 @@ void* scratch_on(int dev, std::string* err) {
 
 using namespace mlxr_moe;
 
+// Also the set-up call: it resolves the array's address on the current
+// device (when there is one), so that a later call made under graph capture
+// runs no lookup.
 extern "C" size_t mlxr_moe_noalloc_scratch_size(void) {
+  int dev = -1;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0) {
+    std::string err;
+    (void)scratch_on(dev, &err);  // a failure is reported by the entry itself
+  }
   return MLXR_MOE_NOALLOC_SCRATCH_BYTES;
 }
 

@@ -6,7 +6,10 @@ with a quantised router, whose weights are bf16); max |out - oracle| <=
 2e-2 * RMS(oracle) with f32 accumulation.  A quantised router makes the
 output bf16, and the GPU's and the oracle's f32 sums (in different orders)
 can round to neighbouring bf16 values, so there each element may also
-differ by one bf16 step of the oracle's value."""
+differ by one bf16 step of the oracle's value.  Every point prints (and,
+with MLXR_PARITY_LOG set, logs) its max|err|/RMS and the count of elements
+past 2e-2 * RMS; that count is held to the measured figure in PAST_BAR
+(zero for the points it does not list)."""
 import sys
 from pathlib import Path
 
@@ -27,6 +30,42 @@ def weights(pkg, cfg_name, dev):
         torch.cuda.empty_cache()
         _WEIGHTS[cfg_name] = pkg.workloads.make_weights(pkg.workloads.CONFIGS[cfg_name], dev)
     return _WEIGHTS[cfg_name]
+
+
+# Elements past the literal bar max|err| <= 2e-2 * RMS, per point, as measured
+# on the MI355X (the rest of the points have none).  Each such element is
+# within one step of a bf16 value it depends on: an intermediate (a SwiGLU
+# activation or an expert row y_k, rounded the other way because the GPU's
+# and the oracle's f32 sums run in different orders; f32-output blocks) or
+# the bf16 output itself (a bf16 block: an element near 4*RMS has a step of
+# ~3% of RMS).  The test holds each point to its measured count.
+PAST_BAR = {
+    "c4_e512_top10_shared T=64": 1, "c4_e512_top10_shared T=512": 1,
+    "c4_e512_top10_shared T=2048": 3,
+    "c6_qwen3_6_35b_a3b_q8router T=9": 1, "c6_qwen3_6_35b_a3b_q8router T=64": 2,
+    "c6_qwen3_6_35b_a3b_q8router T=512": 2, "c6_qwen3_6_35b_a3b_q8router T=2048": 13,
+    "c8_qwen3_6_35b_a3b_bf16 T=512": 1, "c8_qwen3_6_35b_a3b_bf16 T=2048": 11,
+}
+
+
+def record_parity(name, T, got, ref, rms, allowed=None):
+    """Print the parity figures of one block point (max|err|/RMS, the count
+    of elements past 2e-2 * RMS, p99.9 |err|/RMS) and, when MLXR_PARITY_LOG
+    names a file, append them there as a JSON line."""
+    import json
+    import os
+    diff = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+    rec = {"point": f"{name} T={T}", "max_err_over_rms": float(diff.max() / rms),
+           "past_bar": int((diff > 2e-2 * rms).sum()), "elements": int(diff.size),
+           "p999_over_rms": float(np.quantile(diff, 0.999) / rms)}
+    if allowed is not None:
+        rec["past_bar_allowed"] = allowed
+    print("  PARITY " + json.dumps(rec), flush=True)
+    path = os.environ.get("MLXR_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+    return rec
 
 
 def check_gemma(pkg, orc, bw, x, nthreads=16):
@@ -54,9 +93,11 @@ def check_gemma(pkg, orc, bw, x, nthreads=16):
     rms = np.sqrt(np.mean(ref ** 2))
     diff = np.abs(got - ref)
     print(f"  max|err| {diff.max():.3e}  rms {rms:.3e}", flush=True)
+    rec = record_parity(cfg.name, T, got, ref, rms, PAST_BAR.get(f"{cfg.name} T={T}", 0))
     a = np.abs(ref)
     ulp = np.where(a > 0, 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - 7), 0.0)
     assert np.all(diff <= 2e-2 * rms + ulp)
+    assert rec["past_bar"] <= rec["past_bar_allowed"]
     assert pkg.ops.workspace_status(block.last_workspace) == 0
 
 
@@ -119,20 +160,21 @@ def check_block(pkg, orc, bw, x, nthreads=16):
     diff = np.abs(got - ref)
     err = diff.max()
     print(f"  max|err| {err:.3e}  rms {rms:.3e}  ratio {err / rms:.2e}", flush=True)
+    rec = record_parity(cfg.name, T, got, ref, rms, PAST_BAR.get(f"{cfg.name} T={T}", 0))
+    assert rec["past_bar"] <= rec["past_bar_allowed"]
     if cfg.router_bits:
         a = np.abs(ref.astype(np.float64))
         ulp = np.where(a > 0, 2.0 ** (np.floor(np.log2(np.maximum(a, 1e-38))) - 7), 0.0)
         assert np.all(diff <= 2e-2 * rms + ulp)
     elif err > 2e-2 * rms:
-        # Past the bar only through one-step flips of bf16 intermediates:
-        # at most 1e-4 of the elements, each within the bar plus the step
-        # bound of the branch values it sums (the oracle's own).
+        # Past the bar only through one-step flips of bf16 intermediates
+        # (as many elements as PAST_BAR lists), each within the bar plus the
+        # step bound of the branch values it sums (the oracle's own).
         over = diff > 2e-2 * rms
         allow = flip_allowance(pkg, orc, bw, x, ridx, rw, tiled, nthreads)
         print(f"  {int(over.sum())} of {over.size} elements past 2e-2*rms; "
               f"max excess / flip bound {((diff - 2e-2 * rms) / allow)[over].max():.2f}",
               flush=True)
-        assert over.sum() <= 1e-4 * over.size
         assert np.all(diff <= 2e-2 * rms + allow)
     # the bulk of the elements sit well inside the bar
     q = np.quantile(diff, 0.999)
@@ -319,23 +361,74 @@ def test_block_token_permutation_equivariance(pkg, dev):
     assert torch.equal(c, a[perm])
 
 
-@pytest.mark.parametrize("cfg", ["c2", "c5"])
-def test_single_token_combine_in_down_launch(pkg, dev, cfg):
+@pytest.mark.parametrize("cfg", ["c2", "c5", "c4", "c6"])
+def test_single_token_combine_in_down_launch(pkg, dev, cfg, monkeypatch):
     """At T = 1 the block and SplitSwitchFfn.forward_with_combine sum the
     routed rows inside their down launch; both equal, bit for bit, the
-    separate launches of the same routing: the per-expert rows
-    (SplitSwitchFfn.forward) and the combine op."""
+    separate launches of the same routing: the block run with the fusion
+    switched off (MLXR_MOE_DOWN_COMBINE=0: routed y and, on c4/c6, the folded
+    shared expert's y from the down launch, then the combine op with the
+    shared gate logit), and the per-expert rows (SplitSwitchFfn.forward)
+    with the combine op."""
     bw = weights(pkg, cfg, dev)
     block = bw.block()
+    K, d = bw.cfg.K, bw.cfg.d
     for seed in (11, 12, 13):
         x = pkg.workloads.make_x(bw.cfg, 1, dev, seed=seed)
+        print(f"  single-token combine {cfg} seed={seed}", flush=True)
         out = block(x).clone()
         idx, w = block.last_indices.clone(), block.last_weights.clone()
+        monkeypatch.setenv("MLXR_MOE_DOWN_COMBINE", "0")
+        sep = block(x).clone()
+        monkeypatch.delenv("MLXR_MOE_DOWN_COMBINE")
+        assert torch.equal(block.last_indices, idx)
+        assert out.dtype == sep.dtype and torch.equal(out, sep), seed
         y = bw.switch_mlp.forward(x, idx)
-        ref = pkg.ops.combine(y.reshape(1, bw.cfg.K, bw.cfg.d), w.reshape(1, bw.cfg.K))
-        assert out.dtype == ref.dtype and torch.equal(out, ref), seed
         fused = bw.switch_mlp.forward_with_combine(x, idx, w)
-        assert torch.equal(fused, ref), seed
+        if not bw.cfg.fs:
+            ref = pkg.ops.combine(y.reshape(1, K, d), w.reshape(1, K))
+            assert out.dtype == ref.dtype and torch.equal(out, ref), seed
+        monkeypatch.setenv("MLXR_MOE_DOWN_COMBINE", "0")
+        sep_fwc = bw.switch_mlp.forward_with_combine(x, idx, w)
+        monkeypatch.delenv("MLXR_MOE_DOWN_COMBINE")
+        assert torch.equal(fused, sep_fwc), seed
+        assert torch.equal(fused, pkg.ops.combine(y.reshape(1, K, d), w.reshape(1, K))), seed
+
+
+@pytest.mark.parametrize("cfg,ids", [("c2", [3, 3, 3, 3, 3, 1, 2, 4]),
+                                     ("c2", [7] * 8),
+                                     ("c2", [5, 9, 5, 9, 5, 9, 5, 9]),
+                                     ("c4", [2] * 10),
+                                     ("c4", [4, 4, 4, 4, 4, 4, 1, 1, 1, 0])])
+def test_single_token_combine_repeated_ids(pkg, dev, cfg, ids, monkeypatch):
+    """forward_with_combine at T = 1 with caller indices that name one
+    expert several times: an expert of more than 4 of the K rows runs in the
+    8-token MFMA form (and, past 8 rows, in two work items), in the fused
+    down + combine launch as in the separate down launch.  Equal bit for bit
+    to SplitSwitchFfn.forward followed by the combine op, and to the
+    separate launches."""
+    bw = weights(pkg, cfg, dev)
+    K, d = bw.cfg.K, bw.cfg.d
+    assert len(ids) == K
+    x = pkg.workloads.make_x(bw.cfg, 1, dev, seed=31)
+    idx = torch.tensor([ids], dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(5)
+    w = torch.rand((1, K), generator=g).to(dev)
+    print(f"  repeated ids {cfg} {ids}", flush=True)
+    y = bw.switch_mlp.forward(x, idx)
+    ref = pkg.ops.combine(y.reshape(1, K, d), w)
+    fused = bw.switch_mlp.forward_with_combine(x, idx, w)
+    torch.cuda.synchronize()
+    # rows of one expert are equal to each other (same x, same weights)
+    yr = y.reshape(K, d)
+    for k in range(1, K):
+        if ids[k] == ids[0]:
+            assert torch.equal(yr[k], yr[0])
+    assert torch.equal(fused, ref)
+    monkeypatch.setenv("MLXR_MOE_DOWN_COMBINE", "0")
+    sep = bw.switch_mlp.forward_with_combine(x, idx, w)
+    monkeypatch.delenv("MLXR_MOE_DOWN_COMBINE")
+    assert torch.equal(fused, sep)
 
 
 def test_switch_glu_forward_matches_composition(pkg, orc, dev):
@@ -465,3 +558,20 @@ def test_checkpoint_round_trip_forward(pkg, orc, dev, tmp_path):
     assert torch.equal(norm.weight, norm_w)
     assert torch.equal(loaded.forward_residual(x, norm),
                        bw.block().forward_residual(x, pkg.nn.RmsNorm(norm_w, 1e-6)))
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c5"])
+def test_zipf_routing_matches_fixture(pkg, dev, cfg):
+    """The Zipf-skewed configurations route as committed: with the fixture's
+    router bias, the block's realised per-expert row counts at every bench
+    T equal tests/golden/zipf_routing.npz's (the routing itself is
+    bit-exact against the oracle in test_block_parity)."""
+    bw = weights(pkg, cfg, dev)
+    block = bw.block()
+    for T in bw.cfg.tokens:
+        want = pkg.workloads.zipf_rows(bw.cfg, T)
+        assert want is not None, f"no committed row counts for {cfg} T={T}"
+        block(pkg.workloads.make_x(bw.cfg, T, dev, seed=T))
+        got = torch.bincount(block.last_indices.reshape(-1).long(), minlength=bw.cfg.E)
+        print(f"  zipf rows {cfg} T={T}: max {int(got.max())}", flush=True)
+        assert np.array_equal(got.cpu().numpy(), want)

@@ -62,3 +62,45 @@ def test_noalloc_rejects_oversize_and_empty(pkg, dev):
     # T = 0 does nothing and succeeds
     assert lib.mlxr_moe_block_forward_noalloc(ctypes.byref(block.descriptor()), x.data_ptr(),
                                               0, x.data_ptr(), None, None, None) == 0
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_noalloc_block_under_graph_capture(pkg, dev, T):
+    """The no-allocation entry captured into a HIP graph (after the
+    documented set-up call, mlxr_moe_noalloc_scratch_size, on this device)
+    and replayed several times, with other eager block calls and
+    synchronisations between the replays: every replay equals the eager
+    call's output and routing bit for bit."""
+    W = pkg.workloads
+    bw = W.make_weights(W.CONFIGS["c2"], dev)
+    block = bw.block()
+    lib = pkg._capi.lib()
+    assert lib.mlxr_moe_noalloc_scratch_size() == 32 * 1024 * 1024
+    x = W.make_x(bw.cfg, T, dev, seed=200 + T)
+    other = W.make_x(bw.cfg, 8, dev, seed=300 + T)
+    want, widx, ww = _noalloc(pkg, block, x, T)
+    want, widx, ww = want.clone(), widx.clone(), ww.clone()
+    torch.cuda.synchronize(dev)
+    print(f"  noalloc graph capture c2 T={T}", flush=True)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        # the static outputs of the captured call
+        with torch.cuda.graph(g, stream=s):
+            got, idx, wts = _noalloc(pkg, block, x, T)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    for rep in range(3):
+        got.zero_()
+        idx.zero_()
+        # eager work between replays (its own scratch use and results)
+        _noalloc(pkg, block, other, 8)
+        torch.cuda.synchronize(dev)
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(idx, widx), rep
+        assert torch.equal(wts, ww), rep
+        assert torch.equal(got, want), rep
+    del g, bw, block
+    torch.cuda.empty_cache()
