@@ -594,6 +594,78 @@ def test_geglu_closed_forms_and_fp64_bound(orc):
     assert np.all(np.abs(got - exact) <= 2.0 ** -5 * (np.abs(gd) + 0.05) * np.abs(ud))
 
 
+def _geglu_torch_bf16(g, u):
+    """gelu_approximate_in_dtype(g) * u op for op as activations.rs:246-259
+    builds it, on torch's CPU bfloat16 arithmetic (every op computed in f32
+    and rounded to bf16, the constants cast to bf16 first): an
+    implementation of the same op graph independent of the oracle's C."""
+    import math
+
+    import torch
+    bf = torch.bfloat16
+    c = lambda v: torch.tensor(v, dtype=torch.float32).to(bf)  # noqa: E731
+    x = torch.from_numpy(np.asarray(g, np.float32)).to(bf)
+    uu = torch.from_numpy(np.asarray(u, np.float32)).to(bf)
+    half, one = c(0.5), c(1.0)
+    s2p, k = c(math.sqrt(2.0 / math.pi)), c(0.044715)
+    x3 = x * x * x
+    t = torch.tanh(s2p * (x + k * x3))
+    return ((half * x * (one + t)) * uu).float().numpy()
+
+
+def test_geglu_bf16_chain_pinned(orc):
+    """The tanh-approximate GELU in bf16 (activations.rs:246-259), pinned
+    where the erf GELU and the approximation part: on every bf16 g with
+    |g| <= 6 (and random u) the oracle equals the same op graph on torch's
+    bf16 arithmetic bit for bit.  Hand-worked: g = -3, u = 1 gives
+    x^3 = -27, k*x^3 = bf16(0.044677734375 * -27) = -1.203125,
+    inner = bf16(-4.203125) = -4.1875 (tie to even),
+    bf16(0.796875 * -4.1875) = -3.34375, bf16(tanh) = -0.99609375,
+    1 + t = 2^-8, out = -1.5 * 2^-8 = -0.005859375 -- where the fp64
+    tanh form gives -0.00364 and the erf GELU -0.00405."""
+    f = lambda h: orc.bf16_to_f32(h).astype(np.float64)  # noqa: E731
+    bf = lambda a: orc.f32_to_bf16(np.asarray(a, np.float32))  # noqa: E731
+    assert f(orc.geglu(bf([-3.0]), bf([1.0])))[0] == -0.005859375
+    allb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    gv = orc.bf16_to_f32(allb)
+    g = allb[np.isfinite(gv) & (np.abs(gv) <= 6.0)]
+    rng = np.random.default_rng(53)
+    for u in (np.ones(g.size, np.float32), rng.standard_normal(g.size).astype(np.float32)):
+        ub = bf(u)
+        want = _geglu_torch_bf16(orc.bf16_to_f32(g), orc.bf16_to_f32(ub))
+        got = orc.bf16_to_f32(orc.geglu(g, ub))
+        assert np.array_equal(got, want)
+    # the test tells the two GELUs apart: on [-4, -2.5] the erf form moves
+    # most outputs by many bf16 steps
+    tail = g[(orc.bf16_to_f32(g) >= -4.0) & (orc.bf16_to_f32(g) <= -2.5)]
+    import math
+    gt = orc.bf16_to_f32(tail).astype(np.float64)
+    erf = bf(0.5 * gt * (1 + np.array([math.erf(v / math.sqrt(2)) for v in gt])))
+    assert np.mean(orc.geglu(tail, bf(np.ones(tail.size))) != erf) > 0.5
+
+
+def test_rms_norm_eps_pinned(orc):
+    """fast::rms_norm's eps (normalization.rs:272-276): a row where eps
+    dominates the mean square (x = 2^-10, mean(x^2) = 2^-20, eps = 1e-3)
+    gives w * x / sqrt(mean(x^2) + eps) = 0.03087 within one bf16 rounding
+    (without eps it would be 1.0); and the reference's own known answer
+    (fast.rs:726-741: [1, 2, 3, 4] with eps 1e-5, no weight, against
+    x * rsqrt(mean(x^2) + eps)) with a unit weight, within one bf16
+    rounding."""
+    d = 512
+    x = orc.f32_to_bf16(np.full((1, d), 2.0 ** -10, np.float32))
+    w = orc.f32_to_bf16(np.ones(d, np.float32))
+    got = orc.bf16_to_f32(orc.rms_norm(x, w, 1e-3)).astype(np.float64)
+    want = 2.0 ** -10 / np.sqrt(2.0 ** -20 + float(np.float32(1e-3)))
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * want)
+    assert np.all(np.abs(got - 1.0) > 0.5)
+    a = np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)
+    got = orc.bf16_to_f32(orc.rms_norm(orc.f32_to_bf16(a), orc.f32_to_bf16(np.ones(4, np.float32)),
+                                       1e-5)).astype(np.float64)
+    want = a / np.sqrt((a.astype(np.float64) ** 2).mean() + 1e-5)
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want))
+
+
 def test_rms_norm_exact_and_fp64_bound(orc):
     """fast::rms_norm: a constant row 2 with eps 0 normalises to 1, so the
     output is the weight exactly; elsewhere within two bf16 roundings of
