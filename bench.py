@@ -168,15 +168,25 @@ class Runner:
 
     def timed(self, steps, warmup):
         """Mean seconds per forward over `steps` steps."""
+        return self.timed_regions(steps, warmup, 1)[0]
+
+    def timed_regions(self, steps, warmup, repeats):
+        """Seconds per forward of each of `repeats` timed regions, each
+        `steps` steps bracketed by a synchronisation on both sides, after
+        `warmup` untimed steps."""
         torch = self.torch
         for _ in range(warmup):
             self.step()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            self.step()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / steps / len(self.blocks)
+        out = []
+        for _ in range(repeats):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                self.step()
+            torch.cuda.synchronize()
+            out.append((time.perf_counter() - t0) / steps / len(self.blocks))
+        return out
 
     def median(self, steps):
         """Median seconds per forward, each step bracketed by events on the
@@ -333,7 +343,13 @@ def main():
     fpg = graph_forwards(args.steps, args.forwards_per_graph, args.launch)
     r = Runner(pkg, bw, T, dev, args.launch, repeat=fpg)
     U = W.distinct(r.idx)
-    sec = r.timed(args.steps // fpg, max(1, args.warmup // fpg))
+    # the timed region is exactly --steps forwards; it runs `repeats` times
+    # (at least 10, and at least 50 timed forwards in all) after at least 10
+    # warm-up forwards, and the median region gives ms_per_step
+    repeats = max(10, -(-50 // max(1, args.steps)))
+    warm = max(args.warmup, 10)
+    regions = r.timed_regions(args.steps // fpg, -(-warm // fpg), repeats)
+    sec = float(np.median(regions))
     tok_s = T / sec
     block_bytes = W.algorithmic_bytes(cfg, T, U)
     med = r.median(args.steps // fpg)
@@ -440,6 +456,11 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(sec * 1e3, 5),
+        "timed_regions": {"repeats": repeats, "steps_each": args.steps,
+                          "warmup_forwards": -(-warm // fpg) * fpg,
+                          "ms_per_step_mean": round(float(np.mean(regions)) * 1e3, 5),
+                          "ms_per_step_min": round(min(regions) * 1e3, 5),
+                          "ms_per_step_max": round(max(regions) * 1e3, 5)},
         "ms_per_step_median": round(med * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",

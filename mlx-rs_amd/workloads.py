@@ -19,7 +19,9 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
+from pathlib import Path
 
+import numpy as np
 import torch
 
 from . import nn, ops
@@ -83,27 +85,32 @@ def make_x(cfg: MoEConfig, T: int, device, seed: int | None = None) -> torch.Ten
     return _normal((T, cfg.d), 1.0, device, seed, 1).to(torch.bfloat16)
 
 
-def zipf_bias(cfg: MoEConfig, gate_w: torch.Tensor, device, iters: int = 20,
-              n_cal: int = 4096) -> torch.Tensor:
-    """Per-expert router bias giving a Zipf(alpha) top-K load over a seeded
-    permutation of experts, calibrated by fixed-point iterations
-    b += log p - log p_hat on a separate calibration batch (seed 1)."""
-    E, K = cfg.E, cfg.K
-    perm = torch.randperm(E, generator=_gen("cpu", cfg.seed, 7))
-    rank = torch.empty(E)
-    rank[perm] = torch.arange(1, E + 1, dtype=torch.float32)
-    p = rank.pow(-cfg.zipf_alpha)
-    p = (p / p.sum()).to(device)
-    b = p.log()
-    xc = _normal((n_cal, cfg.d), 1.0, device, 1, 11).to(torch.bfloat16).float()
-    base = xc @ gate_w.t()
-    for _ in range(iters):
-        top = (base + b).topk(K, dim=-1).indices
-        load = torch.bincount(top.reshape(-1), minlength=E).float() / (n_cal * K)
-        if (load - p).abs().sum() < 0.05:
-            break
-        b = b + (p.log() - (load + 1e-6).log()) * 0.5
-    return b.float()
+# The Zipf routing fixture (tests/golden/make_zipf_routing.py writes it):
+# per configuration the router logit bias and the realised row counts.
+ZIPF_FIXTURE = Path(__file__).resolve().parent.parent / "tests" / "golden" / "zipf_routing.npz"
+
+
+def zipf_bias(cfg: MoEConfig, device) -> torch.Tensor:
+    """Per-expert router bias giving `cfg` its Zipf(alpha) top-K load over a
+    seeded permutation of the experts, from the committed fixture (the
+    calibration that made it runs once, in make_zipf_routing.py)."""
+    key = f"{cfg.name}__bias"
+    with np.load(ZIPF_FIXTURE) as z:
+        if key not in z.files:
+            raise KeyError(f"{ZIPF_FIXTURE.name} has no bias for {cfg.name}: run "
+                           "tests/golden/make_zipf_routing.py on a GPU")
+        b = z[key]
+    if b.shape != (cfg.E,):
+        raise ValueError(f"{ZIPF_FIXTURE.name}: bias of {cfg.name} has shape {b.shape}")
+    return torch.from_numpy(b.astype(np.float32)).to(device)
+
+
+def zipf_rows(cfg: MoEConfig, T: int):
+    """The committed per-expert row counts of `cfg` at T tokens (None when
+    the fixture does not hold them)."""
+    key = f"{cfg.name}__rows_T{T}"
+    with np.load(ZIPF_FIXTURE) as z:
+        return z[key].copy() if key in z.files else None
 
 
 @dataclass
@@ -130,7 +137,7 @@ def make_weights(cfg: MoEConfig, device) -> BlockWeights:
     """Seeded weights for `cfg`, quantised on `device` by this library."""
     s = cfg.seed
     gate_w = _normal((cfg.E, cfg.d), 0.02, device, s, 2)
-    gate_b = zipf_bias(cfg, gate_w, device) if cfg.zipf_alpha else None
+    gate_b = zipf_bias(cfg, device) if cfg.zipf_alpha else None
 
     def qrouter(w):
         if cfg.router_bits == 16:
@@ -267,6 +274,6 @@ def expert_bytes_per_row(cfg: MoEConfig, K_dim: int) -> float:
     return K_dim * weight_bytes_per_element(cfg)
 
 
-__all__ = ["MoEConfig", "CONFIGS", "make_x", "make_weights", "BlockWeights", "zipf_bias",
+__all__ = ["MoEConfig", "CONFIGS", "make_x", "make_weights", "BlockWeights", "zipf_bias", "zipf_rows",
            "clone_weights", "bank_bytes", "rows_per_expert",
            "algorithmic_bytes", "weight_bytes_per_element", "algorithmic_flops", "distinct", "math", "ops"]

@@ -95,3 +95,30 @@ def test_noalloc_refuses_oversize_on_host(pkg):
     assert rc == -1 and "scratch" in C.last_error() and str(T) in C.last_error()
     assert lib.mlxr_moe_block_forward_noalloc(None, None, 1, None, None, None, None) == -1
     assert "null module" in C.last_error()
+
+
+@pytest.mark.parametrize("key", ["c3", "c5"])
+def test_zipf_fixture(pkg, key):
+    """The committed Zipf routing fixture (tests/golden/zipf_routing.npz,
+    written by make_zipf_routing.py): a finite bias per expert, and at
+    every bench T row counts that sum to T*K, never exceed T (top-K picks an
+    expert at most once per token) and follow the Zipf(1.1) order of the
+    seeded permutation (the expert of rank 1 the fullest, the top decile
+    of ranks holding most of the rows)."""
+    import numpy as np
+    W = pkg.workloads
+    cfg = W.CONFIGS[key]
+    b = W.zipf_bias(cfg, "cpu")
+    assert tuple(b.shape) == (cfg.E,) and bool(torch.isfinite(b).all())
+    with np.load(W.ZIPF_FIXTURE) as z:
+        perm = z[f"{cfg.name}__perm"]
+    assert sorted(perm.tolist()) == list(range(cfg.E))
+    for T in cfg.tokens:
+        rows = W.zipf_rows(cfg, T)
+        assert rows is not None and rows.shape == (cfg.E,)
+        assert int(rows.sum()) == T * cfg.K and int(rows.max()) <= T
+        by_rank = rows[perm]
+        assert by_rank[0] == rows.max()
+        if T >= 512:
+            top = by_rank[: cfg.E // 10].sum()
+            assert top > 0.5 * T * cfg.K
