@@ -278,6 +278,37 @@ def measured_traffic(workload: str, kernel: str):
     return data.get("kernels", {}).get(kernel, {}).get("traffic_bytes")
 
 
+def read_ceiling(pkg, dev, chunk, reps=20):
+    """Bytes per second of a plain streaming read (mlxr_moe_profile_read) of
+    `chunk` bytes per launch, the launches rotating over eight chunks of one
+    buffer (more than the 256 MB last-level cache holds, so each reads from
+    HBM), event-timed like the GEMMs: the practical read ceiling of this
+    GPU beside which the GEMMs' rates are set."""
+    import ctypes
+    import torch
+    C = pkg._capi
+    lib = C.lib()
+    chunk = max(16, chunk // 256 * 256)
+    buf = torch.empty(8 * chunk, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    base = buf.data_ptr()
+    for i in range(2):
+        C.check(lib.mlxr_moe_profile_read(base + i * chunk, chunk, sink.data_ptr(), stream))
+    torch.cuda.synchronize()
+    C.check(lib.mlxr_moe_profile_start(b"read_probe"))
+    for i in range(reps):
+        C.check(lib.mlxr_moe_profile_read(base + (i % 8) * chunk, chunk, sink.data_ptr(),
+                                          stream))
+    n = ctypes.c_int64()
+    tot, mn, mx = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    C.check(lib.mlxr_moe_profile_stop(ctypes.byref(n), ctypes.byref(tot), ctypes.byref(mn),
+                                      ctypes.byref(mx)))
+    del buf
+    torch.cuda.empty_cache()
+    return chunk / (tot.value / n.value / 1e3), chunk
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as fh:
@@ -385,6 +416,12 @@ def main():
                     frac=round(achieved / HBM_PEAK_GBS, 4),
                     traffic=measured_traffic(f"{cfg.name} T={T}", "qgemm_gated"),
                     algorithmic_bytes=traffic_alg)
+        # the same byte count read by a kernel that only reads
+        rate, nbytes = read_ceiling(pkg, dev, traffic_alg)
+        roof["read_ceiling"] = dict(gbs=round(rate / 1e9, 1), bytes=nbytes,
+                                    frac_of_ceiling=round(achieved / (rate / 1e9), 4))
+        print(f"bench: plain read of {nbytes} bytes {rate / 1e9:.1f} GB/s", file=sys.stderr,
+              flush=True)
     else:
         achieved = gated_flops(cfg, T, folds_shared(cfg, T)) / kt / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 2), peak=BF16_PEAK_TFLOPS,

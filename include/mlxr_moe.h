@@ -415,14 +415,21 @@ int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,
  * `kernel` is armed, each launch of that kernel is bracketed by HIP events
  * on the stream it is launched on.  Names: "router_logits", "router_topk",
  * "dispatch", "qgemm_gated", "qgemm_down", "combine", the shared
- * expert's GEMMs "shared_gated", "shared_down", and "rms_norm".  NULL
- * disarms.  Not
- * for use while the stream is being captured into a graph. */
+ * expert's GEMMs "shared_gated", "shared_down", "rms_norm", and
+ * "read_probe" (mlxr_moe_profile_read).  NULL disarms.  Not for use while
+ * the stream is being captured into a graph. */
 int mlxr_moe_profile_start(const char* kernel);
 /* Waits for the armed kernel's last launch, returns the number of launches
  * and their elapsed time (total / min / max, milliseconds), and disarms. */
 int mlxr_moe_profile_stop(int64_t* launches, double* total_ms, double* min_ms,
                           double* max_ms);
+/* One plain streaming read of `bytes` (a multiple of 16) from the 16-byte
+ * aligned device buffer `buf` on `stream`, profiled as the kernel
+ * "read_probe": the HBM read rate a kernel that does nothing but read
+ * reaches, measured beside the GEMMs (no counterpart in the reference;
+ * measurement only).  `sink`: one device word it may write. */
+int mlxr_moe_profile_read(const void* buf, size_t bytes, void* sink,
+                          mlxr_moe_stream stream);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,7 @@ SOURCES = [
     "profile.cpp",
     "capi.cpp",
     "noalloc.hip",
+    "probe.hip",
 ]
 
 COMMON = [

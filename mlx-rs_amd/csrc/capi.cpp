@@ -822,7 +822,7 @@ int mlxr_moe_profile_start(const char* kernel) {
                                        "dispatch",      "qgemm_gated",
                                        "qgemm_down",    "combine",
                                        "shared_gated",  "shared_down",
-                                       "rms_norm"};
+                                       "rms_norm",      "read_probe"};
   if (kernel && *kernel) {
     bool known = false;
     for (const char* n : kNames) known = known || std::strcmp(n, kernel) == 0;
@@ -839,6 +839,16 @@ int mlxr_moe_profile_stop(int64_t* launches, double* total_ms, double* min_ms,
   if (profile_collect(launches, total_ms, min_ms, max_ms, &err) != 0)
     return fail(err);
   return 0;
+}
+
+int mlxr_moe_profile_read(const void* buf, size_t bytes, void* sink,
+                          mlxr_moe_stream stream) {
+  if (!buf || !sink) return fail("profile_read: buf and sink are required");
+  if (bytes % 16 || (reinterpret_cast<uintptr_t>(buf) & 15))
+    return fail("profile_read: buf must be 16-byte aligned and bytes a multiple of 16");
+  return finish(from_hip(
+      launch_read_probe(buf, bytes, static_cast<uint32_t*>(sink), as_stream(stream)),
+      "profile_read"));
 }
 
 int mlxr_moe_workspace_status(const void* workspace, size_t workspace_size,

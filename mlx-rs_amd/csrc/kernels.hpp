@@ -294,4 +294,9 @@ hipError_t launch_combine(const uint16_t* y, const void* w, bool w_bf16,
                           int64_t shared_ld, const uint16_t* residual,
                           void* out, bool bf16, hipStream_t s);
 
+// ---------------------------------------------------------------- probe.hip
+// One plain streaming read of bytes (a multiple of 16) from buf, timed as
+// the profile kernel "read_probe"; sink: one device word it may write.
+hipError_t launch_read_probe(const void* buf, size_t bytes, uint32_t* sink, hipStream_t s);
+
 }  // namespace mlxr_moe

@@ -189,3 +189,14 @@ def test_dense_linear_descriptors_validation(pkg):
     assert lib.mlxr_moe_switch_glu_forward(ctypes.byref(mixed), None, 1, None, None, 2, None,
                                            None, 0, None) == -1
     assert "share bits" in _err(pkg)
+
+
+def test_profile_read_validation(pkg):
+    lib, C = pkg._capi.lib(), pkg._capi
+    assert lib.mlxr_moe_profile_read(None, 1024, None, None) == -1
+    assert "buf and sink" in _err(pkg)
+    # a size that is not whole 16-byte vectors, an unaligned buffer
+    assert lib.mlxr_moe_profile_read(16, 1000, 16, None) == -1
+    assert "multiple of 16" in _err(pkg)
+    assert lib.mlxr_moe_profile_read(8, 1024, 16, None) == -1
+    assert "aligned" in _err(pkg)

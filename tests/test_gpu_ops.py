@@ -454,3 +454,28 @@ def test_argpartition_and_softmax(pkg, dev):
     assert torch.allclose(s, torch.softmax(a, -1), rtol=1e-5, atol=1e-7)
     with pytest.raises(pkg.MlxrMoeError):
         pkg.ops.argpartition_axis(a, 128, -1)
+
+
+# ------------------------------------------------------- read probe
+def test_profile_read_times_one_launch_per_call(pkg, dev):
+    """The plain read of the bench's read ceiling: one profiled launch per
+    call, a positive time, the buffer unchanged, the sink written only on
+    the sentinel (never for this data)."""
+    C = pkg._capi
+    lib = C.lib()
+    buf = torch.arange(1 << 20, dtype=torch.int32, device=dev)  # 4 MiB
+    keep = buf.clone()
+    sink = torch.full((1,), 7, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    C.check(lib.mlxr_moe_profile_start(b"read_probe"))
+    for _ in range(3):
+        C.check(lib.mlxr_moe_profile_read(buf.data_ptr(), buf.numel() * 4, sink.data_ptr(),
+                                          stream))
+    n = ctypes.c_int64()
+    tot, mn, mx = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    C.check(lib.mlxr_moe_profile_stop(ctypes.byref(n), ctypes.byref(tot), ctypes.byref(mn),
+                                      ctypes.byref(mx)))
+    assert n.value == 3 and 0.0 < mn.value <= mx.value
+    torch.cuda.synchronize(dev)
+    assert torch.equal(buf, keep)
+    assert sink.item() == 7
