@@ -56,21 +56,42 @@ __device__ __forceinline__ WRow router_row(const RouterWeights& rw, int e,
 // Weights j..j+3 of a row (j % 4 == 0): four f32, four bf16 (BITS 16: a
 // dense bf16 Linear), or four codes (one word at 8 bits, half a word at 4,
 // little end first) dequantised in f32 as fmaf(code, scale, bias) with the
-// scale and bias of group j / 64.
+// scale and bias of group j / 64.  In two steps: router_raw4 only loads
+// (the words as stored, and for codes the group's scale and bias bits),
+// router_cvt4 only computes.  The kernels hold the raw words while the
+// loads are in flight and convert them where they use them (a conversion
+// next to its load would wait for the load there).  All-zero words convert
+// to four zeros.
+struct WRaw4 {
+  uint32_t a, b, c, d;
+};
 template <int BITS>
-__device__ __forceinline__ float4 router_w4(const WRow& r, int j) {
+__device__ __forceinline__ WRaw4 router_raw4(const WRow& r, int j) {
   if constexpr (BITS == 0) {
-    return *reinterpret_cast<const float4*>(static_cast<const float*>(r.w) + j);
+    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const float*>(r.w) + j);
+    return WRaw4{u.x, u.y, u.z, u.w};
   } else if constexpr (BITS == 16) {
     const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(r.w) + j);
-    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                       __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+    return WRaw4{u.x, u.y, 0u, 0u};
   } else {
     const uint8_t* p = static_cast<const uint8_t*>(r.w);
     const uint32_t c = BITS == 8
                            ? *reinterpret_cast<const uint32_t*>(p + j)
                            : (uint32_t)*reinterpret_cast<const uint16_t*>(p + j / 2);
-    const float sc = bf16_to_f32(r.s[j >> 6]), bi = bf16_to_f32(r.b[j >> 6]);
+    return WRaw4{c, (uint32_t)r.s[j >> 6], (uint32_t)r.b[j >> 6], 0u};
+  }
+}
+template <int BITS>
+__device__ __forceinline__ float4 router_cvt4(const WRaw4& w) {
+  if constexpr (BITS == 0) {
+    return make_float4(__uint_as_float(w.a), __uint_as_float(w.b), __uint_as_float(w.c),
+                       __uint_as_float(w.d));
+  } else if constexpr (BITS == 16) {
+    return make_float4(__uint_as_float(w.a << 16), __uint_as_float(w.a & 0xffff0000u),
+                       __uint_as_float(w.b << 16), __uint_as_float(w.b & 0xffff0000u));
+  } else {
+    const uint32_t c = w.a;
+    const float sc = __uint_as_float(w.b << 16), bi = __uint_as_float(w.c << 16);
     constexpr uint32_t m = (1u << BITS) - 1u;
     return make_float4(__builtin_fmaf((float)(c & m), sc, bi),
                        __builtin_fmaf((float)((c >> BITS) & m), sc, bi),
@@ -142,7 +163,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 
   const int steps = (d + 255) / 256;
   for (int i0 = 0; i0 < steps; i0 += U) {
-    float4 wv[U][EB];
+    WRaw4 wv[U][EB];
     uint2 xv[U][TB];
     uint2 nwv[U];
 #pragma unroll
@@ -151,8 +172,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
       const bool in = j < d;
 #pragma unroll
       for (int q = 0; q < EB; ++q)
-        wv[u][q] = (in && wrow[q].w) ? router_w4<BITS>(wrow[q], j)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[u][q] = (in && wrow[q].w) ? router_raw4<BITS>(wrow[q], j) : WRaw4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int tt = 0; tt < TB; ++tt)
         xv[u][tt] = in ? *reinterpret_cast<const uint2*>(xrow[tt] + j)
@@ -164,6 +184,9 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     // elements past d contribute fmaf(0, 0, acc) = acc exactly
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      float4 wf[EB];
+#pragma unroll
+      for (int q = 0; q < EB; ++q) wf[q] = router_cvt4<BITS>(wv[u][q]);
 #pragma unroll
       for (int tt = 0; tt < TB; ++tt) {
         if constexpr (NORM) {
@@ -189,10 +212,10 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 #pragma unroll
         for (int q = 0; q < EB; ++q) {
           float a = acc[q][tt];
-          a = __builtin_fmaf(x0, wv[u][q].x, a);
-          a = __builtin_fmaf(x1, wv[u][q].y, a);
-          a = __builtin_fmaf(x2, wv[u][q].z, a);
-          a = __builtin_fmaf(x3, wv[u][q].w, a);
+          a = __builtin_fmaf(x0, wf[q].x, a);
+          a = __builtin_fmaf(x1, wf[q].y, a);
+          a = __builtin_fmaf(x2, wf[q].z, a);
+          a = __builtin_fmaf(x3, wf[q].w, a);
           acc[q][tt] = a;
         }
       }
@@ -259,7 +282,7 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
 #pragma unroll
   for (int k = 0; k < 4; ++k) wp[k] = router_row<BITS>(rw, e0 + ((tid + 256 * k) >> 6), E, d);
   u32x4_t xr[XK];
-  float4 wr[4];
+  WRaw4 wr[4];  // raw: converted when staged, so the loads stay in flight
   auto fetch = [&](int i) {
     const int j0 = 256 * i;
 #pragma unroll
@@ -273,8 +296,8 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
     for (int k = 0; k < 4; ++k) {
       const int id = tid + 256 * k;
       wr[k] = (wp[k].w && j0 + (id & 63) * 4 < d)
-                  ? router_w4<BITS>(wp[k], j0 + (id & 63) * 4)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+                  ? router_raw4<BITS>(wp[k], j0 + (id & 63) * 4)
+                  : WRaw4{0u, 0u, 0u, 0u};
     }
   };
   const int steps = (d + 255) / 256;
@@ -288,7 +311,7 @@ __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int id = tid + 256 * k;
-      *reinterpret_cast<float4*>(&ws[id >> 6][(id & 63) * 4]) = wr[k];
+      *reinterpret_cast<float4*>(&ws[id >> 6][(id & 63) * 4]) = router_cvt4<BITS>(wr[k]);
     }
     __syncthreads();
     if (i + 1 < steps) fetch(i + 1);
