@@ -118,17 +118,16 @@ __device__ __forceinline__ float router_finish(float v, const float* bias,
 // rms_norm_kernel does before its FMA, so the logits and the normalised rows
 // are bit-identical to the two-kernel sequence; the first wave of the first
 // expert block also writes the normalised rows (nm.out) for the experts.
+// router_logits_wave is one wave's share: columns e0 .. e0 + EB - 1 for
+// tokens t0 .. t0 + TB - 1 (those below T; t0 < T); `writer`: this wave
+// also writes the normalised rows.
 template <int EB, int TB, int U, int BITS, bool NORM>
-__global__ __launch_bounds__(256) void router_logits_kernel(
-    const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
+__device__ __forceinline__ void router_logits_wave(
+    const uint16_t* __restrict__ x, int T, int d, const RouterWeights& rw,
     const float* __restrict__ bias, int E, float* __restrict__ logits,
-    int64_t ld, const RouterNorm nm) {
+    int64_t ld, const RouterNorm& nm, int e0, int t0, bool writer) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int e_tot = E + (rw.w_extra ? 1 : 0);
-  const int e0 = (blockIdx.x * 4 + wave) * EB;
-  if (e0 >= e_tot) return;
-  const int t0 = blockIdx.y * TB;
   const int nt = min(TB, T - t0);
 
   WRow wrow[EB];
@@ -144,7 +143,6 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt) acc[q][tt] = 0.0f;
   float rs[TB];
-  const bool writer = NORM && nm.out && blockIdx.x == 0 && wave == 0;
   if constexpr (NORM) {
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt) {
@@ -233,6 +231,19 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   }
 }
 
+template <int EB, int TB, int U, int BITS, bool NORM>
+__global__ __launch_bounds__(256) void router_logits_kernel(
+    const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
+    const float* __restrict__ bias, int E, float* __restrict__ logits,
+    int64_t ld, const RouterNorm nm) {
+  const int wave = threadIdx.x >> 6;
+  const int e0 = (blockIdx.x * 4 + wave) * EB;
+  if (e0 >= E + (rw.w_extra ? 1 : 0)) return;
+  router_logits_wave<EB, TB, U, BITS, NORM>(x, T, d, rw, bias, E, logits, ld, nm, e0,
+                                            blockIdx.y * TB,
+                                            NORM && nm.out && blockIdx.x == 0 && wave == 0);
+}
+
 // Many tokens: one workgroup computes 32 tokens x 16 logit columns.  Each
 // 256-wide step of d is staged in LDS (x as bf16, the weights as f32; the
 // next step's loads are in flight in registers meanwhile) and every wave
@@ -245,12 +256,25 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 // kRtCol experts x 4 * WT tokens per workgroup (WT tokens per wave: 8, or
 // 4 where 8 would leave CUs idle)
 constexpr int kRtCol = 16;
+// With `extra` the grid's last column of workgroups computes one more logit
+// column (weights rx, written at lx): the lone extra column (the shared
+// expert's gate beside 16k experts) in router_logits_wave's lane order, WT
+// tokens per wave, instead of a round of 16-column blocks or a launch of
+// its own.
 template <int BITS, int WT>
 __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
     const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
     const float* __restrict__ bias, int E, float* __restrict__ logits,
-    int64_t ld) {
+    int64_t ld, bool extra, const RouterWeights rx, float* __restrict__ lx) {
   constexpr int kRtTok = 4 * WT, kRtWaveTok = WT;
+  if (extra && blockIdx.x == gridDim.x - 1) {
+    const int t0 = (int)blockIdx.y * kRtTok + (int)(threadIdx.x >> 6) * WT;
+    if (t0 < T)
+      router_logits_wave<1, WT, 2, BITS, false>(x, T, d, rx, nullptr, 1, lx, ld,
+                                                RouterNorm{nullptr, 0.0f, nullptr}, 0, t0,
+                                                false);
+    return;
+  }
   constexpr int XK = kRtTok / 8;  // 16-byte x chunks per thread per step
   constexpr int CPR = 32 / WT;    // columns per round of the final sums
   static_assert(WT == 4 || WT == 8, "tokens per wave");
@@ -631,9 +655,9 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
       MLXR_RL_N(MLXR_RL_MID_EB, MLXR_RL_MID_TB, MLXR_RL_MID_U, false);
   } else {
     // A lone extra column (the shared expert's gate beside 16k experts)
-    // would add a round of whole column blocks: the tiled kernel takes the
-    // E expert columns and the per-wave kernel the extra one (the same
-    // lane order and butterfly, so the same bits).
+    // would add a round of whole column blocks: the tiled blocks take the
+    // E expert columns and per-wave code the extra one (the same lane order
+    // and butterfly, so the same bits).
     const bool split = w.w_extra && e_tot % kRtCol == 1;
     RouterWeights wm = w;
     if (split) wm.w_extra = nullptr, wm.scales_extra = nullptr, wm.biases_extra = nullptr;
@@ -641,17 +665,27 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     // 8 tokens per wave, or 4 where 8 would make fewer workgroups than
     // the GPU's 2 x 256 slots (c3 T=512: 128 workgroups)
     const int64_t cb = (cols + kRtCol - 1) / kRtCol;
-    if (cb * ((T + 31) / 32) >= 512)
+    // The extra column, when split off: one more column of workgroups in
+    // the same grid while the grid fits the GPU's workgroup slots at once
+    // (two per CU at 8 tokens per wave, three at 4: the registers allow no
+    // more; c6 T=512 logits 23.5 to 21.1 µs); on a larger grid those light
+    // workgroups would add a round of slots (c6 T=2048 57.0 to 63.1 µs), so
+    // there they run as a launch of their own after it.
+    const RouterWeights we{w.bits, w.w_extra, w.scales_extra, w.biases_extra,
+                           nullptr, nullptr, nullptr};
+    const bool wt8 = cb * ((T + 31) / 32) >= 512;
+    const int64_t rows = wt8 ? (T + 31) / 32 : (T + 15) / 16;
+    const bool fold = split && (cb + 1) * rows <= (wt8 ? 512 : 768);
+    const unsigned gx = (unsigned)cb + (fold ? 1u : 0u);
+    if (wt8)
       router_logits_tiled_kernel<BITS, 8>
-          <<<dim3((unsigned)cb, (unsigned)((T + 31) / 32)), 256, 0, s>>>(
-              x, (int)T, (int)d, wm, bias, (int)E, logits, ld);
+          <<<dim3(gx, (unsigned)rows), 256, 0, s>>>(
+              x, (int)T, (int)d, wm, bias, (int)E, logits, ld, fold, we, logits + E);
     else
       router_logits_tiled_kernel<BITS, 4>
-          <<<dim3((unsigned)cb, (unsigned)((T + 15) / 16)), 256, 0, s>>>(
-              x, (int)T, (int)d, wm, bias, (int)E, logits, ld);
-    if (split) {
-      const RouterWeights we{w.bits, w.w_extra, w.scales_extra, w.biases_extra,
-                             nullptr, nullptr, nullptr};
+          <<<dim3(gx, (unsigned)rows), 256, 0, s>>>(
+              x, (int)T, (int)d, wm, bias, (int)E, logits, ld, fold, we, logits + E);
+    if (split && !fold) {
       constexpr int kTB = MLXR_RL_MID_TB;
       router_logits_kernel<1, kTB, 2, BITS, false>
           <<<dim3(1u, (unsigned)((T + kTB - 1) / kTB)), 256, 0, s>>>(
