@@ -575,3 +575,50 @@ def test_zipf_routing_matches_fixture(pkg, dev, cfg):
         got = torch.bincount(block.last_indices.reshape(-1).long(), minlength=bw.cfg.E)
         print(f"  zipf rows {cfg} T={T}: max {int(got.max())}", flush=True)
         assert np.array_equal(got.cpu().numpy(), want)
+
+
+# Largest sizes of the suite, sampled: each token's output depends on its own
+# row only (routing and every expert product are per token), so the oracle
+# runs on a seeded sample of the rows, with the numerics the library picks at
+# the full T.  (point, T, sampled tokens, elements past 2e-2 * RMS allowed:
+# the measured count, as PAST_BAR)
+LARGE_T = [("c2", 16384, 256, 0), ("c6", 8192, 256, 1)]
+
+
+@pytest.mark.parametrize("cfg,T,n,allowed", LARGE_T)
+def test_block_parity_large_T_sampled(pkg, orc, dev, cfg, T, n, allowed):
+    """c2 at T = 16384 (131072 routed rows: the three-kernel dispatch, 512
+    M-tiles of 256 rows, the largest x, activations and y buffers of the
+    suite) and the Qwen3.6 block at T = 8192 (the folded shared expert,
+    8-bit router) against the oracle on n of their tokens, the first and the
+    last among them: routing bit-exact, values within check_block's bar."""
+    bw = weights(pkg, cfg, dev)
+    c = bw.cfg
+    x = pkg.workloads.make_x(c, T, dev, seed=T)
+    block = bw.block()
+    print(f"  large T {cfg} T={T}", flush=True)
+    out = block(x)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(T)
+    sel = np.unique(np.concatenate([[0, T - 1], rng.choice(T, n - 2, replace=False)]))
+    tiled = (pkg.ops.gather_qmm_tiled(T * c.K, c.E), pkg.ops.gather_qmm_tiled(T, 1))
+    ref, ridx, rw = orc.block_forward(orc.block_params(bw), orc.to_np(x)[sel], nthreads=16,
+                                      tiled=tiled)
+    assert np.array_equal(block.last_indices.cpu().numpy()[sel], ridx), "routing indices differ"
+    if c.router_bits:
+        assert np.array_equal(block.last_weights.cpu().numpy()[sel], rw)
+        got = orc.bf16_to_f32(orc.to_np(out)[sel]).astype(np.float64)
+        ref = orc.bf16_to_f32(ref).astype(np.float64)
+    else:
+        assert np.allclose(block.last_weights.cpu().numpy()[sel], rw, rtol=2e-6, atol=1e-7)
+        got = out.cpu().numpy()[sel].astype(np.float64)
+    rms = np.sqrt(np.mean(ref ** 2))
+    diff = np.abs(got - ref)
+    rec = record_parity(c.name + " sampled", T, got, ref, rms, allowed)
+    if c.router_bits:
+        assert np.all(diff <= 2e-2 * rms + _step(ref))
+    assert rec["past_bar"] <= rec["past_bar_allowed"]
+    assert np.quantile(diff, 0.999) <= 1e-2 * rms
+    assert pkg.ops.workspace_status(block.last_workspace) == 0
+    del out, block, bw
+    torch.cuda.empty_cache()
