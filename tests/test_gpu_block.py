@@ -650,7 +650,11 @@ def test_block_parity_large_T_sampled(pkg, orc, dev, cfg, T, n, allowed):
 SWEEP = {("c2", 4): 0, ("c2", 17): 0, ("c2", 33): 0, ("c2", 129): 0, ("c2", 257): 0,
          ("c2", 383): 0, ("c2", 777): 0,
          ("c6", 2): 0, ("c6", 17): 0, ("c6", 100): 0, ("c6", 257): 5, ("c6", 300): 2,
-         ("c6", 700): 11, ("c6", 1100): 11}
+         ("c6", 700): 11, ("c6", 1100): 11,
+         ("c4", 7): 0, ("c4", 130): 0, ("c4", 1000): 21,
+         ("c5", 9): 0, ("c5", 100): 0, ("c5", 300): 0,
+         ("c7", 9): 0, ("c7", 200): 0, ("c7", 1000): 0,
+         ("c8", 9): 0, ("c8", 200): 2, ("c8", 1000): 10}
 
 
 @pytest.mark.parametrize("cfg,T", sorted(SWEEP))
