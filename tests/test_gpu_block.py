@@ -654,7 +654,8 @@ SWEEP = {("c2", 4): 0, ("c2", 17): 0, ("c2", 33): 0, ("c2", 129): 0, ("c2", 257)
          ("c4", 7): 0, ("c4", 130): 0, ("c4", 1000): 21,
          ("c5", 9): 0, ("c5", 100): 0, ("c5", 300): 0,
          ("c7", 9): 0, ("c7", 200): 0, ("c7", 1000): 0,
-         ("c8", 9): 0, ("c8", 200): 2, ("c8", 1000): 10}
+         ("c8", 9): 0, ("c8", 200): 2, ("c8", 1000): 10,
+         ("c3", 1000): 0, ("c3", 1100): 0, ("c3", 3000): 0, ("c3", 3100): 0}
 
 
 @pytest.mark.parametrize("cfg,T", sorted(SWEEP))
