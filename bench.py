@@ -58,7 +58,53 @@ def parse():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, 20 times (the "
                          "known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--dense-gemm", action="store_true",
+                    help="only time the vendor library's dense bf16 batched GEMM "
+                         "(torch.bmm) at --config/--tokens' expert shapes, the routed "
+                         "rows spread evenly over the experts: the practical ceiling "
+                         "the quantized prefill GEMMs are set beside")
     return ap.parse_args()
+
+
+def dense_gemm_reference(cfg, T: int, reps: int = 50) -> None:
+    """Event-timed torch.bmm (hipBLASLt) in bf16 at the expert shapes of one
+    block forward: [E, rows, d] x [E, d, 2f] (gate and up as one product) and
+    [E, rows, f] x [E, f, d], rows = T*K/E per expert, uniform -- no gather,
+    no skew, no dequantisation, no SwiGLU -- and the same rows as one flat
+    [E*rows, k] x [k, n] product of a single weight matrix (no expert
+    structure).  One JSON line per projection and form."""
+    import torch
+    dev = torch.device("cuda:0")
+    rows = max(1, T * cfg.K // cfg.E)
+    for name, k, n in (("gate_up", cfg.d, 2 * cfg.f), ("down", cfg.f, cfg.d)):
+        a = torch.randn(cfg.E, rows, k, device=dev, dtype=torch.bfloat16)
+        b = torch.randn(cfg.E, k, n, device=dev, dtype=torch.bfloat16).contiguous()
+        o = torch.empty(cfg.E, rows, n, device=dev, dtype=torch.bfloat16)
+        a2, b2 = a.reshape(cfg.E * rows, k), b[0].contiguous()
+        o2 = o.reshape(cfg.E * rows, n)
+        flops = 2.0 * cfg.E * rows * k * n
+        for form, fn, shape in (
+                ("torch.bmm bf16", lambda: torch.bmm(a, b, out=o), [cfg.E, rows, k, n]),
+                ("torch.mm bf16 flat", lambda: torch.mm(a2, b2, out=o2),
+                 [cfg.E * rows, k, n])):
+            for _ in range(5):
+                fn()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(reps):
+                fn()
+            t1.record()
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) / reps * 1e3
+            print(json.dumps({"library_gemm": form, "config": cfg.name, "tokens": T,
+                              "projection": name, "shape": shape, "us": round(us, 1),
+                              "tflops": round(flops / us / 1e6, 1),
+                              "frac_of_bf16_peak": round(flops / us / 1e6 / BF16_PEAK_TFLOPS,
+                                                         3)}),
+                  flush=True)
+        del a, b, o, a2, b2, o2
+    torch.cuda.empty_cache()
 
 
 def copy_calibration(mib: int) -> None:
@@ -367,6 +413,9 @@ def main():
     dev = torch.device("cuda:0")
     W = pkg.workloads
     cfg = W.CONFIGS[args.config]
+    if args.dense_gemm:
+        dense_gemm_reference(cfg, args.tokens)
+        return
     T = args.tokens
     print(f"bench: {cfg.name} T={T} on {torch.cuda.get_device_name(dev)}", file=sys.stderr,
           flush=True)

@@ -24,7 +24,7 @@ def test_help_lists_the_driver_options_and_the_sweep_forms():
     r = _run("--help")
     assert r.returncode == 0
     for opt in ("--gpus", "--steps", "--warmup", "--sweep", "--cpu-seconds",
-                "--forwards-per-graph"):
+                "--forwards-per-graph", "--dense-gemm"):
         assert opt in r.stdout
     assert "cfg:T:res" in r.stdout
 
