@@ -24,6 +24,11 @@ namespace mlxr_moe {
 namespace {
 
 constexpr int kWaves = kDispatchBlock / 64;
+// tokens per workgroup of route_fused_kernel (a wave each; the other waves
+// only join the sort of the last workgroup)
+#ifndef MLXR_ROUTE_FUSED_TPW
+#define MLXR_ROUTE_FUSED_TPW 4
+#endif
 #ifndef MLXR_ROUTE_SMALL_TOKENS
 #define MLXR_ROUTE_SMALL_TOKENS 16
 #endif
@@ -245,6 +250,57 @@ __global__ __launch_bounds__(kDispatchBlock) void route_wave_kernel(
   }
 }
 
+// Decode routing of 16 < T tokens whose T * K ids fit one workgroup, in one
+// launch: a wave per token for the top-K (MLXR_ROUTE_FUSED_TPW tokens per
+// workgroup: spread over as many CUs as the separate top-K kernel), then the
+// workgroup that finishes last runs the counting sort of all T * K ids.
+// Measured against the top-K kernel plus the one-workgroup sort (graph steps
+// of 8 forwards): c2 T=64 97.3 to 95.8 µs, c2 T=32 82.0 to 80.7, c4 T=64
+// 185.2 to 183.9, c6 T=64 125.8 to 124.1; 16 tokens per workgroup lost at
+// c4 T=64 (185.2 to 188.7).
+// Every workgroup stores its ids with agent-scope atomic stores (written
+// through to where every XCD reads them), waits until those stores have
+// completed, then adds one to *counter; the workgroup whose add returns
+// gridDim.x - 1 reads the ids back with agent-scope atomic loads.  No release
+// or acquire fence: on this part those write back and invalidate the whole
+// L2.  *counter is 0 when the launch starts (the logits launch before it
+// clears it); the status word is cleared and set by the last workgroup only.
+template <int SLOTS, bool BF16>
+__global__ __launch_bounds__(kDispatchBlock) void route_fused_kernel(
+    const float* __restrict__ logits, int64_t ld, int T, int E, int K,
+    int32_t* idx, float* __restrict__ wts, int tile_rows, DispatchBuffers b,
+    int32_t* counter) {
+  __shared__ DispatchScratch ls;
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = (int)blockIdx.x * MLXR_ROUTE_FUSED_TPW + wave;
+  if (wave < MLXR_ROUTE_FUSED_TPW && t < T) {
+    int id;
+    float wt;
+    wave_topk<SLOTS, BF16>(logits + (int64_t)t * ld, E, K, nullptr, &id, &wt);
+    if (lane < K) {
+      __hip_atomic_store(idx + (int64_t)t * K + lane, id, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      wts[(int64_t)t * K + lane] = wt;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (int)gridDim.x - 1;
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0) *b.status = 0;
+  __syncthreads();
+  const int n = T * K;
+  const int id = (int)threadIdx.x < n
+                     ? __hip_atomic_load(idx + threadIdx.x, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT)
+                     : -1;
+  block_dispatch(id, n, E, tile_rows, b, &ls);
+}
+
 __global__ __launch_bounds__(256) void dispatch_identity_kernel(
     int n, int tile_rows, DispatchBuffers b) {
   const int tid = threadIdx.x;
@@ -363,11 +419,41 @@ void route_small_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
 #undef MLXR_RS
 }
 
+template <bool BF16>
+void route_fused_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
+                        int64_t K, int32_t* idx, float* wts, int tile_rows,
+                        const DispatchBuffers& b, int32_t* counter, hipStream_t s) {
+  const int slots = (int)((E + 63) / 64);
+  const unsigned grid = (unsigned)((T + MLXR_ROUTE_FUSED_TPW - 1) / MLXR_ROUTE_FUSED_TPW);
+#define MLXR_RF(S)                                                                 \
+  route_fused_kernel<S, BF16><<<grid, kDispatchBlock, 0, s>>>(                     \
+      logits, ld, (int)T, (int)E, (int)K, idx, wts, tile_rows, b, counter)
+  if (slots <= 1)
+    MLXR_RF(1);
+  else if (slots <= 2)
+    MLXR_RF(2);
+  else if (slots <= 4)
+    MLXR_RF(4);
+  else if (slots <= 8)
+    MLXR_RF(8);
+  else
+    MLXR_RF(16);
+#undef MLXR_RF
+}
+
 hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
                         int64_t K, bool bf16, int32_t* idx, float* wts,
                         int tile_rows, const DispatchBuffers& b,
-                        hipStream_t s) {
+                        hipStream_t s, int32_t* counter) {
   if (T == 0) return launch_zero_status(b.status, s);
+  if (counter && T > MLXR_ROUTE_SMALL_TOKENS && T * K <= kDispatchBlock) {
+    ProfileScope prof("router_topk", s);
+    if (bf16)
+      route_fused_launch<true>(logits, ld, T, E, K, idx, wts, tile_rows, b, counter, s);
+    else
+      route_fused_launch<false>(logits, ld, T, E, K, idx, wts, tile_rows, b, counter, s);
+    return hipGetLastError();
+  }
   // one workgroup while the T*K ids fit it and its 16 waves have at most
   // MLXR_ROUTE_SMALL_TOKENS / 16 tokens each; beyond that the top-k spreads
   // over the GPU (a wave per token) before the sort

@@ -68,11 +68,13 @@ struct RouterNorm {
 // column E from the extra row.  Quantised weights give bf16 logits (stored
 // as their f32 values).  ld = row stride of logits.  With norm, the logits
 // of rms_norm(x) (and the normalised rows in norm->out), bit-identical to
-// launch_rms_norm followed by this call on its output.
+// launch_rms_norm followed by this call on its output.  With clear, the
+// launch also sets *clear to 0 (the routing counter of launch_route).
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 const RouterWeights& w, const float* bias,
                                 int64_t E, float* logits, int64_t ld,
-                                hipStream_t s, const RouterNorm* norm = nullptr);
+                                hipStream_t s, const RouterNorm* norm = nullptr,
+                                int32_t* clear = nullptr);
 // One wave per token; clears *status first when status != nullptr.  bf16:
 // the logits are bf16 and the selection is on their bf16 probabilities,
 // with bf16 weights (stored as f32).
@@ -145,13 +147,19 @@ hipError_t launch_zero_status(int32_t* status, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
                            int tile_rows, const DispatchBuffers& b,
                            bool reset_status, hipStream_t s);
+// The one-launch routing (route_fused_kernel) for the block forward.
+#ifndef MLXR_ROUTE_FUSED
+#define MLXR_ROUTE_FUSED 1
+#endif
 // Top-K + renormalised weights of every token from its logits, then the
 // counting sort of the T*K ids, clearing *b.status first.  T <= 16 runs as
-// one workgroup; larger T as the top-k kernel plus launch_dispatch.
+// one workgroup; larger T as the top-k kernel plus launch_dispatch, or, with
+// counter (an int that is 0 when this launch starts) and T*K <= 1024, as one
+// launch whose last workgroup sorts.
 hipError_t launch_route(const float* logits, int64_t ld, int64_t T, int64_t E,
                         int64_t K, bool bf16, int32_t* idx, float* wts,
                         int tile_rows, const DispatchBuffers& b,
-                        hipStream_t s);
+                        hipStream_t s, int32_t* counter = nullptr);
 // gather_qmm helper: per flat row r = b*M + m the expert id and x row.
 hipError_t launch_gather_prep(const uint32_t* lhs, const uint32_t* rhs,
                               int64_t B, int64_t M, int64_t x_batch, int64_t E,

@@ -522,15 +522,18 @@ Status Qwen35MoeBlock::forward(const uint16_t* x, int64_t T, void* out,
                        static_cast<const uint16_t*>(sg.scales),
                        static_cast<const uint16_t*>(sg.biases)};
   }
+  // the routing counter of the one-launch top-K and sort: the status
+  // word's slot has room beside it, and the logits launch clears it
+  int32_t* route_counter = MLXR_ROUTE_FUSED ? status + 1 : nullptr;
   Status st = from_hip(
-      launch_router_logits(x, T, d, rw, b_.gate_bias, E, logits, ld, s, norm),
+      launch_router_logits(x, T, d, rw, b_.gate_bias, E, logits, ld, s, norm, route_counter),
       "router logits");
   if (!st.ok) return st;
   if (norm) x = norm->out;  // the experts read the normalised rows
   // softmax, argpartition top-k, renormalise (moe.rs:124-138) + gather_sort
   st = from_hip(launch_route(logits, ld, T, E, K, bf16, idx, wts,
                              prefill_tile_rows(T * K, E, b_.switch_mlp.gate_proj.bits),
-                             db, s),
+                             db, s, route_counter),
                 "router top-k / dispatch");
   if (!st.ok) return st;
   const SplitSwitchFfn mlp(b_.switch_mlp);

@@ -235,8 +235,9 @@ template <int EB, int TB, int U, int BITS, bool NORM>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
     const float* __restrict__ bias, int E, float* __restrict__ logits,
-    int64_t ld, const RouterNorm nm) {
+    int64_t ld, const RouterNorm nm, int32_t* __restrict__ clear) {
   const int wave = threadIdx.x >> 6;
+  if (clear && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *clear = 0;
   const int e0 = (blockIdx.x * 4 + wave) * EB;
   if (e0 >= E + (rw.w_extra ? 1 : 0)) return;
   router_logits_wave<EB, TB, U, BITS, NORM>(x, T, d, rw, bias, E, logits, ld, nm, e0,
@@ -265,8 +266,10 @@ template <int BITS, int WT>
 __global__ __launch_bounds__(256) void router_logits_tiled_kernel(
     const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
     const float* __restrict__ bias, int E, float* __restrict__ logits,
-    int64_t ld, bool extra, const RouterWeights rx, float* __restrict__ lx) {
+    int64_t ld, bool extra, const RouterWeights rx, float* __restrict__ lx,
+    int32_t* __restrict__ clear) {
   constexpr int kRtTok = 4 * WT, kRtWaveTok = WT;
+  if (clear && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *clear = 0;
   if (extra && blockIdx.x == gridDim.x - 1) {
     const int t0 = (int)blockIdx.y * kRtTok + (int)(threadIdx.x >> 6) * WT;
     if (t0 < T)
@@ -610,7 +613,7 @@ template <int BITS>
 void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
                           const RouterWeights& w, const float* bias, int64_t E,
                           float* logits, int64_t ld, const RouterNorm* norm,
-                          hipStream_t s) {
+                          hipStream_t s, int32_t* clear) {
   const int64_t e_tot = E + (w.w_extra ? 1 : 0);
   const RouterNorm nm = norm ? *norm : RouterNorm{nullptr, 0.0f, nullptr};
   // Enough waves to have every CU pulling router weights at small T, and
@@ -619,7 +622,7 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
   router_logits_kernel<EB, TB, U, BITS, N>                                   \
       <<<dim3((unsigned)((e_tot + 4 * EB - 1) / (4 * EB)),                   \
               (unsigned)((T + TB - 1) / TB)),                                \
-         256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld, nm)
+         256, 0, s>>>(x, (int)T, (int)d, w, bias, (int)E, logits, ld, nm, clear)
 #define MLXR_RL(EB, TB, U)           \
   if (norm)                          \
     MLXR_RL_N(EB, TB, U, true);      \
@@ -680,16 +683,18 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     if (wt8)
       router_logits_tiled_kernel<BITS, 8>
           <<<dim3(gx, (unsigned)rows), 256, 0, s>>>(
-              x, (int)T, (int)d, wm, bias, (int)E, logits, ld, fold, we, logits + E);
+              x, (int)T, (int)d, wm, bias, (int)E, logits, ld, fold, we, logits + E,
+              clear);
     else
       router_logits_tiled_kernel<BITS, 4>
           <<<dim3(gx, (unsigned)rows), 256, 0, s>>>(
-              x, (int)T, (int)d, wm, bias, (int)E, logits, ld, fold, we, logits + E);
+              x, (int)T, (int)d, wm, bias, (int)E, logits, ld, fold, we, logits + E,
+              clear);
     if (split && !fold) {
       constexpr int kTB = MLXR_RL_MID_TB;
       router_logits_kernel<1, kTB, 2, BITS, false>
           <<<dim3(1u, (unsigned)((T + kTB - 1) / kTB)), 256, 0, s>>>(
-              x, (int)T, (int)d, we, nullptr, 1, logits + E, ld, nm);
+              x, (int)T, (int)d, we, nullptr, 1, logits + E, ld, nm, nullptr);
     }
   }
 #undef MLXR_RL
@@ -723,20 +728,20 @@ void router_topk_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 const RouterWeights& w, const float* bias,
                                 int64_t E, float* logits, int64_t ld,
-                                hipStream_t s, const RouterNorm* norm) {
+                                hipStream_t s, const RouterNorm* norm, int32_t* clear) {
   if (T == 0) return hipSuccess;
   if (w.bits != 0 && w.bits != 4 && w.bits != 8 && w.bits != 16)
     return hipErrorInvalidValue;
   if (norm && (!norm->w || !norm->out || d % 4)) return hipErrorInvalidValue;
   ProfileScope prof("router_logits", s);
   if (w.bits == 16)
-    router_logits_launch<16>(x, T, d, w, bias, E, logits, ld, norm, s);
+    router_logits_launch<16>(x, T, d, w, bias, E, logits, ld, norm, s, clear);
   else if (w.bits == 8)
-    router_logits_launch<8>(x, T, d, w, bias, E, logits, ld, norm, s);
+    router_logits_launch<8>(x, T, d, w, bias, E, logits, ld, norm, s, clear);
   else if (w.bits == 4)
-    router_logits_launch<4>(x, T, d, w, bias, E, logits, ld, norm, s);
+    router_logits_launch<4>(x, T, d, w, bias, E, logits, ld, norm, s, clear);
   else
-    router_logits_launch<0>(x, T, d, w, bias, E, logits, ld, norm, s);
+    router_logits_launch<0>(x, T, d, w, bias, E, logits, ld, norm, s, clear);
   return hipGetLastError();
 }
 

@@ -376,6 +376,30 @@ def test_block_token_permutation_equivariance(pkg, dev):
     assert torch.equal(c, a[perm])
 
 
+@pytest.mark.parametrize("cfg", ["c2", "c4", "c6"])
+def test_block_routing_counter_in_dirty_reused_workspace(pkg, dev, cfg):
+    """Routing of 16 < T tokens whose T*K ids fit one workgroup runs as one
+    launch whose last workgroup to finish sorts the ids; it counts finished
+    workgroups in the workspace word after the status word, which the logits
+    launch clears.  One workspace filled with garbage, then reused for
+    forwards of T = 64, 17, 33 and 64 tokens, gives every forward's output,
+    indices and weights bit for bit as a zeroed workspace of its own does."""
+    bw = weights(pkg, cfg, dev)
+    block = bw.block()
+    Ts = [64, 17, 33, 64]
+    xs = [pkg.workloads.make_x(bw.cfg, T, dev, seed=200 + i) for i, T in enumerate(Ts)]
+    ws = pkg.ops.workspace(max(block.workspace_size(T) for T in Ts), dev)
+    ws.fill_(0xA5)
+    for T, x in zip(Ts, xs):
+        ref = block(x, workspace=torch.zeros(block.workspace_size(T), dtype=torch.uint8,
+                                             device=dev)).clone()
+        ref_i, ref_w = block.last_indices.clone(), block.last_weights.clone()
+        got = block(x, workspace=ws)
+        assert torch.equal(got, ref), (cfg, T)
+        assert torch.equal(block.last_indices, ref_i) and torch.equal(block.last_weights, ref_w)
+        assert pkg.ops.workspace_status(ws) == 0
+
+
 @pytest.mark.parametrize("cfg", ["c2", "c5", "c4", "c6"])
 def test_single_token_combine_in_down_launch(pkg, dev, cfg, monkeypatch):
     """At T = 1 the block and SplitSwitchFfn.forward_with_combine sum the
