@@ -68,6 +68,31 @@ __device__ __forceinline__ uint16_t swiglu_fast(float g_acc, float u_acc) {
   const float h = bf16_hw(g * sg);
   return __builtin_bit_cast(uint16_t, (__bf16)(h * u));
 }
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// a and b rounded to bf16 by one conversion (round to nearest even), as f32
+__device__ __forceinline__ f32x2_t bf16_hw2(float a, float b) {
+  const uint32_t p =
+      __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+  return f32x2_t{__uint_as_float(p << 16), __uint_as_float(p & 0xffff0000u)};
+}
+// swiglu_fast of two elements, each rounding done for both at once; the
+// results packed, the first in the low half (the same values as two calls)
+__device__ __forceinline__ uint32_t swiglu_fast2(float g0_acc, float u0_acc, float g1_acc,
+                                                 float u1_acc) {
+  const f32x2_t g = bf16_hw2(g0_acc, g1_acc), u = bf16_hw2(u0_acc, u1_acc);
+  const float e0 = __builtin_amdgcn_exp2f(-g.x * 1.4426950408889634f);
+  const float e1 = __builtin_amdgcn_exp2f(-g.y * 1.4426950408889634f);
+  const f32x2_t sg = bf16_hw2(__builtin_amdgcn_rcpf(1.0f + e0), __builtin_amdgcn_rcpf(1.0f + e1));
+  const f32x2_t h = bf16_hw2(g.x * sg.x, g.y * sg.y);
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector(f32x2_t{h.x * u.x, h.y * u.y}, bf16x2_t));
+}
+// a compile-time flag as a type (for generic lambdas)
+template <bool B>
+struct PfFlag {
+  static constexpr bool value = B;
+};
 // q = n / d for 0 <= n < 2^31, 1 <= d <= 2^16: a float estimate and one
 // correction step either way
 __device__ __forceinline__ int div_small(int n, int d, float rd) {
