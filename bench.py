@@ -46,11 +46,12 @@ def parse():
                          "cfg:T:res times the decoder layer's MoE half (RMSNorm, block, "
                          "residual add); cfg:T:cold rotates copies of the weights so "
                          "every forward reads its experts from HBM")
-    ap.add_argument("--forwards-per-graph", type=int, default=8,
+    ap.add_argument("--forwards-per-graph", type=int, default=20,
                     help="forwards of the block one captured graph holds (warm graph "
-                         "replays; a decoder's step graph holds one block per layer, so "
-                         "the replay's own launch cost is shared); the headline uses the "
-                         "largest count up to this that divides --steps")
+                         "replays; a decoder's step graph holds one block per layer -- "
+                         "48 in Qwen3-30B-A3B -- so the replay's own launch cost is "
+                         "shared); the headline uses the largest count up to this that "
+                         "divides --steps")
     ap.add_argument("--sweep-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound of the CPU-baseline sample (0 skips it)")
