@@ -400,6 +400,39 @@ def test_block_routing_counter_in_dirty_reused_workspace(pkg, dev, cfg):
         assert pkg.ops.workspace_status(ws) == 0
 
 
+@pytest.mark.parametrize("E,K,T", [(1024, 1, 100), (1024, 4, 256), (1024, 8, 17),
+                                   (300, 3, 333)])
+def test_block_one_launch_routing_wide_routers(pkg, orc, dev, E, K, T):
+    """The one-launch routing (16 < T, T*K <= 1024 ids) at its widest
+    router (1024 experts: 16 logits per lane), with one expert per token (a
+    workgroup per 4 tokens, up to 84 of them), with exactly 1024 ids, and
+    at an expert count off the powers of two.  Indices bit for bit and
+    weights to 2e-6 of the oracle's; the output bit for bit equal to the
+    switch FFN's forward_with_combine given those indices and weights (its
+    sort runs as separate launches)."""
+    d, f = 256, 64
+    gen = torch.Generator().manual_seed(1000 * K + T)
+
+    def rnd(*shape, sd):
+        return (torch.randn(*shape, generator=gen) * sd)
+
+    router = rnd(E, d, sd=0.05).to(dev)
+    bf = lambda t: t.to(torch.bfloat16).to(dev)  # noqa: E731
+    mlp = pkg.nn.SplitSwitchFfn.from_dense(bf(rnd(E, f, d, sd=0.02)), bf(rnd(E, f, d, sd=0.02)),
+                                           bf(rnd(E, d, f, sd=0.02)))
+    block = pkg.nn.Qwen35MoeBlock(router, mlp, K)
+    x = bf(rnd(T, d, sd=1.0))
+    out = block(x).clone()
+    idx, wts = block.last_indices.clone(), block.last_weights.clone()
+    assert pkg.ops.workspace_status(block.last_workspace) == 0
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    ridx, rw = orc.router_topk(orc.router_logits(xb, router.cpu().numpy()), K)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=0)
+    ref = mlp.forward_with_combine(x, idx, wts)
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("cfg", ["c2", "c5", "c4", "c6"])
 def test_single_token_combine_in_down_launch(pkg, dev, cfg, monkeypatch):
     """At T = 1 the block and SplitSwitchFfn.forward_with_combine sum the
