@@ -146,7 +146,12 @@ hipError_t launch_zero_status(int32_t* status, hipStream_t s);
 // takes three kernels (rank, scan, scatter).
 hipError_t launch_dispatch(const int32_t* ids, int64_t n, int64_t E,
                            int tile_rows, const DispatchBuffers& b,
-                           bool reset_status, hipStream_t s);
+                           bool reset_status, hipStream_t s, int32_t* counter = nullptr);
+// With counter (an int that is 0 when the launch starts), more than 1024 ids
+// rank and scan in one launch (the last workgroup to finish scans).
+#ifndef MLXR_DISPATCH_FUSED
+#define MLXR_DISPATCH_FUSED 1
+#endif
 // The one-launch routing (route_fused_kernel) for the block forward.
 #ifndef MLXR_ROUTE_FUSED
 #define MLXR_ROUTE_FUSED 1
