@@ -606,9 +606,128 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 #define MLXR_RL_TILED_T 256
 #endif
 // most tokens for which the norm in front of the router is folded into it
+// The matrix-core router (router_logits_mfma_kernel) for f32 routers above
+// MLXR_RL_TILED_T tokens, and its chunks of loads in flight per lane.
+#ifndef MLXR_RL_MFMA
+#define MLXR_RL_MFMA 1
+#endif
+#ifndef MLXR_RL_MFMA_MIN_T
+#define MLXR_RL_MFMA_MIN_T 2048
+#endif
+#ifndef MLXR_RL_MFMA_RING
+#define MLXR_RL_MFMA_RING 4
+#endif
+#ifndef MLXR_RL_MFMA_NC
+#define MLXR_RL_MFMA_NC 1
+#endif
+#ifndef MLXR_RL_MFMA_PARTS
+#define MLXR_RL_MFMA_PARTS 4
+#endif
 #ifndef MLXR_RL_NORM_MAX_T
 #define MLXR_RL_NORM_MAX_T 2
 #endif
+// Many tokens and an f32 router: the matrix cores.  One workgroup = 4
+// waves = one tile of 32 tokens x 32 logit columns; wave q takes the q-th
+// quarter of d in chunks of 16 elements.  Per chunk each lane loads 8
+// consecutive x values of its token row (16 bytes; lanes 32-63 the chunk's
+// upper half) and the same 8 weights of its column, then 8
+// v_mfma_f32_32x32x2_f32 add them: MFMA s computes
+// fmaf(x[j+8+s] w[j+8+s], fmaf(x[j+s] w[j+s], acc)) for every (token,
+// column) of the tile (an in-bounds probe of the instruction on this GPU
+// matched that pair of fmaf bit for bit on 20480 outputs).  The quarters
+// meet in LDS and wave 0 adds them in order, ((q0 + q1) + q2) + q3, then the
+// bias.  Rows past T read the last row and columns past the router read
+// zeros; neither is stored.  Needs d % 64 == 0 and 16-byte aligned rows.
+constexpr int kRmRing = MLXR_RL_MFMA_RING;  // chunks of loads in flight
+// NC column tiles of 32 per wave (independent accumulators sharing the x
+// values: the chains of MFMAs interleave)
+template <int NC, int P>
+__global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
+    const uint16_t* __restrict__ x, int T, int d, const float* __restrict__ w,
+    const float* __restrict__ w_extra, const float* __restrict__ bias, int E,
+    float* __restrict__ logits, int64_t ld, int32_t* __restrict__ clear) {
+  __shared__ f32x16_t part[P - 1][NC][64];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6, h = lane >> 5;
+  if (clear && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *clear = 0;
+  const int t0 = (int)blockIdx.y * 32, e0 = (int)blockIdx.x * 32 * NC;
+  const int e_tot = E + (w_extra ? 1 : 0);
+  int ec[NC];
+  bool col_ok[NC];
+  const float* wrow[NC];
+#pragma unroll
+  for (int m = 0; m < NC; ++m) {
+    ec[m] = e0 + 32 * m + (lane & 31);
+    col_ok[m] = ec[m] < e_tot;
+    wrow[m] = ec[m] < E ? w + (int64_t)ec[m] * d : (ec[m] == E && w_extra ? w_extra : w);
+  }
+  const uint16_t* xrow = x + (int64_t)min(t0 + (lane & 31), T - 1) * d;
+  const int dq = d / P, n = dq >> 4;  // chunks per part
+  const int kb = q * dq + 8 * h;        // this lane's first element
+  u32x4_t xr[kRmRing];
+  f32x4_t wr[kRmRing][NC][2];
+  auto load = [&](int i, int c) {
+    const int k = kb + 16 * c;
+    xr[i] = *reinterpret_cast<const u32x4_t*>(xrow + k);
+#pragma unroll
+    for (int m = 0; m < NC; ++m) {
+      wr[i][m][0] = *reinterpret_cast<const f32x4_t*>(wrow[m] + k);
+      wr[i][m][1] = *reinterpret_cast<const f32x4_t*>(wrow[m] + k + 4);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < kRmRing; ++i) load(i, min(i, n - 1));
+  f32x16_t acc[NC];
+#pragma unroll
+  for (int m = 0; m < NC; ++m) acc[m] = f32x16_t{};
+  for (int c = 0; c < n; c += kRmRing) {
+#pragma unroll
+    for (int i = 0; i < kRmRing; ++i) {
+      if (c + i < n) {
+        const u32x4_t xv = xr[i];
+        f32x4_t wv[NC][2];
+#pragma unroll
+        for (int m = 0; m < NC; ++m) {
+          wv[m][0] = col_ok[m] ? wr[i][m][0] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          wv[m][1] = col_ok[m] ? wr[i][m][1] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        load(i, min(c + i + kRmRing, n - 1));
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const uint32_t u = xv[s >> 1];
+          const float a = __uint_as_float((s & 1) ? (u & 0xffff0000u) : (u << 16));
+#pragma unroll
+          for (int m = 0; m < NC; ++m)
+            acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                a, s < 4 ? wv[m][0][s] : wv[m][1][s - 4], acc[m], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if (q > 0) {
+#pragma unroll
+    for (int m = 0; m < NC; ++m) part[q - 1][m][lane] = acc[m];
+  }
+  __syncthreads();
+  if (q != 0) return;
+#pragma unroll
+  for (int m = 0; m < NC; ++m) {
+#pragma unroll
+    for (int j = 0; j < P - 1; ++j) {
+      const f32x16_t pj = part[j][m][lane];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[m][r] = acc[m][r] + pj[r];
+    }
+    if (!col_ok[m]) continue;
+    const float bv = bias && ec[m] < E ? bias[ec[m]] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (t < T)
+        logits[(int64_t)t * ld + ec[m]] = bias && ec[m] < E ? acc[m][r] + bv : acc[m][r];
+    }
+  }
+}
+
 template <int BITS>
 void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
                           const RouterWeights& w, const float* bias, int64_t E,
@@ -640,6 +759,19 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     (void)launch_rms_norm(x, T, d, norm->w, norm->eps, norm->out, s);
     x = norm->out;
     norm = nullptr;
+  }
+  if constexpr (BITS == 0) {
+    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (router_matrix_order(T, d) && !norm && al16(x) && al16(w.w) &&
+        (!w.w_extra || al16(w.w_extra))) {
+      constexpr int NC = MLXR_RL_MFMA_NC, P = MLXR_RL_MFMA_PARTS;
+      router_logits_mfma_kernel<NC, P>
+          <<<dim3((unsigned)((e_tot + 32 * NC - 1) / (32 * NC)), (unsigned)((T + 31) / 32)),
+             64 * P, 0, s>>>(x, (int)T, (int)d, static_cast<const float*>(w.w),
+                          static_cast<const float*>(w.w_extra), bias, (int)E, logits, ld,
+                          clear);
+      return;
+    }
   }
   if (T <= 2) {
     MLXR_RL(1, 1, 8);
@@ -724,6 +856,10 @@ void router_topk_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
 }
 
 }  // namespace
+
+bool router_matrix_order(int64_t T, int64_t d) {
+  return MLXR_RL_MFMA && T >= MLXR_RL_MFMA_MIN_T && d % (16 * MLXR_RL_MFMA_PARTS) == 0;
+}
 
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 const RouterWeights& w, const float* bias,

@@ -333,6 +333,16 @@ def gather_qmm_tiled(rows: int, num_experts: int) -> bool:
     return bool(rc)
 
 
+def router_matrix_order(T: int, d: int) -> bool:
+    """True when an f32 router's logits of T tokens over d inputs are summed
+    in the matrix-core order (the oracle's router_logits(mfma=True)), False
+    for the lane order."""
+    rc = C.lib().mlxr_moe_router_matrix_order(int(T), int(d))
+    if rc < 0:
+        raise MlxrMoeError("router_matrix_order: negative size")
+    return bool(rc)
+
+
 def workspace_status(ws: torch.Tensor) -> int:
     """Device status word of a call's workspace (1 = an index was out of
     range).  Synchronises the current stream."""

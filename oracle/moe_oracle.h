@@ -57,6 +57,11 @@ int orc_dequantize(const uint32_t* wq, const void* scales, const void* biases,
  * fixed lane order described in moe_oracle.c. */
 void orc_router_logits(const uint16_t* x, const float* w, int64_t T,
                        int64_t d, int64_t E, float* logits);
+/* The same logits in the matrix-core router's order (d % 64 == 0, else -1):
+ * four quarters of d, each an fmaf chain over 16-element chunks taken as
+ * j, j+8, j+1, j+9, ..., j+7, j+15, the quarters then added in order. */
+int orc_router_logits_mfma(const uint16_t* x, const float* w, int64_t T,
+                           int64_t d, int64_t E, float* logits);
 
 /* softmax(precise) -> top-K -> renormalise, per row of logits [T, E].
  * idx [T, K] (descending logit, ties -> lower id), weights [T, K]. */
@@ -160,6 +165,9 @@ typedef struct {
   orc_qlinear router_q;
   orc_qlinear shared_gate_q;
   int32_t router_bits;
+  /* f32 router: 1 = orc_router_logits_mfma's order (the GPU's router for
+   * many tokens), 0 = orc_router_logits' lane order */
+  int32_t router_mfma;
 } orc_block;
 
 /* PackedSwitchFfn::forward_with_combine: gate_up [E, 2H, d] (gate rows

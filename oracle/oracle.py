@@ -103,13 +103,21 @@ def dequantize(wq, scales, biases, group_size=64, bits=4, out_bf16=True):
     return out
 
 
-def router_logits(x_bf16, w_f32):
+def router_logits(x_bf16, w_f32, mfma=False):
+    """logits [T, E] of an f32 router in the lane order (orc_router_logits),
+    or with mfma in the matrix-core order (orc_router_logits_mfma, d a
+    multiple of 64)."""
     x = np.ascontiguousarray(x_bf16, np.uint16)
     w = np.ascontiguousarray(w_f32, np.float32)
     T, d = x.shape
     E = w.shape[0]
     out = np.zeros((T, E), np.float32)
-    lib().orc_router_logits(_p(x), _p(w), c_int64(T), c_int64(d), c_int64(E), _p(out))
+    if mfma:
+        if lib().orc_router_logits_mfma(_p(x), _p(w), c_int64(T), c_int64(d), c_int64(E),
+                                        _p(out)):
+            raise ValueError("orc_router_logits_mfma: d must be a multiple of 64")
+    else:
+        lib().orc_router_logits(_p(x), _p(w), c_int64(T), c_int64(d), c_int64(E), _p(out))
     return out
 
 
@@ -336,6 +344,7 @@ class _Block(Structure):
         ("shared_gate", _QL), ("shared_up", _QL), ("shared_down", _QL),
         ("shared_gate_w", c_void_p), ("switch_tiled", c_int32), ("shared_tiled", c_int32),
         ("router_q", _QL), ("shared_gate_q", _QL), ("router_bits", c_int32),
+        ("router_mfma", c_int32),
     ]
 
 
@@ -345,19 +354,24 @@ def _ql(t):
     return _QL(*(None if a is None else a.ctypes.data for a in t))
 
 
-def block_forward_residual(p: dict, norm_w, eps, h, nthreads=1, tiled=(False, False)):
+def block_forward_residual(p: dict, norm_w, eps, h, nthreads=1, tiled=(False, False),
+                           router_mfma=False):
     """out = h + block(rms_norm(h, norm_w, eps)) (layer.rs:134-138), with
     block_forward's parameters.  Returns (out, idx, weights)."""
-    return block_forward(p, h, nthreads, tiled, residual=(norm_w, eps))
+    return block_forward(p, h, nthreads, tiled, residual=(norm_w, eps),
+                         router_mfma=router_mfma)
 
 
-def block_forward(p: dict, x, nthreads=1, tiled=(False, False), residual=None):
+def block_forward(p: dict, x, nthreads=1, tiled=(False, False), residual=None,
+                  router_mfma=False):
     """p: numpy block parameters -- d, E, K, f, fs, bits, group_size,
     router_w, router_b (or None), gate/up/down = (wq, scales, biases),
     shared_gate/shared_up/shared_down, shared_gate_w (None when fs == 0).
     A quantised router instead: router_q = (wq, scales, biases) [E, ...],
     shared_gate_q likewise [1, ...], router_bits; then the block is bf16.
     tiled: gather_qmm numerics of (routed experts, shared expert).
+    router_mfma: an f32 router's logits (and the shared gate's) in
+    router_logits(mfma=True)'s order.
     Returns (out [T, d] -- f32, or bf16 as uint16 with a quantised router --,
     idx [T, K], weights [T, K])."""
     keep = []
@@ -387,7 +401,8 @@ def block_forward(p: dict, x, nthreads=1, tiled=(False, False), residual=None):
                  _ql(q(p.get("shared_gate"))), _ql(q(p.get("shared_up"))),
                  _ql(q(p.get("shared_down"))), None if sgw is None else sgw.ctypes.data,
                  1 if tiled[0] else 0, 1 if tiled[1] else 0,
-                 _ql(q(rq)), _ql(q(p.get("shared_gate_q"))), p.get("router_bits", 0))
+                 _ql(q(rq)), _ql(q(p.get("shared_gate_q"))), p.get("router_bits", 0),
+                 1 if router_mfma else 0)
     out = np.zeros((T, p["d"]), np.uint16 if rq is not None else np.float32)
     idx = np.zeros((T, p["K"]), np.int32)
     w = np.zeros((T, p["K"]), np.float32)

@@ -52,6 +52,9 @@ def calibrate(W, cfg, gate_w, device, iters=20, n_cal=4096):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--out", default=None, help="also copy the fixture into this directory")
+    ap.add_argument("--rows-only", action="store_true",
+                    help="keep the committed bias and permutation; record only the row "
+                         "counts the current routing realises")
     args = ap.parse_args()
     import __graft_entry__ as entry
     pkg = entry.load_package()
@@ -59,14 +62,18 @@ def main() -> int:
     dev = torch.device("cuda:0")
     keys = [k for k, c in W.CONFIGS.items() if c.zipf_alpha]
     data = {}
-    for k in keys:
-        cfg = W.CONFIGS[k]
-        gate_w = W._normal((cfg.E, cfg.d), 0.02, dev, cfg.seed, 2)
-        bias, perm = calibrate(W, cfg, gate_w, dev)
-        data[f"{cfg.name}__bias"] = bias
-        data[f"{cfg.name}__perm"] = perm
-        print(f"{k}: bias [{bias.min():.3f}, {bias.max():.3f}]", flush=True)
-    np.savez(FIXTURE, **data)
+    if args.rows_only:
+        with np.load(FIXTURE) as z:
+            data = {f: z[f] for f in z.files if f.endswith("__bias") or f.endswith("__perm")}
+    else:
+        for k in keys:
+            cfg = W.CONFIGS[k]
+            gate_w = W._normal((cfg.E, cfg.d), 0.02, dev, cfg.seed, 2)
+            bias, perm = calibrate(W, cfg, gate_w, dev)
+            data[f"{cfg.name}__bias"] = bias
+            data[f"{cfg.name}__perm"] = perm
+            print(f"{k}: bias [{bias.min():.3f}, {bias.max():.3f}]", flush=True)
+        np.savez(FIXTURE, **data)
     # the realised load of each token count, through the block's routing
     for k in keys:
         cfg = W.CONFIGS[k]

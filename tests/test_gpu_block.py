@@ -48,6 +48,12 @@ PAST_BAR = {
 }
 
 
+def router_mfma(pkg, cfg, T):
+    """Whether the block's f32 router sums its logits in the matrix-core
+    order at T tokens (the library's own choice; the oracle then follows)."""
+    return not cfg.router_bits and cfg.layout != "gemma" and pkg.ops.router_matrix_order(T, cfg.d)
+
+
 def record_parity(name, T, got, ref, rms, allowed=None):
     """Print the parity figures of one block point (max|err|/RMS, the count
     of elements past 2e-2 * RMS, p99.9 |err|/RMS) and, when MLXR_PARITY_LOG
@@ -133,7 +139,8 @@ def flip_allowance(pkg, orc, bw, x, ridx, rw, tiled, nthreads=16):
             row = lambda a: None if a is None else a.reshape(1, -1)  # noqa: E731
             sl = orc.router_logits_q(orc.to_np(x), row(wq), row(sc), row(bi), cfg.router_bits)
         else:
-            sl = orc.router_logits(orc.to_np(x), p["shared_gate_w"])
+            sl = orc.router_logits(orc.to_np(x), p["shared_gate_w"],
+                                   mfma=pkg.ops.router_matrix_order(T, cfg.d))
         sl = sl[:, 0].astype(np.float64)
         bound += (1.0 / (1.0 + np.exp(-sl)))[:, None] * _step(ys)
     return bound
@@ -150,7 +157,7 @@ def check_block(pkg, orc, bw, x, nthreads=16):
     # the gather_qmm numerics the library picks for each GEMM set
     tiled = (pkg.ops.gather_qmm_tiled(T * cfg.K, cfg.E), pkg.ops.gather_qmm_tiled(T, 1))
     ref, ridx, rw = orc.block_forward(orc.block_params(bw), orc.to_np(x), nthreads=nthreads,
-                                      tiled=tiled)
+                                      tiled=tiled, router_mfma=router_mfma(pkg, cfg, T))
     idx = block.last_indices.cpu().numpy()
     assert np.array_equal(idx, ridx), "routing indices differ"
     if cfg.router_bits:
@@ -325,10 +332,11 @@ def test_block_residual_parity(pkg, orc, dev, cfg, T):
     tiled = (pkg.ops.gather_qmm_tiled(T * c.K, c.E), pkg.ops.gather_qmm_tiled(T, 1))
     p = orc.block_params(bw)
     ref, ridx, rw = orc.block_forward_residual(p, orc.to_np(nw), 1e-6, orc.to_np(h),
-                                               nthreads=16, tiled=tiled)
+                                               nthreads=16, tiled=tiled,
+                                               router_mfma=router_mfma(pkg, c, T))
     assert np.array_equal(idx.cpu().numpy(), ridx)
     mref, _, _ = orc.block_forward(p, orc.rms_norm(orc.to_np(h), orc.to_np(nw), 1e-6),
-                                   nthreads=16, tiled=tiled)
+                                   nthreads=16, tiled=tiled, router_mfma=router_mfma(pkg, c, T))
     if c.router_bits:
         got, ref = orc.bf16_to_f32(orc.to_np(out)), orc.bf16_to_f32(ref)
         mref = orc.bf16_to_f32(mref)
@@ -426,7 +434,8 @@ def test_block_one_launch_routing_wide_routers(pkg, orc, dev, E, K, T):
     idx, wts = block.last_indices.clone(), block.last_weights.clone()
     assert pkg.ops.workspace_status(block.last_workspace) == 0
     xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
-    ridx, rw = orc.router_topk(orc.router_logits(xb, router.cpu().numpy()), K)
+    ridx, rw = orc.router_topk(orc.router_logits(xb, router.cpu().numpy(),
+                                                 mfma=pkg.ops.router_matrix_order(T, d)), K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=0)
     ref = mlp.forward_with_combine(x, idx, wts)
@@ -675,7 +684,7 @@ def test_block_parity_large_T_sampled(pkg, orc, dev, cfg, T, n, allowed):
     sel = np.unique(np.concatenate([[0, T - 1], rng.choice(T, n - 2, replace=False)]))
     tiled = (pkg.ops.gather_qmm_tiled(T * c.K, c.E), pkg.ops.gather_qmm_tiled(T, 1))
     ref, ridx, rw = orc.block_forward(orc.block_params(bw), orc.to_np(x)[sel], nthreads=16,
-                                      tiled=tiled)
+                                      tiled=tiled, router_mfma=router_mfma(pkg, c, T))
     assert np.array_equal(block.last_indices.cpu().numpy()[sel], ridx), "routing indices differ"
     if c.router_bits:
         assert np.array_equal(block.last_weights.cpu().numpy()[sel], rw)

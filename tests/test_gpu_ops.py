@@ -63,7 +63,8 @@ def test_quantize_full_expert_bank_bit_exact(pkg, orc, dev):
 # --------------------------------------------------------- router
 @pytest.mark.parametrize("T,d,E,K", [(16, 512, 8, 2), (1, 2048, 128, 8), (64, 2048, 128, 8),
                                      (64, 2048, 512, 10), (300, 4096, 128, 8),
-                                     (300, 2052, 128, 8)])
+                                     (300, 2052, 128, 8), (2048, 2048, 128, 8),
+                                     (3001, 4096, 513, 10), (2048, 2052, 128, 8)])
 def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
     rng = np.random.default_rng(T * 7 + E)
     print(f"  router_topk T={T} d={d} E={E} K={K}", flush=True)
@@ -75,7 +76,10 @@ def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
     x = buf[:T * d].view(T, d)
     w = torch.from_numpy((rng.standard_normal((E, d)) * 0.02).astype(np.float32)).to(dev)
     idx, wts = pkg.ops.router_topk(x, w, K)
-    lg = orc.router_logits(_np(orc, x), w.cpu().numpy())
+    # (many tokens with d a multiple of 64: the matrix-core order; the
+    # rows past the last token hold NaN, as above, and a 513-column router
+    # has a partial tile of columns)
+    lg = orc.router_logits(_np(orc, x), w.cpu().numpy(), mfma=pkg.ops.router_matrix_order(T, d))
     ridx, rw = orc.router_topk(lg, K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
