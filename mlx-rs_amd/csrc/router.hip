@@ -614,117 +614,120 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 #ifndef MLXR_RL_MFMA_MIN_T
 #define MLXR_RL_MFMA_MIN_T 2048
 #endif
-#ifndef MLXR_RL_MFMA_RING
-#define MLXR_RL_MFMA_RING 4
-#endif
-#ifndef MLXR_RL_MFMA_NC
-#define MLXR_RL_MFMA_NC 1
-#endif
 #ifndef MLXR_RL_MFMA_PARTS
 #define MLXR_RL_MFMA_PARTS 4
 #endif
 #ifndef MLXR_RL_NORM_MAX_T
 #define MLXR_RL_NORM_MAX_T 2
 #endif
-// Many tokens and an f32 router: the matrix cores.  One workgroup = 4
+// Many tokens and an f32 router: the matrix cores.  One workgroup = P
 // waves = one tile of 32 tokens x 32 logit columns; wave q takes the q-th
-// quarter of d in chunks of 16 elements.  Per chunk each lane loads 8
-// consecutive x values of its token row (16 bytes; lanes 32-63 the chunk's
-// upper half) and the same 8 weights of its column, then 8
+// of P equal parts of d, in chunks of 16 elements.  Per chunk each lane
+// holds 8 consecutive x values of its token row (lanes 32-63 the chunk's
+// upper half) and the same 8 weights of its column, and 8
 // v_mfma_f32_32x32x2_f32 add them: MFMA s computes
 // fmaf(x[j+8+s] w[j+8+s], fmaf(x[j+s] w[j+s], acc)) for every (token,
 // column) of the tile (an in-bounds probe of the instruction on this GPU
-// matched that pair of fmaf bit for bit on 20480 outputs).  The quarters
-// meet in LDS and wave 0 adds them in order, ((q0 + q1) + q2) + q3, then the
-// bias.  Rows past T read the last row and columns past the router read
-// zeros; neither is stored.  Needs d % 64 == 0 and 16-byte aligned rows.
-constexpr int kRmRing = MLXR_RL_MFMA_RING;  // chunks of loads in flight
-// NC column tiles of 32 per wave (independent accumulators sharing the x
-// values: the chains of MFMAs interleave)
-template <int NC, int P>
+// matched that pair of fmaf bit for bit on 20480 outputs).  The parts meet
+// in LDS and wave 0 adds them in order, ((q0 + q1) + q2) + ..., then the
+// bias.  Each wave stages 64 elements (4 chunks) of its 32 x rows and 32
+// weight rows at a time through its own LDS region, loaded as whole cache
+// lines (a direct load per fragment touched 32 lines per instruction), the
+// next 64 in flight in registers meanwhile; rows padded by 16 bytes so the
+// fragment reads of 16 rows fall on distinct banks.  Rows past T read the
+// last row and columns past the router read zeros; neither is stored.
+// Needs d % (64 P) == 0 and 16-byte aligned rows.
+constexpr int kRmXs = 144, kRmWs = 272;            // LDS row strides (bytes)
+constexpr int kRmWave = 32 * kRmXs + 32 * kRmWs;   // LDS per wave
+template <int P>
 __global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
     const uint16_t* __restrict__ x, int T, int d, const float* __restrict__ w,
     const float* __restrict__ w_extra, const float* __restrict__ bias, int E,
     float* __restrict__ logits, int64_t ld, int32_t* __restrict__ clear) {
-  __shared__ f32x16_t part[P - 1][NC][64];
-  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6, h = lane >> 5;
+  static_assert((P - 1) * 64 * 64 <= P * kRmWave, "partial sums fit the staging LDS");
+  __shared__ __attribute__((aligned(16))) char lds[P * kRmWave];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6, h = lane >> 5, r = lane & 31;
   if (clear && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *clear = 0;
-  const int t0 = (int)blockIdx.y * 32, e0 = (int)blockIdx.x * 32 * NC;
+  const int t0 = (int)blockIdx.y * 32, e0 = (int)blockIdx.x * 32;
   const int e_tot = E + (w_extra ? 1 : 0);
-  int ec[NC];
-  bool col_ok[NC];
-  const float* wrow[NC];
+  char* xs = lds + q * kRmWave;
+  char* ws = xs + 32 * kRmXs;
+  // staging: x piece id = lane + 64 i (i < 4): row id / 8, 16 bytes id % 8;
+  // weight piece id = lane + 64 i (i < 8): column id / 16, 16 bytes id % 16
+  const uint16_t* xsrc[4];
+  const float* wsrc[8];
+  bool wok[8];
 #pragma unroll
-  for (int m = 0; m < NC; ++m) {
-    ec[m] = e0 + 32 * m + (lane & 31);
-    col_ok[m] = ec[m] < e_tot;
-    wrow[m] = ec[m] < E ? w + (int64_t)ec[m] * d : (ec[m] == E && w_extra ? w_extra : w);
+  for (int i = 0; i < 4; ++i) {
+    const int id = lane + 64 * i;
+    xsrc[i] = x + (int64_t)min(t0 + (id >> 3), T - 1) * d + 8 * (id & 7);
   }
-  const uint16_t* xrow = x + (int64_t)min(t0 + (lane & 31), T - 1) * d;
-  const int dq = d / P, n = dq >> 4;  // chunks per part
-  const int kb = q * dq + 8 * h;        // this lane's first element
-  u32x4_t xr[kRmRing];
-  f32x4_t wr[kRmRing][NC][2];
-  auto load = [&](int i, int c) {
-    const int k = kb + 16 * c;
-    xr[i] = *reinterpret_cast<const u32x4_t*>(xrow + k);
 #pragma unroll
-    for (int m = 0; m < NC; ++m) {
-      wr[i][m][0] = *reinterpret_cast<const f32x4_t*>(wrow[m] + k);
-      wr[i][m][1] = *reinterpret_cast<const f32x4_t*>(wrow[m] + k + 4);
-    }
+  for (int i = 0; i < 8; ++i) {
+    const int id = lane + 64 * i, e = e0 + (id >> 4);
+    wok[i] = e < e_tot;
+    wsrc[i] = (e < E ? w + (int64_t)e * d : (e == E && w_extra ? w_extra : w)) + 4 * (id & 15);
+  }
+  const int dq = d / P, nsc = dq >> 6;  // 64-element stages per part
+  const int kq = q * dq;
+  u32x4_t xg[4];
+  f32x4_t wg[8];
+  auto load = [&](int sc) {
+    const int k = kq + 64 * sc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xg[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + k);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wg[i] = *reinterpret_cast<const f32x4_t*>(wsrc[i] + k);
   };
+  load(0);
+  f32x16_t acc = {};
+  for (int sc = 0; sc < nsc; ++sc) {
 #pragma unroll
-  for (int i = 0; i < kRmRing; ++i) load(i, min(i, n - 1));
-  f32x16_t acc[NC];
+    for (int i = 0; i < 4; ++i) {
+      const int id = lane + 64 * i;
+      *reinterpret_cast<u32x4_t*>(xs + (id >> 3) * kRmXs + 16 * (id & 7)) = xg[i];
+    }
 #pragma unroll
-  for (int m = 0; m < NC; ++m) acc[m] = f32x16_t{};
-  for (int c = 0; c < n; c += kRmRing) {
+    for (int i = 0; i < 8; ++i) {
+      const int id = lane + 64 * i;
+      *reinterpret_cast<f32x4_t*>(ws + (id >> 4) * kRmWs + 16 * (id & 15)) =
+          wok[i] ? wg[i] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    load(min(sc + 1, nsc - 1));
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < kRmRing; ++i) {
-      if (c + i < n) {
-        const u32x4_t xv = xr[i];
-        f32x4_t wv[NC][2];
+    for (int c = 0; c < 4; ++c) {
+      const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + r * kRmXs + 32 * c + 16 * h);
+      const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(ws + r * kRmWs + 64 * c + 32 * h);
+      const f32x4_t w1 =
+          *reinterpret_cast<const f32x4_t*>(ws + r * kRmWs + 64 * c + 32 * h + 16);
 #pragma unroll
-        for (int m = 0; m < NC; ++m) {
-          wv[m][0] = col_ok[m] ? wr[i][m][0] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-          wv[m][1] = col_ok[m] ? wr[i][m][1] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-        load(i, min(c + i + kRmRing, n - 1));
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const uint32_t u = xv[s >> 1];
-          const float a = __uint_as_float((s & 1) ? (u & 0xffff0000u) : (u << 16));
-#pragma unroll
-          for (int m = 0; m < NC; ++m)
-            acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                a, s < 4 ? wv[m][0][s] : wv[m][1][s - 4], acc[m], 0, 0, 0);
-        }
+      for (int s = 0; s < 8; ++s) {
+        const uint32_t u = xv[s >> 1];
+        const float a = __uint_as_float((s & 1) ? (u & 0xffff0000u) : (u << 16));
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, s < 4 ? w0[s] : w1[s - 4], acc, 0, 0, 0);
       }
     }
+    __builtin_amdgcn_wave_barrier();
   }
-  if (q > 0) {
-#pragma unroll
-    for (int m = 0; m < NC; ++m) part[q - 1][m][lane] = acc[m];
-  }
+  __syncthreads();  // the staging regions are free: partial sums in their place
+  f32x16_t* part = reinterpret_cast<f32x16_t*>(lds);
+  if (q > 0) part[(q - 1) * 64 + lane] = acc;
   __syncthreads();
   if (q != 0) return;
 #pragma unroll
-  for (int m = 0; m < NC; ++m) {
+  for (int jq = 0; jq < P - 1; ++jq) {
+    const f32x16_t pj = part[jq * 64 + lane];
 #pragma unroll
-    for (int j = 0; j < P - 1; ++j) {
-      const f32x16_t pj = part[j][m][lane];
+    for (int i = 0; i < 16; ++i) acc[i] = acc[i] + pj[i];
+  }
+  const int ec = e0 + r;
+  if (ec >= e_tot) return;
+  const float bv = bias && ec < E ? bias[ec] : 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[m][r] = acc[m][r] + pj[r];
-    }
-    if (!col_ok[m]) continue;
-    const float bv = bias && ec[m] < E ? bias[ec[m]] : 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (t < T)
-        logits[(int64_t)t * ld + ec[m]] = bias && ec[m] < E ? acc[m][r] + bv : acc[m][r];
-    }
+  for (int i = 0; i < 16; ++i) {
+    const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3);
+    if (t < T) logits[(int64_t)t * ld + ec] = bias && ec < E ? acc[i] + bv : acc[i];
   }
 }
 
@@ -764,10 +767,9 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (router_matrix_order(T, d) && !norm && al16(x) && al16(w.w) &&
         (!w.w_extra || al16(w.w_extra))) {
-      constexpr int NC = MLXR_RL_MFMA_NC, P = MLXR_RL_MFMA_PARTS;
-      router_logits_mfma_kernel<NC, P>
-          <<<dim3((unsigned)((e_tot + 32 * NC - 1) / (32 * NC)), (unsigned)((T + 31) / 32)),
-             64 * P, 0, s>>>(x, (int)T, (int)d, static_cast<const float*>(w.w),
+      constexpr int P = MLXR_RL_MFMA_PARTS;
+      router_logits_mfma_kernel<P>
+          <<<dim3((unsigned)((e_tot + 31) / 32), (unsigned)((T + 31) / 32)), 64 * P, 0, s>>>(x, (int)T, (int)d, static_cast<const float*>(w.w),
                           static_cast<const float*>(w.w_extra), bias, (int)E, logits, ld,
                           clear);
       return;
@@ -858,7 +860,7 @@ void router_topk_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
 }  // namespace
 
 bool router_matrix_order(int64_t T, int64_t d) {
-  return MLXR_RL_MFMA && T >= MLXR_RL_MFMA_MIN_T && d % (16 * MLXR_RL_MFMA_PARTS) == 0;
+  return MLXR_RL_MFMA && T >= MLXR_RL_MFMA_MIN_T && d % (64 * MLXR_RL_MFMA_PARTS) == 0;
 }
 
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,

@@ -204,11 +204,11 @@ def test_profile_read_validation(pkg):
 
 def test_router_matrix_order_rule(pkg):
     """The f32 router's summation order (host logic, no GPU): the lane order
-    below 2048 tokens or with d off a multiple of 64, the matrix-core order
-    from 2048 tokens with d a multiple of 64; negative sizes rejected."""
+    below 2048 tokens or with d off a multiple of 256, the matrix-core order
+    from 2048 tokens with d a multiple of 256; negative sizes rejected."""
     q = pkg._capi.lib().mlxr_moe_router_matrix_order
     assert q(1, 2048) == 0 and q(2047, 2048) == 0 and q(300, 4096) == 0
-    assert q(2048, 2048) == 1 and q(4096, 2048) == 1 and q(16384, 64) == 1
-    assert q(4096, 2052) == 0 and q(4096, 96) == 0
+    assert q(2048, 2048) == 1 and q(4096, 2048) == 1 and q(16384, 256) == 1
+    assert q(4096, 2052) == 0 and q(4096, 320) == 0 and q(4096, 64) == 0
     assert q(-1, 64) == -1 and q(64, -1) == -1
     assert pkg.ops.router_matrix_order(4096, 2048) is True
