@@ -620,7 +620,8 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 #ifndef MLXR_RL_NORM_MAX_T
 #define MLXR_RL_NORM_MAX_T 2
 #endif
-// Many tokens and an f32 router: the matrix cores.  One workgroup = P
+// Many tokens: the matrix cores (any router format: f32, bf16 or 4/8-bit
+// weights, converted to f32 as they are staged).  One workgroup = P
 // waves = one tile of 32 tokens x 32 logit columns; wave q takes the q-th
 // of P equal parts of d, in chunks of 16 elements.  Per chunk each lane
 // holds 8 consecutive x values of its token row (lanes 32-63 the chunk's
@@ -635,49 +636,50 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 // lines (a direct load per fragment touched 32 lines per instruction), the
 // next 64 in flight in registers meanwhile; rows padded by 16 bytes so the
 // fragment reads of 16 rows fall on distinct banks.  Rows past T read the
-// last row and columns past the router read zeros; neither is stored.
+// last row and columns past the router read zeros; neither is stored.  A
+// quantised or bf16 router's logit is the sum rounded to bf16 (its weights
+// the f32 values router_cvt4 gives: fmaf(code, scale, bias), or exact).
 // Needs d % (64 P) == 0 and 16-byte aligned rows.
 constexpr int kRmXs = 144, kRmWs = 272;            // LDS row strides (bytes)
 constexpr int kRmWave = 32 * kRmXs + 32 * kRmWs;   // LDS per wave
-template <int P>
+template <int BITS, int P>
 __global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
-    const uint16_t* __restrict__ x, int T, int d, const float* __restrict__ w,
-    const float* __restrict__ w_extra, const float* __restrict__ bias, int E,
-    float* __restrict__ logits, int64_t ld, int32_t* __restrict__ clear) {
+    const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
+    const float* __restrict__ bias, int E, float* __restrict__ logits, int64_t ld,
+    int32_t* __restrict__ clear) {
   static_assert((P - 1) * 64 * 64 <= P * kRmWave, "partial sums fit the staging LDS");
   __shared__ __attribute__((aligned(16))) char lds[P * kRmWave];
   const int lane = threadIdx.x & 63, q = threadIdx.x >> 6, h = lane >> 5, r = lane & 31;
   if (clear && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *clear = 0;
   const int t0 = (int)blockIdx.y * 32, e0 = (int)blockIdx.x * 32;
-  const int e_tot = E + (w_extra ? 1 : 0);
+  const int e_tot = E + (rw.w_extra ? 1 : 0);
   char* xs = lds + q * kRmWave;
   char* ws = xs + 32 * kRmXs;
   // staging: x piece id = lane + 64 i (i < 4): row id / 8, 16 bytes id % 8;
   // weight piece id = lane + 64 i (i < 8): column id / 16, 16 bytes id % 16
   const uint16_t* xsrc[4];
-  const float* wsrc[8];
-  bool wok[8];
+  int wcol[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int id = lane + 64 * i;
     xsrc[i] = x + (int64_t)min(t0 + (id >> 3), T - 1) * d + 8 * (id & 7);
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int id = lane + 64 * i, e = e0 + (id >> 4);
-    wok[i] = e < e_tot;
-    wsrc[i] = (e < E ? w + (int64_t)e * d : (e == E && w_extra ? w_extra : w)) + 4 * (id & 15);
-  }
+  for (int i = 0; i < 8; ++i) wcol[i] = e0 + ((lane + 64 * i) >> 4);
   const int dq = d / P, nsc = dq >> 6;  // 64-element stages per part
   const int kq = q * dq;
   u32x4_t xg[4];
-  f32x4_t wg[8];
+  WRaw4 wg[8];
   auto load = [&](int sc) {
     const int k = kq + 64 * sc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) xg[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + k);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wg[i] = *reinterpret_cast<const f32x4_t*>(wsrc[i] + k);
+    for (int i = 0; i < 8; ++i) {
+      // (columns past the router: a row of zeros from the first one)
+      const WRow row = router_row<BITS>(rw, wcol[i] < e_tot ? wcol[i] : 0, E, d);
+      wg[i] = router_raw4<BITS>(row, k + 4 * ((lane + 64 * i) & 15));
+    }
   };
   load(0);
   f32x16_t acc = {};
@@ -690,8 +692,9 @@ __global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int id = lane + 64 * i;
+      const float4 v = router_cvt4<BITS>(wg[i]);
       *reinterpret_cast<f32x4_t*>(ws + (id >> 4) * kRmWs + 16 * (id & 15)) =
-          wok[i] ? wg[i] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          wcol[i] < e_tot ? f32x4_t{v.x, v.y, v.z, v.w} : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     load(min(sc + 1, nsc - 1));
     __builtin_amdgcn_wave_barrier();
@@ -723,11 +726,14 @@ __global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
   }
   const int ec = e0 + r;
   if (ec >= e_tot) return;
-  const float bv = bias && ec < E ? bias[ec] : 0.0f;
+  const float bv = BITS == 0 && bias && ec < E ? bias[ec] : 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3);
-    if (t < T) logits[(int64_t)t * ld + ec] = bias && ec < E ? acc[i] + bv : acc[i];
+    if (t < T)
+      logits[(int64_t)t * ld + ec] = BITS != 0                 ? bf16_round(acc[i])
+                                     : bias && ec < E ? acc[i] + bv
+                                                      : acc[i];
   }
 }
 
@@ -763,15 +769,14 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
     x = norm->out;
     norm = nullptr;
   }
-  if constexpr (BITS == 0) {
+  {
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (router_matrix_order(T, d) && !norm && al16(x) && al16(w.w) &&
         (!w.w_extra || al16(w.w_extra))) {
       constexpr int P = MLXR_RL_MFMA_PARTS;
-      router_logits_mfma_kernel<P>
-          <<<dim3((unsigned)((e_tot + 31) / 32), (unsigned)((T + 31) / 32)), 64 * P, 0, s>>>(x, (int)T, (int)d, static_cast<const float*>(w.w),
-                          static_cast<const float*>(w.w_extra), bias, (int)E, logits, ld,
-                          clear);
+      router_logits_mfma_kernel<BITS, P>
+          <<<dim3((unsigned)((e_tot + 31) / 32), (unsigned)((T + 31) / 32)), 64 * P, 0, s>>>(
+              x, (int)T, (int)d, w, bias, (int)E, logits, ld, clear);
       return;
     }
   }

@@ -364,6 +364,43 @@ int orc_router_logits_q(const uint16_t* x, const uint32_t* wq,
   return 0;
 }
 
+/* lane_dot_q in the matrix-core order: the f32 weights (fmaf(code, scale,
+ * bias), or the bf16 values of a dense Linear) through mfma_dot, then one
+ * bf16 rounding. */
+static float mfma_dot_q(const uint16_t* xrow, const uint32_t* wrow,
+                        const uint16_t* srow, const uint16_t* brow, int64_t d,
+                        int bits) {
+  float* wf = (float*)malloc(sizeof(float) * (size_t)d);
+  if (bits == 16) {
+    const uint16_t* w16 = (const uint16_t*)wrow;
+    for (int64_t j = 0; j < d; ++j) wf[j] = orc_bf16_to_f32(w16[j]);
+  } else {
+    const int per_word = 32 / bits;
+    const uint32_t mask = (1u << bits) - 1u;
+    for (int64_t j = 0; j < d; ++j) {
+      const uint32_t code = (wrow[j / per_word] >> ((j % per_word) * bits)) & mask;
+      wf[j] = fmaf((float)code, orc_bf16_to_f32(srow[j / 64]), orc_bf16_to_f32(brow[j / 64]));
+    }
+  }
+  const float v = mfma_dot(xrow, wf, d);
+  free(wf);
+  return orc_bf16_to_f32(orc_f32_to_bf16(v));
+}
+
+int orc_router_logits_q_mfma(const uint16_t* x, const uint32_t* wq,
+                             const uint16_t* scales, const uint16_t* biases,
+                             int bits, int64_t T, int64_t d, int64_t E,
+                             float* logits) {
+  if ((bits != 4 && bits != 8 && bits != 16) || d % 64) return -1;
+  const int64_t wpr = d * bits / 32, gpr = bits == 16 ? 0 : d / 64;
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t e = 0; e < E; ++e)
+      logits[t * E + e] = mfma_dot_q(x + t * d, wq + e * wpr,
+                                     scales ? scales + e * gpr : NULL,
+                                     biases ? biases + e * gpr : NULL, d, bits);
+  return 0;
+}
+
 /* softmax_axis(precise) keeps the input dtype (arithmetic.rs:1298-1311), so
  * bf16 logits give bf16 probabilities, and argpartition (sort.rs:211-226)
  * selects on those: distinct logits can tie.  Here m = max logit;
@@ -733,8 +770,9 @@ int orc_gemma_router(const uint16_t* x, int64_t T, int64_t d, int64_t E,
                      int64_t K, const uint16_t* norm_w, float eps,
                      const uint16_t* proj_bf16, const orc_qlinear* proj_q,
                      int bits, const uint16_t* pes, int32_t* idx,
-                     uint16_t* weights_out) {
+                     uint16_t* weights_out, int mfma) {
   if (K < 1 || K > E || (!proj_bf16 && !proj_q)) return -1;
+  if (mfma && d % 64) return -1;
   if (proj_q && ((bits != 4 && bits != 8) || d % 64)) return -1;
   uint16_t* normed = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(T * d));
   float* wrow = (float*)malloc(sizeof(float) * (size_t)d);
@@ -744,12 +782,12 @@ int orc_gemma_router(const uint16_t* x, int64_t T, int64_t d, int64_t E,
   for (int64_t t = 0; t < T; ++t) {
     for (int64_t e = 0; e < E; ++e) {
       if (proj_q) {
-        sc[e] = lane_dot_q(normed + t * d, proj_q->w + e * (d * bits / 32),
-                           proj_q->scales + e * (d / 64),
-                           proj_q->biases + e * (d / 64), d, bits);
+        sc[e] = (mfma ? mfma_dot_q : lane_dot_q)(normed + t * d, proj_q->w + e * (d * bits / 32),
+                                                 proj_q->scales + e * (d / 64),
+                                                 proj_q->biases + e * (d / 64), d, bits);
       } else {
         for (int64_t j = 0; j < d; ++j) wrow[j] = orc_bf16_to_f32(proj_bf16[e * d + j]);
-        sc[e] = bfr(lane_dot(normed + t * d, wrow, d));
+        sc[e] = bfr(mfma ? mfma_dot(normed + t * d, wrow, d) : lane_dot(normed + t * d, wrow, d));
       }
     }
     memset(taken, 0, (size_t)E);
@@ -826,17 +864,18 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
   /* router: f32 Linear (f32 logits), or a QuantizedLinear or bf16 Linear
    * (router_bits 16; bf16 logits) */
   const int rb = blk->router_bits;
-  /* the f32 router in the matrix-core order (mfma_dot) when asked */
-  const int mf = !qr && blk->router_mfma && d % 64 == 0;
+  /* the router in the matrix-core order (mfma_dot / mfma_dot_q) when asked */
+  const int mf = blk->router_mfma && d % 64 == 0;
 #pragma omp parallel for schedule(static) num_threads(nthreads)
   for (int64_t t = 0; t < T; ++t) {
     for (int64_t e = 0; e < E; ++e) {
       float v;
       if (qr) {
         const int64_t gr = rb == 16 ? 0 : d / 64;  /* bf16 Linear: none */
-        v = lane_dot_q(x + t * d, blk->router_q.w + e * (d * rb / 32),
-                       rb == 16 ? NULL : blk->router_q.scales + e * gr,
-                       rb == 16 ? NULL : blk->router_q.biases + e * gr, d, rb);
+        v = (mf ? mfma_dot_q : lane_dot_q)(x + t * d, blk->router_q.w + e * (d * rb / 32),
+                                           rb == 16 ? NULL : blk->router_q.scales + e * gr,
+                                           rb == 16 ? NULL : blk->router_q.biases + e * gr,
+                                           d, rb);
       } else {
         v = mf ? mfma_dot(x + t * d, blk->router_w + e * d, d)
                : lane_dot(x + t * d, blk->router_w + e * d, d);
@@ -845,9 +884,9 @@ int orc_block_forward(const orc_block* blk, const uint16_t* x, int64_t T,
       logits[t * E + e] = v;
     }
     if (fs)
-      sg[t] = qr ? lane_dot_q(x + t * d, blk->shared_gate_q.w,
-                              blk->shared_gate_q.scales,
-                              blk->shared_gate_q.biases, d, rb)
+      sg[t] = qr ? (mf ? mfma_dot_q : lane_dot_q)(x + t * d, blk->shared_gate_q.w,
+                                                  blk->shared_gate_q.scales,
+                                                  blk->shared_gate_q.biases, d, rb)
             : mf ? mfma_dot(x + t * d, blk->shared_gate_w, d)
                  : lane_dot(x + t * d, blk->shared_gate_w, d);
   }

@@ -76,6 +76,12 @@ int orc_router_logits_q(const uint16_t* x, const uint32_t* wq,
                         const uint16_t* scales, const uint16_t* biases,
                         int bits, int64_t T, int64_t d, int64_t E,
                         float* logits);
+/* orc_router_logits_q in the matrix-core order (orc_router_logits_mfma on
+ * the same f32 weights, then the bf16 rounding). */
+int orc_router_logits_q_mfma(const uint16_t* x, const uint32_t* wq,
+                             const uint16_t* scales, const uint16_t* biases,
+                             int bits, int64_t T, int64_t d, int64_t E,
+                             float* logits);
 
 /* Top-K of bf16 logits [T, E] with bf16 probabilities: selection on the
  * probabilities (descending, ties -> lower id), weights bf16 (as f32). */
@@ -185,12 +191,13 @@ int orc_packed_switch_glu(const uint16_t* x, int64_t T, int64_t d, int64_t H,
                           int nthreads);
 
 /* gemma4 Router::forward: idx [T, K], weights_out bf16 [T, K].  proj_bf16
- * [E, d] bf16, or proj_q (4/8-bit, group 64) with bits.  Returns 0 or -1. */
+ * [E, d] bf16, or proj_q (4/8-bit, group 64) with bits.  mfma: the scores
+ * in the matrix-core order (d % 64 == 0).  Returns 0 or -1. */
 int orc_gemma_router(const uint16_t* x, int64_t T, int64_t d, int64_t E,
                      int64_t K, const uint16_t* norm_w, float eps,
                      const uint16_t* proj_bf16, const orc_qlinear* proj_q,
                      int bits, const uint16_t* pes, int32_t* idx,
-                     uint16_t* weights_out);
+                     uint16_t* weights_out, int mfma);
 
 /* Qwen35MoeBlock::forward on x bf16 [T, d] -> out [T, d], f32 with an f32
  * router, bf16 (uint16 bits) with a quantised one.  idx_out/w_out

@@ -130,9 +130,10 @@ def router_topk(logits, K):
     return idx, w
 
 
-def router_logits_q(x_bf16, wq, scales, biases, bits):
+def router_logits_q(x_bf16, wq, scales, biases, bits, mfma=False):
     """QuantizedLinear router (or, bits 16, a bf16 Linear: wq the bf16 bits
-    [E, d], scales and biases None): bf16 logits (as f32) [T, E]."""
+    [E, d], scales and biases None): bf16 logits (as f32) [T, E]; with mfma
+    in the matrix-core order."""
     x = np.ascontiguousarray(x_bf16, np.uint16)
     wq = np.ascontiguousarray(wq, np.uint16 if bits == 16 else np.uint32)
     T, d = x.shape
@@ -140,7 +141,8 @@ def router_logits_q(x_bf16, wq, scales, biases, bits):
     out = np.zeros((T, E), np.float32)
     sc = None if scales is None else np.ascontiguousarray(scales, np.uint16)
     bi = None if biases is None else np.ascontiguousarray(biases, np.uint16)
-    rc = lib().orc_router_logits_q(_p(x), _p(wq), _p(sc), _p(bi), c_int(bits),
+    fn = lib().orc_router_logits_q_mfma if mfma else lib().orc_router_logits_q
+    rc = fn(_p(x), _p(wq), _p(sc), _p(bi), c_int(bits),
                                    c_int64(T), c_int64(d), c_int64(E), _p(out))
     if rc:
         raise ValueError("orc_router_logits_q rejected the arguments")
@@ -266,10 +268,11 @@ def rms_norm(x, w, eps):
     return out
 
 
-def gemma_router(x, norm_w, eps, proj, pes, K, bits=0):
+def gemma_router(x, norm_w, eps, proj, pes, K, bits=0, mfma=False):
     """gemma4 Router::forward.  proj: bf16 [E, d] (uint16) when bits == 0,
-    else (wq, scales, biases) of a QuantizedLinear.  Returns (idx [T, K],
-    weights bf16 [T, K] as uint16)."""
+    else (wq, scales, biases) of a QuantizedLinear; mfma: the scores in the
+    matrix-core order.  Returns (idx [T, K], weights bf16 [T, K] as
+    uint16)."""
     x = np.ascontiguousarray(x, np.uint16)
     T, d = x.shape
     keep = []
@@ -290,7 +293,7 @@ def gemma_router(x, norm_w, eps, proj, pes, K, bits=0):
     rc = lib().orc_gemma_router(_p(x), c_int64(T), c_int64(d), c_int64(E), c_int64(K),
                                 _p(np.ascontiguousarray(norm_w, np.uint16)), c_float(eps),
                                 pb, pq, c_int(bits), _p(np.ascontiguousarray(pes, np.uint16)),
-                                _p(idx), _p(w))
+                                _p(idx), _p(w), c_int(1 if mfma else 0))
     if rc:
         raise ValueError("orc_gemma_router rejected the arguments")
     return idx, w

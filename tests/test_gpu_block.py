@@ -49,9 +49,9 @@ PAST_BAR = {
 
 
 def router_mfma(pkg, cfg, T):
-    """Whether the block's f32 router sums its logits in the matrix-core
-    order at T tokens (the library's own choice; the oracle then follows)."""
-    return not cfg.router_bits and cfg.layout != "gemma" and pkg.ops.router_matrix_order(T, cfg.d)
+    """Whether the block's router sums its logits in the matrix-core order
+    at T tokens (the library's own choice; the oracle then follows)."""
+    return pkg.ops.router_matrix_order(T, cfg.d)
 
 
 def record_parity(name, T, got, ref, rms, allowed=None):
@@ -85,7 +85,8 @@ def check_gemma(pkg, orc, bw, x, nthreads=16):
     print(f"  gemma block {cfg.name} T={T}", flush=True)
     r = block.router
     ridx, rw = orc.gemma_router(orc.to_np(x), orc.to_np(r.norm_weight), r.eps, orc.to_np(r.proj),
-                                orc.to_np(r.per_expert_scale), cfg.K)
+                                orc.to_np(r.per_expert_scale), cfg.K,
+                                mfma=pkg.ops.router_matrix_order(x.shape[0], cfg.d))
     assert np.array_equal(block.last_indices.cpu().numpy(), ridx), "routing indices differ"
     assert np.array_equal(orc.to_np(block.last_weights), rw)
     m = bw.switch_mlp
@@ -137,7 +138,8 @@ def flip_allowance(pkg, orc, bw, x, ridx, rw, tiled, nthreads=16):
         if "shared_gate_q" in p:  # quantised shared gate (bf16 block)
             wq, sc, bi = p["shared_gate_q"]
             row = lambda a: None if a is None else a.reshape(1, -1)  # noqa: E731
-            sl = orc.router_logits_q(orc.to_np(x), row(wq), row(sc), row(bi), cfg.router_bits)
+            sl = orc.router_logits_q(orc.to_np(x), row(wq), row(sc), row(bi), cfg.router_bits,
+                                     mfma=pkg.ops.router_matrix_order(T, cfg.d))
         else:
             sl = orc.router_logits(orc.to_np(x), p["shared_gate_w"],
                                    mfma=pkg.ops.router_matrix_order(T, cfg.d))

@@ -87,7 +87,8 @@ def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
 
 @pytest.mark.parametrize("T,d,E,K,bits", [(1, 2048, 256, 8, 8), (40, 2048, 256, 8, 8),
                                           (1024, 2048, 256, 8, 8), (16, 512, 8, 2, 4),
-                                          (300, 4096, 128, 8, 4), (7, 2048, 512, 10, 8)])
+                                          (300, 4096, 128, 8, 4), (7, 2048, 512, 10, 8),
+                                          (2048, 2048, 256, 8, 8), (2100, 4096, 128, 8, 4)])
 def test_router_topk_quantized_bit_exact(pkg, orc, dev, T, d, E, K, bits):
     """QuantizedLinear router (layers/quantized.rs:356-373): bf16 logits,
     top-K on the bf16 probabilities and bf16 weights, all bit for bit
@@ -101,7 +102,7 @@ def test_router_topk_quantized_bit_exact(pkg, orc, dev, T, d, E, K, bits):
     idx, wts = pkg.ops.router_topk_quantized(x, gate, K)
     wq, sc, bi = (_np(orc, t) for t in (gate.weight, gate.scales, gate.biases))
     lg = orc.router_logits_q(_np(orc, x), wq.reshape(E, -1), sc.reshape(E, -1),
-                             bi.reshape(E, -1), bits)
+                             bi.reshape(E, -1), bits, mfma=pkg.ops.router_matrix_order(T, d))
     ridx, rw = orc.router_topk_bf16(lg, K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.array_equal(wts.cpu().numpy(), rw)
@@ -109,7 +110,8 @@ def test_router_topk_quantized_bit_exact(pkg, orc, dev, T, d, E, K, bits):
 
 @pytest.mark.parametrize("T,d,E,K,bits", [(1, 2048, 128, 8, 16), (40, 2048, 128, 8, 16),
                                           (300, 2048, 128, 8, 16), (33, 2048, 256, 8, 8),
-                                          (7, 512, 8, 2, 16), (300, 516, 64, 4, 16)])
+                                          (7, 512, 8, 2, 16), (300, 516, 64, 4, 16),
+                                          (2048, 2048, 128, 8, 16), (2048, 2048, 256, 8, 8)])
 def test_gemma_router_bit_exact(pkg, orc, dev, T, d, E, K, bits):
     """gemma4 Router::forward (text.rs:621-665): RMSNorm, bf16 (or 8-bit)
     projection, top-K of the bf16 scores, softmax of the K scores times
@@ -126,7 +128,8 @@ def test_gemma_router_bit_exact(pkg, orc, dev, T, d, E, K, bits):
     oproj = ((_np(orc, proj.weight).reshape(E, -1), _np(orc, proj.scales).reshape(E, -1),
               _np(orc, proj.biases).reshape(E, -1)) if bits == 8 else _np(orc, projf))
     ridx, rw = orc.gemma_router(_np(orc, x), _np(orc, r.norm_weight), r.eps, oproj,
-                                _np(orc, pes), K, bits=8 if bits == 8 else 0)
+                                _np(orc, pes), K, bits=8 if bits == 8 else 0,
+                                mfma=pkg.ops.router_matrix_order(T, d))
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.array_equal(_np(orc, w), rw)
 
@@ -397,17 +400,18 @@ def test_gather_mm_is_tiled_gather_qmm_of_dequant(pkg, orc, dev, bits):
     assert torch.equal(q, m)
 
 
-@pytest.mark.parametrize("T,E", [(1, 256), (40, 256), (1024, 128)])
+@pytest.mark.parametrize("T,E", [(1, 256), (40, 256), (1024, 128), (2048, 256)])
 def test_router_topk_bf16_linear_bit_exact(pkg, orc, dev, T, E):
     """A bf16 Linear router (an unquantised checkpoint's mlp.gate): bf16
-    logits in the lane order, top-K on the bf16 probabilities, bit for bit,
-    through each logits kernel."""
+    logits in the lane order (the matrix-core order from 2048 tokens), top-K
+    on the bf16 probabilities, bit for bit, through each logits kernel."""
     rng = np.random.default_rng(T + E)
     d, K = 2048, 8
     x = _bf16(orc, rng.standard_normal((T, d)).astype(np.float32), dev)
     w = _bf16(orc, (rng.standard_normal((E, d)) * 0.05).astype(np.float32), dev)
     idx, wts = pkg.ops.router_topk_quantized(x, pkg.nn.Linear(w), K)
-    lg = orc.router_logits_q(_np(orc, x), _np(orc, w), None, None, 16)
+    lg = orc.router_logits_q(_np(orc, x), _np(orc, w), None, None, 16,
+                             mfma=pkg.ops.router_matrix_order(T, d))
     ridx, rw = orc.router_topk_bf16(lg, K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.array_equal(wts.cpu().numpy(), rw)

@@ -259,6 +259,28 @@ def test_router_topk_matches_full_sort(orc):
 
 
 # ---------------------------------------------- quantised (bf16) router
+@pytest.mark.parametrize("bits", [4, 8, 16])
+def test_router_logits_q_mfma_is_dequant_then_bf16(orc, bits):
+    """The quantised (and bf16) router in the matrix-core order: the f32
+    router's matrix-core order on the f32-dequantised weights (bits 16: the
+    bf16 values), rounded once to bf16 -- and unlike the lane order's
+    rounding on inputs where the two orders' f32 sums differ."""
+    rng = np.random.default_rng(50 + bits)
+    T, d, E = 6, 2048, 16
+    x = orc.f32_to_bf16(rng.standard_normal((T, d)).astype(np.float32))
+    w = orc.f32_to_bf16((rng.standard_normal((E, d)) * 0.02).astype(np.float32))
+    if bits == 16:
+        wq, sc, bi, wd = w, None, None, orc.bf16_to_f32(w)
+    else:
+        wq, sc, bi = orc.quantize(w, 64, bits)
+        wd = orc.dequantize(wq, sc, bi, 64, bits, out_bf16=False)
+    got = orc.router_logits_q(x, wq, sc, bi, bits, mfma=True)
+    want = orc.bf16_to_f32(orc.f32_to_bf16(orc.router_logits(x, wd, mfma=True)))
+    assert np.array_equal(got, want)
+    # the order reaches the result: pre-rounding f32 sums differ somewhere
+    assert not np.array_equal(orc.router_logits(x, wd, mfma=True), orc.router_logits(x, wd))
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_router_logits_q_is_dequant_then_bf16(orc, bits):
     """QuantizedLinear router (layers/quantized.rs:356-373): the f32 router
