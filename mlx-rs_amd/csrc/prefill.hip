@@ -221,10 +221,20 @@ namespace tile64n {
 
 }  // namespace
 
+// 8-bit weights take the 64-row tiles too (1) or always 128 (0)
+#ifndef MLXR_PF8_SHORT
+#define MLXR_PF8_SHORT 0
+#endif
+// the 64-row gate/up of 8-bit weights in the narrow form (1) or the wide one (0)
+#ifndef MLXR_PF8_NARROW64
+#define MLXR_PF8_NARROW64 1
+#endif
+
 int prefill_tile_rows(int64_t rows, int64_t experts, int bits) {
   const int64_t e = experts > 0 ? experts : 1;
   if (rows >= (int64_t)MLXR_PREFILL_TALL_ROWS * e) return tile256::kBM;
-  if (rows >= (int64_t)MLXR_PREFILL_SHORT_ROWS * e || bits == 8) return tile128::kBM;
+  if (rows >= (int64_t)MLXR_PREFILL_SHORT_ROWS * e || (bits == 8 && !MLXR_PF8_SHORT))
+    return tile128::kBM;
   return tile64::kBM;
 }
 
@@ -247,7 +257,7 @@ hipError_t launch_qgemm_prefill(const QGemmArgs& a, int64_t x_rows,
   // (the dispatch's M-tiles fix the height; the width is the launch's own)
   if (tile_rows == tile128::kBM && a.bits != 8)
     return tile128n::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
-  if (tile_rows == tile64::kBM && a.gated)
+  if (tile_rows == tile64::kBM && a.gated && (a.bits != 8 || MLXR_PF8_NARROW64))
     return tile64n::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
   if (tile_rows == tile128::kBM)
     return tile128::launch(a, x_rows, max_tiles, s, profile, shared, shared_rows);
