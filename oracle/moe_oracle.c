@@ -42,6 +42,10 @@
  *   orc_router_logits_q  equals orc_router_logits on the dequantised
  *                     weights, then one bf16 rounding (same lane order);
  *                     fp64 bound.
+ *   orc_router_logits_q_mfma  equals orc_router_logits_mfma (pinned
+ *                     above) on the dequantised weights, then one bf16
+ *                     rounding, at 4, 8 and 16 bits; orc_gemma_router's
+ *                     mfma flag takes the same order.
  *   orc_router_topk_bf16 full sort of the bf16 probabilities on small E,
  *                     ties to the lower id; probabilities within one bf16
  *                     rounding of the exact softmax.

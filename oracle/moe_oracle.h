@@ -171,8 +171,9 @@ typedef struct {
   orc_qlinear router_q;
   orc_qlinear shared_gate_q;
   int32_t router_bits;
-  /* f32 router: 1 = orc_router_logits_mfma's order (the GPU's router for
-   * many tokens), 0 = orc_router_logits' lane order */
+  /* router and shared gate, any format: 1 = the matrix-core order
+   * (orc_router_logits_mfma / orc_router_logits_q_mfma, the GPU's router
+   * for many tokens; needs d % 64 == 0), 0 = the lane order */
   int32_t router_mfma;
 } orc_block;
 
