@@ -136,16 +136,20 @@ int mlxr_moe_gather_mm(const void* a, int a_dtype, int64_t a_batch, int64_t M,
  * Both accumulate in f32.  Returns -1 for negative sizes. */
 int mlxr_moe_gather_qmm_tiled(int64_t rows, int64_t num_experts);
 
-/* The summation order of an f32 router's logits for T tokens over d inputs
- * (no counterpart in the reference, whose MLX matmul picks its own order):
- * 1 = the matrix-core order, for many tokens -- d in four quarters, each a
- * chain of fused multiply-adds over 16-element chunks taken as j, j+8, j+1,
- * j+9, ..., j+7, j+15, the quarters then added in order; 0 = the lane
- * order of the small-T kernels.  Both are f32 dot products of the same
- * inputs; top-K can differ between them only where two logits tie to
- * within their last bits.  (Rows of x or weights off 16-byte alignment
- * take the lane order.)  Returns -1 for negative sizes. */
-int mlxr_moe_router_matrix_order(int64_t T, int64_t d);
+/* The summation order of a router's logits for T tokens over d inputs and
+ * `columns` logit columns (the experts, plus one when a shared-expert gate
+ * rides in the same pass), for f32, bf16 and quantised routers alike (no
+ * counterpart in the reference, whose MLX matmul picks its own order).
+ * 1 = the matrix-core order, taken from 512 tokens when d is a multiple of
+ * 256 and the logits make at least 192 tiles of 32 tokens x 32 columns: d
+ * in four quarters, each a chain of fused multiply-adds over 16-element
+ * chunks taken as j, j+8, j+1, j+9, ..., j+7, j+15, the quarters then
+ * added in order.  0 = the lane order of the other kernels.  Both are f32
+ * dot products of the same inputs (a quantised or bf16 router rounds the
+ * sum to bf16 after); top-K can differ between them only where two logits
+ * tie to within their last bits.  (Rows of x or weights off 16-byte
+ * alignment take the lane order.)  Returns -1 for negative sizes. */
+int mlxr_moe_router_matrix_order(int64_t T, int64_t d, int64_t columns);
 
 /* Indices that partition each row of a [rows, n] f32 (axis = -1 or 1):
  * out[.., kth] holds the element of sorted rank kth, smaller before, larger

@@ -140,7 +140,7 @@ SIGNATURES = {
     "mlxr_moe_noalloc_scratch_size": (c_size_t, []),
     "mlxr_moe_block_forward_noalloc": (c_int, [POINTER(Block), P, c_int64, P, P, P, P]),
     "mlxr_moe_gather_qmm_tiled": (c_int, [c_int64, c_int64]),
-    "mlxr_moe_router_matrix_order": (c_int, [c_int64, c_int64]),
+    "mlxr_moe_router_matrix_order": (c_int, [c_int64, c_int64, c_int64]),
     "mlxr_moe_profile_start": (c_int, [c_char_p]),
     "mlxr_moe_profile_read": (c_int, [P, c_size_t, P, P]),
     "mlxr_moe_profile_stop": (c_int, [POINTER(c_int64), POINTER(c_double), POINTER(c_double),

@@ -282,9 +282,9 @@ int mlxr_moe_gather_mm(const void* a, int a_dtype, int64_t a_batch, int64_t M,
                     workspace_size, as_stream(stream));
 }
 
-int mlxr_moe_router_matrix_order(int64_t T, int64_t d) {
-  if (T < 0 || d < 0) return -1;
-  return router_matrix_order(T, d) ? 1 : 0;
+int mlxr_moe_router_matrix_order(int64_t T, int64_t d, int64_t columns) {
+  if (T < 0 || d < 0 || columns < 0) return -1;
+  return router_matrix_order(T, d, columns) ? 1 : 0;
 }
 
 int mlxr_moe_gather_qmm_tiled(int64_t rows, int64_t num_experts) {

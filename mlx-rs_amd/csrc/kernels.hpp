@@ -75,10 +75,11 @@ hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,
                                 int64_t E, float* logits, int64_t ld,
                                 hipStream_t s, const RouterNorm* norm = nullptr,
                                 int32_t* clear = nullptr);
-// True when an f32 router's logits of T tokens over d inputs take the
-// matrix-core order (router_logits_mfma_kernel; 16-byte aligned x and
-// weights), false for the lane order.
-bool router_matrix_order(int64_t T, int64_t d);
+// True when a router's logits of T tokens over d inputs, cols logit columns
+// (the experts, plus one for a shared-expert gate), take the matrix-core
+// order (router_logits_mfma_kernel; 16-byte aligned x and weights), false
+// for the lane order.
+bool router_matrix_order(int64_t T, int64_t d, int64_t cols);
 // One wave per token; clears *status first when status != nullptr.  bf16:
 // the logits are bf16 and the selection is on their bf16 probabilities,
 // with bf16 weights (stored as f32).

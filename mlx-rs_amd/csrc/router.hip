@@ -612,7 +612,14 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 #define MLXR_RL_MFMA 1
 #endif
 #ifndef MLXR_RL_MFMA_MIN_T
-#define MLXR_RL_MFMA_MIN_T 2048
+#define MLXR_RL_MFMA_MIN_T 512
+#endif
+// ... and from this many 32 x 32 tiles (workgroups): below it the grid
+// leaves too many SIMDs without a wave (measured at T = 1024: c3, 128
+// tiles, 17.7 to 19.0-20.1 us; c4, 544, 53.6 to 36.2; c6, 288, 33.5 to
+// 29.9; c8, 256, 32.3 to 27.0; c3 T = 1536, 192, 22.1 to 20.5)
+#ifndef MLXR_RL_MFMA_MIN_WG
+#define MLXR_RL_MFMA_MIN_WG 192
 #endif
 #ifndef MLXR_RL_MFMA_PARTS
 #define MLXR_RL_MFMA_PARTS 4
@@ -771,7 +778,7 @@ void router_logits_launch(const uint16_t* x, int64_t T, int64_t d,
   }
   {
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    if (router_matrix_order(T, d) && !norm && al16(x) && al16(w.w) &&
+    if (router_matrix_order(T, d, e_tot) && !norm && al16(x) && al16(w.w) &&
         (!w.w_extra || al16(w.w_extra))) {
       constexpr int P = MLXR_RL_MFMA_PARTS;
       router_logits_mfma_kernel<BITS, P>
@@ -864,8 +871,9 @@ void router_topk_launch(const float* logits, int64_t ld, int64_t T, int64_t E,
 
 }  // namespace
 
-bool router_matrix_order(int64_t T, int64_t d) {
-  return MLXR_RL_MFMA && T >= MLXR_RL_MFMA_MIN_T && d % (64 * MLXR_RL_MFMA_PARTS) == 0;
+bool router_matrix_order(int64_t T, int64_t d, int64_t cols) {
+  return MLXR_RL_MFMA && T >= MLXR_RL_MFMA_MIN_T && d % (64 * MLXR_RL_MFMA_PARTS) == 0 &&
+         (cols + 31) / 32 * ((T + 31) / 32) >= MLXR_RL_MFMA_MIN_WG;
 }
 
 hipError_t launch_router_logits(const uint16_t* x, int64_t T, int64_t d,

@@ -333,11 +333,12 @@ def gather_qmm_tiled(rows: int, num_experts: int) -> bool:
     return bool(rc)
 
 
-def router_matrix_order(T: int, d: int) -> bool:
-    """True when an f32 router's logits of T tokens over d inputs are summed
-    in the matrix-core order (the oracle's router_logits(mfma=True)), False
-    for the lane order."""
-    rc = C.lib().mlxr_moe_router_matrix_order(int(T), int(d))
+def router_matrix_order(T: int, d: int, columns: int) -> bool:
+    """True when a router's logits of T tokens over d inputs, `columns`
+    logit columns (the experts, plus one for a shared-expert gate computed
+    beside them), are summed in the matrix-core order (the oracle's
+    router_logits(mfma=True)), False for the lane order."""
+    rc = C.lib().mlxr_moe_router_matrix_order(int(T), int(d), int(columns))
     if rc < 0:
         raise MlxrMoeError("router_matrix_order: negative size")
     return bool(rc)

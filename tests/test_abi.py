@@ -203,12 +203,21 @@ def test_profile_read_validation(pkg):
 
 
 def test_router_matrix_order_rule(pkg):
-    """The f32 router's summation order (host logic, no GPU): the lane order
-    below 2048 tokens or with d off a multiple of 256, the matrix-core order
-    from 2048 tokens with d a multiple of 256; negative sizes rejected."""
+    """The router's summation order (host logic, no GPU): the matrix-core
+    order from 512 tokens with d a multiple of 256 and at least 192 tiles of
+    32 tokens x 32 logit columns, else the lane order; negative sizes
+    rejected."""
     q = pkg._capi.lib().mlxr_moe_router_matrix_order
-    assert q(1, 2048) == 0 and q(2047, 2048) == 0 and q(300, 4096) == 0
-    assert q(2048, 2048) == 1 and q(4096, 2048) == 1 and q(16384, 256) == 1
-    assert q(4096, 2052) == 0 and q(4096, 320) == 0 and q(4096, 64) == 0
-    assert q(-1, 64) == -1 and q(64, -1) == -1
-    assert pkg.ops.router_matrix_order(4096, 2048) is True
+    assert q(1, 2048, 128) == 0 and q(300, 4096, 1024) == 0 and q(511, 2048, 1024) == 0
+    # tiles: 4 x 64, 4 x 128, 4 x 512, 4 x 48 (the fewest taken)
+    assert q(2048, 2048, 128) == 1 and q(4096, 2048, 128) == 1
+    assert q(16384, 256, 128) == 1 and q(1536, 2048, 128) == 1
+    # 4 x 32, 2 x 64, 4 x 47: too few tiles
+    assert q(1024, 2048, 128) == 0 and q(2048, 2048, 64) == 0 and q(1504, 2048, 128) == 0
+    # a shared-expert gate's column adds a column of tiles: 9 x 32, 17 x 16
+    assert q(1024, 2048, 257) == 1 and q(512, 2048, 513) == 1 and q(1024, 2048, 256) == 1
+    assert q(1024, 2048, 160) == 0 and q(1024, 2048, 161) == 1  # 5 x 32 / 6 x 32
+    assert q(4096, 2052, 128) == 0 and q(4096, 320, 128) == 0 and q(4096, 64, 128) == 0
+    assert q(-1, 64, 8) == -1 and q(64, -1, 8) == -1 and q(64, 64, -1) == -1
+    assert pkg.ops.router_matrix_order(4096, 2048, 128) is True
+    assert pkg.ops.router_matrix_order(1024, 2048, 128) is False

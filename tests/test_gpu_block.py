@@ -50,8 +50,9 @@ PAST_BAR = {
 
 def router_mfma(pkg, cfg, T):
     """Whether the block's router sums its logits in the matrix-core order
-    at T tokens (the library's own choice; the oracle then follows)."""
-    return pkg.ops.router_matrix_order(T, cfg.d)
+    at T tokens (the library's own choice; the oracle then follows).  A
+    shared expert's gate is one more logit column of the same pass."""
+    return pkg.ops.router_matrix_order(T, cfg.d, cfg.E + (1 if cfg.fs else 0))
 
 
 def record_parity(name, T, got, ref, rms, allowed=None):
@@ -86,7 +87,7 @@ def check_gemma(pkg, orc, bw, x, nthreads=16):
     r = block.router
     ridx, rw = orc.gemma_router(orc.to_np(x), orc.to_np(r.norm_weight), r.eps, orc.to_np(r.proj),
                                 orc.to_np(r.per_expert_scale), cfg.K,
-                                mfma=pkg.ops.router_matrix_order(x.shape[0], cfg.d))
+                                mfma=pkg.ops.router_matrix_order(x.shape[0], cfg.d, cfg.E))
     assert np.array_equal(block.last_indices.cpu().numpy(), ridx), "routing indices differ"
     assert np.array_equal(orc.to_np(block.last_weights), rw)
     m = bw.switch_mlp
@@ -139,10 +140,10 @@ def flip_allowance(pkg, orc, bw, x, ridx, rw, tiled, nthreads=16):
             wq, sc, bi = p["shared_gate_q"]
             row = lambda a: None if a is None else a.reshape(1, -1)  # noqa: E731
             sl = orc.router_logits_q(orc.to_np(x), row(wq), row(sc), row(bi), cfg.router_bits,
-                                     mfma=pkg.ops.router_matrix_order(T, cfg.d))
+                                     mfma=router_mfma(pkg, cfg, T))
         else:
             sl = orc.router_logits(orc.to_np(x), p["shared_gate_w"],
-                                   mfma=pkg.ops.router_matrix_order(T, cfg.d))
+                                   mfma=router_mfma(pkg, cfg, T))
         sl = sl[:, 0].astype(np.float64)
         bound += (1.0 / (1.0 + np.exp(-sl)))[:, None] * _step(ys)
     return bound
@@ -437,7 +438,7 @@ def test_block_one_launch_routing_wide_routers(pkg, orc, dev, E, K, T):
     assert pkg.ops.workspace_status(block.last_workspace) == 0
     xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
     ridx, rw = orc.router_topk(orc.router_logits(xb, router.cpu().numpy(),
-                                                 mfma=pkg.ops.router_matrix_order(T, d)), K)
+                                                 mfma=pkg.ops.router_matrix_order(T, d, E)), K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=0)
     ref = mlp.forward_with_combine(x, idx, wts)

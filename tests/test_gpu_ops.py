@@ -64,7 +64,9 @@ def test_quantize_full_expert_bank_bit_exact(pkg, orc, dev):
 @pytest.mark.parametrize("T,d,E,K", [(16, 512, 8, 2), (1, 2048, 128, 8), (64, 2048, 128, 8),
                                      (64, 2048, 512, 10), (300, 4096, 128, 8),
                                      (300, 2052, 128, 8), (2048, 2048, 128, 8),
-                                     (3001, 4096, 513, 10), (2048, 2052, 128, 8)])
+                                     (3001, 4096, 513, 10), (2048, 2052, 128, 8),
+                                     (1024, 2048, 256, 8), (1024, 2048, 128, 8),
+                                     (520, 2048, 513, 10)])
 def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
     rng = np.random.default_rng(T * 7 + E)
     print(f"  router_topk T={T} d={d} E={E} K={K}", flush=True)
@@ -79,7 +81,7 @@ def test_router_topk_bit_exact(pkg, orc, dev, T, d, E, K):
     # (many tokens with d a multiple of 64: the matrix-core order; the
     # rows past the last token hold NaN, as above, and a 513-column router
     # has a partial tile of columns)
-    lg = orc.router_logits(_np(orc, x), w.cpu().numpy(), mfma=pkg.ops.router_matrix_order(T, d))
+    lg = orc.router_logits(_np(orc, x), w.cpu().numpy(), mfma=pkg.ops.router_matrix_order(T, d, E))
     ridx, rw = orc.router_topk(lg, K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
@@ -102,7 +104,7 @@ def test_router_topk_quantized_bit_exact(pkg, orc, dev, T, d, E, K, bits):
     idx, wts = pkg.ops.router_topk_quantized(x, gate, K)
     wq, sc, bi = (_np(orc, t) for t in (gate.weight, gate.scales, gate.biases))
     lg = orc.router_logits_q(_np(orc, x), wq.reshape(E, -1), sc.reshape(E, -1),
-                             bi.reshape(E, -1), bits, mfma=pkg.ops.router_matrix_order(T, d))
+                             bi.reshape(E, -1), bits, mfma=pkg.ops.router_matrix_order(T, d, E))
     ridx, rw = orc.router_topk_bf16(lg, K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.array_equal(wts.cpu().numpy(), rw)
@@ -129,7 +131,7 @@ def test_gemma_router_bit_exact(pkg, orc, dev, T, d, E, K, bits):
               _np(orc, proj.biases).reshape(E, -1)) if bits == 8 else _np(orc, projf))
     ridx, rw = orc.gemma_router(_np(orc, x), _np(orc, r.norm_weight), r.eps, oproj,
                                 _np(orc, pes), K, bits=8 if bits == 8 else 0,
-                                mfma=pkg.ops.router_matrix_order(T, d))
+                                mfma=pkg.ops.router_matrix_order(T, d, E))
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.array_equal(_np(orc, w), rw)
 
@@ -411,7 +413,7 @@ def test_router_topk_bf16_linear_bit_exact(pkg, orc, dev, T, E):
     w = _bf16(orc, (rng.standard_normal((E, d)) * 0.05).astype(np.float32), dev)
     idx, wts = pkg.ops.router_topk_quantized(x, pkg.nn.Linear(w), K)
     lg = orc.router_logits_q(_np(orc, x), _np(orc, w), None, None, 16,
-                             mfma=pkg.ops.router_matrix_order(T, d))
+                             mfma=pkg.ops.router_matrix_order(T, d, E))
     ridx, rw = orc.router_topk_bf16(lg, K)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert np.array_equal(wts.cpu().numpy(), rw)
