@@ -9,9 +9,12 @@
 namespace mlxr_moe {
 namespace {
 
-// Grid-stride over n vectors, four loads in flight per thread.  Every vector
-// is folded into an XOR that is stored (to the caller's sink word) only when
-// it equals a constant, so the compiler keeps the loads.
+// Grid-stride over n vectors, four loads in flight per thread, each with the
+// non-temporal hint (every byte is read once: measured on this GPU, 224 MB
+// streams at 6.4-6.8 TB/s that way against 5.6-6.0 with plain loads, over
+// grids of 256 to 4096 workgroups).  Every vector is folded into an XOR that
+// is stored (to the caller's sink word) only when it equals a constant, so
+// the compiler keeps the loads.
 constexpr int kReadThreads = 256, kReadUnroll = 4, kReadGrid = 4096;
 __global__ __launch_bounds__(kReadThreads) void read_probe_kernel(const u32x4_t* __restrict__ p,
                                                                   int64_t n, uint32_t* sink) {
@@ -23,7 +26,7 @@ __global__ __launch_bounds__(kReadThreads) void read_probe_kernel(const u32x4_t*
 #pragma unroll
     for (int u = 0; u < kReadUnroll; ++u) {
       const int64_t j = i + (int64_t)kReadThreads * u;
-      v[u] = j < n ? p[j] : u32x4_t{0u, 0u, 0u, 0u};
+      v[u] = j < n ? __builtin_nontemporal_load(p + j) : u32x4_t{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int u = 0; u < kReadUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
