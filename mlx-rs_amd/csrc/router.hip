@@ -647,14 +647,22 @@ __global__ __launch_bounds__(256) void gemma_topk_kernel(
 // quantised or bf16 router's logit is the sum rounded to bf16 (its weights
 // the f32 values router_cvt4 gives: fmaf(code, scale, bias), or exact).
 // Needs d % (64 P) == 0 and 16-byte aligned rows.
-constexpr int kRmXs = 144, kRmWs = 272;            // LDS row strides (bytes)
-constexpr int kRmWave = 32 * kRmXs + 32 * kRmWs;   // LDS per wave
+// elements of d per staging step (64 or 32: 4 or 2 chunks of 16; 32 halves
+// the LDS, which measured no faster)
+#ifndef MLXR_RL_MFMA_STAGE
+#define MLXR_RL_MFMA_STAGE 64
+#endif
+constexpr int kRmStage = MLXR_RL_MFMA_STAGE;
+constexpr int kRmXp = kRmStage / 8, kRmWp = kRmStage / 4;  // 16-byte pieces of a row
+constexpr int kRmXs = 2 * kRmStage + 16, kRmWs = 4 * kRmStage + 16;  // LDS row strides
+constexpr int kRmWave = 32 * kRmXs + 32 * kRmWs;                     // LDS per wave
 template <int BITS, int P>
 __global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
     const uint16_t* __restrict__ x, int T, int d, const RouterWeights rw,
     const float* __restrict__ bias, int E, float* __restrict__ logits, int64_t ld,
     int32_t* __restrict__ clear) {
   static_assert((P - 1) * 64 * 64 <= P * kRmWave, "partial sums fit the staging LDS");
+  constexpr int XI = 32 * kRmXp / 64, WI = 32 * kRmWp / 64;  // pieces per lane
   __shared__ __attribute__((aligned(16))) char lds[P * kRmWave];
   const int lane = threadIdx.x & 63, q = threadIdx.x >> 6, h = lane >> 5, r = lane & 31;
   if (clear && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *clear = 0;
@@ -662,51 +670,52 @@ __global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
   const int e_tot = E + (rw.w_extra ? 1 : 0);
   char* xs = lds + q * kRmWave;
   char* ws = xs + 32 * kRmXs;
-  // staging: x piece id = lane + 64 i (i < 4): row id / 8, 16 bytes id % 8;
-  // weight piece id = lane + 64 i (i < 8): column id / 16, 16 bytes id % 16
-  const uint16_t* xsrc[4];
-  int wcol[8];
+  // staging: x piece id = lane + 64 i (i < XI): row id / kRmXp, 16 bytes
+  // id % kRmXp; weight piece id = lane + 64 i (i < WI): column id / kRmWp,
+  // 16 bytes id % kRmWp
+  const uint16_t* xsrc[XI];
+  int wcol[WI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < XI; ++i) {
     const int id = lane + 64 * i;
-    xsrc[i] = x + (int64_t)min(t0 + (id >> 3), T - 1) * d + 8 * (id & 7);
+    xsrc[i] = x + (int64_t)min(t0 + id / kRmXp, T - 1) * d + 8 * (id % kRmXp);
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) wcol[i] = e0 + ((lane + 64 * i) >> 4);
-  const int dq = d / P, nsc = dq >> 6;  // 64-element stages per part
+  for (int i = 0; i < WI; ++i) wcol[i] = e0 + (lane + 64 * i) / kRmWp;
+  const int dq = d / P, nsc = dq / kRmStage;  // staging steps per part
   const int kq = q * dq;
-  u32x4_t xg[4];
-  WRaw4 wg[8];
+  u32x4_t xg[XI];
+  WRaw4 wg[WI];
   auto load = [&](int sc) {
-    const int k = kq + 64 * sc;
+    const int k = kq + kRmStage * sc;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xg[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + k);
+    for (int i = 0; i < XI; ++i) xg[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + k);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < WI; ++i) {
       // (columns past the router: a row of zeros from the first one)
       const WRow row = router_row<BITS>(rw, wcol[i] < e_tot ? wcol[i] : 0, E, d);
-      wg[i] = router_raw4<BITS>(row, k + 4 * ((lane + 64 * i) & 15));
+      wg[i] = router_raw4<BITS>(row, k + 4 * ((lane + 64 * i) % kRmWp));
     }
   };
   load(0);
   f32x16_t acc = {};
   for (int sc = 0; sc < nsc; ++sc) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XI; ++i) {
       const int id = lane + 64 * i;
-      *reinterpret_cast<u32x4_t*>(xs + (id >> 3) * kRmXs + 16 * (id & 7)) = xg[i];
+      *reinterpret_cast<u32x4_t*>(xs + id / kRmXp * kRmXs + 16 * (id % kRmXp)) = xg[i];
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < WI; ++i) {
       const int id = lane + 64 * i;
       const float4 v = router_cvt4<BITS>(wg[i]);
-      *reinterpret_cast<f32x4_t*>(ws + (id >> 4) * kRmWs + 16 * (id & 15)) =
+      *reinterpret_cast<f32x4_t*>(ws + id / kRmWp * kRmWs + 16 * (id % kRmWp)) =
           wcol[i] < e_tot ? f32x4_t{v.x, v.y, v.z, v.w} : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     load(min(sc + 1, nsc - 1));
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kRmStage / 16; ++c) {
       const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + r * kRmXs + 32 * c + 16 * h);
       const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(ws + r * kRmWs + 64 * c + 32 * h);
       const f32x4_t w1 =
@@ -718,7 +727,7 @@ __global__ __launch_bounds__(64 * P) void router_logits_mfma_kernel(
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, s < 4 ? w0[s] : w1[s - 4], acc, 0, 0, 0);
       }
     }
-    __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();  // the staging regions are free: partial sums in their place
   f32x16_t* part = reinterpret_cast<f32x16_t*>(lds);
